@@ -1,0 +1,294 @@
+#!/usr/bin/env python3
+"""Benchmark of Dispatcher-Hybrid's hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+Headline (`value`): steady-state batch-1 bf16 greedy decode tok/s of the 292M model at 3840-4096
+context through FusedGraphedHybridDecoder (one HIP-graph replay per token, one gfx950 mixer kernel
+per tree layer). A step is one decode token; prefill and graph capture are outside the timed region
+(reference scripts/benchmark_decode.py:21-28 protocol). Also reported in the same JSON line:
+  decode_b16_*      lockstep batch-16 decode with temperature 0.8 / top-k 50 sampling
+  prefill_*         C2: 292M bf16 forward at B=1, T=1024, fused gates vs eager
+  forward_c5_*      C5: 292M bf16 forward at B=8, T=4096, fused gates vs eager (+ peak HBM)
+  gate_path_c5_*    one mixer layer at the C5 shape, fused vs eager
+  roofline          dh_decode_mixer_step: algorithmic bytes / HIP-event-timed launch duration
+  step_roofline     whole decode step: bf16 weight bytes per token x tok/s vs 8 TB/s
+  cpu_baseline      the oracle's eager torch decoder (reference algorithm) on the host CPU, fp32
+All inputs are synthetic (uniform token ids) and the weights are a random init of the released
+architecture. Rank 0 prints one JSON line.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "dispatcher-hybrid-2_amd"))
+
+METRIC = "decode tok/s @4096 ctx (batch 1 & 16) + prefill tok/s; % HBM roofline"
+N_PARAMS = 292_158_464                 # released config, tied head counted once
+W_BYTES = 2 * N_PARAMS                 # bf16 weight bytes streamed per decode step
+HBM_PEAK_GBS = 8000.0                  # MI355X HBM3E
+MFMA_BF16_TFLOPS = 2500.0              # MI355X dense bf16
+REF_DECODE_TOK_S = 525.1               # reference FusedGraphedHybridDecoder @3900 ctx (A6000, README.md:76-81)
+EOT = 50256
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=3840)
+    ap.add_argument("--skip-extras", action="store_true", help="decode batch-1 only")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=32)
+    ap.add_argument("--cpu-prompt", type=int, default=1024)
+    return ap.parse_args()
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def build_model(torch, dev):
+    from dispatcher_hybrid import DispatcherConfig, DispatcherHybridForCausalLM
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = DispatcherHybridForCausalLM(DispatcherConfig())
+    return model.to(torch.bfloat16).eval()
+
+
+def sync_barrier(torch):
+    torch.cuda.synchronize()
+
+
+def time_decode(torch, model, batch, prompt, warmup, steps, sample):
+    from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder
+    dev = next(model.parameters()).device
+    g = torch.Generator(device=dev).manual_seed(3 if batch == 1 else 4)
+    ids = torch.randint(0, EOT, (1, prompt), device=dev, generator=g).expand(batch, -1).contiguous()
+    dec = FusedGraphedHybridDecoder(model)
+    logits = dec.prefill(ids)[:, -1]
+    torch.manual_seed(5)
+
+    def next_tok(lg):
+        if not sample:
+            return lg.argmax(-1)
+        lg = lg.float() / 0.8
+        kth = torch.topk(lg, 50, dim=-1).values[:, -1:]
+        lg = lg.masked_fill(lg < kth, float("-inf"))
+        return torch.multinomial(torch.softmax(lg, dim=-1), 1)[:, 0]
+
+    for _ in range(warmup):
+        logits = dec.step(next_tok(logits))
+    sync_barrier(torch)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        logits = dec.step(next_tok(logits))
+    sync_barrier(torch)
+    dt = time.perf_counter() - t0
+    return batch * steps / dt, 1e3 * dt / steps, dec
+
+
+def time_forward(torch, model, ids, fused, reps=3):
+    model.enable_fused_gates(fused)
+    with torch.no_grad():
+        model(ids)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            model(ids)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / reps
+    peak = torch.cuda.max_memory_allocated()
+    model.enable_fused_gates(False)
+    return ids.numel() / dt, dt * 1e3, peak
+
+
+def time_mixer(torch, mixer, x, mask, fused, reps=5):
+    mixer.use_fused_gates = fused
+    with torch.no_grad():
+        mixer(x, mask)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            mixer(x, mask)
+        torch.cuda.synchronize()
+    mixer.use_fused_gates = False
+    return (time.perf_counter() - t0) / reps * 1e3
+
+
+def decode_kernel_roofline(torch, model, dec, copies=400):
+    """Average duration of dh_decode_mixer_step at B=1, t=4000 (all 12 levels live), each launch
+    bracketed by HIP events on the launch stream. The gate weights cycle through `copies` distinct
+    copies (> 256 MB in total, more than the MI355X last-level cache) so every launch streams its
+    weights from HBM as it does inside the decode step."""
+    from dispatcher_hybrid import fused_step
+    dev = next(model.parameters()).device
+    mx = next(b.mixer for b in model.blocks if hasattr(b, "mixer"))
+    cache = next(c for c in dec.inner.caches if hasattr(c, "V_ring"))
+    L, H, GH, d = mx.levels, mx.num_heads, mx.gate_hidden.out_features, model.config.d_model
+    Ws = [torch.stack([mx.gate_out, mx.forget_out, mx.reset_out]).clone() for _ in range(copies)]
+    bi, bf, br = mx.gate_out_bias, mx.forget_out_bias, mx.reset_out_bias
+    A = torch.randn(1, GH, device=dev, dtype=torch.bfloat16)
+    V0 = torch.randn(1, d, device=dev, dtype=torch.bfloat16)
+    Y = torch.empty(1, d, device=dev, dtype=torch.bfloat16)
+    t_buf = torch.full((1,), 4000, dtype=torch.long, device=dev)
+    B_hist = torch.zeros(1, 4096, GH, device=dev, dtype=torch.bfloat16)
+    rg = torch.zeros(1, 4096, L, H, device=dev, dtype=torch.bfloat16)
+    ring = torch.zeros(1, cache.S, d, device=dev, dtype=torch.bfloat16)
+    ws = fused_step.decode_workspace(1, L, H, dev)
+    stream = torch.cuda.current_stream()
+
+    def launch(i):
+        W = Ws[i % copies]
+        fused_step.decode_mixer_step(A, B_hist, W[0], W[1], W[2], bi, bf, br, t_buf, rg, ring, V0, Y, ws)
+
+    for i in range(32):
+        launch(i)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(copies)]
+    for i in range(copies):
+        ev[i][0].record(stream)
+        launch(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    avg_us = 1e3 * sum(a.elapsed_time(b) for a, b in ev) / copies
+    s = 2
+    B = 1
+    nbytes = 3 * L * H * GH * s + 3 * L * H * s + B * (L * GH + GH + 2 * L * H + 2 * L * d + 2 * d) * s
+    return nbytes, avg_us
+
+
+def cpu_baseline(torch, model, prompt, steps):
+    """The oracle's eager decoder (the reference's eager torch path) in fp32 on the host cores."""
+    sys.path.insert(0, ROOT)
+    from oracle import torch_eager
+    n = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(n)
+    sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    if "lm_head.weight" not in sd:
+        sd["lm_head.weight"] = sd["embedding.weight"]
+    spec = torch_eager.Spec(model.config)
+    g = torch.Generator().manual_seed(3)
+    ids = torch.randint(0, EOT, (1, prompt), generator=g)
+    dec = torch_eager.EagerDecoder(sd, spec)
+    logits = dec.prefill(ids)[:, -1]
+    logits = dec.step(logits.argmax(-1))                    # warm-up step
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        logits = dec.step(logits.argmax(-1))
+    dt = time.perf_counter() - t0
+    model_name = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model_name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": n, "kind": "port",
+            "sample": f"fp32 eager decode (oracle/torch_eager.EagerDecoder, reference algorithm), "
+                      f"batch 1, {steps} timed steps after a {prompt}-token prefill (per-token cost "
+                      f"is flat in context past the tree's O(log t) reads); host CPU: {model_name}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    model = build_model(torch, dev)
+    max_len = model.config.max_len
+    prompt = min(args.prompt, max_len - args.warmup - args.steps)
+    if prompt < 1:
+        raise SystemExit("--steps + --warmup exceed the 4096-token context")
+    log(f"C3 decode: B=1 prompt={prompt} warmup={args.warmup} steps={args.steps}")
+    tok_s, ms_step, dec1 = time_decode(torch, model, 1, prompt, args.warmup, args.steps, sample=False)
+    log(f"C3 decode: {tok_s:.1f} tok/s ({ms_step * 1e3:.1f} us/token)")
+    out = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": round(tok_s / REF_DECODE_TOK_S, 3), "dtype": "bf16",
+        "data": "synthetic: uniform random token ids; random init of the released 292M architecture",
+        "config": {"workload": "C3: 292M bf16 batch-1 greedy decode via FusedGraphedHybridDecoder, "
+                               f"prompt {prompt} then {args.warmup}+{args.steps} steps "
+                               f"(context {prompt}-{prompt + args.warmup + args.steps})",
+                   "batch": 1, "prompt_len": prompt, "max_len": max_len},
+        "vs_baseline_ref": "reference FusedGraphedHybridDecoder 525.1 tok/s @3900 ctx on A6000 (README.md:76-81)",
+    }
+    step_gbs = W_BYTES * tok_s / 1e9
+    out["step_roofline"] = {"bound": "hbm", "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+                            "what": "bf16 weight bytes per decode token (584,316,928 B) x tok/s"}
+
+    nbytes, avg_us = decode_kernel_roofline(torch, model, dec1)
+    achieved = nbytes / (avg_us * 1e-6) / 1e9
+    out["roofline"] = {"kernel": "dh_decode_mixer_step (decode_mixer_step_kernel<bf16>)", "bound": "hbm",
+                       "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                       "bytes_per_launch": nbytes, "avg_launch_us": round(avg_us, 3)}
+    log(f"decode mixer kernel: {avg_us:.2f} us/launch, {achieved:.0f} GB/s")
+    del dec1
+    torch.cuda.empty_cache()
+
+    if not args.skip_extras:
+        steps16 = min(args.steps, 128)
+        p16 = min(args.prompt, max_len - args.warmup - steps16)
+        tok16, ms16, d16 = time_decode(torch, model, 16, p16, args.warmup, steps16, sample=True)
+        del d16
+        log(f"C4 decode B=16: {tok16:.1f} tok/s")
+        out["decode_b16_tok_s"] = round(tok16, 1)
+        out["decode_b16_ms_per_step"] = round(ms16, 4)
+        out["decode_b16_step_roofline_frac"] = round(W_BYTES * tok16 / 16 / 1e9 / HBM_PEAK_GBS, 4)
+
+        g = torch.Generator(device=dev).manual_seed(2)
+        ids = torch.randint(0, 50257, (1, 1024), device=dev, generator=g)
+        f_tok, f_ms, _ = time_forward(torch, model, ids, True, reps=5)
+        e_tok, e_ms, _ = time_forward(torch, model, ids, False, reps=5)
+        flops = 2 * N_PARAMS * 1024          # weight matmuls; the mixer gate readout adds ~2%
+        out["prefill_tok_s"] = round(f_tok, 1)
+        out["prefill_eager_tok_s"] = round(e_tok, 1)
+        out["prefill_speedup_vs_eager"] = round(f_tok / e_tok, 3)
+        out["prefill_mfma_frac"] = round(flops / (f_ms * 1e-3) / 1e12 / MFMA_BF16_TFLOPS, 4)
+        log(f"C2 prefill: fused {f_tok:.0f} tok/s, eager {e_tok:.0f} tok/s")
+
+        g = torch.Generator(device=dev).manual_seed(6)
+        ids = torch.randint(0, 50257, (8, 4096), device=dev, generator=g)
+        ids[:, 1000] = EOT
+        f_tok, f_ms, f_peak = time_forward(torch, model, ids, True, reps=2)
+        e_tok, e_ms, e_peak = time_forward(torch, model, ids, False, reps=2)
+        out["forward_c5_tok_s"] = round(f_tok, 1)
+        out["forward_c5_eager_tok_s"] = round(e_tok, 1)
+        out["forward_c5_speedup_vs_eager"] = round(f_tok / e_tok, 3)
+        out["forward_c5_peak_gb"] = round(f_peak / 1e9, 2)
+        out["forward_c5_eager_peak_gb"] = round(e_peak / 1e9, 2)
+        log(f"C5 forward: fused {f_tok:.0f} tok/s ({f_peak / 1e9:.1f} GB), eager {e_tok:.0f} tok/s ({e_peak / 1e9:.1f} GB)")
+
+        mixer = next(b.mixer for b in model.blocks if hasattr(b, "mixer"))
+        x = torch.randn(8, 4096, 1024, device=dev, dtype=torch.bfloat16, generator=g)
+        mask = model._tree_mask(ids, 4096)
+        fm = time_mixer(torch, mixer, x, mask, True)
+        em = time_mixer(torch, mixer, x, mask, False)
+        out["gate_path_c5_fused_ms"] = round(fm, 3)
+        out["gate_path_c5_eager_ms"] = round(em, 3)
+        out["gate_path_c5_speedup"] = round(em / fm, 2)
+        log(f"C5 mixer layer: fused {fm:.2f} ms, eager {em:.2f} ms")
+
+    if not args.no_cpu_baseline:
+        log("CPU baseline ...")
+        out["cpu_baseline"] = cpu_baseline(torch, model, args.cpu_prompt, args.cpu_steps)
+        log(f"CPU baseline: {out['cpu_baseline']['value']} tok/s on {out['cpu_baseline']['cores']} threads")
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,73 @@
+// Shared device and host helpers for libdh_mixer.so (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dh_mixer.h"
+
+// ----------------------------------------------------------------------------------------------
+// host side: thread-local error message + status helpers (defined in dh_abi.hip)
+// ----------------------------------------------------------------------------------------------
+int dh_fail(int status, const char* fmt, ...);
+int dh_check_launch(const char* what);
+
+#define DH_REQUIRE(cond, status, ...)            \
+  do {                                           \
+    if (!(cond)) return dh_fail((status), __VA_ARGS__); \
+  } while (0)
+
+// ----------------------------------------------------------------------------------------------
+// element types: fp32 and bf16 (stored as raw uint16 bits)
+// ----------------------------------------------------------------------------------------------
+typedef uint16_t bf16_t;
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t x) { return __uint_as_float(((uint32_t)x) << 16); }
+
+// round-to-nearest-even fp32 -> bf16; NaN stays NaN (quiet bit set)
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (bf16_t)((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  __device__ __forceinline__ static float load(const float* p) { return *p; }
+  __device__ __forceinline__ static void store(float* p, float v) { *p = v; }
+  __device__ __forceinline__ static float round(float v) { return v; }
+};
+template <> struct Elem<bf16_t> {
+  __device__ __forceinline__ static float load(const bf16_t* p) { return bf16_to_f32(*p); }
+  __device__ __forceinline__ static void store(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+  __device__ __forceinline__ static float round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+};
+
+// Load 4 consecutive elements as fp32 (8-byte load for bf16, 16-byte for fp32). p must be aligned
+// to 4 elements.
+__device__ __forceinline__ void load4(const float* p, float (&o)[4]) {
+  float4 v = *reinterpret_cast<const float4*>(p);
+  o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+}
+__device__ __forceinline__ void load4(const bf16_t* p, float (&o)[4]) {
+  uint2 v = *reinterpret_cast<const uint2*>(p);
+  o[0] = __uint_as_float(v.x << 16);
+  o[1] = __uint_as_float(v.x & 0xffff0000u);
+  o[2] = __uint_as_float(v.y << 16);
+  o[3] = __uint_as_float(v.y & 0xffff0000u);
+}
+
+// logistic function from the hardware exp: 1 / (1 + e^-x). Saturates to exactly 1.0 for x >= ~17
+// and to exactly 0.0 for x <= -~104 (e^-x overflows to +inf).
+__device__ __forceinline__ float dh_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// full-wavefront (64 lanes) sum; every lane gets the result
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__host__ __device__ __forceinline__ int64_t ring_offset(int j) { return ((int64_t)2 << j) - 2; }
+__host__ __device__ __forceinline__ int64_t ring_mask(int j) { return ((int64_t)2 << j) - 1; }

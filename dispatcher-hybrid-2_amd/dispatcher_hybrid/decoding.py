@@ -1,0 +1,410 @@
+"""Incremental decoders: per-token cost O(log t) in the tree layers, flat in context.
+
+Same classes, constructor arguments and public behaviour as the reference
+(reference dispatcher_hybrid/decoding.py:50-488):
+
+    IncrementalDecoder          exact, eager torch ops
+    GraphedHybridDecoder        the whole step captured once as a HIP graph and replayed per token
+    FusedGraphedHybridDecoder   graphed, with each tree layer's gate readouts + level recurrence as
+                                ONE gfx950 kernel (dispatcher_hybrid.fused_step.decode_mixer_step)
+
+All rows of a batch advance in lockstep (one shared position t). Tree-layer state per layer:
+    B_hist  (B, Tmax, gh)     W1s.h1 of every position (the level-l source row is t - 2^l)
+    rg_hist (B, Tmax, L, H)   transmit gates, stored at their source position
+    V_ring  (B, S, d)         ring j (offset 2^(j+1)-2, 2^(j+1) slots) holds the state entering
+                              level j for the last 2^(j+1) positions; S = 2^(L+1) - 2
+Attention layers keep a (B, H, Tmax, hd) K/V cache with RoPE applied at the absolute position.
+"""
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+from .modeling_dispatcher import (AttentionBlock, active_levels, causal_window_attention,
+                                  level_gate_matmul, rope_rotate)
+
+
+class _TreeLayerCache:
+    """Decode state of one tree layer (layout: reference decoding.py:50-76)."""
+
+    def __init__(self, mixer, batch, max_len, device, dtype):
+        gh = mixer.gate_hidden.out_features
+        self.L = L = mixer.levels
+        self.H = H = mixer.num_heads
+        self.hd = mixer.head_dim
+        self.B_hist = torch.zeros(batch, max_len, gh, device=device, dtype=dtype)
+        self.rg_hist = torch.zeros(batch, max_len, L, H, device=device, dtype=dtype)
+        self.S = (2 << L) - 2
+        self.V_ring = torch.zeros(batch, self.S, H * self.hd, device=device, dtype=dtype)
+        self.offsets = torch.tensor([(2 << j) - 2 for j in range(L)], device=device)
+        self.masks = torch.tensor([(2 << j) - 1 for j in range(L)], device=device)
+
+    def slot(self, j, p):
+        """Ring slot of position p (int or tensor) at level j."""
+        return ((2 << j) - 2) + (p & ((2 << j) - 1))
+
+    def write_slab(self, j, slab):
+        """Store the level-j states of a (B, T, d) prefill slab. Only the last 2^(j+1) positions
+        can still be read, and consecutive positions occupy distinct slots."""
+        T = slab.shape[1]
+        p0 = max(0, T - (2 << j))
+        pos = torch.arange(p0, T, device=slab.device)
+        self.V_ring[:, self.slot(j, pos)] = slab[:, p0:]
+
+
+class _AttnCache:
+    def __init__(self, attn, batch, max_len, device, dtype):
+        self.k = torch.zeros(batch, attn.num_heads, max_len, attn.head_dim, device=device, dtype=dtype)
+        self.v = torch.zeros_like(self.k)
+        # materialised RoPE tables: graph capture needs stable device tensors to index
+        self.rope_cos, self.rope_sin = attn.rope_tables(max_len, device, dtype)
+
+
+def _check_single_document(model, idx):
+    """The decoders apply the wrap mask only, not the doc-reset mask, so a prompt that spans
+    documents would diverge from the parallel forward (reference decoding.py:89-98)."""
+    if getattr(model.config, "doc_reset", False):
+        if bool((idx == model.config.eot_token).any()):
+            raise ValueError(
+                f"prompt contains the document separator (token {model.config.eot_token}) and this "
+                f"model was trained with doc_reset=True; the incremental decoders assume a single "
+                f"document. Remove the separator, or use model.generate().")
+
+
+class IncrementalDecoder:
+    """Exact per-token decoder on eager torch ops.
+
+        dec = IncrementalDecoder(model)
+        logits = dec.prefill(ids)     # ids (T,) or (B, T) -> (T, V) or (B, T, V)
+        logits = dec.step(tokens)     # (B,) or scalar -> (B, V) or (V,)
+    """
+
+    def __init__(self, model, max_len=None, dtype=None):
+        self.m = model
+        self.max_len = max_len or model.config.max_len
+        param_dtype = next(model.parameters()).dtype
+        # caches and activations share the weights' dtype; cast the model to pick precision
+        if dtype is not None and dtype != param_dtype:
+            raise ValueError(f"decoder dtype {dtype} != model dtype {param_dtype}; cast the "
+                             f"model first, e.g. model.to(torch.bfloat16)")
+        self.dtype = param_dtype
+        self.device = next(model.parameters()).device
+        self.caches = None
+        self.batch = None
+        self.t = 0
+
+    def _alloc(self, batch):
+        if self.caches is not None and self.batch == batch:
+            return
+        self.batch = batch
+        self.caches = [
+            _AttnCache(blk.attn, batch, self.max_len, self.device, self.dtype)
+            if isinstance(blk, AttentionBlock) else
+            _TreeLayerCache(blk.mixer, batch, self.max_len, self.device, self.dtype)
+            for blk in self.m.blocks]
+
+    # ---------- tree layer ----------
+    def _tree_prefill(self, blk, cache, x):
+        """Parallel mixer over the prompt that also fills B_hist, rg_hist and the rings
+        (reference decoding.py:143-185)."""
+        mx = blk.mixer
+        Bb, T = x.shape[0], x.shape[1]
+        L, H, hd = cache.L, cache.H, cache.hd
+        h1 = blk.norm1(x)
+        A = mx.gate_hidden(h1)
+        Bs = mx.gate_hidden_src(h1)
+        cache.B_hist[:, :T] = Bs
+        n_lv = active_levels(L, T)
+        V = mx.linear_in(h1).view(Bb, T, H, hd)
+        cache.write_slab(0, V.reshape(Bb, T, H * hd))
+        t = torch.arange(T, device=x.device)
+        wrap = torch.stack([(t >= (1 << l)) for l in range(n_lv)], dim=1).to(x.dtype).unsqueeze(-1)
+        lagged = torch.stack([torch.roll(Bs, shifts=1 << l, dims=1) for l in range(n_lv)], dim=2)
+        hidden = torch.relu(A.unsqueeze(2) + lagged * wrap) ** 2
+        pre_i, pre_f, pre_r = (level_gate_matmul(hidden, W[:n_lv]) + b[:n_lv]
+                               for W, b in mx._gate_params())
+        ig = torch.sigmoid(pre_i) * wrap
+        fg = torch.sigmoid(pre_f) * wrap + (1.0 - wrap)
+        rg = torch.sigmoid(pre_r)
+        cache.rg_hist[:, :T, :n_lv] = rg
+        if n_lv < L:
+            # levels beyond the prompt's horizon send no message yet, but later tokens read the
+            # transmit gates of these positions at those levels
+            hid0 = torch.relu(A) ** 2
+            for l in range(n_lv, L):
+                cache.rg_hist[:, :T, l] = torch.sigmoid(F.linear(hid0, mx.reset_out[l]) + mx.reset_out_bias[l])
+        for l in range(n_lv):
+            msg = torch.roll(rg[:, :, l].unsqueeze(-1) * V, shifts=1 << l, dims=1)
+            V = fg[:, :, l].unsqueeze(-1) * V + ig[:, :, l].unsqueeze(-1) * msg
+            if l + 1 < L:
+                cache.write_slab(l + 1, V.reshape(Bb, T, H * hd))
+        for j in range(n_lv + 1, L):                  # beyond the horizon the state passes through
+            cache.write_slab(j, V.reshape(Bb, T, H * hd))
+        x = x + mx.linear_out(V.reshape(Bb, T, H * hd))
+        return x + blk.ffn(blk.norm2(x))
+
+    def _tree_step(self, blk, cache, x, t):
+        """One position through a tree layer (reference decoding.py:187-222)."""
+        mx = blk.mixer
+        Bb = x.shape[0]
+        L, H, hd = cache.L, cache.H, cache.hd
+        h1 = blk.norm1(x)
+        A = mx.gate_hidden(h1)
+        cache.B_hist[:, t] = mx.gate_hidden_src(h1)
+        V = mx.linear_in(h1).view(Bb, H, hd)
+        cache.V_ring[:, cache.slot(0, t)] = V.reshape(Bb, -1)
+        lev = torch.arange(L, device=x.device)
+        src = t - torch.pow(2, lev)
+        ok = src >= 0
+        src_c = src.clamp(min=0)
+        okf = ok.view(1, L, 1)
+        hid = torch.relu(A.unsqueeze(1) + cache.B_hist[:, src_c] * okf) ** 2        # (B, L, gh)
+        gates = [level_gate_matmul(hid.unsqueeze(1), W)[:, 0] + b for W, b in mx._gate_params()]
+        i_ = torch.sigmoid(gates[0]) * okf
+        f_ = torch.sigmoid(gates[1])
+        f_ = f_ * okf + (~okf).to(f_.dtype)                                         # masked: f = 1
+        r_ = torch.sigmoid(gates[2])
+        cache.rg_hist[:, t] = r_
+        rg_src = cache.rg_hist[:, src_c, lev]                                       # (B, L, H)
+        V_src = cache.V_ring[:, cache.offsets + (src_c & cache.masks)].view(Bb, L, H, hd)
+        msg = rg_src.unsqueeze(-1) * V_src
+        for l in range(L):
+            V = f_[:, l].unsqueeze(-1) * V + i_[:, l].unsqueeze(-1) * msg[:, l]
+            if l + 1 < L:
+                cache.V_ring[:, cache.slot(l + 1, t)] = V.reshape(Bb, -1)
+        x = x + mx.linear_out(V.reshape(Bb, -1))
+        return x + blk.ffn(blk.norm2(x))
+
+    # ---------- attention layer ----------
+    def _attn_prefill(self, blk, cache, x):
+        at = blk.attn
+        Bb, T = x.shape[0], x.shape[1]
+        h1 = blk.norm1(x)
+        shape = (Bb, T, at.num_heads, at.head_dim)
+        q = at.apply_rope(at.linear_q(h1).view(shape).transpose(1, 2), T)
+        k = at.apply_rope(at.linear_k(h1).view(shape).transpose(1, 2), T)
+        v = at.linear_v(h1).view(shape).transpose(1, 2)
+        cache.k[:, :, :T] = k
+        cache.v[:, :, :T] = v
+        window = at.window if 0 < at.window < T else 0
+        y = causal_window_attention(q, k, v, window)
+        x = x + at.linear_out(y.transpose(1, 2).reshape(Bb, T, at.embed_dim))
+        return x + blk.ffn(blk.norm2(x))
+
+    def _attn_step(self, blk, cache, x, t):
+        at = blk.attn
+        Bb = x.shape[0]
+        h1 = blk.norm1(x)
+        cos, sin = cache.rope_cos[t], cache.rope_sin[t]
+        q = rope_rotate(at.linear_q(h1).view(Bb, at.num_heads, at.head_dim), cos, sin)
+        cache.k[:, :, t] = rope_rotate(at.linear_k(h1).view(Bb, at.num_heads, at.head_dim), cos, sin)
+        cache.v[:, :, t] = at.linear_v(h1).view(Bb, at.num_heads, at.head_dim)
+        lo = max(0, t + 1 - at.window) if at.window > 0 else 0
+        k = cache.k[:, :, lo:t + 1]
+        v = cache.v[:, :, lo:t + 1]
+        scores = torch.matmul(k, q.unsqueeze(-1)).squeeze(-1) / math.sqrt(at.head_dim)
+        att = torch.softmax(scores, dim=-1)                      # model-dtype softmax, as eager
+        y = torch.matmul(att.unsqueeze(2), v).squeeze(2).reshape(Bb, -1)
+        x = x + at.linear_out(y)
+        return x + blk.ffn(blk.norm2(x))
+
+    # ---------- public ----------
+    @torch.no_grad()
+    def prefill(self, idx):
+        """idx: (T,) or (B, T) token ids. Returns (T, vocab) or (B, T, vocab) logits."""
+        self._squeeze = idx.dim() == 1
+        ids = idx.view(1, -1) if self._squeeze else idx
+        _check_single_document(self.m, ids)
+        if ids.shape[1] > self.max_len:
+            raise ValueError(f"prompt of {ids.shape[1]} exceeds max_len {self.max_len}")
+        self._alloc(ids.shape[0])
+        x = self.m.embedding(ids).to(self.dtype)
+        for blk, cache in zip(self.m.blocks, self.caches):
+            x = (self._attn_prefill(blk, cache, x) if isinstance(blk, AttentionBlock)
+                 else self._tree_prefill(blk, cache, x))
+        self.t = ids.shape[1]
+        out = self.m.lm_head(self.m.norm_out(x))
+        return out[0] if self._squeeze else out
+
+    @torch.no_grad()
+    def step(self, tokens):
+        """tokens: scalar, (1,) or (B,). Returns (vocab,) or (B, vocab) logits."""
+        if self.t >= self.max_len:
+            raise ValueError(f"context exhausted at max_len {self.max_len}")
+        t = self.t
+        toks = tokens.view(-1)
+        if toks.shape[0] != self.batch and not (self.batch == 1 and toks.shape[0] == 1):
+            raise ValueError(f"got {toks.shape[0]} tokens for batch {self.batch}")
+        x = self.m.embedding(toks).to(self.dtype)
+        for blk, cache in zip(self.m.blocks, self.caches):
+            x = (self._attn_step(blk, cache, x, t) if isinstance(blk, AttentionBlock)
+                 else self._tree_step(blk, cache, x, t))
+        self.t = t + 1
+        out = self.m.lm_head(self.m.norm_out(x))
+        return out[0] if self._squeeze else out
+
+
+# ==============================================================================================
+# Graph-replayed decoders. The per-token work is small and launch-bound, so the whole step is
+# captured once (after an eager prefill) and replayed per token. The position lives on the device
+# (t_buf) so one graph serves every position; attention reads the full padded cache under a
+# validity mask so its shapes are capture-stable.
+# ==============================================================================================
+
+
+class _GraphedBase:
+    def _capture(self, step_fn):
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):                      # warm-ups: allocator pools, library handles
+                step_fn()
+                self.t_buf.fill_(self.t)            # undo the warm-up's position advance
+        torch.cuda.current_stream().wait_stream(side)
+        with torch.cuda.graph(g):
+            step_fn()
+        self.graph = g
+
+    @torch.no_grad()
+    def step(self, tokens):
+        if self.t >= self.max_len:
+            raise ValueError(f"context exhausted at max_len {self.max_len}")
+        self.token_buf.copy_(tokens.view(-1))
+        self.graph.replay()
+        self.t += 1
+        # the graph overwrites logits_out on the next replay: hand out a copy
+        out = self.logits_out.clone()
+        return out[0] if self._squeeze else out
+
+
+class GraphedHybridDecoder(_GraphedBase):
+    """Eager prefill, then one HIP-graph replay per generated token."""
+
+    def __init__(self, model, max_len=None, dtype=None):
+        if not torch.cuda.is_available():
+            raise RuntimeError("GraphedHybridDecoder requires a GPU")
+        self.inner = IncrementalDecoder(model, max_len, dtype=dtype)
+        self.m = model
+        self.max_len = self.inner.max_len
+        self.dtype = self.inner.dtype
+        self.t = 0
+
+    @torch.no_grad()
+    def prefill(self, idx):
+        out = self.inner.prefill(idx)
+        self._squeeze = self.inner._squeeze
+        self.t = self.inner.t
+        dev = next(self.m.parameters()).device
+        Bb = self.inner.batch
+        self.token_buf = torch.zeros(Bb, dtype=torch.long, device=dev)
+        self.t_buf = torch.full((1,), self.t, dtype=torch.long, device=dev)
+        self.logits_out = torch.zeros(Bb, self.m.lm_head.out_features, device=dev, dtype=self.dtype)
+        self.arangeT = torch.arange(self.max_len, device=dev)
+        self._prepare()
+        self._capture(self._step_all)
+        return out
+
+    def _prepare(self):
+        # level-major transposed gate weights (L, gh, H) for the batched readout bmm
+        self._gate_wt = {}
+        for i, blk in enumerate(self.m.blocks):
+            if hasattr(blk, "mixer"):
+                self._gate_wt[i] = [W.transpose(1, 2).contiguous() for W, _ in blk.mixer._gate_params()]
+
+    def _tree_step_g(self, i, blk, cache, x):
+        mx = blk.mixer
+        Bb = x.shape[0]
+        L, H, hd = cache.L, cache.H, cache.hd
+        dev = x.device
+        h1 = blk.norm1(x)
+        A = mx.gate_hidden(h1)
+        cache.B_hist.index_copy_(1, self.t_buf, mx.gate_hidden_src(h1).unsqueeze(1))
+        V = mx.linear_in(h1).view(Bb, H, hd)
+        lev = torch.arange(L, device=dev)
+        src = self.t_buf - torch.pow(2, lev)
+        ok = src >= 0
+        src_c = src.clamp(min=0)
+        okf = ok.view(1, L, 1)
+        hid = torch.relu(A.unsqueeze(1) + cache.B_hist.index_select(1, src_c) * okf) ** 2  # (B, L, gh)
+        hid_l = hid.transpose(0, 1).contiguous()                                          # (L, B, gh)
+        (_, bi), (_, bf), (_, br) = mx._gate_params()
+        wi, wf, wr = self._gate_wt[i]
+        i_ = torch.sigmoid(torch.bmm(hid_l, wi).transpose(0, 1) + bi) * okf
+        f_ = torch.sigmoid(torch.bmm(hid_l, wf).transpose(0, 1) + bf)
+        f_ = f_ * okf + (~okf).to(f_.dtype)
+        r_ = torch.sigmoid(torch.bmm(hid_l, wr).transpose(0, 1) + br)
+        cache.rg_hist.index_copy_(1, self.t_buf, r_.unsqueeze(1))
+        rg_src = cache.rg_hist.index_select(1, src_c)[:, lev, lev]
+        V_src = cache.V_ring.index_select(1, cache.offsets + (src_c & cache.masks)).view(Bb, L, H, hd)
+        msg = rg_src.unsqueeze(-1) * V_src
+        levs = [V.reshape(Bb, -1)]
+        for l in range(L):                          # unrolled at capture time
+            V = f_[:, l].unsqueeze(-1) * V + i_[:, l].unsqueeze(-1) * msg[:, l]
+            if l + 1 < L:
+                levs.append(V.reshape(Bb, -1))
+        slots_w = cache.offsets + (self.t_buf & cache.masks)
+        cache.V_ring.index_copy_(1, slots_w, torch.stack(levs, dim=1))
+        x = x + mx.linear_out(V.reshape(Bb, -1))
+        return x + blk.ffn(blk.norm2(x))
+
+    def _attn_step_g(self, blk, cache, x):
+        at = blk.attn
+        Bb = x.shape[0]
+        h1 = blk.norm1(x)
+        cos = cache.rope_cos.index_select(0, self.t_buf)[0]
+        sin = cache.rope_sin.index_select(0, self.t_buf)[0]
+        q = rope_rotate(at.linear_q(h1).view(Bb, at.num_heads, at.head_dim), cos, sin)
+        k_new = rope_rotate(at.linear_k(h1).view(Bb, at.num_heads, at.head_dim), cos, sin)
+        cache.k.index_copy_(2, self.t_buf, k_new.unsqueeze(2))
+        cache.v.index_copy_(2, self.t_buf, at.linear_v(h1).view(Bb, at.num_heads, at.head_dim).unsqueeze(2))
+        valid = self.arangeT <= self.t_buf
+        if at.window > 0:
+            valid = valid & (self.arangeT > self.t_buf - at.window)
+        scores = torch.matmul(cache.k, q.unsqueeze(-1)).squeeze(-1) / math.sqrt(at.head_dim)  # (B, H, Tmax)
+        scores = scores.masked_fill(~valid.view(1, 1, -1), float("-inf"))
+        att = torch.softmax(scores.float(), dim=-1).to(x.dtype)
+        y = torch.matmul(att.unsqueeze(2), cache.v).squeeze(2).reshape(Bb, -1)
+        x = x + at.linear_out(y)
+        return x + blk.ffn(blk.norm2(x))
+
+    def _step_all(self):
+        x = self.m.embedding(self.token_buf).to(self.dtype)
+        for i, (blk, cache) in enumerate(zip(self.m.blocks, self.inner.caches)):
+            x = (self._attn_step_g(blk, cache, x) if isinstance(blk, AttentionBlock)
+                 else self._tree_step_g(i, blk, cache, x))
+        self.logits_out.copy_(self.m.lm_head(self.m.norm_out(x)))
+        self.t_buf.add_(1)
+
+
+class FusedGraphedHybridDecoder(GraphedHybridDecoder):
+    """Graphed decoder whose tree step is one gfx950 kernel per layer (gate readouts for every
+    level + the level recurrence over the rings), in place of ~15 torch ops. Same caches, same
+    graph harness. Raises ImportError when the kernel library is missing."""
+
+    def __init__(self, model, max_len=None, dtype=None):
+        from . import fused_step                          # loads libdh_mixer.so
+        self._fused_step = fused_step
+        super().__init__(model, max_len, dtype)
+
+    def _prepare(self):
+        dev = next(self.m.parameters()).device
+        mix0 = next(b.mixer for b in self.m.blocks if hasattr(b, "mixer"))
+        Bb = self.inner.batch
+        # per-call scratch shared by every layer (stream-ordered; left zeroed by each call)
+        self.workspace = self._fused_step.decode_workspace(Bb, mix0.levels, mix0.num_heads, dev)
+        self.y_buf = torch.zeros(Bb, self.m.config.d_model, device=dev, dtype=self.dtype)
+
+    def _tree_step_g(self, i, blk, cache, x):
+        mx = blk.mixer
+        h1 = blk.norm1(x)
+        A = mx.gate_hidden(h1)
+        cache.B_hist.index_copy_(1, self.t_buf, mx.gate_hidden_src(h1).unsqueeze(1))
+        V0 = mx.linear_in(h1)
+        self._fused_step.decode_mixer_step(
+            A, cache.B_hist, mx.gate_out, mx.forget_out, mx.reset_out,
+            mx.gate_out_bias, mx.forget_out_bias, mx.reset_out_bias, self.t_buf,
+            cache.rg_hist, cache.V_ring, V0, self.y_buf, self.workspace)
+        x = x + mx.linear_out(self.y_buf)
+        return x + blk.ffn(blk.norm2(x))

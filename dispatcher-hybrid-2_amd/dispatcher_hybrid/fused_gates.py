@@ -1,0 +1,208 @@
+"""Fused gate pipeline of the parallel (prefill / training) forward, on gfx950 HIP kernels.
+
+    model.enable_fused_gates()
+
+Drop-in for the reference module of the same name (reference dispatcher_hybrid/fused_gates.py):
+the custom ops ``dispatcher::gate_preacts_fwd`` / ``dispatcher::gate_preacts_bwd`` keep their
+schemas (reference :186-190, :225-229), fake implementations and autograd registration, and
+``fused_gate_preacts`` keeps its signature (reference :307-314). They compute
+
+    hidden = relu(A + m * roll(B, 2^l))^2            (never materialised)
+    pre_x  = hidden . W_x[l] + b_x[l]                x in {i, f, r}
+
+in one kernel (``dh_gate_preacts_fwd``). Dtype rule: bf16 (and fp16) inputs compute in bf16 with
+fp32 accumulation and return bf16, like the reference; fp32 inputs compute and return fp32 (the
+reference op rounds fp32 models to bf16, which cannot meet a 1e-4 relative tolerance).
+
+Also registered here: ``dispatcher::level_scan_fwd``, the sigmoid/mask/level-scan half of the
+mixer (``dh_level_scan_fwd``), which the reference runs as eager torch ops
+(reference dispatcher_hybrid/modeling_dispatcher.py:86-88, 111-121).
+
+Importing this module loads the kernel library and raises ImportError if it is missing.
+"""
+
+from typing import List, Optional
+
+import torch
+
+from . import _hip
+
+
+def _compute_dtype(x):
+    return torch.float32 if x.dtype == torch.float32 else torch.bfloat16
+
+
+def _mask_view(mask, cd):
+    """(b, T, n_lv) mask in dtype `cd` with a unit innermost stride (no copy when it already is)."""
+    if mask is None:
+        return None, 0, 0
+    m = mask.to(cd)
+    if m.stride(-1) != 1:
+        m = m.contiguous()
+    return m, m.stride(0), m.stride(1)
+
+
+# ---------------------------------------------------------------------------------------------
+# dispatcher::gate_preacts_fwd
+# ---------------------------------------------------------------------------------------------
+@torch.library.custom_op("dispatcher::gate_preacts_fwd", mutates_args=(), device_types="cuda")
+def _gate_preacts_fwd_op(A: torch.Tensor, B: torch.Tensor,
+                         Wi: torch.Tensor, Wf: torch.Tensor, Wr: torch.Tensor,
+                         bi: torch.Tensor, bf: torch.Tensor, br: torch.Tensor,
+                         n_lv: int, mask: Optional[torch.Tensor]) -> List[torch.Tensor]:
+    b, T, GH = A.shape
+    H = Wi.shape[1]
+    cd = _compute_dtype(A)
+    outs = [torch.empty(b, T, n_lv, H, device=A.device, dtype=cd) for _ in range(3)]
+    if b == 0 or T == 0:
+        return outs
+    A_ = A.contiguous().to(cd)
+    B_ = B.contiguous().to(cd)
+    Wi_, Wf_, Wr_ = (w[:n_lv].contiguous().to(cd) for w in (Wi, Wf, Wr))
+    bi_, bf_, br_ = (v[:n_lv].contiguous().float() for v in (bi, bf, br))
+    m_, smb, smt = _mask_view(mask, cd)
+    p = _hip.ptr
+    st = _hip.lib.dh_gate_preacts_fwd(
+        _hip.dtype_code(cd), p(A_), p(B_), A_.stride(0), A_.stride(1),
+        p(Wi_), p(Wf_), p(Wr_), Wi_.stride(0), Wi_.stride(1),
+        p(bi_), p(bf_), p(br_), p(m_), smb, smt,
+        p(outs[0]), p(outs[1]), p(outs[2]), b, T, GH, H, n_lv, _hip.stream_handle(A.device))
+    _hip.check(st, "dispatcher::gate_preacts_fwd")
+    return outs
+
+
+@_gate_preacts_fwd_op.register_fake
+def _(A, B, Wi, Wf, Wr, bi, bf, br, n_lv, mask):
+    b, T, _ = A.shape
+    H = Wi.shape[1]
+    cd = _compute_dtype(A)
+    return [A.new_empty(b, T, n_lv, H, dtype=cd) for _ in range(3)]
+
+
+# ---------------------------------------------------------------------------------------------
+# dispatcher::gate_preacts_bwd
+# ---------------------------------------------------------------------------------------------
+@torch.library.custom_op("dispatcher::gate_preacts_bwd", mutates_args=(), device_types="cuda")
+def _gate_preacts_bwd_op(A: torch.Tensor, B: torch.Tensor,
+                         Wi: torch.Tensor, Wf: torch.Tensor, Wr: torch.Tensor,
+                         dPi: torch.Tensor, dPf: torch.Tensor, dPr: torch.Tensor,
+                         n_lv: int, mask: Optional[torch.Tensor]) -> List[torch.Tensor]:
+    b, T, GH = A.shape
+    H = Wi.shape[1]
+    dev = A.device
+    f32 = torch.float32
+    outs = [torch.empty(b, T, GH, device=dev, dtype=f32), torch.empty(b, T, GH, device=dev, dtype=f32)]
+    outs += [torch.empty(n_lv, H, GH, device=dev, dtype=f32) for _ in range(3)]
+    outs += [torch.empty(n_lv, H, device=dev, dtype=f32) for _ in range(3)]
+    if b == 0 or T == 0:
+        for o in outs:
+            o.zero_()
+        return outs
+    cd = _compute_dtype(A)
+    A_ = A.contiguous().to(cd)
+    B_ = B.contiguous().to(cd)
+    Wi_, Wf_, Wr_ = (w[:n_lv].contiguous().to(cd) for w in (Wi, Wf, Wr))
+    dPi_, dPf_, dPr_ = (g.contiguous().to(cd) for g in (dPi, dPf, dPr))
+    m_, smb, smt = _mask_view(mask, cd)
+    p = _hip.ptr
+    st = _hip.lib.dh_gate_preacts_bwd(
+        _hip.dtype_code(cd), p(A_), p(B_), A_.stride(0), A_.stride(1),
+        p(Wi_), p(Wf_), p(Wr_), Wi_.stride(0), Wi_.stride(1),
+        p(dPi_), p(dPf_), p(dPr_), p(m_), smb, smt,
+        *[p(o) for o in outs], b, T, GH, H, n_lv, _hip.stream_handle(dev))
+    _hip.check(st, "dispatcher::gate_preacts_bwd")
+    return outs
+
+
+@_gate_preacts_bwd_op.register_fake
+def _(A, B, Wi, Wf, Wr, dPi, dPf, dPr, n_lv, mask):
+    b, T, GH = A.shape
+    H = Wi.shape[1]
+    f32 = torch.float32
+    return ([A.new_empty(b, T, GH, dtype=f32), A.new_empty(b, T, GH, dtype=f32)]
+            + [A.new_empty(n_lv, H, GH, dtype=f32) for _ in range(3)]
+            + [A.new_empty(n_lv, H, dtype=f32) for _ in range(3)])
+
+
+def _setup_context(ctx, inputs, output):
+    A, B, Wi, Wf, Wr, bi, bf, br, n_lv, mask = inputs
+    ctx.save_for_backward(A, B, Wi, Wf, Wr)
+    ctx.n_lv = n_lv
+    ctx.mask = mask
+    ctx.dtypes = (A.dtype, B.dtype, Wi.dtype, bi.dtype)
+
+
+def _backward(ctx, grads):
+    dPi, dPf, dPr = grads
+    A, B, Wi, Wf, Wr = ctx.saved_tensors
+    n_lv = ctx.n_lv
+    z = lambda g: g if g is not None else torch.zeros(
+        A.shape[0], A.shape[1], n_lv, Wi.shape[1], device=A.device, dtype=_compute_dtype(A))
+    dA, dB, dWi, dWf, dWr, dbi, dbf, dbr = torch.ops.dispatcher.gate_preacts_bwd(
+        A, B, Wi, Wf, Wr, z(dPi), z(dPf), z(dPr), n_lv, ctx.mask)
+    a_dt, b_dt, w_dt, bias_dt = ctx.dtypes
+    levels = Wi.shape[0]
+
+    def pad(g, dt):
+        if g.shape[0] == levels:
+            return g.to(dt)
+        out = torch.zeros((levels,) + tuple(g.shape[1:]), device=g.device, dtype=dt)
+        out[:n_lv] = g
+        return out
+
+    return (dA.to(a_dt), dB.to(b_dt), pad(dWi, w_dt), pad(dWf, w_dt), pad(dWr, w_dt),
+            pad(dbi, bias_dt), pad(dbf, bias_dt), pad(dbr, bias_dt), None, None)
+
+
+torch.library.register_autograd("dispatcher::gate_preacts_fwd", _backward, setup_context=_setup_context)
+
+
+def fused_gate_preacts(A, B, Wi, Wf, Wr, bi, bf, br, n_lv, mask=None):
+    """(pre_i, pre_f, pre_r), each (b, T, n_lv, H), differentiable and opaque to torch.compile.
+
+    Equal to einsum('btlg,lhg->btlh', relu(A.unsqueeze(2) + m * roll(B, 2^l))**2, W_x[:n_lv]) +
+    b_x[:n_lv]; `mask` is the optional (b, T, n_lv) doc-reset mask, the wrap mask t >= 2^l is
+    always applied. Same signature as reference dispatcher_hybrid/fused_gates.py:307-314.
+    """
+    out = torch.ops.dispatcher.gate_preacts_fwd(A, B, Wi, Wf, Wr, bi, bf, br, n_lv, mask)
+    return out[0], out[1], out[2]
+
+
+# ---------------------------------------------------------------------------------------------
+# dispatcher::level_scan_fwd
+# ---------------------------------------------------------------------------------------------
+@torch.library.custom_op("dispatcher::level_scan_fwd", mutates_args=(), device_types="cuda")
+def _level_scan_fwd_op(pre_i: torch.Tensor, pre_f: torch.Tensor, pre_r: torch.Tensor,
+                       mask: Optional[torch.Tensor], V0: torch.Tensor, num_heads: int,
+                       n_lv: int) -> torch.Tensor:
+    b, T, d = V0.shape
+    out = torch.empty(b, T, d, device=V0.device, dtype=V0.dtype)
+    if b == 0 or T == 0:
+        return out
+    cd = V0.dtype
+    V0_ = V0 if V0.stride(-1) == 1 else V0.contiguous()
+    pi, pf, pr = (g.contiguous().to(cd) for g in (pre_i, pre_f, pre_r))
+    m_, smb, smt = _mask_view(mask, cd)
+    p = _hip.ptr
+    st = _hip.lib.dh_level_scan_fwd(
+        _hip.dtype_code(cd), p(pi), p(pf), p(pr), p(m_), smb, smt,
+        p(V0_), V0_.stride(0), V0_.stride(1), p(out), b, T, num_heads, d // num_heads, n_lv,
+        _hip.stream_handle(V0.device))
+    _hip.check(st, "dispatcher::level_scan_fwd")
+    return out
+
+
+@_level_scan_fwd_op.register_fake
+def _(pre_i, pre_f, pre_r, mask, V0, num_heads, n_lv):
+    return torch.empty_like(V0)
+
+
+def fused_level_scan(pre_i, pre_f, pre_r, mask, V0, num_heads, n_lv):
+    """Scanned mixer state (b, T, d) from the pre-activations and V0 = linear_in(x) (b, T, d).
+
+    Applies a = sigmoid(pre_i)*M, f = sigmoid(pre_f)*M + (1-M), r = sigmoid(pre_r) and the n_lv
+    updates V[t] <- f*V[t] + a*r[t-2^l]*V[t-2^l] (reference dispatcher_hybrid/modeling_dispatcher.py
+    :111-121), with M = [t >= 2^l] * mask. The result is in (b, T, H*hd) layout, ready for
+    linear_out (no heads-first transposes). Inference only (no autograd).
+    """
+    return torch.ops.dispatcher.level_scan_fwd(pre_i, pre_f, pre_r, mask, V0, num_heads, n_lv)

@@ -1,0 +1,129 @@
+"""Per-token decode step of a tree layer on gfx950 HIP kernels.
+
+Drop-in for the reference module of the same name (reference dispatcher_hybrid/fused_step.py),
+whose two Triton kernels run the gate readouts over (row, level) and the level recurrence over
+(row, head). Here the whole step is ONE kernel per layer (``dh_decode_mixer_step``):
+workgroup (head, level) streams its gate weight rows once for every batch row, and the workgroup
+that finishes a head's last level runs that head's L-level recurrence over the ring buffers.
+
+Ring layout (unchanged, reference dispatcher_hybrid/decoding.py:28-37, fused_step.py:13-16):
+level j's state is read only at lag 2^j, so ring j keeps 2^(j+1) slots at offset 2^(j+1)-2 and
+position p lives in slot offset_j + (p & (2^(j+1)-1)).
+
+``step_gates_kernel`` / ``step_scan_kernel`` keep the reference's launch syntax
+(``kernel[grid](...)``, reference decoding.py:477-486) for callers that drive the two halves by
+name; they run the two halves of the same HIP kernel as separate launches.
+
+Importing this module loads the kernel library and raises ImportError if it is missing.
+"""
+
+import torch
+
+from . import _hip
+
+
+def ring_offset(j):
+    return (2 << j) - 2
+
+
+def ring_mask(j):
+    return (2 << j) - 1
+
+
+def decode_workspace(batch, levels, heads, device):
+    """Zero-filled scratch for ``decode_mixer_step`` (per-head counters + fp32 gate values).
+
+    The kernel leaves it zeroed after every call, so one buffer serves every layer and every
+    graph replay of a decoder.
+    """
+    n = _hip.lib.dh_decode_workspace_bytes(batch, levels, heads)
+    return torch.zeros(max(int(n), 1), dtype=torch.uint8, device=device)
+
+
+def _check_contig(name, t):
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def decode_mixer_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring, V0, Y, workspace):
+    """One tree layer's decode step at the position held in the device tensor `t_buf`.
+
+    A (B, GH) current destination features; B_hist (B, Tmax, GH) with row t written;
+    Wi/Wf/Wr (L, H, GH); bi/bf/br (L, H); rg_hist (B, Tmax, L, H) (row t written);
+    V_ring (B, S, H*hd) (slots of position t written); V0 (B, H*hd) linear_in output;
+    Y (B, H*hd) output. Everything in the model dtype (fp32 or bf16), on one GPU.
+    """
+    _hip.require_gpu(A, "decode_mixer_step")
+    Bb, GH = A.shape
+    Tmax = B_hist.shape[1]
+    L, H = Wi.shape[0], Wi.shape[1]
+    S, d = V_ring.shape[1], V_ring.shape[2]
+    dt = A.dtype
+    for name, t in (("A", A), ("B_hist", B_hist), ("Wi", Wi), ("Wf", Wf), ("Wr", Wr), ("bi", bi),
+                    ("bf", bf), ("br", br), ("rg_hist", rg_hist), ("V_ring", V_ring), ("V0", V0),
+                    ("Y", Y)):
+        _check_contig(name, t)
+        if t.dtype != dt:
+            raise TypeError(f"decode_mixer_step: {name} has dtype {t.dtype}, expected {dt}")
+    if t_buf.dtype != torch.int64 or t_buf.numel() < 1:
+        raise TypeError("t_buf must be an int64 device tensor")
+    if tuple(rg_hist.shape) != (Bb, Tmax, L, H) or tuple(V0.shape) != (Bb, d) or tuple(Y.shape) != (Bb, d):
+        raise ValueError("decode_mixer_step: inconsistent cache / buffer shapes")
+    if workspace.numel() < _hip.lib.dh_decode_workspace_bytes(Bb, L, H):
+        raise ValueError("decode_mixer_step: workspace too small")
+    p = _hip.ptr
+    st = _hip.lib.dh_decode_mixer_step(
+        _hip.dtype_code(dt), p(A), p(B_hist), p(Wi), p(Wf), p(Wr), p(bi), p(bf), p(br), p(t_buf),
+        p(rg_hist), p(V_ring), p(V0), p(Y), p(workspace), Bb, Tmax, S, GH, H, d // H, L,
+        _hip.stream_handle(A.device))
+    _hip.check(st, "dh_decode_mixer_step")
+    return Y
+
+
+class _Launcher:
+    """`kernel[grid](*args, **meta)` call syntax of a Triton kernel, mapped onto a HIP entry."""
+
+    def __init__(self, fn, name):
+        self._fn = fn
+        self.__name__ = name
+
+    def __getitem__(self, grid):
+        return lambda *args, **meta: self._fn(tuple(grid), *args, **meta)
+
+
+def _step_gates(grid, A, B_hist, Wi, Wf, Wr, bi, bf, br, T_buf, IG, FG, RG_hist, T_max,
+                GH=None, H=None, L=None, BK=None):
+    """Reference contract (fused_step.py:26-59): grid (B, L); writes IG/FG fp32 (B, L*H) and
+    RG_hist[:, t] (model dtype). BK is accepted for compatibility; the HIP kernel tiles itself."""
+    _hip.require_gpu(A, "step_gates_kernel")
+    Bb = A.shape[0]
+    GH = A.shape[1] if GH is None else GH
+    L = Wi.shape[0] if L is None else L
+    H = Wi.shape[1] if H is None else H
+    if grid[0] != Bb or (len(grid) > 1 and grid[1] != L):
+        raise ValueError(f"step_gates_kernel grid {grid} must be (B={Bb}, L={L})")
+    p = _hip.ptr
+    st = _hip.lib.dh_step_gates(_hip.dtype_code(A.dtype), p(A), p(B_hist), p(Wi), p(Wf), p(Wr),
+                                p(bi), p(bf), p(br), p(T_buf), p(IG), p(FG), p(RG_hist),
+                                Bb, int(T_max), GH, H, L, _hip.stream_handle(A.device))
+    _hip.check(st, "dh_step_gates")
+
+
+def _step_scan(grid, V0, IG, FG, RG_hist, V_ring, T_buf, Y, T_max, S, L=None, HD=None, H=None):
+    """Reference contract (fused_step.py:62-88): grid (B, H); writes the ring slots of position
+    t for levels 0..L-1 and Y."""
+    _hip.require_gpu(V0, "step_scan_kernel")
+    Bb, d = V0.shape
+    if H is None or HD is None or L is None:
+        raise ValueError("step_scan_kernel needs L=, HD= and H=")
+    if grid[0] != Bb or (len(grid) > 1 and grid[1] != H):
+        raise ValueError(f"step_scan_kernel grid {grid} must be (B={Bb}, H={H})")
+    p = _hip.ptr
+    st = _hip.lib.dh_step_scan(_hip.dtype_code(V0.dtype), p(V0), p(IG), p(FG), p(RG_hist),
+                               p(V_ring), p(T_buf), p(Y), Bb, int(T_max), int(S), H, HD, L,
+                               _hip.stream_handle(V0.device))
+    _hip.check(st, "dh_step_scan")
+
+
+step_gates_kernel = _Launcher(_step_gates, "step_gates_kernel")
+step_scan_kernel = _Launcher(_step_scan, "step_scan_kernel")

@@ -1,0 +1,148 @@
+/*
+ * dh_mixer.h — C-ABI of libdh_mixer.so, the gfx950 (MI355X) kernels of Dispatcher-Hybrid's gated
+ * dyadic shift-and-sum mixer.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor pointers are caller-owned DEVICE pointers; the library never allocates device
+ *     memory, never synchronises and never reads device memory on the host. Work is enqueued on
+ *     `stream` (a hipStream_t), so every call is safe inside hipGraph stream capture.
+ *   - `dtype` selects the element type of the activation/weight tensors: DH_F32 or DH_BF16.
+ *     Accumulation is always fp32.
+ *   - Return value: DH_OK, or a DH_ERR_* code; dh_last_error() then holds a thread-local message.
+ *   - Shape limits checked by every entry point: GH % 64 == 0, 1 <= H <= 64, hd in {16,32,64,128},
+ *     1 <= L <= 16, T >= 1.
+ *
+ * Mixer semantics (one layer, model dtype tau), for level l with lag 2^l:
+ *   M[b,t,l]      = [t >= 2^l] * mask[b,t,l]                (mask optional: doc-reset mask)
+ *   hid[b,t,l,:]  = relu(A[b,t,:] + M[b,t,l] * B[b,t-2^l,:])^2
+ *   pre_x[b,t,l,h]= hid[b,t,l,:] . W_x[l,h,:] + b_x[l,h]      x in {i (admit), f (forget), r (transmit)}
+ *   a = sigmoid(pre_i)*M ; f = sigmoid(pre_f)*M + (1-M) ; r = sigmoid(pre_r)
+ *   for l < n_lv:  V[t] <- f[t,l]*V[t] + a[t,l]*r[t-2^l,l]*V[t-2^l]     (V starts at V0 = W_in.x)
+ */
+#ifndef DH_MIXER_H
+#define DH_MIXER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DH_ABI_VERSION 1
+
+enum dh_status {
+  DH_OK = 0,
+  DH_ERR_INVALID_ARG = 1,
+  DH_ERR_UNSUPPORTED_SHAPE = 2,
+  DH_ERR_UNSUPPORTED_DTYPE = 3,
+  DH_ERR_LAUNCH_FAILED = 4,
+  DH_ERR_UNIMPLEMENTED = 5
+};
+
+enum dh_dtype { DH_F32 = 0, DH_BF16 = 1 };
+
+/* ABI version of the loaded library (DH_ABI_VERSION at build time). */
+int dh_abi_version(void);
+
+/* Thread-local message describing the last non-zero status returned on this thread. */
+const char* dh_last_error(void);
+
+/*
+ * Parallel gate pre-activations (prefill / training forward).
+ * Replaces the Triton kernel `_gate_pipeline_fwd` and its op `dispatcher::gate_preacts_fwd`
+ * (reference dispatcher_hybrid/fused_gates.py:38-93 kernel, :186-214 op, :307-314 wrapper).
+ *   A, B      (b, T, GH) rows `stride_at` elements apart, batches `stride_ab` apart; innermost dim
+ *             contiguous.
+ *   Wi,Wf,Wr  (>= n_lv, H, GH): level stride `stride_wl`, head stride `stride_wh` (elements);
+ *             innermost contiguous.
+ *   bi,bf,br  fp32, (>= n_lv, H) contiguous.
+ *   mask      nullable; dtype `dtype`, value > 0 means "edge allowed", element [b,t,l] at
+ *             b*stride_mb + t*stride_mt + l. The wrap mask t >= 2^l is always applied in-kernel.
+ *   out_i/f/r (b, T, n_lv, H) contiguous, dtype `dtype`.
+ */
+int dh_gate_preacts_fwd(int dtype, const void* A, const void* B, int64_t stride_ab, int64_t stride_at,
+                        const void* Wi, const void* Wf, const void* Wr, int64_t stride_wl,
+                        int64_t stride_wh, const float* bi, const float* bf, const float* br,
+                        const void* mask, int64_t stride_mb, int64_t stride_mt, void* out_i,
+                        void* out_f, void* out_r, int b, int T, int GH, int H, int n_lv,
+                        void* stream);
+
+/*
+ * Backward of dh_gate_preacts_fwd (autograd of the fused op).
+ * Replaces the Triton kernel `_gate_pipeline_bwd` and op `dispatcher::gate_preacts_bwd`
+ * (reference dispatcher_hybrid/fused_gates.py:96-173 kernel, :225-257 op).
+ *   dPi/dPf/dPr (b, T, n_lv, H) contiguous, dtype `dtype`.
+ *   dA, dB      fp32 (b, T, GH) contiguous; dWi/dWf/dWr fp32 (n_lv, H, GH); dbi/dbf/dbr fp32 (n_lv, H).
+ *   Every output is overwritten (the library zero-fills with a kernel, then accumulates dB, dW and
+ *   db with fp32 atomics, so summation order is not deterministic, as in the reference).
+ */
+int dh_gate_preacts_bwd(int dtype, const void* A, const void* B, int64_t stride_ab, int64_t stride_at,
+                        const void* Wi, const void* Wf, const void* Wr, int64_t stride_wl,
+                        int64_t stride_wh, const void* dPi, const void* dPf, const void* dPr,
+                        const void* mask, int64_t stride_mb, int64_t stride_mt, float* dA, float* dB,
+                        float* dWi, float* dWf, float* dWr, float* dbi, float* dbf, float* dbr,
+                        int b, int T, int GH, int H, int n_lv, void* stream);
+
+/*
+ * Parallel level scan with the gate activations fused in (sigmoid, masks, heads-first layout).
+ * Replaces reference dispatcher_hybrid/modeling_dispatcher.py:86-88, 111-121 (heads_first, the
+ * admit/forget/transmit activations and the n_lv-level roll/update loop).
+ *   pre_i/f/r (b, T, n_lv, H) contiguous, dtype `dtype` (output of dh_gate_preacts_fwd).
+ *   mask      nullable, as in dh_gate_preacts_fwd.
+ *   V0        (b, T, H*hd): V0[b,t,h*hd+e] at b*stride_vb + t*stride_vt + h*hd + e (linear_in output).
+ *   V         (b, T, H*hd) contiguous output, the scanned state in the layout linear_out consumes.
+ */
+int dh_level_scan_fwd(int dtype, const void* pre_i, const void* pre_f, const void* pre_r,
+                      const void* mask, int64_t stride_mb, int64_t stride_mt, const void* V0,
+                      int64_t stride_vb, int64_t stride_vt, void* V, int b, int T, int H, int hd,
+                      int n_lv, void* stream);
+
+/*
+ * One decode step of one tree layer: all L levels' gate readouts plus the L-level recurrence over
+ * the ring buffers, as ONE kernel launch.
+ * Replaces the Triton kernels `step_gates_kernel` + `step_scan_kernel` (reference
+ * dispatcher_hybrid/fused_step.py:26-59 and :62-88) as launched by
+ * FusedGraphedHybridDecoder._tree_step_g (reference dispatcher_hybrid/decoding.py:477-486).
+ *   A         (B, GH) destination features W1x.h1 of the current token.
+ *   B_hist    (B, Tmax, GH); row t (the current token) already written.
+ *   Wi,Wf,Wr  (L, H, GH) contiguous; bi,bf,br (L, H) contiguous, dtype `dtype`.
+ *   t_dev     device int64[1]: the current position t (read on the device: graph-stable).
+ *   rg_hist   (B, Tmax, L, H): row t is written, rows t-2^l are read.
+ *   V_ring    (B, S, H*hd), S = 2^(L+1)-2: ring j occupies slots [2^(j+1)-2, 2^(j+2)-2) and holds the
+ *             state entering level j; position p lives in slot 2^(j+1)-2 + (p & (2^(j+1)-1)).
+ *   V0        (B, H*hd) linear_in output of the current token (ring 0's new entry).
+ *   Y         (B, H*hd) output: state after level L-1.
+ *   workspace dh_decode_workspace_bytes(B, L, H) bytes, zero-filled once before its first use; every
+ *             call leaves it zeroed again. Calls sharing a workspace must be stream-ordered.
+ *   If t_dev holds a position outside [0, Tmax) the kernel writes nothing.
+ */
+size_t dh_decode_workspace_bytes(int B, int L, int H);
+
+int dh_decode_mixer_step(int dtype, const void* A, const void* B_hist, const void* Wi,
+                         const void* Wf, const void* Wr, const void* bi, const void* bf,
+                         const void* br, const int64_t* t_dev, void* rg_hist, void* V_ring,
+                         const void* V0, void* Y, void* workspace, int B, int Tmax, int S, int GH,
+                         int H, int hd, int L, void* stream);
+
+/*
+ * The two halves of dh_decode_mixer_step as separate launches, with the reference's own buffer
+ * contract, for callers that drive the Triton kernels by name.
+ * dh_step_gates replaces `step_gates_kernel` (reference dispatcher_hybrid/fused_step.py:26-59):
+ *   IG, FG fp32 (B, L*H) outputs; rg_hist row t written.
+ * dh_step_scan replaces `step_scan_kernel` (reference dispatcher_hybrid/fused_step.py:62-88).
+ */
+int dh_step_gates(int dtype, const void* A, const void* B_hist, const void* Wi, const void* Wf,
+                  const void* Wr, const void* bi, const void* bf, const void* br,
+                  const int64_t* t_dev, float* IG, float* FG, void* rg_hist, int B, int Tmax,
+                  int GH, int H, int L, void* stream);
+
+int dh_step_scan(int dtype, const void* V0, const float* IG, const float* FG, const void* rg_hist,
+                 void* V_ring, const int64_t* t_dev, void* Y, int B, int Tmax, int S, int H, int hd,
+                 int L, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DH_MIXER_H */

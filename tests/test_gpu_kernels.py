@@ -1,0 +1,276 @@
+"""Kernel-level parity of the HIP entry points against the float64 C oracle (oracle/dh_oracle.c).
+
+Bars: fp32 kernels within 1e-5 relative of the oracle (the north-star fp32 bar is 1e-4); bf16
+kernels against the oracle evaluated on the same bf16-rounded inputs, within bf16 rounding;
+ring-buffer slot indexing bit-exact (integer-valued known-answer test with saturated gates).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import rel_err
+from oracle import mixer as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _cuda(x, dtype):
+    return torch.as_tensor(np.asarray(x), dtype=torch.float64).to(dtype).to(DEV)
+
+
+def _np(t):
+    return t.detach().double().cpu().numpy()
+
+
+# --------------------------------------------------------------------------------------------
+# gate pre-activations
+# --------------------------------------------------------------------------------------------
+PREACT_CASES = [
+    # b, T, GH, H, L, with_mask
+    (1, 1, 64, 2, 3, False),
+    (2, 37, 64, 4, 6, True),
+    (1, 100, 128, 20, 7, True),          # H > 16: two MFMA column tiles, one partly padded
+    (1, 256, 512, 8, 8, False),          # C1 shape (d 512, 8 levels, T 256)
+    (2, 200, 1024, 16, 12, True),        # release widths
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", PREACT_CASES)
+def test_gate_preacts_fwd_matches_oracle(case, dtype):
+    from dispatcher_hybrid import fused_gates  # noqa: F401
+    b, T, GH, H, L, with_mask = case
+    print(f"gate_preacts case={case} dtype={dtype}", flush=True)
+    rng = np.random.default_rng(hash(case) % 2**32)
+    n_lv = om.active_levels(L, T)
+    A = rng.normal(size=(b, T, GH)) * 0.7
+    B = rng.normal(size=(b, T, GH)) * 0.7
+    Ws = [rng.normal(size=(L, H, GH)) / np.sqrt(GH) for _ in range(3)]
+    bs = [rng.normal(size=(L, H)) for _ in range(3)]
+    mask = (rng.random((b, T, L)) > 0.25).astype(np.float64) if with_mask else None
+    tA, tB = _cuda(A, dtype), _cuda(B, dtype)
+    tW = [_cuda(w, dtype) for w in Ws]
+    tb = [_cuda(x, torch.float32) for x in bs]
+    tm = None if mask is None else _cuda(mask, dtype)[..., :n_lv]
+    outs = torch.ops.dispatcher.gate_preacts_fwd(tA, tB, *tW, *tb, n_lv, tm)
+    torch.cuda.synchronize()
+    # oracle on exactly the values the kernel saw
+    ref = om.gate_preacts(_np(tA), _np(tB), *[_np(w) for w in tW], *bs, n_lv,
+                          None if mask is None else mask[..., :n_lv])
+    for x in range(3):
+        assert outs[x].dtype == dtype and tuple(outs[x].shape) == (b, T, n_lv, H)
+        err = rel_err(_np(outs[x]), ref[x])
+        # bf16: a+b and hid rounded to bf16 (as the eager bf16 path rounds), output rounded
+        assert err < (1e-5 if dtype == torch.float32 else 1.5e-2), f"gate {x}: rel {err:.3e}"
+
+
+def test_gate_preacts_reference_dtype_rule():
+    """bf16 in -> bf16 out (the reference op's rule); fp16 is computed in bf16 too."""
+    b, T, GH, H, L = 1, 8, 64, 2, 3
+    A = torch.randn(b, T, GH, device=DEV, dtype=torch.float16)
+    W = torch.randn(L, H, GH, device=DEV)
+    bias = torch.zeros(L, H, device=DEV)
+    outs = torch.ops.dispatcher.gate_preacts_fwd(A, A, W, W, W, bias, bias, bias, 3, None)
+    assert all(o.dtype == torch.bfloat16 for o in outs)
+
+
+# --------------------------------------------------------------------------------------------
+# level scan
+# --------------------------------------------------------------------------------------------
+SCAN_CASES = [
+    # b, T, H, hd, n_lv, with_mask
+    (1, 1, 2, 64, 1, False),
+    (2, 45, 4, 16, 6, True),
+    (1, 256, 8, 64, 8, False),           # C1
+    (1, 600, 2, 32, 10, True),           # PPT = 2
+    (2, 1024, 16, 64, 11, True),         # C2 length
+    (1, 4096, 2, 128, 12, True),         # full context, hd 128
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", SCAN_CASES)
+def test_level_scan_matches_oracle(case, dtype):
+    from dispatcher_hybrid.fused_gates import fused_level_scan
+    b, T, H, hd, n_lv, with_mask = case
+    print(f"level_scan case={case} dtype={dtype}", flush=True)
+    rng = np.random.default_rng(hash(case) % 2**32)
+    pres = [rng.normal(size=(b, T, n_lv, H)) * 2 for _ in range(3)]
+    V0 = rng.normal(size=(b, T, H * hd))
+    mask = (rng.random((b, T, n_lv)) > 0.2).astype(np.float64) if with_mask else None
+    tp = [_cuda(p, dtype) for p in pres]
+    tV0 = _cuda(V0, dtype)
+    tm = None if mask is None else _cuda(mask, dtype)
+    V = fused_level_scan(*tp, tm, tV0, H, n_lv)
+    torch.cuda.synchronize()
+    ref = om.level_scan(*[_np(p) for p in tp], _np(tV0), H, mask)
+    err = rel_err(_np(V), ref)
+    assert err < (1e-5 if dtype == torch.float32 else 2e-2), f"rel {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_level_scan_known_answers_exact(dtype):
+    """Saturated gates with one-hot V0 rows: window sums / pure shifts are 0/1 vectors, which
+    every dtype represents exactly, so the kernel must reproduce them bit for bit."""
+    from dispatcher_hybrid.fused_gates import fused_level_scan
+    T, H, hd = 128, 2, 64
+    V0 = torch.zeros(1, T, H * hd, dtype=dtype, device=DEV)
+    V0[0, torch.arange(T), torch.arange(T)] = 1
+    for n_lv in (1, 3, 7):
+        on = torch.full((1, T, n_lv, H), 30.0, dtype=dtype, device=DEV)
+        off = torch.full((1, T, n_lv, H), -200.0, dtype=dtype, device=DEV)
+        V = fused_level_scan(on, on, on, None, V0, H, n_lv)       # window sums of width 2^n_lv
+        t = torch.arange(T, device=DEV)
+        win = ((t[None, :] <= t[:, None]) & (t[None, :] > t[:, None] - (1 << n_lv))).to(dtype)
+        assert torch.equal(V[0, :, :T], win)
+        V = fused_level_scan(on, off, on, None, V0, H, n_lv)      # pure shift by 2^n_lv - 1
+        src = (t - ((1 << n_lv) - 1)).clamp(min=0)
+        assert torch.equal(V[0], V0[0, src])
+
+
+# --------------------------------------------------------------------------------------------
+# decode step
+# --------------------------------------------------------------------------------------------
+class _DecodeState:
+    def __init__(self, Bb, Tmax, GH, H, hd, L, dtype, sentinel=0.0):
+        self.S = (2 << L) - 2
+        d = H * hd
+        self.B_hist = torch.zeros(Bb, Tmax, GH, dtype=dtype, device=DEV)
+        self.rg_hist = torch.zeros(Bb, Tmax, L, H, dtype=dtype, device=DEV)
+        self.V_ring = torch.full((Bb, self.S, d), sentinel, dtype=dtype, device=DEV)
+        self.Y = torch.zeros(Bb, d, dtype=dtype, device=DEV)
+        self.t_buf = torch.zeros(1, dtype=torch.long, device=DEV)
+
+
+DECODE_CASES = [
+    # B, T(steps), Tmax, GH, H, hd, L
+    (1, 40, 64, 64, 2, 64, 6),
+    (3, 70, 128, 128, 4, 16, 7),
+    (16, 20, 64, 64, 2, 32, 6),
+    (2, 24, 4096, 1024, 16, 64, 12),    # release shapes (first positions)
+]
+
+
+def _run_decode(case, dtype, seed, split=False, W_zero=False, bias=None, V0_onehot=False, sentinel=0.0):
+    from dispatcher_hybrid import fused_step
+    Bb, T, Tmax, GH, H, hd, L = case
+    d = H * hd
+    rng = np.random.default_rng(seed)
+    A = rng.normal(size=(Bb, T, GH)) * 0.7
+    Bs = rng.normal(size=(Bb, T, GH)) * 0.7
+    V0 = rng.normal(size=(Bb, T, d))
+    if V0_onehot:
+        V0 = np.zeros((Bb, T, d))
+        for b in range(Bb):
+            V0[b, np.arange(T), (np.arange(T) + b) % d] = 1.0
+    Ws = [(np.zeros((L, H, GH)) if W_zero else rng.normal(size=(L, H, GH)) / np.sqrt(GH)) for _ in range(3)]
+    bs = [np.full((L, H), v) for v in bias] if bias is not None else [rng.normal(size=(L, H)) for _ in range(3)]
+    tA, tBs, tV0 = _cuda(A, dtype), _cuda(Bs, dtype), _cuda(V0, dtype)
+    tW = [_cuda(w, dtype) for w in Ws]
+    tb = [_cuda(x, dtype) for x in bs]
+    st = _DecodeState(Bb, Tmax, GH, H, hd, L, dtype, sentinel)
+    ws = fused_step.decode_workspace(Bb, L, H, DEV)
+    IG = torch.zeros(Bb, L * H, dtype=torch.float32, device=DEV)
+    FG = torch.zeros_like(IG)
+    Ys = []
+    for t in range(T):
+        st.B_hist[:, t] = tBs[:, t]
+        st.t_buf.fill_(t)
+        if split:
+            fused_step.step_gates_kernel[(Bb, L)](tA[:, t].contiguous(), st.B_hist, *tW, *tb, st.t_buf,
+                                                  IG, FG, st.rg_hist, Tmax, GH=GH, H=H, L=L, BK=128)
+            fused_step.step_scan_kernel[(Bb, H)](tV0[:, t].contiguous(), IG, FG, st.rg_hist, st.V_ring,
+                                                 st.t_buf, st.Y, Tmax, st.S, L=L, HD=hd, H=H)
+        else:
+            fused_step.decode_mixer_step(tA[:, t].contiguous(), st.B_hist, *tW, *tb, st.t_buf,
+                                         st.rg_hist, st.V_ring, tV0[:, t].contiguous(), st.Y, ws)
+        Ys.append(st.Y.clone())
+    torch.cuda.synchronize()
+    inputs = dict(A=_np(tA), Bs=_np(tBs), V0=_np(tV0), W=[_np(w) for w in tW], b=[_np(x) for x in tb])
+    return st, torch.stack(Ys, 1), ws, inputs
+
+
+def _oracle_decode(case, inp, sentinel=0.0):
+    Bb, T, Tmax, GH, H, hd, L = case
+    S = (2 << L) - 2
+    rg = np.zeros((Bb, Tmax, L, H))
+    ring = np.full((Bb, S, H * hd), sentinel)
+    B_hist = np.zeros((Bb, Tmax, GH))
+    Ys = []
+    for t in range(T):
+        B_hist[:, t] = inp["Bs"][:, t]
+        Ys.append(om.decode_step(inp["A"][:, t], B_hist, *inp["W"], *inp["b"], t, rg, ring, inp["V0"][:, t]))
+    return np.stack(Ys, 1), rg, ring
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", DECODE_CASES)
+def test_decode_mixer_step_matches_oracle(case, dtype):
+    print(f"decode case={case} dtype={dtype}", flush=True)
+    st, Y, ws, inp = _run_decode(case, dtype, seed=11)
+    Yo, rgo, ringo = _oracle_decode(case, inp)
+    T = case[1]
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert rel_err(_np(Y), Yo) < tol
+    assert rel_err(_np(st.rg_hist[:, :T]), rgo[:, :T]) < (1e-6 if dtype == torch.float32 else 8e-3)
+    assert rel_err(_np(st.V_ring), ringo) < tol
+    assert int(torch.count_nonzero(ws)) == 0, "workspace must be left zeroed"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_ring_slots_bit_exact(dtype):
+    """f = a = r = 1 (W = 0, biases +800) and one-hot V0 rows: every ring entry is a 0/1 window
+    sum, exact in any dtype, and unwritten slots keep a sentinel. The whole ring, rg_hist and
+    every output must equal the oracle's bit for bit."""
+    case = (2, 100, 128, 64, 2, 64, 7)
+    st, Y, _, inp = _run_decode(case, dtype, seed=3, W_zero=True, bias=(800.0, 800.0, 800.0),
+                                V0_onehot=True, sentinel=-3.0)
+    Yo, rgo, ringo = _oracle_decode(case, inp, sentinel=-3.0)
+    assert np.array_equal(_np(st.V_ring), ringo)
+    assert np.array_equal(_np(st.rg_hist), rgo)
+    assert np.array_equal(_np(Y), Yo)
+
+
+def test_split_launches_equal_fused_kernel():
+    """step_gates_kernel + step_scan_kernel (reference launch syntax) == one fused launch."""
+    case = (3, 30, 64, 128, 4, 16, 6)
+    for dtype in (torch.float32, torch.bfloat16):
+        a, Ya, _, _ = _run_decode(case, dtype, seed=5)
+        b, Yb, _, _ = _run_decode(case, dtype, seed=5, split=True)
+        assert torch.equal(Ya, Yb)
+        assert torch.equal(a.V_ring, b.V_ring) and torch.equal(a.rg_hist, b.rg_hist)
+
+
+def test_decode_position_out_of_range_writes_nothing():
+    from dispatcher_hybrid import fused_step
+    Bb, Tmax, GH, H, hd, L = 2, 32, 64, 2, 64, 5
+    st = _DecodeState(Bb, Tmax, GH, H, hd, L, torch.float32, sentinel=1.5)
+    A = torch.randn(Bb, GH, device=DEV)
+    W = torch.randn(L, H, GH, device=DEV)
+    bias = torch.zeros(L, H, device=DEV)
+    V0 = torch.randn(Bb, H * hd, device=DEV)
+    ws = fused_step.decode_workspace(Bb, L, H, DEV)
+    before = (st.rg_hist.clone(), st.V_ring.clone(), st.Y.clone())
+    for t in (Tmax, Tmax + 5, -1):
+        st.t_buf.fill_(t)
+        fused_step.decode_mixer_step(A, st.B_hist, W, W, W, bias, bias, bias, st.t_buf, st.rg_hist,
+                                     st.V_ring, V0, st.Y, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(before[0], st.rg_hist) and torch.equal(before[1], st.V_ring)
+    assert torch.equal(before[2], st.Y)
+    assert int(torch.count_nonzero(ws)) == 0
+
+
+def test_decode_wrapper_rejects_mixed_dtypes():
+    from dispatcher_hybrid import fused_step
+    Bb, Tmax, GH, H, hd, L = 1, 16, 64, 2, 64, 4
+    st = _DecodeState(Bb, Tmax, GH, H, hd, L, torch.float32)
+    W = torch.randn(L, H, GH, device=DEV, dtype=torch.bfloat16)
+    bias = torch.zeros(L, H, device=DEV)
+    ws = fused_step.decode_workspace(Bb, L, H, DEV)
+    with pytest.raises(TypeError, match="dtype"):
+        fused_step.decode_mixer_step(torch.randn(Bb, GH, device=DEV), st.B_hist, W, W, W, bias, bias,
+                                     bias, st.t_buf, st.rg_hist, st.V_ring,
+                                     torch.randn(Bb, H * hd, device=DEV), st.Y, ws)

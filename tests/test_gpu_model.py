@@ -1,0 +1,245 @@
+"""Model-level parity of the fused HIP paths (enable_fused_gates, FusedGraphedHybridDecoder,
+fast_generate(decoder="fused")) against the oracle, the reference's golden vectors and the reference
+tests' contracts (reference tests/test_decoding.py:33-178)."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (argmax_agree, decisive_argmax_agree, golden, max_abs, product_model, rel_err,
+                     tiny)
+from oracle import torch_eager as te
+from weights import RELEASE_CONFIG, TINY_CONFIGS, make_state_dict
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", params=sorted(TINY_CONFIGS))
+def tiny_gpu(request):
+    cfgd, sd = tiny(request.param)
+    return request.param, cfgd, sd, product_model(cfgd, sd, device=DEV)
+
+
+def test_fused_forward_fp32_matches_reference(tiny_gpu):
+    """enable_fused_gates() in fp32 (doc-reset masks active) vs the reference's logits."""
+    name, cfgd, sd, m = tiny_gpu
+    g = golden(name)
+    ids = torch.from_numpy(g["ids"]).to(DEV)
+    m.enable_fused_gates()
+    try:
+        with torch.no_grad():
+            got = m(ids).logits
+    finally:
+        m.enable_fused_gates(False)
+    assert rel_err(got.cpu(), g["logits"]) < 1e-4
+
+
+def test_fused_forward_bf16_tracks_eager(tiny_gpu):
+    """reference tests/test_decoding.py:108-118: fused bf16 prefill argmax agreement > 0.95."""
+    name, cfgd, sd, m = tiny_gpu
+    mb = product_model(cfgd, sd, device=DEV, dtype=torch.bfloat16)
+    torch.manual_seed(0)
+    ids = torch.randint(0, cfgd["vocab_size"] - 1, (2, 64), device=DEV)
+    with torch.no_grad():
+        eager = mb(ids).logits.float()
+        mb.enable_fused_gates()
+        fused = mb(ids).logits.float()
+    ref = te.forward(sd, te.Spec(type("C", (), cfgd)), ids.cpu())
+    assert argmax_agree(fused.cpu(), ref) > 0.95
+    assert argmax_agree(fused, eager) > 0.95
+
+
+def test_fused_autograd_matches_eager():
+    """Gradients through dispatcher::gate_preacts_fwd/bwd equal the eager mixer's (fp32)."""
+    cfgd, sd = tiny("tiny_a")
+    m_e = product_model(cfgd, sd, device=DEV).train()
+    m_f = product_model(cfgd, sd, device=DEV).train().enable_fused_gates()
+    g = golden("tiny_a")
+    ids = torch.from_numpy(g["ids"]).to(DEV)
+    labels = ids.clone()
+    loss_e = m_e(ids, labels=labels).loss
+    loss_f = m_f(ids, labels=labels).loss
+    loss_e.backward()
+    loss_f.backward()
+    assert abs(loss_e.item() - loss_f.item()) < 1e-5 * abs(loss_e.item())
+    for (n, pe), (_, pf) in zip(m_e.named_parameters(), m_f.named_parameters()):
+        assert rel_err(pf.grad, pe.grad) < 1e-3, n
+
+
+def _compare_decoder(dec_cls, m, vocab, device, prompt=40, steps=12, tol=1e-4):
+    """reference tests/test_decoding.py:33-44 on seeded weights."""
+    torch.manual_seed(0)
+    ids = torch.randint(0, vocab - 1, (prompt + steps,), device=device)
+    with torch.no_grad():
+        ref = m(ids.unsqueeze(0)).logits[0, prompt:].float()
+    dec = dec_cls(m)
+    dec.prefill(ids[:prompt])
+    got = torch.stack([dec.step(ids[t]).float() for t in range(prompt, prompt + steps)])
+    assert (got.argmax(-1) == ref.argmax(-1)).all(), "argmax disagrees with the parallel forward"
+    gap = (got - ref).abs().max().item()
+    assert gap < tol, f"{dec_cls.__name__}: max|dlogit| {gap:.3e}"
+
+
+def test_graphed_decoder_matches_parallel_forward(tiny_gpu):
+    from dispatcher_hybrid.decoding import GraphedHybridDecoder
+    name, cfgd, sd, m = tiny_gpu
+    _compare_decoder(GraphedHybridDecoder, m, cfgd["vocab_size"], DEV)
+
+
+def test_fused_decoder_matches_parallel_forward(tiny_gpu):
+    from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder
+    name, cfgd, sd, m = tiny_gpu
+    _compare_decoder(FusedGraphedHybridDecoder, m, cfgd["vocab_size"], DEV)
+
+
+def test_fused_decoder_matches_reference_golden(tiny_gpu):
+    """Fused decoder logits and layer-0 state vs the reference's eager decoder (fp32)."""
+    from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder
+    name, cfgd, sd, m = tiny_gpu
+    g = golden(name)
+    dec = FusedGraphedHybridDecoder(m)
+    pl = dec.prefill(torch.from_numpy(g["prompts"]).to(DEV))
+    assert rel_err(pl.cpu(), g["prefill_logits"]) < 1e-4
+    st = torch.stack([dec.step(torch.from_numpy(g["nexts"][:, j]).to(DEV)) for j in range(8)], 1)
+    assert rel_err(st.cpu(), g["step_logits"]) < 1e-4
+    c0 = dec.inner.caches[0]
+    Tn = g["B_hist0"].shape[1]
+    assert max_abs(c0.B_hist[:, :Tn].cpu(), g["B_hist0"]) < 1e-4
+    assert max_abs(c0.rg_hist[:, :Tn].cpu(), g["rg_hist0"]) < 1e-4
+    assert max_abs(c0.V_ring.cpu(), g["V_ring0"]) < 1e-4
+
+
+def test_fused_decoder_state_equals_eager_decoder_state():
+    """Ring slots, rg_hist and B_hist written by the fused step match the eager step's."""
+    from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder, IncrementalDecoder
+    cfgd, sd = tiny("tiny_b")
+    m = product_model(cfgd, sd, device=DEV)
+    torch.manual_seed(3)
+    prompts = torch.randint(0, 250, (3, 9), device=DEV)
+    nexts = torch.randint(0, 250, (3, 20), device=DEV)
+    decs = [IncrementalDecoder(m), FusedGraphedHybridDecoder(m)]
+    for d in decs:
+        d.prefill(prompts)
+        for j in range(nexts.shape[1]):
+            d.step(nexts[:, j])
+    for ce, cf in zip(decs[0].caches, decs[1].inner.caches):
+        if hasattr(ce, "V_ring"):
+            assert max_abs(cf.V_ring, ce.V_ring) < 1e-5
+            assert max_abs(cf.rg_hist, ce.rg_hist) < 1e-5
+            assert max_abs(cf.B_hist, ce.B_hist) < 1e-5
+
+
+def test_batched_graphed_and_fused_bf16():
+    """reference tests/test_decoding.py:156-178 (bf16, 4 rows)."""
+    from dispatcher_hybrid.decoding import (FusedGraphedHybridDecoder, GraphedHybridDecoder,
+                                            IncrementalDecoder)
+    cfgd, sd = tiny("tiny_a", scheme="reference")
+    sd = dict(sd)
+    m = product_model(cfgd, sd, device=DEV, dtype=torch.bfloat16)
+    torch.manual_seed(0)
+    prompts = torch.randint(0, 250, (4, 40), device=DEV)
+    nexts = torch.randint(0, 250, (4, 6), device=DEV)
+
+    def run(cls):
+        dec = cls(m)
+        out = [dec.prefill(prompts)[:, -1].float()]
+        out += [dec.step(nexts[:, j]).float() for j in range(6)]
+        return torch.stack(out, 1)
+
+    ref = run(IncrementalDecoder)
+    for cls in (GraphedHybridDecoder, FusedGraphedHybridDecoder):
+        got = run(cls)
+        assert (got - ref).abs().max().item() < 1.0
+        assert decisive_argmax_agree(got, ref)
+
+
+def test_fast_generate_fused_equals_eager_greedy():
+    cfgd, sd = tiny("tiny_a")
+    m = product_model(cfgd, sd, device=DEV)
+    g = golden("tiny_a")
+    prompt = torch.from_numpy(g["gen"][:, :6]).to(DEV)
+    n = g["gen"].shape[1] - 6
+    fused = m.fast_generate(prompt, max_new_tokens=n, decoder="fused")
+    eager = m.fast_generate(prompt, max_new_tokens=n, decoder="eager")
+    assert torch.equal(fused, eager)
+    assert np.array_equal(fused.cpu().numpy(), g["gen"])
+    auto = m.fast_generate(prompt, max_new_tokens=n, decoder="auto")
+    assert torch.equal(auto, eager)
+
+
+def test_fused_decoder_context_exhausted_raises():
+    from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder
+    cfgd, sd = tiny("tiny_b")
+    m = product_model(cfgd, sd, device=DEV)
+    dec = FusedGraphedHybridDecoder(m)
+    dec.prefill(torch.randint(0, 250, (cfgd["max_len"] - 1,), device=DEV))
+    dec.step(torch.tensor(3, device=DEV))
+    with pytest.raises(ValueError, match="context exhausted"):
+        dec.step(torch.tensor(3, device=DEV))
+
+
+# --------------------------------------------------------------------------------------------
+# release shapes (292M, bf16)
+# --------------------------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def release_models():
+    """292M random init (reference scheme, but W1s ~ N(0, 0.02) so lag indexing is exercised),
+    in bf16 and fp32 on the GPU."""
+    cfgd = RELEASE_CONFIG
+    sd = make_state_dict(cfgd, 0, scheme="reference")
+    g = torch.Generator().manual_seed(1)
+    for k in list(sd):
+        if k.endswith("gate_hidden_src.weight"):
+            sd[k] = torch.randn(sd[k].shape, generator=g) * 0.02
+    m32 = product_model(cfgd, sd, device=DEV)
+    m16 = product_model(cfgd, sd, device=DEV, dtype=torch.bfloat16)
+    return cfgd, m32, m16
+
+
+def test_release_prefill_fused_gates_tolerances(release_models):
+    """C2: T=1024 prefill. fp32 fused vs fp32 eager: rel <= 1e-4. bf16 fused vs bf16 eager:
+    logit max-abs <= 3e-2 and greedy-argmax agreement >= 99%."""
+    cfgd, m32, m16 = release_models
+    torch.manual_seed(2)
+    ids = torch.randint(0, cfgd["vocab_size"], (1, 1024), device=DEV)
+    ids[0, 300] = cfgd["eot_token"]                       # exercise the doc-reset mask
+    with torch.no_grad():
+        e32 = m32(ids).logits
+        f32 = m32.enable_fused_gates()(ids).logits
+        m32.enable_fused_gates(False)
+        e16 = m16(ids).logits.float()
+        f16 = m16.enable_fused_gates()(ids).logits.float()
+        m16.enable_fused_gates(False)
+    r32 = rel_err(f32, e32)
+    gap16 = max_abs(f16, e16)
+    agree16 = argmax_agree(f16, e16)
+    print(f"C2 fp32 rel={r32:.2e}  bf16 max|d|={gap16:.3e} argmax={agree16:.4f}", flush=True)
+    assert r32 <= 1e-4
+    assert gap16 <= 3e-2
+    assert agree16 >= 0.99
+
+
+def test_release_decode_fused_tolerances(release_models):
+    """C3-style decode: prefill + 16 steps; fused vs eager decoder. fp32: rel <= 1e-4.
+    bf16: max-abs <= 3e-2, argmax agreement >= 99%."""
+    from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder, IncrementalDecoder
+    cfgd, m32, m16 = release_models
+    torch.manual_seed(3)
+    ids = torch.randint(0, cfgd["vocab_size"] - 1, (1, 1040), device=DEV)
+    for m, dt in ((m32, "fp32"), (m16, "bf16")):
+        outs = []
+        for cls in (IncrementalDecoder, FusedGraphedHybridDecoder):
+            dec = cls(m)
+            dec.prefill(ids[:, :1024])
+            outs.append(torch.stack([dec.step(ids[:, t]).float() for t in range(1024, 1040)], 1))
+        if dt == "fp32":
+            r = rel_err(outs[1], outs[0])
+            print(f"C3 fp32 rel={r:.2e}", flush=True)
+            assert r <= 1e-4
+        else:
+            gap = max_abs(outs[1], outs[0])
+            agree = argmax_agree(outs[1], outs[0])
+            print(f"C3 bf16 max|d|={gap:.3e} argmax={agree:.4f}", flush=True)
+            assert gap <= 3e-2
+            assert agree >= 0.99
