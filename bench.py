@@ -141,12 +141,11 @@ def decode_kernel_roofline(torch, model, dec, copies=400):
     B_hist = torch.zeros(1, 4096, GH, device=dev, dtype=torch.bfloat16)
     rg = torch.zeros(1, 4096, L, H, device=dev, dtype=torch.bfloat16)
     ring = torch.zeros(1, cache.S, d, device=dev, dtype=torch.bfloat16)
-    ws = fused_step.decode_workspace(1, L, H, dev)
     stream = torch.cuda.current_stream()
 
     def launch(i):
         W = Ws[i % copies]
-        fused_step.decode_mixer_step(A, B_hist, W[0], W[1], W[2], bi, bf, br, t_buf, rg, ring, V0, Y, ws)
+        fused_step.decode_mixer_step(A, B_hist, W[0], W[1], W[2], bi, bf, br, t_buf, rg, ring, V0, Y)
 
     for i in range(32):
         launch(i)

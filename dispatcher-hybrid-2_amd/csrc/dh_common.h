@@ -62,11 +62,24 @@ __device__ __forceinline__ void load4(const bf16_t* p, float (&o)[4]) {
 // and to exactly 0.0 for x <= -~104 (e^-x overflows to +inf).
 __device__ __forceinline__ float dh_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
-// full-wavefront (64 lanes) sum; every lane gets the result
+// DPP lane move of a float: lanes in the rows of ROWMASK read the lane CTRL selects, others get 0
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWMASK, 0xf, false));
+}
+
+// Full-wavefront (64 lanes) sum; every lane gets the result. DPP steps (no LDS traffic): butterflies
+// within quads (quad_perm 1,0,3,2 and 2,3,0,1), then half-row and row mirrors complete each 16-lane
+// row; row_bcast:15 and row_bcast:31 carry row sums upward so lane 63 holds the total, which
+// readlane broadcasts.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_move<0xb1, 0xf>(v);    // quad_perm(1,0,3,2)
+  v += dpp_move<0x4e, 0xf>(v);    // quad_perm(2,3,0,1)
+  v += dpp_move<0x141, 0xf>(v);   // row_half_mirror
+  v += dpp_move<0x140, 0xf>(v);   // row_mirror
+  v += dpp_move<0x142, 0xa>(v);   // row_bcast:15 into rows 1, 3
+  v += dpp_move<0x143, 0xc>(v);   // row_bcast:31 into rows 2, 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __host__ __device__ __forceinline__ int64_t ring_offset(int j) { return ((int64_t)2 << j) - 2; }

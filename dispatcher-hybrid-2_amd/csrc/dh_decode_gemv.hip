@@ -1,0 +1,363 @@
+// Decode-step matrix-vector products with their neighbouring elementwise work fused in, for gfx950.
+//
+// One launch computes, for each batch row b and output row n of up to three concatenated weight
+// segments W_s (N_s x K, row-major, in the model dtype):
+//     h      = RMSNorm(x[b]) * g            (optional prologue; fp32 math, rounded to the dtype)
+//     acc    = W_s[n] . h                   (fp32 accumulation)
+//     out    = round(acc)                                     plain
+//            | round(round(acc) + resid[b, n])                residual add (segment 0 only)
+//            | round(round(silu(round(acc_gate))) * round(acc_up))   SwiGLU (segments gate, up)
+// and writes out to segment s's destination at b * out_bstride + t * t_stride + n (t = the device
+// position, for the B_hist[t] row of the mixer's source projection). The rounding points are those
+// of the eager torch step (reference dispatcher_hybrid/decoding.py:473-476 and :487-488,
+// dispatcher_hybrid/modeling_dispatcher.py:196-197, 207-212, 348-351).
+//
+// Work decomposition: 256-thread workgroups (4 wave64s); each wave owns R consecutive output rows
+// and every lane owns the same CG 16-byte chunks of K in each of them, so all of a wave's weight
+// bytes are requested by one burst of loads issued before anything else (no load is guarded by a
+// divergent branch: addresses are clamped and predicates applied to values). The activations x are
+// staged once per workgroup in LDS, the RMSNorm scale comes from one wave-level reduction per row,
+// and each (row, batch row) dot product is finished with a butterfly shuffle reduction, after which
+// every lane holds every sum and lane j writes output j.
+#include "dh_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxSeg = 3;
+constexpr int kBP = 4;          // batch rows per accumulation pass
+constexpr int kMaxBch = 64;     // batch rows staged in LDS at once
+constexpr int kLdsBytes = 64 * 1024;
+constexpr int kXU = 4;          // activation chunks in flight per thread while staging
+
+struct Seg {
+  const void* W;
+  void* out;
+  int64_t out_bstride;
+  int64_t t_stride;
+  int N;
+};
+
+struct GemvArgs {
+  const void* x;
+  int64_t x_bstride;
+  const int64_t* x_rows;        // nullable: x row of batch b is x_rows[b] (embedding gather)
+  const void* g;                // nullable RMSNorm weight (K)
+  float eps;
+  const void* resid;            // nullable residual (B, N0)
+  int64_t resid_bstride;
+  const int64_t* resid_rows;    // nullable: residual row of batch b is resid_rows[b]
+  const int64_t* t_dev;         // device position (always a valid pointer)
+  Seg seg[kMaxSeg];
+  int nseg;
+  int B, K, Nrows, bch;
+};
+
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+template <typename T> struct Vec;
+template <> struct Vec<bf16_t> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void unpack(const uint4& v, float (&o)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o[2 * j] = __uint_as_float(w[j] << 16);
+      o[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+    }
+  }
+};
+template <> struct Vec<float> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void unpack(const uint4& v, float (&o)[4]) {
+    o[0] = __uint_as_float(v.x);
+    o[1] = __uint_as_float(v.y);
+    o[2] = __uint_as_float(v.z);
+    o[3] = __uint_as_float(v.w);
+  }
+};
+
+__device__ __forceinline__ float silu(float x) { return x * dh_sigmoid(x); }
+
+// raw element bits: the conversion (the load's first consumer) can sit after the whole burst
+template <typename T> struct Raw;
+template <> struct Raw<bf16_t> {
+  __device__ __forceinline__ static uint32_t load(const bf16_t* p) { return *p; }
+  __device__ __forceinline__ static float f(uint32_t r) { return __uint_as_float(r << 16); }
+};
+template <> struct Raw<float> {
+  __device__ __forceinline__ static uint32_t load(const float* p) { return __float_as_uint(*p); }
+  __device__ __forceinline__ static float f(uint32_t r) { return __uint_as_float(r); }
+};
+
+template <typename T, int R, int CG, bool SW>
+__global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* xs = reinterpret_cast<T*>(smem);                 // staged activations [bch][K]
+  __shared__ float rscale[kMaxBch];
+  constexpr int V = Vec<T>::N;
+  constexpr int NW = SW ? 2 : 1;                      // weight rows per output row
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int K = a.K, B = a.B;
+  const int nchunk = K / V;
+  const bool has_norm = a.g != nullptr;
+
+  // ---- weights: every load of the wave in one burst
+  const int rbase = (blockIdx.x * kWaves + wave) * R;
+  const T* wrow[R][NW];
+  int segi[R];
+  int local[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = min(rbase + r, a.Nrows - 1);
+    int s = 0, n0 = 0;
+    if (!SW) {
+#pragma unroll
+      for (int q = 0; q < kMaxSeg - 1; ++q)
+        if (q + 1 < a.nseg && n - n0 >= a.seg[s].N) { n0 += a.seg[s].N; ++s; }
+    }
+    segi[r] = s;
+    local[r] = n - n0;
+    wrow[r][0] = (const T*)a.seg[s].W + (int64_t)local[r] * K;
+    if (SW) wrow[r][NW - 1] = (const T*)a.seg[1].W + (int64_t)local[r] * K;
+  }
+  uint4 w[R][NW][CG];
+#pragma unroll
+  for (int c = 0; c < CG; ++c) {
+    const int ch = min(lane + 64 * c, nchunk - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int q = 0; q < NW; ++q) w[r][q][c] = ld16(wrow[r][q] + (int64_t)ch * V);
+  }
+  uint4 gv[CG];
+  if (has_norm) {                                      // uniform
+#pragma unroll
+    for (int c = 0; c < CG; ++c) gv[c] = ld16((const T*)a.g + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
+  }
+  const int64_t t = *a.t_dev;
+  // residual operand of the output this lane writes in the first pass (output j = lane: row j % R,
+  // batch row j / R), fetched with the weights; later passes (B > kBP) load theirs in the epilogue
+  const bool has_resid = a.resid != nullptr;
+  uint32_t resid_raw = 0;
+  if (has_resid) {                                     // uniform
+    const int b = min(lane / R, B - 1);
+    const int n = min(rbase + lane % R, a.Nrows - 1);
+    const int64_t rrow = a.resid_rows ? a.resid_rows[b] : (int64_t)b;
+    resid_raw = Raw<T>::load((const T*)a.resid + rrow * a.resid_bstride + n);
+  }
+
+  for (int bb = 0; bb < B; bb += a.bch) {
+    const int nb = min(a.bch, B - bb);
+    // ---- stage x rows [bb, bb + nb) in LDS (gathered through x_rows when given)
+    for (int i0 = 0; i0 < nb * nchunk; i0 += kThreads * kXU) {
+      uint4 xr[kXU];
+#pragma unroll
+      for (int u = 0; u < kXU; ++u) {
+        const int i = min(i0 + tid + u * kThreads, nb * nchunk - 1);
+        const int rr = i / nchunk, kc = i % nchunk;
+        const int64_t xrow = a.x_rows ? a.x_rows[bb + rr] : (int64_t)(bb + rr);
+        xr[u] = ld16((const T*)a.x + xrow * a.x_bstride + (int64_t)kc * V);
+      }
+#pragma unroll
+      for (int u = 0; u < kXU; ++u) {
+        const int i = i0 + tid + u * kThreads;
+        if (i < nb * nchunk) *reinterpret_cast<uint4*>(xs + (int64_t)i * V) = xr[u];
+      }
+    }
+    __syncthreads();
+    // ---- RMSNorm scale per staged row: one wave per row
+    if (has_norm) {
+      for (int rr = wave; rr < nb; rr += kWaves) {
+        float ss = 0.f;
+        for (int k = lane; k < K; k += 64) {
+          const float v = Elem<T>::load(xs + (int64_t)rr * K + k);
+          ss += v * v;
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) rscale[rr] = rsqrtf(ss / (float)K + a.eps);
+      }
+      __syncthreads();
+    }
+    // ---- dot products, kBP batch rows per pass
+    for (int b0 = 0; b0 < nb; b0 += kBP) {
+      float acc[R][NW][kBP];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int q = 0; q < NW; ++q)
+#pragma unroll
+          for (int bp = 0; bp < kBP; ++bp) acc[r][q][bp] = 0.f;
+#pragma unroll
+      for (int c = 0; c < CG; ++c) {
+        const int chr = lane + 64 * c;
+        const bool live = chr < nchunk;
+        const int ch = min(chr, nchunk - 1);
+        float gw[V];
+        if (has_norm) Vec<T>::unpack(gv[c], gw);
+#pragma unroll
+        for (int bp = 0; bp < kBP; ++bp) {
+          if (b0 + bp < nb) {                          // uniform
+            float hv[V];
+            Vec<T>::unpack(*reinterpret_cast<const uint4*>(xs + ((int64_t)(b0 + bp) * K) + (int64_t)ch * V), hv);
+            if (has_norm) {
+              const float rs = rscale[b0 + bp];
+#pragma unroll
+              for (int e = 0; e < V; ++e) hv[e] = Elem<T>::round(hv[e] * rs * gw[e]);
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+              for (int q = 0; q < NW; ++q) {
+                float wv[V];
+                Vec<T>::unpack(w[r][q][c], wv);
+                float s = 0.f;
+#pragma unroll
+                for (int e = 0; e < V; ++e) s += wv[e] * hv[e];
+                acc[r][q][bp] += live ? s : 0.f;
+              }
+          }
+        }
+      }
+      // butterfly reduction: every lane ends with every (row, batch row) sum
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int q = 0; q < NW; ++q)
+#pragma unroll
+          for (int bp = 0; bp < kBP; ++bp) acc[r][q][bp] = wave_sum(acc[r][q][bp]);
+      // epilogue: lane j writes output (row j % R, batch row b0 + j / R)
+      const int r = lane % R, bp = lane / R;
+      if (bp < kBP && b0 + bp < nb && rbase + r < a.Nrows) {
+        float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr)
+#pragma unroll
+          for (int pp = 0; pp < kBP; ++pp)
+            if (rr == r && pp == bp) {
+              v0 = acc[rr][0][pp];
+              v1 = acc[rr][NW - 1][pp];
+            }
+        float out;
+        if (SW) {
+          out = Elem<T>::round(Elem<T>::round(silu(Elem<T>::round(v0))) * Elem<T>::round(v1));
+        } else {
+          out = Elem<T>::round(v0);
+          if (has_resid) {
+            const int64_t b = bb + b0 + bp;
+            float rv;
+            if (bb == 0 && b0 == 0) {
+              rv = Raw<T>::f(resid_raw);
+            } else {
+              const int64_t rrow = a.resid_rows ? a.resid_rows[b] : b;
+              rv = Elem<T>::load((const T*)a.resid + rrow * a.resid_bstride + rbase + r);
+            }
+            out = Elem<T>::round(out + rv);
+          }
+        }
+        int s = 0;
+        int loc = 0;
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr)
+          if (rr == r) {
+            s = segi[rr];
+            loc = local[rr];
+          }
+        const Seg& sg = a.seg[s];
+        const int64_t b = bb + b0 + bp;
+        Elem<T>::store((T*)sg.out + b * sg.out_bstride + t * sg.t_stride + loc, out);
+      }
+    }
+    __syncthreads();                                   // xs / rscale reused by the next chunk
+  }
+}
+
+template <typename T, int R, int CG, bool SW>
+void launch(const GemvArgs& a, hipStream_t s) {
+  const int rows_per_block = kWaves * R;
+  const int grid = (a.Nrows + rows_per_block - 1) / rows_per_block;
+  const size_t lds = (size_t)a.bch * a.K * sizeof(T);
+  decode_gemv_kernel<T, R, CG, SW><<<dim3(grid), dim3(kThreads), lds, s>>>(a);
+}
+
+template <typename T, int CG, bool SW>
+void pick_r(const GemvArgs& a, int R, hipStream_t s) {
+  if (R >= 4 && !SW) launch<T, 4, CG, SW>(a, s);
+  else if (R >= 2) launch<T, 2, CG, SW>(a, s);
+  else launch<T, 1, CG, SW>(a, s);
+}
+
+template <typename T, bool SW>
+void pick_cg(const GemvArgs& a, int C, int R, hipStream_t s) {
+  if (C <= 2) pick_r<T, 2, SW>(a, R, s);
+  else if (C <= 4) pick_r<T, 4, SW>(a, R, s);
+  else if (C <= 6) pick_r<T, 6, SW>(a, 1, s);
+  else pick_r<T, 12, SW>(a, 1, s);
+}
+
+bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
+
+}  // namespace
+
+extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const int64_t* x_rows,
+                              const void* norm_w, float eps, int nseg, const void* const* W,
+                              void* const* out, const int64_t* out_bstride, const int64_t* out_t_stride,
+                              const int* N, const void* resid, int64_t resid_bstride,
+                              const int64_t* resid_rows, int swiglu, const int64_t* t_dev, int B, int K,
+                              void* stream) {
+  const char* who = "dh_decode_gemv";
+  DH_REQUIRE(dtype == DH_F32 || dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d", who, dtype);
+  const int vec = dtype == DH_BF16 ? 8 : 4;             // elements per 16-byte chunk
+  DH_REQUIRE(B >= 1 && K >= vec && K % vec == 0, DH_ERR_UNSUPPORTED_SHAPE,
+             "%s: B=%d K=%d (K must be a multiple of %d: rows are read in 16-byte chunks)", who, B, K, vec);
+  DH_REQUIRE(nseg >= 1 && nseg <= kMaxSeg, DH_ERR_INVALID_ARG, "%s: nseg=%d not in [1,%d]", who, nseg, kMaxSeg);
+  DH_REQUIRE(!swiglu || nseg == 2, DH_ERR_INVALID_ARG, "%s: SwiGLU needs exactly the gate and up segments", who);
+  DH_REQUIRE(!swiglu || !resid, DH_ERR_INVALID_ARG, "%s: SwiGLU and residual cannot be combined", who);
+  DH_REQUIRE(!resid || nseg == 1, DH_ERR_INVALID_ARG, "%s: a residual needs a single segment", who);
+  DH_REQUIRE(x && W && out && out_bstride && out_t_stride && N && t_dev, DH_ERR_INVALID_ARG, "%s: null pointer argument",
+             who);
+  DH_REQUIRE(aligned(x, 16) && (x_bstride * (dtype == DH_BF16 ? 2 : 4)) % 16 == 0 && (!norm_w || aligned(norm_w, 16)),
+             DH_ERR_INVALID_ARG, "%s: x rows and the norm weight need 16-byte alignment", who);
+  GemvArgs a{};
+  a.x = x;
+  a.x_bstride = x_bstride;
+  a.x_rows = x_rows;
+  a.g = norm_w;
+  a.eps = eps;
+  a.resid = resid;
+  a.resid_bstride = resid_bstride;
+  a.resid_rows = resid_rows;
+  a.t_dev = t_dev;
+  a.nseg = nseg;
+  a.B = B;
+  a.K = K;
+  int total = 0;
+  for (int s = 0; s < nseg; ++s) {
+    DH_REQUIRE(W[s] && out[s] && N[s] >= 1, DH_ERR_INVALID_ARG, "%s: segment %d incomplete", who, s);
+    DH_REQUIRE(aligned(W[s], 16), DH_ERR_INVALID_ARG, "%s: segment %d weights need 16-byte alignment", who, s);
+    a.seg[s] = Seg{W[s], out[s], out_bstride[s], out_t_stride[s], N[s]};
+    total += N[s];
+  }
+  if (swiglu) {
+    DH_REQUIRE(N[0] == N[1], DH_ERR_INVALID_ARG, "%s: gate and up rows differ (%d, %d)", who, N[0], N[1]);
+    total = N[0];
+  }
+  a.Nrows = total;
+  const size_t esz = dtype == DH_BF16 ? 2 : 4;
+  int bch = (int)(kLdsBytes / ((size_t)K * esz));
+  bch = bch > kMaxBch ? kMaxBch : bch;
+  DH_REQUIRE(bch >= 1, DH_ERR_UNSUPPORTED_SHAPE, "%s: K=%d too large to stage one row in LDS", who, K);
+  a.bch = bch < B ? bch : B;
+  const int C = (K / vec + 63) / 64;
+  DH_REQUIRE(C <= 12, DH_ERR_UNSUPPORTED_SHAPE, "%s: K=%d exceeds %d elements per row", who, K, 12 * 64 * vec);
+  // rows per wave: enough workgroups to cover the chip, more bytes per wave when rows abound
+  const int R = a.Nrows >= 16384 ? 4 : (a.Nrows >= 2048 ? 2 : 1);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == DH_BF16) {
+    if (swiglu) pick_cg<bf16_t, true>(a, C, R, s); else pick_cg<bf16_t, false>(a, C, R, s);
+  } else {
+    if (swiglu) pick_cg<float, true>(a, C, R, s); else pick_cg<float, false>(a, C, R, s);
+  }
+  return dh_check_launch(who);
+}

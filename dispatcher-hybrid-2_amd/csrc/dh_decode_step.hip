@@ -13,15 +13,20 @@
 //               if l + 1 < L: ring_{l+1}[slot(l+1, t)] = V
 //   Y = V ;  slot(j, p) = 2^(j+1) - 2 + (p & (2^(j+1) - 1))
 //
-// Work decomposition (MI355X: 256 CUs in 8 XCDs, wave64):
-//   grid = H * L workgroups of 256 threads. Workgroup (h, l) streams its three GH-long weight rows
-//   W_x[l, h, :] once and reduces them against every batch row's hidden vector, so gate weights
-//   are read once per step whatever the batch size. The workgroup that completes a head's last
-//   level (a device-scope counter per head) runs that head's L-level recurrence for all rows: one
-//   lane per element of the head's hd-wide slice, all L ring/rg sources prefetched up front since
-//   the slot written at t never aliases the slot read at t - 2^l. When H is a multiple of 8, the
-//   L workgroups of one head share blockIdx % 8, i.e. one XCD under round-robin dispatch, so the
-//   hand-off stays within one L2.
+// Work decomposition of the fused kernel (MI355X: 256 CUs in 8 XCDs, wave64): one workgroup of
+// 512 threads per (head h, block of batch rows); no workgroup depends on another, so the kernel
+// needs no device-scope fences (which on gfx950 write back and invalidate the per-XCD L2s).
+//   1. Every thread that owns a (row, element) of the recurrence prefetches its L ring sources and
+//      transmit gates first: the slot written at t never aliases the slot read at t - 2^l, and
+//      rg_hist rows t - 2^l < t are final, so these loads overlap the gate phase.
+//   2. Gate readouts: the (level, 16-byte k-chunk) items of head h's 3*L weight rows are spread over
+//      the threads; each item's three weight chunks are loaded once and applied to every row of the
+//      block; partial dots are reduced across the lanes sharing a level with shuffles and
+//      accumulated in LDS.
+//   3. Sigmoid heads and masks, rg_hist[t] stores, then the L-level recurrence per (row, element),
+//      all in registers, writing ring slots and Y.
+// The separately launched halves (dh_step_gates: one workgroup per (head, level) over all rows;
+// dh_step_scan: one workgroup per head) keep the reference's two-kernel buffer contract.
 #include "dh_common.h"
 
 namespace {
@@ -29,8 +34,9 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxL = 16;
-constexpr int kRowChunk = 8;         // batch rows reduced together per weight pass
-constexpr int kCounterStride = 32;   // uint32s between per-head counters (128-byte lines)
+constexpr int kRowChunk = 8;          // batch rows reduced together per weight pass (split kernels)
+constexpr int kFusedThreads = 1024;   // fused kernel workgroup (16 wave64s)
+constexpr int kMaxHd = 128;
 
 struct StepArgs {
   const void* A;
@@ -48,8 +54,8 @@ struct StepArgs {
   void* Y;
   float* IG;
   float* FG;
-  unsigned int* counters;
   int B, Tmax, S, GH, H, hd, L;
+  int rows_per_block;
 };
 
 __device__ __forceinline__ void block_coords(int bid, int H, int L, int& h, int& l) {
@@ -178,28 +184,223 @@ __device__ void scan_phase(const StepArgs& a, int h, int64_t t) {
   }
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) void decode_mixer_step_kernel(StepArgs a) {
-  const int64_t t = *a.t_dev;
-  if (t < 0 || t >= a.Tmax) return;  // every workgroup leaves: no counter is touched
-  int h, l;
-  block_coords(blockIdx.x, a.H, a.L, h, l);
-  gates_phase<T>(a, h, l, t);
+// 16-byte chunks of a row: 8 bf16 or 4 fp32 values, kept packed until used
+template <typename T> struct Chunk;
+template <> struct Chunk<bf16_t> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void unpack(const uint4& v, float (&o)[8]) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o[2 * j] = __uint_as_float(w[j] << 16);
+      o[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+    }
+  }
+};
+template <> struct Chunk<float> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void unpack(const uint4& v, float (&o)[4]) {
+    o[0] = __uint_as_float(v.x);
+    o[1] = __uint_as_float(v.y);
+    o[2] = __uint_as_float(v.z);
+    o[3] = __uint_as_float(v.w);
+  }
+};
 
-  // publish this workgroup's IG/FG/rg stores device-wide, then count the level in
-  __threadfence();
-  __syncthreads();
-  __shared__ int is_last;
-  if (threadIdx.x == 0) {
-    unsigned int* c = a.counters + (int64_t)h * kCounterStride;
-    const unsigned int prev = __hip_atomic_fetch_add(c, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (prev == (unsigned int)(a.L - 1));
-    if (is_last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Raw element bits, so a load's consumer (the conversion) can sit after every load is issued.
+template <typename T> struct Raw;
+template <> struct Raw<bf16_t> {
+  __device__ __forceinline__ static uint32_t load(const bf16_t* p) { return *p; }
+  __device__ __forceinline__ static float f(uint32_t r) { return __uint_as_float(r << 16); }
+};
+template <> struct Raw<float> {
+  __device__ __forceinline__ static uint32_t load(const float* p) { return __float_as_uint(*p); }
+  __device__ __forceinline__ static float f(uint32_t r) { return __uint_as_float(r); }
+};
+
+// Memory round trips are the cost of this latency-bound kernel, so loads are issued in exactly two
+// waves before any barrier: (1) the position t together with everything that does not depend on
+// it (gate weights, destination features A, V0, biases); (2) everything addressed through t
+// (source rows of B_hist, ring slots, transmit gates). Every load is unconditional, at an address
+// clamped to a valid element, with the predicate applied to the value afterwards: a load under a
+// divergent branch whose value is consumed inside the branch makes the compiler wait for it on the
+// spot, serialising the round trips. Barriers (which wait on outstanding loads) only come once
+// every load is in flight.
+// Gate phase: wave l owns level l (L <= 16 waves); its lanes cover K in 16-byte chunks (C per
+// lane), so each (row, gate) dot product ends in one DPP wave reduction and one plain LDS store.
+// RPB = batch rows per workgroup, C = chunks per lane; both compile-time so the operands stay in
+// registers.
+template <typename T, int RPB, int C, int LMAX>
+__global__ __launch_bounds__(kFusedThreads) void decode_mixer_step_kernel(StepArgs a) {
+  constexpr int V = Chunk<T>::N;
+  const int h = blockIdx.x;
+  const int b0 = blockIdx.y * RPB;
+  const int nb = min(RPB, a.B - b0);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int L = a.L, H = a.H, hd = a.hd, GH = a.GH;   // host: L <= LMAX
+  const int64_t d = (int64_t)H * hd;
+  const int nchunk = GH / V;                   // host: nchunk <= 64 * C
+  const int gl = min(wave, L - 1);             // gate role: wave gl owns level gl (waves < L)
+  const bool gate_wave = wave < L;             // wave-uniform
+  const int scan_waves = (nb * hd + 63) / 64;
+  const bool scan_wave = wave < scan_waves;    // wave-uniform
+  __shared__ float acc[RPB][LMAX][3];
+  __shared__ float gate_i[RPB][LMAX];
+  __shared__ float gate_f[RPB][LMAX];
+  __shared__ float src_v[RPB][LMAX][kMaxHd];   // ring_l[slot(l, t - 2^l)] per (row, level, element)
+  __shared__ float src_r[RPB][LMAX];           // rg_hist[t - 2^l, l, h] per (row, level)
+
+  // ---- load wave 1: t and the position-independent operands
+  const int64_t t = *a.t_dev;
+  uint4 w[3][C];
+  uint4 av[RPB][C];
+  const int64_t wrow = ((int64_t)gl * H + h) * GH;
+  if (gate_wave) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int64_t k = (int64_t)min(lane + 64 * c, nchunk - 1) * V;
+      w[0][c] = ld16((const T*)a.Wi + wrow + k);
+      w[1][c] = ld16((const T*)a.Wf + wrow + k);
+      w[2][c] = ld16((const T*)a.Wr + wrow + k);
+#pragma unroll
+      for (int r = 0; r < RPB; ++r) av[r][c] = ld16((const T*)a.A + (int64_t)(b0 + min(r, nb - 1)) * GH + k);
+    }
+  }
+  const int sr = tid / hd, se = tid % hd;      // recurrence role: (row, element)
+  const bool scan_role = sr < nb;
+  const int64_t brow = b0 + (scan_role ? sr : 0);
+  const int ar = tid / L, al = tid % L;        // activation role: (row, level)
+  const bool act_role = tid < nb * L;
+  uint32_t v0raw = 0, bir = 0, bfr = 0, brr = 0;
+  if (scan_wave) v0raw = Raw<T>::load((const T*)a.V0 + brow * d + (int64_t)h * hd + se);
+  if (wave < (nb * L + 63) / 64) {
+    const int64_t gi = (int64_t)al * H + h;
+    bir = Raw<T>::load((const T*)a.bi + gi);
+    bfr = Raw<T>::load((const T*)a.bf + gi);
+    brr = Raw<T>::load((const T*)a.br + gi);
+  }
+  if (t < 0 || t >= a.Tmax) return;             // uniform: every thread read the same t
+
+  // ---- load wave 2: operands addressed through t
+  const int64_t gsrc = t - ((int64_t)1 << gl);
+  const int64_t gsc = gsrc < 0 ? 0 : gsrc;
+  uint4 bv[RPB][C];
+  if (gate_wave) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int64_t k = (int64_t)min(lane + 64 * c, nchunk - 1) * V;
+#pragma unroll
+      for (int r = 0; r < RPB; ++r)
+        bv[r][c] = ld16((const T*)a.B_hist + ((int64_t)(b0 + min(r, nb - 1)) * a.Tmax + gsc) * GH + k);
+    }
+  }
+  T* ring = (T*)a.V_ring + brow * a.S * d + (int64_t)h * hd + se;
+  uint32_t vraw[LMAX], rraw[LMAX];
+  if (scan_wave) {
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l) {            // straight-line: levels past L re-read level L-1
+      const int lc = min(l, L - 1);
+      const int64_t sc = max(t - ((int64_t)1 << lc), (int64_t)0);
+      vraw[l] = Raw<T>::load(ring + (ring_offset(lc) + (sc & ring_mask(lc))) * d);
+      rraw[l] = Raw<T>::load((const T*)a.rg_hist + ((brow * a.Tmax + sc) * L + lc) * H + h);
+    }
+  }
+
+  // ---- gate readouts of level gl: per-lane partial dots, one wave reduction per (row, gate)
+  if (gate_wave) {
+    const bool ok = gsrc >= 0;
+#pragma unroll
+    for (int r = 0; r < RPB; ++r) {
+      float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        float wi[V], wf[V], wr[V], x1[V], x2[V];
+        Chunk<T>::unpack(w[0][c], wi);
+        Chunk<T>::unpack(w[1][c], wf);
+        Chunk<T>::unpack(w[2][c], wr);
+        Chunk<T>::unpack(av[r][c], x1);
+        Chunk<T>::unpack(bv[r][c], x2);
+        const float live = (lane + 64 * c) < nchunk ? 1.f : 0.f;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          float x = fmaxf(x1[e] + (ok ? x2[e] : 0.f), 0.f);
+          x = x * x * live;
+          s0 += wi[e] * x;
+          s1 += wf[e] * x;
+          s2 += wr[e] * x;
+        }
+      }
+      s0 = wave_sum(s0);
+      s1 = wave_sum(s1);
+      s2 = wave_sum(s2);
+      if (lane == 0 && r < nb) {
+        acc[r][gl][0] = s0;
+        acc[r][gl][1] = s1;
+        acc[r][gl][2] = s2;
+      }
+    }
+  }
+  __syncthreads();                                // acc complete; every load above has landed
+
+  // ---- sigmoid heads, masks, transmit gate of position t; stage the recurrence's sources
+  if (act_role) {
+    const float okf = (t - ((int64_t)1 << al)) >= 0 ? 1.f : 0.f;
+    gate_i[ar][al] = dh_sigmoid(acc[ar][al][0] + Raw<T>::f(bir)) * okf;
+    gate_f[ar][al] = dh_sigmoid(acc[ar][al][1] + Raw<T>::f(bfr)) * okf + (1.f - okf);
+    const float rg = dh_sigmoid(acc[ar][al][2] + Raw<T>::f(brr));
+    Elem<T>::store((T*)a.rg_hist + (((int64_t)(b0 + ar) * a.Tmax + t) * L + al) * H + h, rg);
+  }
+  if (scan_role) {
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l) {
+      if (l < L) {
+        const bool live = (t - ((int64_t)1 << l)) >= 0;
+        src_v[sr][l][se] = live ? Raw<T>::f(vraw[l]) : 0.f;
+        if (se == 0) src_r[sr][l] = live ? Raw<T>::f(rraw[l]) : 0.f;
+      }
+    }
   }
   __syncthreads();
-  if (!is_last) return;
-  __threadfence();  // acquire the other levels' IG/FG
-  scan_phase<T>(a, h, t);
+
+  // ---- the level recurrence over the ring buffers
+  if (scan_role) {
+    float v = Raw<T>::f(v0raw);
+    Elem<T>::store(ring + (t & 1) * d, v);
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l) {
+      if (l < L) {
+        v = gate_f[sr][l] * v + gate_i[sr][l] * src_r[sr][l] * src_v[sr][l][se];
+        if (l + 1 < L) Elem<T>::store(ring + (ring_offset(l + 1) + (t & ring_mask(l + 1))) * d, v);
+      }
+    }
+    Elem<T>::store((T*)a.Y + (int64_t)(b0 + sr) * d + (int64_t)h * hd + se, v);
+  }
+}
+
+template <typename T, int RPB, int C, int LMAX>
+void launch_fused(const StepArgs& a, hipStream_t s) {
+  dim3 grid(a.H, (a.B + RPB - 1) / RPB), block(kFusedThreads);
+  decode_mixer_step_kernel<T, RPB, C, LMAX><<<grid, block, 0, s>>>(a);
+}
+
+template <typename T, int LMAX>
+void dispatch_rc(const StepArgs& a, int rpb, int C, hipStream_t s) {
+  if (C <= 1) {
+    if (rpb == 1) launch_fused<T, 1, 1, LMAX>(a, s); else launch_fused<T, 2, 1, LMAX>(a, s);
+  } else if (C == 2) {
+    if (rpb == 1) launch_fused<T, 1, 2, LMAX>(a, s); else launch_fused<T, 2, 2, LMAX>(a, s);
+  } else {
+    launch_fused<T, 1, 4, LMAX>(a, s);
+  }
+}
+
+template <typename T>
+void dispatch_fused(const StepArgs& a, int rpb, int C, hipStream_t s) {
+  if (a.L <= 8) dispatch_rc<T, 8>(a, rpb, C, s);
+  else if (a.L <= 12) dispatch_rc<T, 12>(a, rpb, C, s);
+  else dispatch_rc<T, 16>(a, rpb, C, s);
 }
 
 template <typename T>
@@ -218,6 +419,7 @@ __global__ __launch_bounds__(kThreads) void step_scan_kernel(StepArgs a) {
   scan_phase<T>(a, blockIdx.x, t);
 }
 
+
 bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
 
 int check_common(const char* who, int dtype, int B, int Tmax, int GH, int H, int hd, int L) {
@@ -233,37 +435,33 @@ int check_common(const char* who, int dtype, int B, int Tmax, int GH, int H, int
 
 }  // namespace
 
-extern "C" size_t dh_decode_workspace_bytes(int B, int L, int H) {
-  if (B < 1 || L < 1 || H < 1) return 0;
-  return (size_t)H * kCounterStride * sizeof(unsigned int) + 2 * (size_t)B * L * H * sizeof(float);
-}
-
 extern "C" int dh_decode_mixer_step(int dtype, const void* A, const void* B_hist, const void* Wi,
                                     const void* Wf, const void* Wr, const void* bi, const void* bf,
                                     const void* br, const int64_t* t_dev, void* rg_hist,
-                                    void* V_ring, const void* V0, void* Y, void* workspace, int B,
-                                    int Tmax, int S, int GH, int H, int hd, int L, void* stream) {
+                                    void* V_ring, const void* V0, void* Y, int B, int Tmax, int S, int GH,
+                                    int H, int hd, int L, void* stream) {
   const char* who = "dh_decode_mixer_step";
   int st = check_common(who, dtype, B, Tmax, GH, H, hd, L);
   if (st) return st;
   DH_REQUIRE(S == (int)ring_offset(L), DH_ERR_INVALID_ARG, "%s: S=%d but L=%d needs %lld ring slots", who, S, L,
              (long long)ring_offset(L));
-  DH_REQUIRE(A && B_hist && Wi && Wf && Wr && bi && bf && br && t_dev && rg_hist && V_ring && V0 && Y && workspace,
+  DH_REQUIRE(A && B_hist && Wi && Wf && Wr && bi && bf && br && t_dev && rg_hist && V_ring && V0 && Y,
              DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
-  DH_REQUIRE(aligned(A, 16) && aligned(B_hist, 16) && aligned(Wi, 16) && aligned(Wf, 16) && aligned(Wr, 16) &&
-                 aligned(workspace, 128),
-             DH_ERR_INVALID_ARG, "%s: A/B_hist/W need 16-byte and workspace 128-byte alignment", who);
-  StepArgs a{A, B_hist, Wi, Wf, Wr, bi, bf, br, t_dev, rg_hist, V_ring, V0, Y, nullptr, nullptr, nullptr,
-             B, Tmax, S, GH, H, hd, L};
-  a.counters = (unsigned int*)workspace;
-  a.IG = (float*)((char*)workspace + (size_t)H * kCounterStride * sizeof(unsigned int));
-  a.FG = a.IG + (size_t)B * L * H;
-  dim3 grid(H * L), block(kThreads);
+  DH_REQUIRE(aligned(A, 16) && aligned(B_hist, 16) && aligned(Wi, 16) && aligned(Wf, 16) && aligned(Wr, 16),
+             DH_ERR_INVALID_ARG, "%s: A/B_hist/W need 16-byte alignment", who);
+  const int vec = dtype == DH_BF16 ? 8 : 4;
+  const int C = (GH / vec + 63) / 64;          // 16-byte chunks per lane of one weight row
+  DH_REQUIRE(C <= 4, DH_ERR_UNSUPPORTED_SHAPE, "%s: GH=%d exceeds %d elements per gate row", who, GH, 4 * 64 * vec);
+  // two rows per workgroup once the batch has more than one, while two rows' operands still fit
+  // the register budget
+  const int rpb = (B >= 2 && C <= 2 && 2 * hd <= kFusedThreads) ? 2 : 1;
+  StepArgs a{A, B_hist, Wi, Wf, Wr, bi, bf, br, t_dev, rg_hist, V_ring, V0, Y, nullptr, nullptr,
+             B, Tmax, S, GH, H, hd, L, rpb};
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DH_F32)
-    decode_mixer_step_kernel<float><<<grid, block, 0, s>>>(a);
+    dispatch_fused<float>(a, rpb, C, s);
   else
-    decode_mixer_step_kernel<bf16_t><<<grid, block, 0, s>>>(a);
+    dispatch_fused<bf16_t>(a, rpb, C, s);
   return dh_check_launch(who);
 }
 
@@ -278,8 +476,8 @@ extern "C" int dh_step_gates(int dtype, const void* A, const void* B_hist, const
              DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
   DH_REQUIRE(aligned(A, 16) && aligned(B_hist, 16) && aligned(Wi, 16) && aligned(Wf, 16) && aligned(Wr, 16),
              DH_ERR_INVALID_ARG, "%s: A/B_hist/W need 16-byte alignment", who);
-  StepArgs a{A, B_hist, Wi, Wf, Wr, bi, bf, br, t_dev, rg_hist, nullptr, nullptr, nullptr, IG, FG, nullptr,
-             B, Tmax, 0, GH, H, 64, L};
+  StepArgs a{A, B_hist, Wi, Wf, Wr, bi, bf, br, t_dev, rg_hist, nullptr, nullptr, nullptr, IG, FG,
+             B, Tmax, 0, GH, H, 64, L, 0};
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DH_F32)
     step_gates_kernel<float><<<dim3(H * L), dim3(kThreads), 0, s>>>(a);
@@ -299,7 +497,7 @@ extern "C" int dh_step_scan(int dtype, const void* V0, const float* IG, const fl
   DH_REQUIRE(V0 && IG && FG && rg_hist && V_ring && t_dev && Y, DH_ERR_INVALID_ARG, "%s: null pointer argument",
              who);
   StepArgs a{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, t_dev, (void*)rg_hist,
-             V_ring, V0, Y, (float*)IG, (float*)FG, nullptr, B, Tmax, S, 64, H, hd, L};
+             V_ring, V0, Y, (float*)IG, (float*)FG, B, Tmax, S, 64, H, hd, L, 0};
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DH_F32)
     step_scan_kernel<float><<<dim3(H), dim3(kThreads), 0, s>>>(a);

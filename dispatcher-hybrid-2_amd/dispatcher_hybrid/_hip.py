@@ -47,7 +47,7 @@ def _load():
         lib = ctypes.CDLL(path)
     except OSError as e:  # pragma: no cover - depends on the host
         raise ImportError(f"cannot load {path}: {e}") from e
-    vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
     sigs = {
         "dh_abi_version": ([], i32),
         "dh_last_error": ([], ctypes.c_char_p),
@@ -58,9 +58,10 @@ def _load():
                                  i32, i32, i32, i32, i32, vp], i32),
         "dh_level_scan_fwd": ([i32, vp, vp, vp, vp, i64, i64, vp, i64, i64, vp,
                                i32, i32, i32, i32, i32, vp], i32),
-        "dh_decode_workspace_bytes": ([i32, i32, i32], sz),
-        "dh_decode_mixer_step": ([i32] + [vp] * 14 + [i32] * 7 + [vp], i32),
+        "dh_decode_mixer_step": ([i32] + [vp] * 13 + [i32] * 7 + [vp], i32),
         "dh_step_gates": ([i32] + [vp] * 12 + [i32] * 5 + [vp], i32),
+        "dh_decode_gemv": ([i32, vp, i64, vp, vp, ctypes.c_float, i32, vp, vp, vp, vp, vp,
+                            vp, i64, vp, i32, vp, i32, i32, vp], i32),
         "dh_step_scan": ([i32] + [vp] * 7 + [i32] * 6 + [vp], i32),
     }
     for name, (argtypes, restype) in sigs.items():

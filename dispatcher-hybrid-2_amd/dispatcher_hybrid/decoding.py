@@ -379,9 +379,19 @@ class GraphedHybridDecoder(_GraphedBase):
 
 
 class FusedGraphedHybridDecoder(GraphedHybridDecoder):
-    """Graphed decoder whose tree step is one gfx950 kernel per layer (gate readouts for every
-    level + the level recurrence over the rings), in place of ~15 torch ops. Same caches, same
-    graph harness. Raises ImportError when the kernel library is missing."""
+    """Graphed decoder whose step runs on gfx950 kernels: per tree layer five launches
+
+        dh_decode_gemv       RMSNorm1 + [W_in; W1x; W1s] -> V0, A, B_hist[t]
+        dh_decode_mixer_step gate readouts of all L levels + the level recurrence over the rings
+        dh_decode_gemv       linear_out + residual
+        dh_decode_gemv       RMSNorm2 + [W_gate; W_up] + SwiGLU
+        dh_decode_gemv       linear_down + residual
+
+    in place of ~17 torch ops, the embedding gather folded into the first launch and RMSNorm_out +
+    lm_head as one launch. Attention layers use dh_decode_gemv for their projections and torch for
+    RoPE and the windowed softmax. Same caches, same graph harness; raises ImportError when the
+    kernel library is missing.
+    """
 
     def __init__(self, model, max_len=None, dtype=None):
         from . import fused_step                          # loads libdh_mixer.so
@@ -389,22 +399,90 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         super().__init__(model, max_len, dtype)
 
     def _prepare(self):
+        super()._prepare()
         dev = next(self.m.parameters()).device
+        cfg = self.m.config
+        Bb, dt = self.inner.batch, self.dtype
         mix0 = next(b.mixer for b in self.m.blocks if hasattr(b, "mixer"))
-        Bb = self.inner.batch
-        # per-call scratch shared by every layer (stream-ordered; left zeroed by each call)
-        self.workspace = self._fused_step.decode_workspace(Bb, mix0.levels, mix0.num_heads, dev)
-        self.y_buf = torch.zeros(Bb, self.m.config.d_model, device=dev, dtype=self.dtype)
+        gh = mix0.gate_hidden.out_features
+        z = lambda n: torch.zeros(Bb, n, device=dev, dtype=dt)
+        self.x_buf = z(cfg.d_model)            # residual stream
+        self.v0_buf, self.y_buf = z(cfg.d_model), z(cfg.d_model)
+        self.a_buf = z(gh)
+        self.h_buf = z(cfg.dim_feedforward)
+        self.q_buf, self.k_buf, self.v_buf = z(cfg.d_model), z(cfg.d_model), z(cfg.d_model)
 
-    def _tree_step_g(self, i, blk, cache, x):
+    @staticmethod
+    def _eps(norm, dtype):
+        # nn.RMSNorm(eps=None) takes the epsilon of torch's math type, fp32 for fp32 and bf16 inputs
+        return norm.eps if norm.eps is not None else torch.finfo(torch.float32).eps
+
+    def _ffn_g(self, blk):
+        fs = self._fused_step
+        f, d = blk.ffn, self.x_buf.shape[1]
+        ff = self.h_buf.shape[1]
+        fs.decode_gemv(self.x_buf, [(f.linear_gate.weight, self.h_buf, ff, 0),
+                                    (f.linear_up.weight, self.h_buf, ff, 0)], self.t_buf,
+                       norm_weight=blk.norm2.weight, eps=self._eps(blk.norm2, self.dtype), swiglu=True)
+        fs.decode_gemv(self.h_buf, [(f.linear_down.weight, self.x_buf, d, 0)], self.t_buf,
+                       resid=self.x_buf)
+
+    def _input(self, first):
+        """The block's input rows: the embedding rows of the tokens for the first block."""
+        if first:
+            return self.m.embedding.weight, self.token_buf
+        return self.x_buf, None
+
+    def _tree_step_f(self, blk, cache, first):
+        fs = self._fused_step
         mx = blk.mixer
-        h1 = blk.norm1(x)
-        A = mx.gate_hidden(h1)
-        cache.B_hist.index_copy_(1, self.t_buf, mx.gate_hidden_src(h1).unsqueeze(1))
-        V0 = mx.linear_in(h1)
-        self._fused_step.decode_mixer_step(
-            A, cache.B_hist, mx.gate_out, mx.forget_out, mx.reset_out,
-            mx.gate_out_bias, mx.forget_out_bias, mx.reset_out_bias, self.t_buf,
-            cache.rg_hist, cache.V_ring, V0, self.y_buf, self.workspace)
-        x = x + mx.linear_out(self.y_buf)
-        return x + blk.ffn(blk.norm2(x))
+        d, gh = self.x_buf.shape[1], self.a_buf.shape[1]
+        x_in, rows = self._input(first)
+        fs.decode_gemv(x_in, [(mx.linear_in.weight, self.v0_buf, d, 0),
+                              (mx.gate_hidden.weight, self.a_buf, gh, 0),
+                              (mx.gate_hidden_src.weight, cache.B_hist, cache.B_hist.stride(0), gh)],
+                       self.t_buf, norm_weight=blk.norm1.weight, eps=self._eps(blk.norm1, self.dtype),
+                       x_rows=rows)
+        fs.decode_mixer_step(self.a_buf, cache.B_hist, mx.gate_out, mx.forget_out, mx.reset_out,
+                             mx.gate_out_bias, mx.forget_out_bias, mx.reset_out_bias, self.t_buf,
+                             cache.rg_hist, cache.V_ring, self.v0_buf, self.y_buf)
+        fs.decode_gemv(self.y_buf, [(mx.linear_out.weight, self.x_buf, d, 0)], self.t_buf,
+                       resid=x_in, resid_rows=rows)
+        self._ffn_g(blk)
+
+    def _attn_step_f(self, blk, cache, first):
+        fs = self._fused_step
+        at = blk.attn
+        Bb, d = self.x_buf.shape
+        x_in, rows = self._input(first)
+        fs.decode_gemv(x_in, [(at.linear_q.weight, self.q_buf, d, 0), (at.linear_k.weight, self.k_buf, d, 0),
+                              (at.linear_v.weight, self.v_buf, d, 0)], self.t_buf,
+                       norm_weight=blk.norm1.weight, eps=self._eps(blk.norm1, self.dtype), x_rows=rows)
+        cos = cache.rope_cos.index_select(0, self.t_buf)[0]
+        sin = cache.rope_sin.index_select(0, self.t_buf)[0]
+        H, hd = at.num_heads, at.head_dim
+        q = rope_rotate(self.q_buf.view(Bb, H, hd), cos, sin)
+        cache.k.index_copy_(2, self.t_buf, rope_rotate(self.k_buf.view(Bb, H, hd), cos, sin).unsqueeze(2))
+        cache.v.index_copy_(2, self.t_buf, self.v_buf.view(Bb, H, hd).unsqueeze(2))
+        valid = self.arangeT <= self.t_buf
+        if at.window > 0:
+            valid = valid & (self.arangeT > self.t_buf - at.window)
+        scores = torch.matmul(cache.k, q.unsqueeze(-1)).squeeze(-1) / math.sqrt(hd)
+        scores = scores.masked_fill(~valid.view(1, 1, -1), float("-inf"))
+        att = torch.softmax(scores.float(), dim=-1).to(self.dtype)
+        self.y_buf.copy_(torch.matmul(att.unsqueeze(2), cache.v).squeeze(2).reshape(Bb, -1))
+        fs.decode_gemv(self.y_buf, [(at.linear_out.weight, self.x_buf, d, 0)], self.t_buf,
+                       resid=x_in, resid_rows=rows)
+        self._ffn_g(blk)
+
+    def _step_all(self):
+        for i, (blk, cache) in enumerate(zip(self.m.blocks, self.inner.caches)):
+            if isinstance(blk, AttentionBlock):
+                self._attn_step_f(blk, cache, i == 0)
+            else:
+                self._tree_step_f(blk, cache, i == 0)
+        V = self.logits_out.shape[1]
+        self._fused_step.decode_gemv(self.x_buf, [(self.m.lm_head.weight, self.logits_out, V, 0)],
+                                     self.t_buf, norm_weight=self.m.norm_out.weight,
+                                     eps=self._eps(self.m.norm_out, self.dtype))
+        self.t_buf.add_(1)

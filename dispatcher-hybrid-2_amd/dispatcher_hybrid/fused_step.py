@@ -2,9 +2,10 @@
 
 Drop-in for the reference module of the same name (reference dispatcher_hybrid/fused_step.py),
 whose two Triton kernels run the gate readouts over (row, level) and the level recurrence over
-(row, head). Here the whole step is ONE kernel per layer (``dh_decode_mixer_step``):
-workgroup (head, level) streams its gate weight rows once for every batch row, and the workgroup
-that finishes a head's last level runs that head's L-level recurrence over the ring buffers.
+(row, head). Here the whole step is ONE kernel per layer (``dh_decode_mixer_step``): one
+workgroup per (head, block of rows) reads its head's 3*L gate weight rows once, reduces them
+against every row's hidden vectors for all L levels, and runs the head's L-level recurrence over
+the ring buffers; no workgroup waits on another and no scratch memory is needed.
 
 Ring layout (unchanged, reference dispatcher_hybrid/decoding.py:28-37, fused_step.py:13-16):
 level j's state is read only at lag 2^j, so ring j keeps 2^(j+1) slots at offset 2^(j+1)-2 and
@@ -16,6 +17,8 @@ name; they run the two halves of the same HIP kernel as separate launches.
 
 Importing this module loads the kernel library and raises ImportError if it is missing.
 """
+
+import ctypes
 
 import torch
 
@@ -30,22 +33,12 @@ def ring_mask(j):
     return (2 << j) - 1
 
 
-def decode_workspace(batch, levels, heads, device):
-    """Zero-filled scratch for ``decode_mixer_step`` (per-head counters + fp32 gate values).
-
-    The kernel leaves it zeroed after every call, so one buffer serves every layer and every
-    graph replay of a decoder.
-    """
-    n = _hip.lib.dh_decode_workspace_bytes(batch, levels, heads)
-    return torch.zeros(max(int(n), 1), dtype=torch.uint8, device=device)
-
-
 def _check_contig(name, t):
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
 
 
-def decode_mixer_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring, V0, Y, workspace):
+def decode_mixer_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring, V0, Y):
     """One tree layer's decode step at the position held in the device tensor `t_buf`.
 
     A (B, GH) current destination features; B_hist (B, Tmax, GH) with row t written;
@@ -69,15 +62,48 @@ def decode_mixer_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring,
         raise TypeError("t_buf must be an int64 device tensor")
     if tuple(rg_hist.shape) != (Bb, Tmax, L, H) or tuple(V0.shape) != (Bb, d) or tuple(Y.shape) != (Bb, d):
         raise ValueError("decode_mixer_step: inconsistent cache / buffer shapes")
-    if workspace.numel() < _hip.lib.dh_decode_workspace_bytes(Bb, L, H):
-        raise ValueError("decode_mixer_step: workspace too small")
     p = _hip.ptr
     st = _hip.lib.dh_decode_mixer_step(
         _hip.dtype_code(dt), p(A), p(B_hist), p(Wi), p(Wf), p(Wr), p(bi), p(bf), p(br), p(t_buf),
-        p(rg_hist), p(V_ring), p(V0), p(Y), p(workspace), Bb, Tmax, S, GH, H, d // H, L,
+        p(rg_hist), p(V_ring), p(V0), p(Y), Bb, Tmax, S, GH, H, d // H, L,
         _hip.stream_handle(A.device))
     _hip.check(st, "dh_decode_mixer_step")
     return Y
+
+
+def decode_gemv(x, segments, t_buf, norm_weight=None, eps=None, resid=None, swiglu=False,
+                x_rows=None, resid_rows=None):
+    """Fused matrix-vector products of the decode step (``dh_decode_gemv``).
+
+    x: (B, K) activations (or the embedding table with ``x_rows`` = token ids: row b is
+    x[x_rows[b]]). segments: up to three (W, out, out_bstride, t_stride) with W (N, K) and
+    out[b * out_bstride + t * t_stride + n] receiving output n of batch row b (t = t_buf[0]).
+    norm_weight: RMSNorm weight applied to x first (eps defaults to the fp32 epsilon 2^-23, which
+    nn.RMSNorm(eps=None) takes from torch's fp32 math type for fp32 and bf16 inputs alike). resid: (B, N) added to segment 0's result (rows through
+    ``resid_rows`` when given); swiglu: segments are (gate, up) and silu(gate) * up goes to the
+    gate segment's destination. Everything in one dtype (fp32 or bf16) on one GPU.
+    """
+    _hip.require_gpu(x, "decode_gemv")
+    dt = x.dtype
+    K = x.shape[-1]
+    B = x_rows.numel() if x_rows is not None else x.shape[0]
+    n = len(segments)
+    Ws = (ctypes.c_void_p * n)(*[W.data_ptr() for W, _, _, _ in segments])
+    outs = (ctypes.c_void_p * n)(*[o.data_ptr() for _, o, _, _ in segments])
+    obs = (ctypes.c_int64 * n)(*[int(bs) for _, _, bs, _ in segments])
+    ots = (ctypes.c_int64 * n)(*[int(ts) for _, _, _, ts in segments])
+    Ns = (ctypes.c_int * n)(*[W.shape[0] for W, _, _, _ in segments])
+    for W, o, _, _ in segments:
+        if W.dtype != dt or o.dtype != dt or W.shape[1] != K or not W.is_contiguous():
+            raise ValueError("decode_gemv: segment weights must be contiguous (N, K) in the activation dtype")
+    if norm_weight is not None and eps is None:
+        eps = torch.finfo(torch.float32).eps
+    p = _hip.ptr
+    st = _hip.lib.dh_decode_gemv(
+        _hip.dtype_code(dt), p(x), x.stride(0), p(x_rows), p(norm_weight), float(eps or 0.0), n,
+        Ws, outs, obs, ots, Ns, p(resid), resid.stride(0) if resid is not None else 0, p(resid_rows),
+        int(bool(swiglu)), p(t_buf), B, K, _hip.stream_handle(x.device))
+    _hip.check(st, "dh_decode_gemv")
 
 
 class _Launcher:

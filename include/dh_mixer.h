@@ -113,17 +113,37 @@ int dh_level_scan_fwd(int dtype, const void* pre_i, const void* pre_f, const voi
  *             state entering level j; position p lives in slot 2^(j+1)-2 + (p & (2^(j+1)-1)).
  *   V0        (B, H*hd) linear_in output of the current token (ring 0's new entry).
  *   Y         (B, H*hd) output: state after level L-1.
- *   workspace dh_decode_workspace_bytes(B, L, H) bytes, zero-filled once before its first use; every
- *             call leaves it zeroed again. Calls sharing a workspace must be stream-ordered.
  *   If t_dev holds a position outside [0, Tmax) the kernel writes nothing.
+ *   Needs no scratch memory: one workgroup per (head, block of rows), none waiting on another.
  */
-size_t dh_decode_workspace_bytes(int B, int L, int H);
-
 int dh_decode_mixer_step(int dtype, const void* A, const void* B_hist, const void* Wi,
                          const void* Wf, const void* Wr, const void* bi, const void* bf,
                          const void* br, const int64_t* t_dev, void* rg_hist, void* V_ring,
-                         const void* V0, void* Y, void* workspace, int B, int Tmax, int S, int GH,
-                         int H, int hd, int L, void* stream);
+                         const void* V0, void* Y, int B, int Tmax, int S, int GH, int H, int hd,
+                         int L, void* stream);
+
+/*
+ * Matrix-vector products of the decode step with their neighbouring elementwise work fused in.
+ * Replaces the torch GEMV chain around the mixer step in FusedGraphedHybridDecoder._tree_step_g and
+ * _step_all (reference dispatcher_hybrid/decoding.py:473-476, :487-488, :442) and the SwiGLU and
+ * RMSNorm they call (reference dispatcher_hybrid/modeling_dispatcher.py:196-197, 207-212, 276):
+ *   h = norm_w ? RMSNorm(x[b], eps) * norm_w : x[b]           (x[b] = x + x_rows[b]*x_bstride when
+ *                                                              x_rows is given, else x + b*x_bstride)
+ *   segment s (s < nseg <= 3): W[s] is (N[s], K) row-major; for n < N[s]:
+ *     out[s][b*out_bstride[s] + t*out_t_stride[s] + n] =
+ *         round(W[s][n].h)                                     plain
+ *       | round(round(W[0][n].h) + resid[b, n])               resid != NULL (nseg == 1); resid[b] as x
+ *       | round(round(silu(round(W[0][n].h))) * round(W[1][n].h)) into out[0]   swiglu (nseg == 2)
+ *   t = *t_dev (device position; e.g. the B_hist row of the source projection).
+ * All activations and weights in dtype; fp32 accumulation. The array arguments W, out, out_bstride,
+ * out_t_stride and N are host arrays of nseg entries. K must be a multiple of 8 (bf16) or 4 (fp32):
+ * rows are read in 16-byte chunks.
+ */
+int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const int64_t* x_rows,
+                   const void* norm_w, float eps, int nseg, const void* const* W, void* const* out,
+                   const int64_t* out_bstride, const int64_t* out_t_stride, const int* N,
+                   const void* resid, int64_t resid_bstride, const int64_t* resid_rows, int swiglu,
+                   const int64_t* t_dev, int B, int K, void* stream);
 
 /*
  * The two halves of dh_decode_mixer_step as separate launches, with the reference's own buffer

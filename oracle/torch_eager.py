@@ -4,7 +4,7 @@ A functional restatement (no nn.Module tree) of the reference model's eager forw
 eager incremental decoder, run on the CPU. It is the end-to-end checker for the HIP paths and the
 timed CPU baseline of bench.py. Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline
 leg import it. It uses the same torch operations as the reference's eager branch (roll, einsum,
-scaled_dot_product_attention, rms_norm with eps = finfo(dtype).eps), so its bf16 rounding points
+scaled_dot_product_attention, rms_norm with eps=None, i.e. the fp32 epsilon), so its bf16 rounding points
 are those of the reference.
 
 Reference lines followed (/root/reference/dispatcher_hybrid/...):
@@ -41,7 +41,7 @@ class Spec:
 
 
 def _norm(x, w):
-    return F.rms_norm(x, (x.shape[-1],), w)                 # eps=None -> finfo(x.dtype).eps
+    return F.rms_norm(x, (x.shape[-1],), w)                 # eps=None -> 2^-23 (fp32 math type)
 
 
 def _w(sd, name):

@@ -20,7 +20,7 @@ def declared_functions():
 def test_header_declares_the_entry_points():
     names = declared_functions()
     for must in ("dh_abi_version", "dh_last_error", "dh_gate_preacts_fwd", "dh_gate_preacts_bwd",
-                 "dh_level_scan_fwd", "dh_decode_workspace_bytes", "dh_decode_mixer_step",
+                 "dh_level_scan_fwd", "dh_decode_mixer_step",
                  "dh_step_gates", "dh_step_scan"):
         assert must in names
 
@@ -38,23 +38,22 @@ def test_status_codes_without_device_work():
     lib = _hip.lib
     S = None
     # unsupported dtype
-    st = lib.dh_decode_mixer_step(7, *([S] * 14), 1, 8, 14, 64, 2, 64, 3, S)
+    st = lib.dh_decode_mixer_step(7, *([S] * 13), 1, 8, 14, 64, 2, 64, 3, S)
     assert st == 3 and b"dtype" in lib.dh_last_error()
     # unsupported head width
-    st = lib.dh_decode_mixer_step(1, *([S] * 14), 1, 8, 14, 64, 2, 48, 3, S)
+    st = lib.dh_decode_mixer_step(1, *([S] * 13), 1, 8, 14, 64, 2, 48, 3, S)
     assert st == 2 and b"hd=48" in lib.dh_last_error()
     # S inconsistent with L
-    st = lib.dh_decode_mixer_step(1, *([S] * 14), 1, 8, 13, 64, 2, 64, 3, S)
+    st = lib.dh_decode_mixer_step(1, *([S] * 13), 1, 8, 13, 64, 2, 64, 3, S)
     assert st == 1
     # null pointers
-    st = lib.dh_decode_mixer_step(1, *([S] * 14), 1, 8, 14, 64, 2, 64, 3, S)
+    st = lib.dh_decode_mixer_step(1, *([S] * 13), 1, 8, 14, 64, 2, 64, 3, S)
     assert st == 1 and b"null" in lib.dh_last_error()
     st = lib.dh_gate_preacts_fwd(0, *([S] * 2), 0, 0, *([S] * 3), 0, 0, *([S] * 4), 0, 0,
                                  *([S] * 3), 1, 8, 60, 2, 3, S)
     assert st == 2 and b"GH=60" in lib.dh_last_error()
     st = lib.dh_level_scan_fwd(1, *([S] * 4), 0, 0, S, 0, 0, S, 1, 40000, 2, 64, 3, S)
     assert st == 2 and b"32768" in lib.dh_last_error()
-    assert lib.dh_decode_workspace_bytes(16, 12, 16) == 16 * 128 + 2 * 16 * 12 * 16 * 4
 
 
 def test_python_wrapper_maps_status_to_exceptions():

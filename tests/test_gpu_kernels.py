@@ -171,7 +171,6 @@ def _run_decode(case, dtype, seed, split=False, W_zero=False, bias=None, V0_oneh
     tW = [_cuda(w, dtype) for w in Ws]
     tb = [_cuda(x, dtype) for x in bs]
     st = _DecodeState(Bb, Tmax, GH, H, hd, L, dtype, sentinel)
-    ws = fused_step.decode_workspace(Bb, L, H, DEV)
     IG = torch.zeros(Bb, L * H, dtype=torch.float32, device=DEV)
     FG = torch.zeros_like(IG)
     Ys = []
@@ -185,11 +184,11 @@ def _run_decode(case, dtype, seed, split=False, W_zero=False, bias=None, V0_oneh
                                                  st.t_buf, st.Y, Tmax, st.S, L=L, HD=hd, H=H)
         else:
             fused_step.decode_mixer_step(tA[:, t].contiguous(), st.B_hist, *tW, *tb, st.t_buf,
-                                         st.rg_hist, st.V_ring, tV0[:, t].contiguous(), st.Y, ws)
+                                         st.rg_hist, st.V_ring, tV0[:, t].contiguous(), st.Y)
         Ys.append(st.Y.clone())
     torch.cuda.synchronize()
     inputs = dict(A=_np(tA), Bs=_np(tBs), V0=_np(tV0), W=[_np(w) for w in tW], b=[_np(x) for x in tb])
-    return st, torch.stack(Ys, 1), ws, inputs
+    return st, torch.stack(Ys, 1), inputs
 
 
 def _oracle_decode(case, inp, sentinel=0.0):
@@ -209,14 +208,13 @@ def _oracle_decode(case, inp, sentinel=0.0):
 @pytest.mark.parametrize("case", DECODE_CASES)
 def test_decode_mixer_step_matches_oracle(case, dtype):
     print(f"decode case={case} dtype={dtype}", flush=True)
-    st, Y, ws, inp = _run_decode(case, dtype, seed=11)
+    st, Y, inp = _run_decode(case, dtype, seed=11)
     Yo, rgo, ringo = _oracle_decode(case, inp)
     T = case[1]
     tol = 1e-5 if dtype == torch.float32 else 2e-2
     assert rel_err(_np(Y), Yo) < tol
     assert rel_err(_np(st.rg_hist[:, :T]), rgo[:, :T]) < (1e-6 if dtype == torch.float32 else 8e-3)
     assert rel_err(_np(st.V_ring), ringo) < tol
-    assert int(torch.count_nonzero(ws)) == 0, "workspace must be left zeroed"
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -225,7 +223,7 @@ def test_decode_ring_slots_bit_exact(dtype):
     sum, exact in any dtype, and unwritten slots keep a sentinel. The whole ring, rg_hist and
     every output must equal the oracle's bit for bit."""
     case = (2, 100, 128, 64, 2, 64, 7)
-    st, Y, _, inp = _run_decode(case, dtype, seed=3, W_zero=True, bias=(800.0, 800.0, 800.0),
+    st, Y, inp = _run_decode(case, dtype, seed=3, W_zero=True, bias=(800.0, 800.0, 800.0),
                                 V0_onehot=True, sentinel=-3.0)
     Yo, rgo, ringo = _oracle_decode(case, inp, sentinel=-3.0)
     assert np.array_equal(_np(st.V_ring), ringo)
@@ -233,14 +231,16 @@ def test_decode_ring_slots_bit_exact(dtype):
     assert np.array_equal(_np(Y), Yo)
 
 
-def test_split_launches_equal_fused_kernel():
-    """step_gates_kernel + step_scan_kernel (reference launch syntax) == one fused launch."""
+def test_split_launches_match_fused_kernel():
+    """step_gates_kernel + step_scan_kernel (reference launch syntax) agree with one fused
+    launch (different reduction trees: equal to rounding)."""
     case = (3, 30, 64, 128, 4, 16, 6)
-    for dtype in (torch.float32, torch.bfloat16):
-        a, Ya, _, _ = _run_decode(case, dtype, seed=5)
-        b, Yb, _, _ = _run_decode(case, dtype, seed=5, split=True)
-        assert torch.equal(Ya, Yb)
-        assert torch.equal(a.V_ring, b.V_ring) and torch.equal(a.rg_hist, b.rg_hist)
+    for dtype, tol in ((torch.float32, 1e-6), (torch.bfloat16, 2e-2)):
+        a, Ya, _ = _run_decode(case, dtype, seed=5)
+        b, Yb, _ = _run_decode(case, dtype, seed=5, split=True)
+        assert rel_err(_np(Ya), _np(Yb)) < tol
+        assert rel_err(_np(a.V_ring), _np(b.V_ring)) < tol
+        assert rel_err(_np(a.rg_hist), _np(b.rg_hist)) < tol
 
 
 def test_decode_position_out_of_range_writes_nothing():
@@ -251,16 +251,14 @@ def test_decode_position_out_of_range_writes_nothing():
     W = torch.randn(L, H, GH, device=DEV)
     bias = torch.zeros(L, H, device=DEV)
     V0 = torch.randn(Bb, H * hd, device=DEV)
-    ws = fused_step.decode_workspace(Bb, L, H, DEV)
     before = (st.rg_hist.clone(), st.V_ring.clone(), st.Y.clone())
     for t in (Tmax, Tmax + 5, -1):
         st.t_buf.fill_(t)
         fused_step.decode_mixer_step(A, st.B_hist, W, W, W, bias, bias, bias, st.t_buf, st.rg_hist,
-                                     st.V_ring, V0, st.Y, ws)
+                                     st.V_ring, V0, st.Y)
     torch.cuda.synchronize()
     assert torch.equal(before[0], st.rg_hist) and torch.equal(before[1], st.V_ring)
     assert torch.equal(before[2], st.Y)
-    assert int(torch.count_nonzero(ws)) == 0
 
 
 def test_decode_wrapper_rejects_mixed_dtypes():
@@ -269,8 +267,7 @@ def test_decode_wrapper_rejects_mixed_dtypes():
     st = _DecodeState(Bb, Tmax, GH, H, hd, L, torch.float32)
     W = torch.randn(L, H, GH, device=DEV, dtype=torch.bfloat16)
     bias = torch.zeros(L, H, device=DEV)
-    ws = fused_step.decode_workspace(Bb, L, H, DEV)
     with pytest.raises(TypeError, match="dtype"):
         fused_step.decode_mixer_step(torch.randn(Bb, GH, device=DEV), st.B_hist, W, W, W, bias, bias,
                                      bias, st.t_buf, st.rg_hist, st.V_ring,
-                                     torch.randn(Bb, H * hd, device=DEV), st.Y, ws)
+                                     torch.randn(Bb, H * hd, device=DEV), st.Y)
