@@ -4,8 +4,9 @@
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 
 Headline (`value`): steady-state batch-1 bf16 greedy decode tok/s of the 292M model at 3840-4096
-context through FusedGraphedHybridDecoder (one HIP-graph replay per token, one gfx950 mixer kernel
-per tree layer). A step is one decode token; prefill and graph capture are outside the timed region
+context through FusedGraphedHybridDecoder (one HIP-graph replay per token; five gfx950 launches
+per tree layer: fused RMSNorm/projections, the mixer step, out-projection + residual, RMSNorm +
+SwiGLU, down-projection + residual). A step is one decode token; prefill and graph capture are outside the timed region
 (reference scripts/benchmark_decode.py:21-28 protocol). Also reported in the same JSON line:
   decode_b16_*      lockstep batch-16 decode with temperature 0.8 / top-k 50 sampling
   prefill_*         C2: 292M bf16 forward at B=1, T=1024, fused gates vs eager
@@ -34,6 +35,10 @@ HBM_PEAK_GBS = 8000.0                  # MI355X HBM3E
 MFMA_BF16_TFLOPS = 2500.0              # MI355X dense bf16
 REF_DECODE_TOK_S = 525.1               # reference FusedGraphedHybridDecoder @3900 ctx (A6000, README.md:76-81)
 EOT = 50256
+# HBM bytes per dh_decode_mixer_step launch (bf16, B=1, 12 levels): rocprofv3 --pmc FETCH_SIZE
+# (1,613,665 B after scaling by the 256 MiB copy probe's reading, x1.9997) + WRITE_SIZE (29,696 B,
+# x1.0), from profiles/decode_c3_b1_kernels.md
+TRAFFIC_MIXER_STEP = 1_643_361
 
 
 def parse():
@@ -122,11 +127,12 @@ def time_mixer(torch, mixer, x, mask, fused, reps=5):
     return (time.perf_counter() - t0) / reps * 1e3
 
 
-def decode_kernel_roofline(torch, model, dec, copies=400):
-    """Average duration of dh_decode_mixer_step at B=1, t=4000 (all 12 levels live), each launch
-    bracketed by HIP events on the launch stream. The gate weights cycle through `copies` distinct
-    copies (> 256 MB in total, more than the MI355X last-level cache) so every launch streams its
-    weights from HBM as it does inside the decode step."""
+def decode_kernel_roofline(torch, model, dec, copies=400, reps=5):
+    """Average duration of dh_decode_mixer_step at B=1, t=4000 (all 12 levels live). The launches
+    run as they do inside the decode step: captured back to back in one HIP graph on the launch
+    stream, the graph replayed between two HIP events on that stream. The gate weights cycle
+    through `copies` distinct copies (> 256 MB in total, more than the MI355X last-level cache) so
+    every launch streams its weights from HBM. The figure includes the graph's inter-node gap."""
     from dispatcher_hybrid import fused_step
     dev = next(model.parameters()).device
     mx = next(b.mixer for b in model.blocks if hasattr(b, "mixer"))
@@ -141,25 +147,47 @@ def decode_kernel_roofline(torch, model, dec, copies=400):
     B_hist = torch.zeros(1, 4096, GH, device=dev, dtype=torch.bfloat16)
     rg = torch.zeros(1, 4096, L, H, device=dev, dtype=torch.bfloat16)
     ring = torch.zeros(1, cache.S, d, device=dev, dtype=torch.bfloat16)
-    stream = torch.cuda.current_stream()
 
     def launch(i):
         W = Ws[i % copies]
         fused_step.decode_mixer_step(A, B_hist, W[0], W[1], W[2], bi, bf, br, t_buf, rg, ring, V0, Y)
 
-    for i in range(32):
-        launch(i)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(copies)]
-    for i in range(copies):
-        ev[i][0].record(stream)
-        launch(i)
-        ev[i][1].record(stream)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(8):
+            launch(i)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(copies):
+            launch(i)
+    graph.replay()
     torch.cuda.synchronize()
-    avg_us = 1e3 * sum(a.elapsed_time(b) for a, b in ev) / copies
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    avg_us = 1e3 * e0.elapsed_time(e1) / (reps * copies)
+    del graph
     s = 2
     B = 1
     nbytes = 3 * L * H * GH * s + 3 * L * H * s + B * (L * GH + GH + 2 * L * H + 2 * L * d + 2 * d) * s
-    return nbytes, avg_us
+    return nbytes, avg_us, reps * copies
+
+
+def copy_probe(torch, dev, mib=256):
+    """One plain device-to-device copy of `mib` MiB (read once, written once). Under rocprofv3
+    --pmc its FETCH_SIZE / WRITE_SIZE readings turn those counters into bytes for the other
+    kernels of the same run."""
+    a = torch.zeros(mib << 20, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
 
 
 def cpu_baseline(torch, model, prompt, steps):
@@ -204,6 +232,7 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    copy_probe(torch, dev)
     model = build_model(torch, dev)
     max_len = model.config.max_len
     prompt = min(args.prompt, max_len - args.warmup - args.steps)
@@ -229,12 +258,12 @@ def main():
                             "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4),
                             "what": "bf16 weight bytes per decode token (584,316,928 B) x tok/s"}
 
-    nbytes, avg_us = decode_kernel_roofline(torch, model, dec1)
+    nbytes, avg_us, nl = decode_kernel_roofline(torch, model, dec1)
     achieved = nbytes / (avg_us * 1e-6) / 1e9
-    out["roofline"] = {"kernel": "dh_decode_mixer_step (decode_mixer_step_kernel<bf16>)", "bound": "hbm",
-                       "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                       "bytes_per_launch": nbytes, "avg_launch_us": round(avg_us, 3)}
+    out["roofline"] = {"kernel": "dh_decode_mixer_step (decode_mixer_step_kernel<bf16,1,2,12>)",
+                       "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_MIXER_STEP,
+                       "bytes_per_launch": nbytes, "avg_launch_us": round(avg_us, 3), "launches_timed": nl}
     log(f"decode mixer kernel: {avg_us:.2f} us/launch, {achieved:.0f} GB/s")
     del dec1
     torch.cuda.empty_cache()
