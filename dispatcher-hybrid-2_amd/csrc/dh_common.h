@@ -58,9 +58,10 @@ __device__ __forceinline__ void load4(const bf16_t* p, float (&o)[4]) {
   o[3] = __uint_as_float(v.y & 0xffff0000u);
 }
 
-// logistic function from the hardware exp: 1 / (1 + e^-x). Saturates to exactly 1.0 for x >= ~17
-// and to exactly 0.0 for x <= -~104 (e^-x overflows to +inf).
-__device__ __forceinline__ float dh_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// logistic function from the hardware exp and reciprocal (v_exp_f32, v_rcp_f32: 1 ulp): 1 / (1 + e^-x).
+// Saturates to exactly 1.0 for x >= ~17 (1 + e^-x rounds to 1, whose reciprocal is exact) and to
+// exactly 0.0 for x <= -~89 (e^-x overflows to +inf).
+__device__ __forceinline__ float dh_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 // DPP lane move of a float: lanes in the rows of ROWMASK read the lane CTRL selects, others get 0
 template <int CTRL, int ROWMASK>

@@ -5,16 +5,21 @@
 //   ok[b,t,l]      = t < T && t >= 2^l && (mask == null || mask[b,t,l] > 0)
 //   hid[b,t,l,k]   = relu(A[b,t,k] + ok * B[b,t-2^l,k])^2
 //   pre_x[b,t,l,h] = sum_k hid[b,t,l,k] * W_x[l,h,k] + b_x[l,h]          x in {i, f, r}
-// bf16 mode rounds a+b and hid to bf16 (the points where the eager bf16 path rounds), multiplies
-// on bf16 MFMA with fp32 accumulation, adds the fp32 bias and rounds once on store. fp32 mode uses
-// fp32 MFMA throughout.
+// bf16 mode rounds a+b and hid to bf16 (the points where the eager bf16 path rounds; the hardware
+// v_cvt_pk_bf16_f32 rounds to nearest even), multiplies on bf16 MFMA with fp32 accumulation, adds
+// the fp32 bias and rounds once on store. fp32 mode uses fp32 MFMA throughout. The outputs are
+// written through element strides, so a caller can ask for the (b, T, n_lv, H) layout of the
+// reference op or for the head-major (b, H, n_lv, T) layout the level scan reads best.
 //
-// Work decomposition: one workgroup (4 wave64s) per (batch row, 64-position tile); wave w owns
-// positions 16w..16w+15 of the tile and walks every level, so the A tile is fetched from HBM once
-// and re-read per level from L2. For each level the hidden tile is formed directly in the MFMA
-// A-operand registers (lane -> row lane%16, k-chunk lane/16) from A[t] and the lagged B[t-2^l] row,
-// and multiplied against W_x[l] (the B operand: lane -> head lane%16, same k-chunk) for the three
-// gates: N = 16 heads per MFMA tile, ceil(H/16) tiles per gate.
+// Work decomposition: one workgroup (4 wave64s) per (64-position tile, group of LG levels, batch
+// row); wave w owns positions 16w..16w+15 of the tile. For each k-chunk the lane's A fragment is
+// loaded once and reused by all LG levels of the group; each level adds its lagged B fragment,
+// forms the hidden tile in MFMA A-operand registers (lane -> row lane%16, k-chunk lane/16) and
+// multiplies it against W_x[l] (B operand: lane -> head lane%16) for the three gates, N = 16 heads
+// per MFMA tile. The k-loop is software-pipelined: the fragments of step k+1 are requested before
+// the MFMAs of step k are issued. The host picks LG so that tiles x groups fills the chip (small
+// prefills get one level per workgroup, long ones reuse A over four) and KU, the k-chunks per step,
+// so every step keeps enough bytes in flight.
 #include "dh_common.h"
 
 namespace {
@@ -24,6 +29,7 @@ constexpr int kTileT = 64;
 
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 struct FwdArgs {
   const void* A;
@@ -37,153 +43,221 @@ struct FwdArgs {
   const float* bf;
   const float* br;
   const void* mask;
-  int64_t smb, smt;
+  int64_t smb, smt, sml;
   void* oi;
   void* of;
   void* orr;
+  int64_t sob, sot, sol, soh;
   int b, T, GH, H, n_lv;
+  int vec_out;                  // outputs take 4-position vector stores (head-major, aligned)
+  int activate;                 // write the scan's gates a, f, r instead of pre-activations
 };
-
-template <typename T>
-__device__ __forceinline__ bool mask_ok(const FwdArgs& a, int b, int t, int l) {
-  if (!a.mask) return true;
-  return Elem<T>::load((const T*)a.mask + (int64_t)b * a.smb + (int64_t)t * a.smt + l) > 0.f;
-}
 
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
-// bf16 forward
-__global__ __launch_bounds__(kThreads) void gate_preacts_fwd_bf16(FwdArgs a) {
+// two fp32 -> packed bf16 (round to nearest even, hardware conversion)
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2_t v;
+  v.x = (__bf16)lo;
+  v.y = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Element math of the two modes. KC = k elements one 16-byte fragment per lane covers across the
+// wave's four lane groups; mma3 adds hid(a, b) . W_x for the three gates.
+struct MathBf16 {
+  typedef bf16_t T;
+  static constexpr int KC = 32;
+  static constexpr int KL = 8;      // k elements per lane fragment
+  __device__ __forceinline__ static void mma3(f32x4 (&acc)[3], const uint4& av, const uint4& bv, uint32_t keep,
+                                              const uint4 (&w)[3]) {
+    const uint32_t aw[4] = {av.x, av.y, av.z, av.w};
+    const uint32_t bw[4] = {bv.x & keep, bv.y & keep, bv.z & keep, bv.w & keep};
+    uint32_t hw[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float s0 = fmaxf(__uint_as_float(aw[j] << 16) + __uint_as_float(bw[j] << 16), 0.f);
+      const float s1 = fmaxf(__uint_as_float(aw[j] & 0xffff0000u) + __uint_as_float(bw[j] & 0xffff0000u), 0.f);
+      const uint32_t r = pack_bf16x2(s0, s1);                 // relu(round(a+b)) = round(relu(a+b))
+      const float x0 = __uint_as_float(r << 16), x1 = __uint_as_float(r & 0xffff0000u);
+      hw[j] = pack_bf16x2(x0 * x0, x1 * x1);
+    }
+    bf16x8 hid, wi, wf, wr;
+    __builtin_memcpy(&hid, hw, 16);
+    __builtin_memcpy(&wi, &w[0], 16);
+    __builtin_memcpy(&wf, &w[1], 16);
+    __builtin_memcpy(&wr, &w[2], 16);
+    acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hid, wi, acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hid, wf, acc[1], 0, 0, 0);
+    acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hid, wr, acc[2], 0, 0, 0);
+  }
+  __device__ __forceinline__ static T out(float v) { return f32_to_bf16(v); }
+  __device__ __forceinline__ static float rnd(float v) { return __uint_as_float(pack_bf16x2(v, 0.f) << 16); }
+  __device__ __forceinline__ static void store4(T* p, const float (&v)[4]) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+  }
+};
+
+// fp32: 16x16x4 fp32 MFMA; lane group g holds k = 4g..4g+3 of the 16-wide chunk and issues 4 MFMAs
+// per gate, MFMA j taking k = 4g + j on both operands.
+struct MathF32 {
+  typedef float T;
+  static constexpr int KC = 16;
+  static constexpr int KL = 4;
+  __device__ __forceinline__ static void mma3(f32x4 (&acc)[3], const uint4& av, const uint4& bv, uint32_t keep,
+                                              const uint4 (&w)[3]) {
+    const uint32_t aw[4] = {av.x, av.y, av.z, av.w};
+    const uint32_t bw[4] = {bv.x & keep, bv.y & keep, bv.z & keep, bv.w & keep};
+    const uint32_t wi[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
+    const uint32_t wf[4] = {w[1].x, w[1].y, w[1].z, w[1].w};
+    const uint32_t wr[4] = {w[2].x, w[2].y, w[2].z, w[2].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float x = fmaxf(__uint_as_float(aw[j]) + __uint_as_float(bw[j]), 0.f);
+      x = x * x;
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, __uint_as_float(wi[j]), acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, __uint_as_float(wf[j]), acc[1], 0, 0, 0);
+      acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, __uint_as_float(wr[j]), acc[2], 0, 0, 0);
+    }
+  }
+  __device__ __forceinline__ static T out(float v) { return v; }
+  __device__ __forceinline__ static float rnd(float v) { return v; }
+  __device__ __forceinline__ static void store4(T* p, const float (&v)[4]) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+
+template <typename M, int LG, int KU, bool HAS_MASK>
+__global__ __launch_bounds__(kThreads) void gate_preacts_fwd_kernel(FwdArgs a) {
+  typedef typename M::T T;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int b = blockIdx.y;
-  const int t = blockIdx.x * kTileT + wave * 16 + r;  // row this lane feeds into the MFMA
+  const int b = blockIdx.z;
+  const int l0 = blockIdx.y * LG;
+  const int t = blockIdx.x * kTileT + wave * 16 + r;   // row this lane feeds into the MFMA
   const bool t_ok = t < a.T;
-  const bf16_t* Ab = (const bf16_t*)a.A + (int64_t)b * a.sab;
-  const bf16_t* Bb = (const bf16_t*)a.B + (int64_t)b * a.sab;
+  const int tc = t_ok ? t : a.T - 1;
+  const T* Ab = (const T*)a.A + (int64_t)b * a.sab;
+  const T* Bb = (const T*)a.B + (int64_t)b * a.sab;
+  const T* Arow = Ab + (int64_t)tc * a.sat + g * M::KL;
+
+  int lv[LG];
+  const T* Brow[LG];
+  uint32_t keep[LG];
+  float mv[LG];
+#pragma unroll
+  for (int j = 0; j < LG; ++j) {
+    lv[j] = min(l0 + j, a.n_lv - 1);
+    mv[j] = 1.f;
+    if (HAS_MASK)
+      mv[j] = Elem<T>::load((const T*)a.mask + (int64_t)b * a.smb + (int64_t)tc * a.smt + (int64_t)lv[j] * a.sml);
+  }
+#pragma unroll
+  for (int j = 0; j < LG; ++j) {
+    const int src = tc - (1 << lv[j]);             // rows past T use the clamped row: always < T
+    Brow[j] = Bb + (int64_t)(src > 0 ? src : 0) * a.sat + g * M::KL;
+    keep[j] = (t_ok && src >= 0 && l0 + j < a.n_lv && mv[j] > 0.f) ? 0xffffffffu : 0u;
+  }
+
   const int NT = (a.H + 15) >> 4;
-
-  for (int l = 0; l < a.n_lv; ++l) {
-    const int src = t - (1 << l);
-    const bool ok = t_ok && src >= 0 && mask_ok<bf16_t>(a, b, t, l);
-    const bf16_t* Arow = Ab + (int64_t)(t_ok ? t : 0) * a.sat;
-    const bf16_t* Brow = Bb + (int64_t)(ok ? src : 0) * a.sat;
-    const int64_t wl = (int64_t)l * a.swl;
-    for (int nt = 0; nt < NT; ++nt) {
-      const int n = nt * 16 + r;  // head whose weights this lane feeds
-      const bool n_ok = n < a.H;
-      const int64_t wrow = wl + (int64_t)(n_ok ? n : 0) * a.swh;
-      const bf16_t* wi = (const bf16_t*)a.Wi + wrow;
-      const bf16_t* wf = (const bf16_t*)a.Wf + wrow;
-      const bf16_t* wr = (const bf16_t*)a.Wr + wrow;
-      f32x4 ci = {0.f, 0.f, 0.f, 0.f}, cf = ci, cr = ci;
-
-      for (int k0 = 0; k0 < a.GH; k0 += 32) {
-        const int kk = k0 + g * 8;
-        uint4 av = t_ok ? ld16(Arow + kk) : make_uint4(0, 0, 0, 0);
-        uint4 bv = ok ? ld16(Brow + kk) : make_uint4(0, 0, 0, 0);
-        uint4 vi = n_ok ? ld16(wi + kk) : make_uint4(0, 0, 0, 0);
-        uint4 vf = n_ok ? ld16(wf + kk) : make_uint4(0, 0, 0, 0);
-        uint4 vr = n_ok ? ld16(wr + kk) : make_uint4(0, 0, 0, 0);
-        const uint32_t aw[4] = {av.x, av.y, av.z, av.w};
-        const uint32_t bw[4] = {bv.x, bv.y, bv.z, bv.w};
-        bf16x8 hid;
+  constexpr int STEP = M::KC * KU;
+  for (int nt = 0; nt < NT; ++nt) {
+    const int n = nt * 16 + r;                  // head whose weights this lane feeds
+    const int nc = n < a.H ? n : a.H - 1;
+    const T* W[LG][3];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float a0 = __uint_as_float(aw[j] << 16), a1 = __uint_as_float(aw[j] & 0xffff0000u);
-          const float b0 = __uint_as_float(bw[j] << 16), b1 = __uint_as_float(bw[j] & 0xffff0000u);
-          float x0 = fmaxf(bf16_to_f32(f32_to_bf16(a0 + b0)), 0.f);
-          float x1 = fmaxf(bf16_to_f32(f32_to_bf16(a1 + b1)), 0.f);
-          hid[2 * j] = (short)f32_to_bf16(x0 * x0);
-          hid[2 * j + 1] = (short)f32_to_bf16(x1 * x1);
-        }
-        bf16x8 wiv, wfv, wrv;
-        __builtin_memcpy(&wiv, &vi, 16);
-        __builtin_memcpy(&wfv, &vf, 16);
-        __builtin_memcpy(&wrv, &vr, 16);
-        ci = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hid, wiv, ci, 0, 0, 0);
-        cf = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hid, wfv, cf, 0, 0, 0);
-        cr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hid, wrv, cr, 0, 0, 0);
+    for (int j = 0; j < LG; ++j) {
+      const int64_t off = (int64_t)lv[j] * a.swl + (int64_t)nc * a.swh + g * M::KL;
+      W[j][0] = (const T*)a.Wi + off;
+      W[j][1] = (const T*)a.Wf + off;
+      W[j][2] = (const T*)a.Wr + off;
+    }
+    f32x4 acc[LG][3];
+#pragma unroll
+    for (int j = 0; j < LG; ++j)
+#pragma unroll
+      for (int x = 0; x < 3; ++x) acc[j][x] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    uint4 cA[KU], cB[KU][LG], cW[KU][LG][3];
+    auto fetch = [&](int k0, uint4 (&fA)[KU], uint4 (&fB)[KU][LG], uint4 (&fW)[KU][LG][3]) {
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        const int kk = k0 + u * M::KC;
+        fA[u] = ld16(Arow + kk);
+#pragma unroll
+        for (int j = 0; j < LG; ++j) fB[u][j] = ld16(Brow[j] + kk);
+#pragma unroll
+        for (int j = 0; j < LG; ++j)
+#pragma unroll
+          for (int x = 0; x < 3; ++x) fW[u][j][x] = ld16(W[j][x] + kk);
       }
-      // C fragment: column (head) lane%16, rows 4*(lane/16) + i
-      if (n_ok) {
-        const float bvi = a.bi[l * a.H + n], bvf = a.bf[l * a.H + n], bvr = a.br[l * a.H + n];
-        const int tb = blockIdx.x * kTileT + wave * 16 + g * 4;
+    };
+    fetch(0, cA, cB, cW);
+    for (int k0 = 0; k0 < a.GH; k0 += STEP) {
+      uint4 nA[KU], nB[KU][LG], nW[KU][LG][3];
+      const int kn = k0 + STEP < a.GH ? k0 + STEP : k0;     // last step re-reads its own chunk
+      fetch(kn, nA, nB, nW);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int to = tb + i;
-          if (to < a.T) {
-            const int64_t o = (((int64_t)b * a.T + to) * a.n_lv + l) * a.H + n;
-            ((bf16_t*)a.oi)[o] = f32_to_bf16(ci[i] + bvi);
-            ((bf16_t*)a.of)[o] = f32_to_bf16(cf[i] + bvf);
-            ((bf16_t*)a.orr)[o] = f32_to_bf16(cr[i] + bvr);
-          }
+      for (int u = 0; u < KU; ++u)
+#pragma unroll
+        for (int j = 0; j < LG; ++j) M::mma3(acc[j], cA[u], cB[u][j], keep[j], cW[u][j]);
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        cA[u] = nA[u];
+#pragma unroll
+        for (int j = 0; j < LG; ++j) {
+          cB[u][j] = nB[u][j];
+#pragma unroll
+          for (int x = 0; x < 3; ++x) cW[u][j][x] = nW[u][j][x];
         }
       }
     }
-  }
-}
-
-// fp32 forward: 16x16x4 fp32 MFMA; each lane loads 4 consecutive k and issues 4 MFMAs, lane group
-// g covering k = k0 + 4g + j for MFMA j, on both operands.
-__global__ __launch_bounds__(kThreads) void gate_preacts_fwd_f32(FwdArgs a) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = lane & 15, g = lane >> 4;
-  const int b = blockIdx.y;
-  const int t = blockIdx.x * kTileT + wave * 16 + r;
-  const bool t_ok = t < a.T;
-  const float* Ab = (const float*)a.A + (int64_t)b * a.sab;
-  const float* Bb = (const float*)a.B + (int64_t)b * a.sab;
-  const int NT = (a.H + 15) >> 4;
-
-  for (int l = 0; l < a.n_lv; ++l) {
-    const int src = t - (1 << l);
-    const bool ok = t_ok && src >= 0 && mask_ok<float>(a, b, t, l);
-    const float* Arow = Ab + (int64_t)(t_ok ? t : 0) * a.sat;
-    const float* Brow = Bb + (int64_t)(ok ? src : 0) * a.sat;
-    const int64_t wl = (int64_t)l * a.swl;
-    for (int nt = 0; nt < NT; ++nt) {
-      const int n = nt * 16 + r;
-      const bool n_ok = n < a.H;
-      const int64_t wrow = wl + (int64_t)(n_ok ? n : 0) * a.swh;
-      const float* wi = (const float*)a.Wi + wrow;
-      const float* wf = (const float*)a.Wf + wrow;
-      const float* wr = (const float*)a.Wr + wrow;
-      f32x4 ci = {0.f, 0.f, 0.f, 0.f}, cf = ci, cr = ci;
-
-      for (int k0 = 0; k0 < a.GH; k0 += 16) {
-        const int kk = k0 + g * 4;
-        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        float4 av = t_ok ? *reinterpret_cast<const float4*>(Arow + kk) : z;
-        float4 bv = ok ? *reinterpret_cast<const float4*>(Brow + kk) : z;
-        float4 vi = n_ok ? *reinterpret_cast<const float4*>(wi + kk) : z;
-        float4 vf = n_ok ? *reinterpret_cast<const float4*>(wf + kk) : z;
-        float4 vr = n_ok ? *reinterpret_cast<const float4*>(wr + kk) : z;
-        const float ha[4] = {av.x + bv.x, av.y + bv.y, av.z + bv.z, av.w + bv.w};
-        const float wia[4] = {vi.x, vi.y, vi.z, vi.w};
-        const float wfa[4] = {vf.x, vf.y, vf.z, vf.w};
-        const float wra[4] = {vr.x, vr.y, vr.z, vr.w};
+    // C fragment: column (head) lane%16, rows 4*(lane/16) + i
+    const int tb = blockIdx.x * kTileT + wave * 16 + g * 4;
+    const bool vec = a.vec_out && tb + 3 < a.T;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float x = fmaxf(ha[j], 0.f);
-          x = x * x;
-          ci = __builtin_amdgcn_mfma_f32_16x16x4f32(x, wia[j], ci, 0, 0, 0);
-          cf = __builtin_amdgcn_mfma_f32_16x16x4f32(x, wfa[j], cf, 0, 0, 0);
-          cr = __builtin_amdgcn_mfma_f32_16x16x4f32(x, wra[j], cr, 0, 0, 0);
-        }
-      }
-      if (n_ok) {
-        const float bvi = a.bi[l * a.H + n], bvf = a.bf[l * a.H + n], bvr = a.br[l * a.H + n];
-        const int tb = blockIdx.x * kTileT + wave * 16 + g * 4;
+    for (int j = 0; j < LG; ++j) {
+      const int l = l0 + j;
+      if (l >= a.n_lv || n >= a.H) continue;
+      const float bias[3] = {a.bi[l * a.H + n], a.bf[l * a.H + n], a.br[l * a.H + n]};
+      T* outs[3] = {(T*)a.oi, (T*)a.of, (T*)a.orr};
+      const int64_t base = (int64_t)b * a.sob + (int64_t)l * a.sol + (int64_t)n * a.soh;
+      float v[3][4];
+#pragma unroll
+      for (int x = 0; x < 3; ++x)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[x][i] = acc[j][x][i] + bias[x];
+      if (a.activate) {
+        // a = sigmoid(pre_i) * M, f = sigmoid(pre_f) * M + 1 - M, r = sigmoid(pre_r), rounded where
+        // the eager bf16 path rounds (pre-activation, sigmoid output); M = [t >= 2^l] * [mask > 0]
+        float mval[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int to = tb + i;
-          if (to < a.T) {
-            const int64_t o = (((int64_t)b * a.T + to) * a.n_lv + l) * a.H + n;
-            ((float*)a.oi)[o] = ci[i] + bvi;
-            ((float*)a.of)[o] = cf[i] + bvf;
-            ((float*)a.orr)[o] = cr[i] + bvr;
+          mval[i] = 1.f;
+          if (HAS_MASK) {
+            const int to = min(tb + i, a.T - 1);
+            mval[i] = Elem<T>::load((const T*)a.mask + (int64_t)b * a.smb + (int64_t)to * a.smt + (int64_t)l * a.sml);
           }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float m = (tb + i >= (1 << l) && mval[i] > 0.f) ? 1.f : 0.f;
+          const float si = M::rnd(dh_sigmoid(M::rnd(v[0][i])));
+          const float sf = M::rnd(dh_sigmoid(M::rnd(v[1][i])));
+          const float sr = M::rnd(dh_sigmoid(M::rnd(v[2][i])));
+          v[0][i] = si * m;
+          v[1][i] = sf * m + (1.f - m);
+          v[2][i] = sr;
+        }
+      }
+#pragma unroll
+      for (int x = 0; x < 3; ++x) {
+        if (vec) {
+          M::store4(outs[x] + base + tb, v[x]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (tb + i < a.T) outs[x][base + (int64_t)(tb + i) * a.sot] = M::out(v[x][i]);
         }
       }
     }
@@ -213,7 +287,7 @@ struct BwdArgs {
   const void* dPf;
   const void* dPr;
   const void* mask;
-  int64_t smb, smt;
+  int64_t smb, smt, sml;
   float* dA;
   float* dB;
   float* dWi;
@@ -265,7 +339,8 @@ __global__ __launch_bounds__(kThreads) void gate_preacts_bwd_kernel(BwdArgs a) {
     if (tid < kBwdTile) {
       const int t = t0 + tid;
       int ok = t < a.T && t >= (1 << l);
-      if (ok && a.mask) ok = Elem<T>::load((const T*)a.mask + (int64_t)b * a.smb + (int64_t)t * a.smt + l) > 0.f;
+      if (ok && a.mask)
+        ok = Elem<T>::load((const T*)a.mask + (int64_t)b * a.smb + (int64_t)t * a.smt + (int64_t)l * a.sml) > 0.f;
       okm[tid] = ok;
     }
     __syncthreads();
@@ -339,12 +414,31 @@ int check_shapes(const char* who, int dtype, int b, int T, int GH, int H, int n_
 
 }  // namespace
 
+template <typename M, int LG, int KU>
+void launch_fwd(const FwdArgs& a, dim3 grid, hipStream_t s) {
+  if (a.mask)
+    gate_preacts_fwd_kernel<M, LG, KU, true><<<grid, dim3(kThreads), 0, s>>>(a);
+  else
+    gate_preacts_fwd_kernel<M, LG, KU, false><<<grid, dim3(kThreads), 0, s>>>(a);
+}
+
+template <typename M>
+void dispatch_fwd(const FwdArgs& a, int LG, int KU, dim3 grid, hipStream_t s) {
+  if (LG == 1 && KU == 4) launch_fwd<M, 1, 4>(a, grid, s);
+  else if (LG == 1) launch_fwd<M, 1, 1>(a, grid, s);
+  else if (LG == 2 && KU == 2) launch_fwd<M, 2, 2>(a, grid, s);
+  else if (LG == 2) launch_fwd<M, 2, 1>(a, grid, s);
+  else if (LG == 3) launch_fwd<M, 3, 1>(a, grid, s);
+  else launch_fwd<M, 4, 1>(a, grid, s);
+}
+
 extern "C" int dh_gate_preacts_fwd(int dtype, const void* A, const void* B, int64_t stride_ab, int64_t stride_at,
                                    const void* Wi, const void* Wf, const void* Wr, int64_t stride_wl,
                                    int64_t stride_wh, const float* bi, const float* bf, const float* br,
-                                   const void* mask, int64_t stride_mb, int64_t stride_mt, void* out_i,
-                                   void* out_f, void* out_r, int b, int T, int GH, int H, int n_lv,
-                                   void* stream) {
+                                   const void* mask, int64_t stride_mb, int64_t stride_mt, int64_t stride_ml,
+                                   void* out_i, void* out_f, void* out_r, int64_t stride_ob, int64_t stride_ot,
+                                   int64_t stride_ol, int64_t stride_oh, int activate, int b, int T, int GH,
+                                   int H, int n_lv, void* stream) {
   const char* who = "dh_gate_preacts_fwd";
   int st = check_shapes(who, dtype, b, T, GH, H, n_lv);
   if (st) return st;
@@ -356,21 +450,38 @@ extern "C" int dh_gate_preacts_fwd(int dtype, const void* A, const void* B, int6
              DH_ERR_INVALID_ARG, "%s: A/B/W rows need 16-byte alignment", who);
   DH_REQUIRE(stride_at >= GH && stride_wh >= GH && stride_wl >= (int64_t)H * stride_wh, DH_ERR_INVALID_ARG,
              "%s: strides overlap rows", who);
+  DH_REQUIRE(stride_ob >= 0 && stride_ot >= 0 && stride_ol >= 0 && stride_oh >= 0, DH_ERR_INVALID_ARG,
+             "%s: negative output stride", who);
+  const size_t esz = dtype == DH_BF16 ? 2 : 4;
+  const bool vec_out = stride_ot == 1 && stride_ob % 4 == 0 && stride_ol % 4 == 0 && stride_oh % 4 == 0 &&
+                       aligned(out_i, 4 * esz) && aligned(out_f, 4 * esz) && aligned(out_r, 4 * esz);
   FwdArgs a{A, B, stride_ab, stride_at, Wi, Wf, Wr, stride_wl, stride_wh, bi, bf, br, mask, stride_mb, stride_mt,
-            out_i, out_f, out_r, b, T, GH, H, n_lv};
-  dim3 grid((T + kTileT - 1) / kTileT, b), block(kThreads);
+            stride_ml, out_i, out_f, out_r, stride_ob, stride_ot, stride_ol, stride_oh, b, T, GH, H, n_lv,
+            vec_out ? 1 : 0, activate ? 1 : 0};
+  // level groups: enough workgroups to fill 256 CUs several times over, A reused across <= 4 levels
+  const int tiles = (T + kTileT - 1) / kTileT;
+  const int64_t tile_wgs = (int64_t)tiles * b;
+  const int want_groups = (int)((1024 + tile_wgs - 1) / tile_wgs);
+  int LG = (n_lv + want_groups - 1) / want_groups;
+  LG = LG < 1 ? 1 : (LG > 4 ? 4 : LG);
+  const int ngroups = (n_lv + LG - 1) / LG;
+  const int kc = dtype == DH_BF16 ? 32 : 16;
+  int KU = LG == 1 ? 4 : (LG == 2 ? 2 : 1);
+  if (GH % (kc * KU) != 0) KU = 1;
+  dim3 grid(tiles, ngroups, b);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DH_BF16)
-    gate_preacts_fwd_bf16<<<grid, block, 0, s>>>(a);
+    dispatch_fwd<MathBf16>(a, LG, KU, grid, s);
   else
-    gate_preacts_fwd_f32<<<grid, block, 0, s>>>(a);
+    dispatch_fwd<MathF32>(a, LG, KU, grid, s);
   return dh_check_launch(who);
 }
 
 extern "C" int dh_gate_preacts_bwd(int dtype, const void* A, const void* B, int64_t stride_ab, int64_t stride_at,
                                    const void* Wi, const void* Wf, const void* Wr, int64_t stride_wl,
                                    int64_t stride_wh, const void* dPi, const void* dPf, const void* dPr,
-                                   const void* mask, int64_t stride_mb, int64_t stride_mt, float* dA, float* dB,
+                                   const void* mask, int64_t stride_mb, int64_t stride_mt, int64_t stride_ml,
+                                   float* dA, float* dB,
                                    float* dWi, float* dWf, float* dWr, float* dbi, float* dbf, float* dbr, int b,
                                    int T, int GH, int H, int n_lv, void* stream) {
   const char* who = "dh_gate_preacts_bwd";
@@ -380,7 +491,7 @@ extern "C" int dh_gate_preacts_bwd(int dtype, const void* A, const void* B, int6
              DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
   hipStream_t s = (hipStream_t)stream;
   BwdArgs a{A, B, stride_ab, stride_at, Wi, Wf, Wr, stride_wl, stride_wh, dPi, dPf, dPr, mask, stride_mb,
-            stride_mt, dA, dB, dWi, dWf, dWr, dbi, dbf, dbr, b, T, GH, H, n_lv};
+            stride_mt, stride_ml, dA, dB, dWi, dWf, dWr, dbi, dbf, dbr, b, T, GH, H, n_lv};
   const int64_t nAB = (int64_t)b * T * GH, nW = (int64_t)n_lv * H * GH, nb = (int64_t)n_lv * H;
   fill_zero<<<1024, 256, 0, s>>>(dB, nAB);
   for (float* p : {dWi, dWf, dWr}) fill_zero<<<256, 256, 0, s>>>(p, nW);

@@ -7,13 +7,18 @@
 // Every level reads the previous level's state, so a position's update needs the whole column of
 // the previous level. The reference's roll() wraps future rows into t < 2^l and cancels them with
 // a = 0; here those reads are predicated away, which gives the same result for finite data.
+// With `activated` the gate inputs are already a, f and r (dh_gate_preacts_fwd with `activate`):
+// then a = 0 and f = 1 wherever M = 0, so every position takes the update unpredicated.
 //
 // Work decomposition: one workgroup (8 wave64s) per (batch row b, head h, chunk of C columns of
 // the head's hd). The chunk's state for all T positions lives in registers (PPT positions per
-// thread) and each level exchanges r*V through an LDS column of T*C fp32 (128 KB at T = 4096,
-// C = 8), two barriers per level. Gates are computed once per (position, level) by the thread that
-// owns the position. The hd/C chunk workgroups of one (b, h) read the same V0 cache lines and the
-// same gates, so they are given the same blockIdx % 8 (one XCD under round-robin dispatch) and
+// thread, position t = tid + j*512) and each level exchanges r*V through an LDS column of T*C fp32
+// (128 KB at T = 4096, C = 8), two barriers per level. Gate and mask reads go through element
+// strides; with the head-major gate layout (unit stride in t) a wave's 64 consecutive positions
+// read one contiguous 128-byte line per gate. The next level's gates are requested before the
+// current level's exchange (barriers here wait for LDS only, not for global loads), so their
+// latency hides behind it. The hd/C chunk workgroups of one (b, h) read the same V0 cache lines and
+// the same gates, so they are given the same blockIdx % 8 (one XCD under round-robin dispatch) and
 // consecutive dispatch slots, so those lines are fetched once into that XCD's L2.
 #include "dh_common.h"
 
@@ -21,27 +26,38 @@ namespace {
 
 constexpr int kThreads = 512;
 
+enum { kPreNoMask = 0, kPreMask = 1, kActivated = 2 };
+
 struct ScanArgs {
   const void* pre_i;
   const void* pre_f;
   const void* pre_r;
+  int64_t spb, spt, spl, sph;
   const void* mask;
-  int64_t smb, smt;
+  int64_t smb, smt, sml;
   const void* V0;
   int64_t svb, svt;
   void* V;
   int b, T, H, hd, n_lv;
 };
 
-template <typename T, int C>
-__device__ __forceinline__ void load_chunk(const T* p, float (&v)[C]) {
-#pragma unroll
-  for (int c = 0; c < C; ++c) v[c] = Elem<T>::load(p + c);
-}
+// raw element bits, converted after the loads of a burst have all been issued
+template <typename T> struct Raw;
+template <> struct Raw<bf16_t> {
+  __device__ __forceinline__ static uint32_t load(const bf16_t* p) { return *p; }
+  __device__ __forceinline__ static float f(uint32_t r) { return __uint_as_float(r << 16); }
+};
+template <> struct Raw<float> {
+  __device__ __forceinline__ static uint32_t load(const float* p) { return __float_as_uint(*p); }
+  __device__ __forceinline__ static float f(uint32_t r) { return __uint_as_float(r); }
+};
 
-template <typename T, int C, int PPT>
+template <typename T, int C, int PPT, int MODE>
 __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
   __shared__ float rv[C * PPT * kThreads];
+  // a whole level of raw gates in flight costs 4*PPT registers; past 32 positions per thread the
+  // gates are fetched at the top of their own level instead
+  constexpr bool kPrefetch = PPT <= 32;
   const int nchunks = a.hd / C;
   const int ngroups = a.b * a.H;
   const int bid = blockIdx.x;
@@ -52,50 +68,76 @@ __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
   const int64_t col0 = (int64_t)h * a.hd + (int64_t)c * C;
   const int tid = threadIdx.x;
 
-  const T* pi = (const T*)a.pre_i;
-  const T* pf = (const T*)a.pre_f;
-  const T* pr = (const T*)a.pre_r;
-  const int64_t gbase = (int64_t)b * a.T * a.n_lv * a.H + h;  // gate [b, t, l, h] = gbase + (t*n_lv + l)*H
+  const int64_t gb = (int64_t)b * a.spb + (int64_t)h * a.sph;
+  const T* pi = (const T*)a.pre_i + gb;
+  const T* pf = (const T*)a.pre_f + gb;
+  const T* pr = (const T*)a.pre_r + gb;
+  const T* mk = (const T*)a.mask + (MODE == kPreMask ? (int64_t)b * a.smb : 0);
 
   float V[PPT][C];
 #pragma unroll
   for (int j = 0; j < PPT; ++j) {
     const int t = tid + j * kThreads;
-    if (t < a.T) {
-      load_chunk<T, C>((const T*)a.V0 + (int64_t)b * a.svb + (int64_t)t * a.svt + col0, V[j]);
-    } else {
+    const int tc = t < a.T ? t : a.T - 1;
+    const T* src = (const T*)a.V0 + (int64_t)b * a.svb + (int64_t)tc * a.svt + col0;
 #pragma unroll
-      for (int cc = 0; cc < C; ++cc) V[j][cc] = 0.f;
-    }
+    for (int cc = 0; cc < C; ++cc) V[j][cc] = t < a.T ? Elem<T>::load(src + cc) : 0.f;
   }
 
-  for (int l = 0; l < a.n_lv; ++l) {
-    const int shift = 1 << l;
-    // r * V at every position (the message a level-l destination reads at lag 2^l)
+  uint32_t ri[PPT], rf[PPT], rr[PPT], rm[PPT];
+  auto fetch = [&](int l) {
+    const int64_t lo = (int64_t)l * a.spl, ml = (int64_t)l * a.sml;
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
       const int t = tid + j * kThreads;
-      if (t < a.T) {
-        const float r = dh_sigmoid(Elem<T>::load(pr + gbase + ((int64_t)t * a.n_lv + l) * a.H));
+      const int64_t tc = t < a.T ? t : a.T - 1;
+      const int64_t go = tc * a.spt + lo;
+      ri[j] = Raw<T>::load(pi + go);
+      rf[j] = Raw<T>::load(pf + go);
+      rr[j] = Raw<T>::load(pr + go);
+      if (MODE == kPreMask) rm[j] = Raw<T>::load(mk + tc * a.smt + ml);
+    }
+  };
+  if (kPrefetch) fetch(0);
+
+  for (int l = 0; l < a.n_lv; ++l) {
+    const int shift = 1 << l;
+    if (!kPrefetch) fetch(l);
+    float rg[PPT], ad[PPT], fg[PPT];
+    bool up[PPT];
 #pragma unroll
-        for (int cc = 0; cc < C; ++cc) rv[t * C + cc] = r * V[j][cc];
+    for (int j = 0; j < PPT; ++j) {
+      const int t = tid + j * kThreads;
+      if (MODE == kActivated) {
+        ad[j] = Raw<T>::f(ri[j]);
+        fg[j] = Raw<T>::f(rf[j]);
+        rg[j] = Raw<T>::f(rr[j]);
+        up[j] = true;
+      } else {
+        ad[j] = dh_sigmoid(Raw<T>::f(ri[j]));
+        fg[j] = dh_sigmoid(Raw<T>::f(rf[j]));
+        rg[j] = dh_sigmoid(Raw<T>::f(rr[j]));
+        up[j] = t >= shift && (MODE != kPreMask || Raw<T>::f(rm[j]) > 0.f);
       }
+    }
+    if (kPrefetch) fetch(l + 1 < a.n_lv ? l + 1 : l);   // next level's gates fly during the exchange
+    // r * V at every position (the message a level-l destination reads at lag 2^l); positions past
+    // T are written but never read (every source t - 2^l of a position t < T is below T)
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int t = tid + j * kThreads;
+#pragma unroll
+      for (int cc = 0; cc < C; ++cc) rv[t * C + cc] = rg[j] * V[j][cc];
     }
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
       const int t = tid + j * kThreads;
-      if (t < a.T && t >= shift) {
-        bool m = true;
-        if (a.mask) m = Elem<T>::load((const T*)a.mask + (int64_t)b * a.smb + (int64_t)t * a.smt + l) > 0.f;
-        if (m) {
-          const int64_t gi = gbase + ((int64_t)t * a.n_lv + l) * a.H;
-          const float ad = dh_sigmoid(Elem<T>::load(pi + gi));
-          const float fg = dh_sigmoid(Elem<T>::load(pf + gi));
-          const int s = t - shift;
+      const int s = t >= shift ? t - shift : 0;
 #pragma unroll
-          for (int cc = 0; cc < C; ++cc) V[j][cc] = fg * V[j][cc] + ad * rv[s * C + cc];
-        }
+      for (int cc = 0; cc < C; ++cc) {
+        const float nv = fg[j] * V[j][cc] + ad[j] * rv[s * C + cc];
+        V[j][cc] = up[j] ? nv : V[j][cc];
       }
     }
     __syncthreads();
@@ -113,31 +155,37 @@ __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
 }
 
 template <typename T, int C, int PPT>
-void launch(const ScanArgs& a, hipStream_t s) {
+void launch(const ScanArgs& a, int mode, hipStream_t s) {
   const int nchunks = a.hd / C;
   const int ngroups = a.b * a.H;
   const int grid = ((ngroups + 7) / 8) * 8 * nchunks;
-  level_scan_kernel<T, C, PPT><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
+  if (mode == kActivated)
+    level_scan_kernel<T, C, PPT, kActivated><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
+  else if (mode == kPreMask)
+    level_scan_kernel<T, C, PPT, kPreMask><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
+  else
+    level_scan_kernel<T, C, PPT, kPreNoMask><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
 }
 
 template <typename T>
-int dispatch(const ScanArgs& a, hipStream_t s) {
-  if (a.T <= 512) launch<T, 8, 1>(a, s);
-  else if (a.T <= 1024) launch<T, 8, 2>(a, s);
-  else if (a.T <= 2048) launch<T, 8, 4>(a, s);
-  else if (a.T <= 4096) launch<T, 8, 8>(a, s);
-  else if (a.T <= 8192) launch<T, 4, 16>(a, s);
-  else if (a.T <= 16384) launch<T, 2, 32>(a, s);
-  else launch<T, 1, 64>(a, s);
+int dispatch(const ScanArgs& a, int mode, hipStream_t s) {
+  if (a.T <= 512) launch<T, 8, 1>(a, mode, s);
+  else if (a.T <= 1024) launch<T, 8, 2>(a, mode, s);
+  else if (a.T <= 2048) launch<T, 8, 4>(a, mode, s);
+  else if (a.T <= 4096) launch<T, 8, 8>(a, mode, s);
+  else if (a.T <= 8192) launch<T, 4, 16>(a, mode, s);
+  else if (a.T <= 16384) launch<T, 2, 32>(a, mode, s);
+  else launch<T, 1, 64>(a, mode, s);
   return dh_check_launch("dh_level_scan_fwd");
 }
 
 }  // namespace
 
 extern "C" int dh_level_scan_fwd(int dtype, const void* pre_i, const void* pre_f, const void* pre_r,
-                                 const void* mask, int64_t stride_mb, int64_t stride_mt, const void* V0,
-                                 int64_t stride_vb, int64_t stride_vt, void* V, int b, int T, int H, int hd,
-                                 int n_lv, void* stream) {
+                                 int64_t stride_pb, int64_t stride_pt, int64_t stride_pl, int64_t stride_ph,
+                                 const void* mask, int64_t stride_mb, int64_t stride_mt, int64_t stride_ml,
+                                 const void* V0, int64_t stride_vb, int64_t stride_vt, void* V, int b, int T,
+                                 int H, int hd, int n_lv, int activated, void* stream) {
   const char* who = "dh_level_scan_fwd";
   DH_REQUIRE(dtype == DH_F32 || dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d", who, dtype);
   DH_REQUIRE(b >= 1 && T >= 1, DH_ERR_INVALID_ARG, "%s: b=%d T=%d must be >= 1", who, b, T);
@@ -149,7 +197,11 @@ extern "C" int dh_level_scan_fwd(int dtype, const void* pre_i, const void* pre_f
   DH_REQUIRE(pre_i && pre_f && pre_r && V0 && V, DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
   DH_REQUIRE(stride_vt >= (int64_t)H * hd, DH_ERR_INVALID_ARG, "%s: V0 row stride %lld < H*hd", who,
              (long long)stride_vt);
-  ScanArgs a{pre_i, pre_f, pre_r, mask, stride_mb, stride_mt, V0, stride_vb, stride_vt, V, b, T, H, hd, n_lv};
+  DH_REQUIRE(stride_pb >= 0 && stride_pt >= 0 && stride_pl >= 0 && stride_ph >= 0, DH_ERR_INVALID_ARG,
+             "%s: negative gate stride", who);
+  ScanArgs a{pre_i, pre_f, pre_r, stride_pb, stride_pt, stride_pl, stride_ph, mask, stride_mb, stride_mt,
+             stride_ml, V0, stride_vb, stride_vt, V, b, T, H, hd, n_lv};
+  const int mode = activated ? kActivated : (mask ? kPreMask : kPreNoMask);
   hipStream_t s = (hipStream_t)stream;
-  return dtype == DH_F32 ? dispatch<float>(a, s) : dispatch<bf16_t>(a, s);
+  return dtype == DH_F32 ? dispatch<float>(a, mode, s) : dispatch<bf16_t>(a, mode, s);
 }

@@ -33,13 +33,35 @@ def _compute_dtype(x):
 
 
 def _mask_view(mask, cd):
-    """(b, T, n_lv) mask in dtype `cd` with a unit innermost stride (no copy when it already is)."""
+    """(b, T, n_lv) mask in dtype `cd` and its element strides (any layout; no copy if already cd)."""
     if mask is None:
-        return None, 0, 0
+        return None, 0, 0, 0
     m = mask.to(cd)
-    if m.stride(-1) != 1:
-        m = m.contiguous()
-    return m, m.stride(0), m.stride(1)
+    return m, m.stride(0), m.stride(1), m.stride(2)
+
+
+def _preacts_launch(A_, B_, Wi_, Wf_, Wr_, bi_, bf_, br_, mask, outs, ostrides, activate, n_lv, what):
+    b, T, GH = A_.shape
+    H = Wi_.shape[1]
+    cd = A_.dtype
+    m_, smb, smt, sml = _mask_view(mask, cd)
+    p = _hip.ptr
+    st = _hip.lib.dh_gate_preacts_fwd(
+        _hip.dtype_code(cd), p(A_), p(B_), A_.stride(0), A_.stride(1),
+        p(Wi_), p(Wf_), p(Wr_), Wi_.stride(0), Wi_.stride(1),
+        p(bi_), p(bf_), p(br_), p(m_), smb, smt, sml,
+        p(outs[0]), p(outs[1]), p(outs[2]), *ostrides, int(activate),
+        b, T, GH, H, n_lv, _hip.stream_handle(A_.device))
+    _hip.check(st, what)
+
+
+def _prep_gate_inputs(A, B, Wi, Wf, Wr, bi, bf, br, n_lv):
+    cd = _compute_dtype(A)
+    A_ = A.contiguous().to(cd)
+    B_ = B.contiguous().to(cd)
+    Wi_, Wf_, Wr_ = (w[:n_lv].contiguous().to(cd) for w in (Wi, Wf, Wr))
+    bi_, bf_, br_ = (v[:n_lv].contiguous().float() for v in (bi, bf, br))
+    return A_, B_, Wi_, Wf_, Wr_, bi_, bf_, br_
 
 
 # ---------------------------------------------------------------------------------------------
@@ -56,18 +78,10 @@ def _gate_preacts_fwd_op(A: torch.Tensor, B: torch.Tensor,
     outs = [torch.empty(b, T, n_lv, H, device=A.device, dtype=cd) for _ in range(3)]
     if b == 0 or T == 0:
         return outs
-    A_ = A.contiguous().to(cd)
-    B_ = B.contiguous().to(cd)
-    Wi_, Wf_, Wr_ = (w[:n_lv].contiguous().to(cd) for w in (Wi, Wf, Wr))
-    bi_, bf_, br_ = (v[:n_lv].contiguous().float() for v in (bi, bf, br))
-    m_, smb, smt = _mask_view(mask, cd)
-    p = _hip.ptr
-    st = _hip.lib.dh_gate_preacts_fwd(
-        _hip.dtype_code(cd), p(A_), p(B_), A_.stride(0), A_.stride(1),
-        p(Wi_), p(Wf_), p(Wr_), Wi_.stride(0), Wi_.stride(1),
-        p(bi_), p(bf_), p(br_), p(m_), smb, smt,
-        p(outs[0]), p(outs[1]), p(outs[2]), b, T, GH, H, n_lv, _hip.stream_handle(A.device))
-    _hip.check(st, "dispatcher::gate_preacts_fwd")
+    ins = _prep_gate_inputs(A, B, Wi, Wf, Wr, bi, bf, br, n_lv)
+    o = outs[0]
+    _preacts_launch(*ins, mask, outs, (o.stride(0), o.stride(1), o.stride(2), o.stride(3)), 0, n_lv,
+                    "dispatcher::gate_preacts_fwd")
     return outs
 
 
@@ -103,12 +117,12 @@ def _gate_preacts_bwd_op(A: torch.Tensor, B: torch.Tensor,
     B_ = B.contiguous().to(cd)
     Wi_, Wf_, Wr_ = (w[:n_lv].contiguous().to(cd) for w in (Wi, Wf, Wr))
     dPi_, dPf_, dPr_ = (g.contiguous().to(cd) for g in (dPi, dPf, dPr))
-    m_, smb, smt = _mask_view(mask, cd)
+    m_, smb, smt, sml = _mask_view(mask, cd)
     p = _hip.ptr
     st = _hip.lib.dh_gate_preacts_bwd(
         _hip.dtype_code(cd), p(A_), p(B_), A_.stride(0), A_.stride(1),
         p(Wi_), p(Wf_), p(Wr_), Wi_.stride(0), Wi_.stride(1),
-        p(dPi_), p(dPf_), p(dPr_), p(m_), smb, smt,
+        p(dPi_), p(dPf_), p(dPr_), p(m_), smb, smt, sml,
         *[p(o) for o in outs], b, T, GH, H, n_lv, _hip.stream_handle(dev))
     _hip.check(st, "dispatcher::gate_preacts_bwd")
     return outs
@@ -179,17 +193,24 @@ def _level_scan_fwd_op(pre_i: torch.Tensor, pre_f: torch.Tensor, pre_r: torch.Te
     out = torch.empty(b, T, d, device=V0.device, dtype=V0.dtype)
     if b == 0 or T == 0:
         return out
+    _scan_launch(pre_i, pre_f, pre_r, mask, V0, out, num_heads, n_lv, 0, "dispatcher::level_scan_fwd")
+    return out
+
+
+def _scan_launch(pre_i, pre_f, pre_r, mask, V0, out, num_heads, n_lv, activated, what):
+    b, T, d = V0.shape
     cd = V0.dtype
     V0_ = V0 if V0.stride(-1) == 1 else V0.contiguous()
-    pi, pf, pr = (g.contiguous().to(cd) for g in (pre_i, pre_f, pre_r))
-    m_, smb, smt = _mask_view(mask, cd)
+    pi, pf, pr = (g.to(cd) for g in (pre_i, pre_f, pre_r))       # keeps each tensor's layout
+    if not (pi.stride() == pf.stride() == pr.stride()):
+        pi, pf, pr = pi.contiguous(), pf.contiguous(), pr.contiguous()
+    m_, smb, smt, sml = _mask_view(mask, cd)
     p = _hip.ptr
     st = _hip.lib.dh_level_scan_fwd(
-        _hip.dtype_code(cd), p(pi), p(pf), p(pr), p(m_), smb, smt,
+        _hip.dtype_code(cd), p(pi), p(pf), p(pr), *pi.stride(), p(m_), smb, smt, sml,
         p(V0_), V0_.stride(0), V0_.stride(1), p(out), b, T, num_heads, d // num_heads, n_lv,
-        _hip.stream_handle(V0.device))
-    _hip.check(st, "dispatcher::level_scan_fwd")
-    return out
+        int(activated), _hip.stream_handle(V0.device))
+    _hip.check(st, what)
 
 
 @_level_scan_fwd_op.register_fake
@@ -206,3 +227,46 @@ def fused_level_scan(pre_i, pre_f, pre_r, mask, V0, num_heads, n_lv):
     linear_out (no heads-first transposes). Inference only (no autograd).
     """
     return torch.ops.dispatcher.level_scan_fwd(pre_i, pre_f, pre_r, mask, V0, num_heads, n_lv)
+
+
+# ---------------------------------------------------------------------------------------------
+# dispatcher::gate_scan_fwd -- the whole inference gate path in two launches
+# ---------------------------------------------------------------------------------------------
+@torch.library.custom_op("dispatcher::gate_scan_fwd", mutates_args=(), device_types="cuda")
+def _gate_scan_fwd_op(A: torch.Tensor, B: torch.Tensor,
+                      Wi: torch.Tensor, Wf: torch.Tensor, Wr: torch.Tensor,
+                      bi: torch.Tensor, bf: torch.Tensor, br: torch.Tensor,
+                      mask: Optional[torch.Tensor], V0: torch.Tensor, num_heads: int,
+                      n_lv: int) -> torch.Tensor:
+    b, T, d = V0.shape
+    out = torch.empty(b, T, d, device=V0.device, dtype=V0.dtype)
+    if b == 0 or T == 0:
+        return out
+    ins = _prep_gate_inputs(A, B, Wi, Wf, Wr, bi, bf, br, n_lv)
+    H = num_heads
+    # activated gates in the head-major (b, H, n_lv, T) layout: unit stride along t for the scan
+    g = torch.empty(3, b, H, n_lv, T, device=V0.device, dtype=ins[0].dtype)
+    gates = [g[i].permute(0, 3, 2, 1) for i in range(3)]              # logical (b, T, n_lv, H)
+    _preacts_launch(*ins, mask, gates, gates[0].stride(), 1, n_lv, "dispatcher::gate_scan_fwd")
+    cd = ins[0].dtype
+    res = out if V0.dtype == cd else torch.empty(b, T, d, device=V0.device, dtype=cd)
+    _scan_launch(gates[0], gates[1], gates[2], None, V0.to(cd), res, H, n_lv, 1, "dispatcher::gate_scan_fwd")
+    if res is not out:
+        out.copy_(res)
+    return out
+
+
+@_gate_scan_fwd_op.register_fake
+def _(A, B, Wi, Wf, Wr, bi, bf, br, mask, V0, num_heads, n_lv):
+    return torch.empty_like(V0)
+
+
+def fused_gate_scan(A, B, Wi, Wf, Wr, bi, bf, br, n_lv, mask, V0, num_heads):
+    """Scanned mixer state (b, T, d) straight from the gate hiddens A = gate_hidden(x),
+    B = gate_hidden_src(x) and V0 = linear_in(x): the pre-activations are computed, activated and
+    masked in one kernel (written head-major, never in the reference op's layout) and the level
+    scan consumes them in a second. Inference only (no autograd); equal to
+    fused_level_scan(*fused_gate_preacts(...), mask, V0, num_heads, n_lv) up to the bf16 rounding
+    of the activated gates, which follows the eager path (reference
+    dispatcher_hybrid/modeling_dispatcher.py:86-88, 100-121)."""
+    return torch.ops.dispatcher.gate_scan_fwd(A, B, Wi, Wf, Wr, bi, bf, br, mask, V0, num_heads, n_lv)

@@ -134,7 +134,7 @@ class DispatcherMixer(nn.Module):
         if not x.is_cuda:
             raise RuntimeError("fused gates are enabled but the input is on the CPU; move the model "
                                "to the GPU or call enable_fused_gates(False)")
-        from .fused_gates import fused_gate_preacts, fused_level_scan
+        from .fused_gates import fused_gate_preacts, fused_gate_scan
         Bb, T = x.shape[0], x.shape[1]
         H, hd = self.num_heads, self.head_dim
         V0 = self.linear_in(x)
@@ -142,17 +142,18 @@ class DispatcherMixer(nn.Module):
         Bs = self.gate_hidden_src(x)
         m3 = mask[..., :n_lv] if mask.dim() == 3 else None
         (Wi, bi), (Wf, bf), (Wr, br) = self._gate_params()
-        pre_i, pre_f, pre_r = fused_gate_preacts(A, Bs, Wi, Wf, Wr, bi, bf, br, n_lv, m3)
         needs_grad = torch.is_grad_enabled() and (
             x.requires_grad or any(p.requires_grad for p in self.parameters()))
         if needs_grad:
             # differentiable: the fused pre-activations (custom op with autograd) + torch scan
+            pre_i, pre_f, pre_r = fused_gate_preacts(A, Bs, Wi, Wf, Wr, bi, bf, br, n_lv, m3)
             _, m_heads = self._masks(mask, Bb, T, n_lv)
             V = V0.view(Bb, T, H, hd).transpose(1, 2).reshape(Bb * H, T, hd)
             V = self._scan_eager(V, pre_i, pre_f, pre_r, m_heads.to(V.dtype), Bb, T, n_lv)
             V = V.view(Bb, H, T, hd).transpose(1, 2).reshape(Bb, T, self.embed_dim)
         else:
-            V = fused_level_scan(pre_i, pre_f, pre_r, m3, V0, H, n_lv)
+            # inference: activated gates written head-major, then the level scan (two launches)
+            V = fused_gate_scan(A, Bs, Wi, Wf, Wr, bi, bf, br, n_lv, m3, V0, H)
         return self.linear_out(V)
 
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 1
+#define DH_ABI_VERSION 2
 
 enum dh_status {
   DH_OK = 0,
@@ -58,21 +58,30 @@ const char* dh_last_error(void);
  *             innermost contiguous.
  *   bi,bf,br  fp32, (>= n_lv, H) contiguous.
  *   mask      nullable; dtype `dtype`, value > 0 means "edge allowed", element [b,t,l] at
- *             b*stride_mb + t*stride_mt + l. The wrap mask t >= 2^l is always applied in-kernel.
- *   out_i/f/r (b, T, n_lv, H) contiguous, dtype `dtype`.
+ *             b*stride_mb + t*stride_mt + l*stride_ml. The wrap mask t >= 2^l is always applied
+ *             in-kernel.
+ *   out_i/f/r dtype `dtype`, element [b,t,l,h] at b*stride_ob + t*stride_ot + l*stride_ol +
+ *             h*stride_oh: (T*n_lv*H, n_lv*H, H, 1) is the reference op's contiguous (b, T, n_lv, H)
+ *             layout; (H*n_lv*T, 1, T, n_lv*T) is the head-major (b, H, n_lv, T) layout that
+ *             dh_level_scan_fwd reads with unit-stride loads.
+ *   activate  0: write the pre-activations (the reference op's output). 1: write the level scan's
+ *             gates instead: a = sigmoid(pre_i)*M, f = sigmoid(pre_f)*M + 1 - M, r = sigmoid(pre_r)
+ *             with M = [t >= 2^l] * [mask > 0] (bf16: pre-activation and sigmoid rounded, as the
+ *             eager path rounds them); dh_level_scan_fwd then runs with `activated`.
  */
 int dh_gate_preacts_fwd(int dtype, const void* A, const void* B, int64_t stride_ab, int64_t stride_at,
                         const void* Wi, const void* Wf, const void* Wr, int64_t stride_wl,
                         int64_t stride_wh, const float* bi, const float* bf, const float* br,
-                        const void* mask, int64_t stride_mb, int64_t stride_mt, void* out_i,
-                        void* out_f, void* out_r, int b, int T, int GH, int H, int n_lv,
-                        void* stream);
+                        const void* mask, int64_t stride_mb, int64_t stride_mt, int64_t stride_ml,
+                        void* out_i, void* out_f, void* out_r, int64_t stride_ob, int64_t stride_ot,
+                        int64_t stride_ol, int64_t stride_oh, int activate, int b, int T, int GH, int H,
+                        int n_lv, void* stream);
 
 /*
  * Backward of dh_gate_preacts_fwd (autograd of the fused op).
  * Replaces the Triton kernel `_gate_pipeline_bwd` and op `dispatcher::gate_preacts_bwd`
  * (reference dispatcher_hybrid/fused_gates.py:96-173 kernel, :225-257 op).
- *   dPi/dPf/dPr (b, T, n_lv, H) contiguous, dtype `dtype`.
+ *   dPi/dPf/dPr (b, T, n_lv, H) contiguous, dtype `dtype`; mask as in dh_gate_preacts_fwd.
  *   dA, dB      fp32 (b, T, GH) contiguous; dWi/dWf/dWr fp32 (n_lv, H, GH); dbi/dbf/dbr fp32 (n_lv, H).
  *   Every output is overwritten (the library zero-fills with a kernel, then accumulates dB, dW and
  *   db with fp32 atomics, so summation order is not deterministic, as in the reference).
@@ -80,23 +89,29 @@ int dh_gate_preacts_fwd(int dtype, const void* A, const void* B, int64_t stride_
 int dh_gate_preacts_bwd(int dtype, const void* A, const void* B, int64_t stride_ab, int64_t stride_at,
                         const void* Wi, const void* Wf, const void* Wr, int64_t stride_wl,
                         int64_t stride_wh, const void* dPi, const void* dPf, const void* dPr,
-                        const void* mask, int64_t stride_mb, int64_t stride_mt, float* dA, float* dB,
-                        float* dWi, float* dWf, float* dWr, float* dbi, float* dbf, float* dbr,
+                        const void* mask, int64_t stride_mb, int64_t stride_mt, int64_t stride_ml,
+                        float* dA, float* dB, float* dWi, float* dWf, float* dWr, float* dbi,
+                        float* dbf, float* dbr,
                         int b, int T, int GH, int H, int n_lv, void* stream);
 
 /*
  * Parallel level scan with the gate activations fused in (sigmoid, masks, heads-first layout).
  * Replaces reference dispatcher_hybrid/modeling_dispatcher.py:86-88, 111-121 (heads_first, the
  * admit/forget/transmit activations and the n_lv-level roll/update loop).
- *   pre_i/f/r (b, T, n_lv, H) contiguous, dtype `dtype` (output of dh_gate_preacts_fwd).
- *   mask      nullable, as in dh_gate_preacts_fwd.
+ *   pre_i/f/r dtype `dtype` (output of dh_gate_preacts_fwd), element [b,t,l,h] at b*stride_pb +
+ *             t*stride_pt + l*stride_pl + h*stride_ph; any layout works, the head-major one
+ *             (stride_pt == 1) gives unit-stride loads.
+ *   mask      nullable, as in dh_gate_preacts_fwd; ignored when `activated`.
+ *   activated 0: pre_i/f/r are pre-activations (sigmoid and masks applied here); 1: they are the
+ *             activated, masked gates a, f, r that dh_gate_preacts_fwd writes with `activate`.
  *   V0        (b, T, H*hd): V0[b,t,h*hd+e] at b*stride_vb + t*stride_vt + h*hd + e (linear_in output).
  *   V         (b, T, H*hd) contiguous output, the scanned state in the layout linear_out consumes.
  */
 int dh_level_scan_fwd(int dtype, const void* pre_i, const void* pre_f, const void* pre_r,
-                      const void* mask, int64_t stride_mb, int64_t stride_mt, const void* V0,
-                      int64_t stride_vb, int64_t stride_vt, void* V, int b, int T, int H, int hd,
-                      int n_lv, void* stream);
+                      int64_t stride_pb, int64_t stride_pt, int64_t stride_pl, int64_t stride_ph,
+                      const void* mask, int64_t stride_mb, int64_t stride_mt, int64_t stride_ml,
+                      const void* V0, int64_t stride_vb, int64_t stride_vt, void* V, int b, int T, int H,
+                      int hd, int n_lv, int activated, void* stream);
 
 /*
  * One decode step of one tree layer: all L levels' gate readouts plus the L-level recurrence over
