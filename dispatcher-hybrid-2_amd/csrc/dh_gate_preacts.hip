@@ -55,6 +55,16 @@ struct FwdArgs {
 
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
+// Raw buffer access: a descriptor (base, byte range) held in scalar registers, a per-lane byte
+// offset (voffset) and a uniform byte offset (soffset); no per-lane 64-bit address arithmetic, and
+// a read past the range returns zeros. dword3 = 0x00020000 is the gfx9-family raw-buffer format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
 // two fp32 -> packed bf16 (round to nearest even, hardware conversion)
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   bf16x2_t v;
@@ -63,23 +73,41 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// bf16-valued fp32 from fp32 in ONE instruction: v_cvt_pk_bf16_f32(0, x) puts bf16(x) in the high
+// half and bf16(0) = 0 in the low half, which are exactly the fp32 bits of the rounded value
+// (written as the instruction itself: the compiler otherwise converts into the low half and then
+// permutes, two instructions)
+__device__ __forceinline__ float round_bf16(float x) {
+  float r;
+  asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
 // Element math of the two modes. KC = k elements one 16-byte fragment per lane covers across the
-// wave's four lane groups; mma3 adds hid(a, b) . W_x for the three gates.
+// wave's four lane groups. unpack_a converts the A fragment once per k-step (shared by every level
+// of the group); mma3 adds hid(a, b) . W_x for the three gates of one level. A masked row's B
+// fragment arrives as zeros (out-of-range buffer read), so no masking happens here.
 struct MathBf16 {
   typedef bf16_t T;
   static constexpr int KC = 32;
   static constexpr int KL = 8;      // k elements per lane fragment
-  __device__ __forceinline__ static void mma3(f32x4 (&acc)[3], const uint4& av, const uint4& bv, uint32_t keep,
-                                              const uint4 (&w)[3]) {
+  __device__ __forceinline__ static void unpack_a(const uint4& av, float (&af)[8]) {
     const uint32_t aw[4] = {av.x, av.y, av.z, av.w};
-    const uint32_t bw[4] = {bv.x & keep, bv.y & keep, bv.z & keep, bv.w & keep};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      af[2 * j] = __uint_as_float(aw[j] << 16);
+      af[2 * j + 1] = __uint_as_float(aw[j] & 0xffff0000u);
+    }
+  }
+  __device__ __forceinline__ static void mma3(f32x4 (&acc)[3], const float (&af)[8], const uint4& bv,
+                                              const uint4 (&w)[3]) {
+    const uint32_t bw[4] = {bv.x, bv.y, bv.z, bv.w};
     uint32_t hw[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float s0 = fmaxf(__uint_as_float(aw[j] << 16) + __uint_as_float(bw[j] << 16), 0.f);
-      const float s1 = fmaxf(__uint_as_float(aw[j] & 0xffff0000u) + __uint_as_float(bw[j] & 0xffff0000u), 0.f);
-      const uint32_t r = pack_bf16x2(s0, s1);                 // relu(round(a+b)) = round(relu(a+b))
-      const float x0 = __uint_as_float(r << 16), x1 = __uint_as_float(r & 0xffff0000u);
+      // relu(round(a+b)) = round(relu(a+b)); its square is exact in fp32 and rounded once
+      const float x0 = round_bf16(fmaxf(af[2 * j] + __uint_as_float(bw[j] << 16), 0.f));
+      const float x1 = round_bf16(fmaxf(af[2 * j + 1] + __uint_as_float(bw[j] & 0xffff0000u), 0.f));
       hw[j] = pack_bf16x2(x0 * x0, x1 * x1);
     }
     bf16x8 hid, wi, wf, wr;
@@ -92,7 +120,7 @@ struct MathBf16 {
     acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hid, wr, acc[2], 0, 0, 0);
   }
   __device__ __forceinline__ static T out(float v) { return f32_to_bf16(v); }
-  __device__ __forceinline__ static float rnd(float v) { return __uint_as_float(pack_bf16x2(v, 0.f) << 16); }
+  __device__ __forceinline__ static float rnd(float v) { return round_bf16(v); }
   __device__ __forceinline__ static void store4(T* p, const float (&v)[4]) {
     *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
   }
@@ -104,16 +132,21 @@ struct MathF32 {
   typedef float T;
   static constexpr int KC = 16;
   static constexpr int KL = 4;
-  __device__ __forceinline__ static void mma3(f32x4 (&acc)[3], const uint4& av, const uint4& bv, uint32_t keep,
+  __device__ __forceinline__ static void unpack_a(const uint4& av, float (&af)[4]) {
+    af[0] = __uint_as_float(av.x);
+    af[1] = __uint_as_float(av.y);
+    af[2] = __uint_as_float(av.z);
+    af[3] = __uint_as_float(av.w);
+  }
+  __device__ __forceinline__ static void mma3(f32x4 (&acc)[3], const float (&af)[4], const uint4& bv,
                                               const uint4 (&w)[3]) {
-    const uint32_t aw[4] = {av.x, av.y, av.z, av.w};
-    const uint32_t bw[4] = {bv.x & keep, bv.y & keep, bv.z & keep, bv.w & keep};
+    const uint32_t bw[4] = {bv.x, bv.y, bv.z, bv.w};
     const uint32_t wi[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
     const uint32_t wf[4] = {w[1].x, w[1].y, w[1].z, w[1].w};
     const uint32_t wr[4] = {w[2].x, w[2].y, w[2].z, w[2].w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float x = fmaxf(__uint_as_float(aw[j]) + __uint_as_float(bw[j]), 0.f);
+      float x = fmaxf(af[j] + __uint_as_float(bw[j]), 0.f);
       x = x * x;
       acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, __uint_as_float(wi[j]), acc[0], 0, 0, 0);
       acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, __uint_as_float(wf[j]), acc[1], 0, 0, 0);
@@ -137,13 +170,15 @@ __global__ __launch_bounds__(kThreads) void gate_preacts_fwd_kernel(FwdArgs a) {
   const int t = blockIdx.x * kTileT + wave * 16 + r;   // row this lane feeds into the MFMA
   const bool t_ok = t < a.T;
   const int tc = t_ok ? t : a.T - 1;
-  const T* Ab = (const T*)a.A + (int64_t)b * a.sab;
-  const T* Bb = (const T*)a.B + (int64_t)b * a.sab;
-  const T* Arow = Ab + (int64_t)tc * a.sat + g * M::KL;
+  // addresses: workgroup-uniform base pointers plus per-lane 32-bit byte offsets (the host checks
+  // they fit), so every load is one scalar-base + vector-offset access with no 64-bit arithmetic
+  const uint32_t row_bytes = (uint32_t)((int64_t)a.T * a.sat * (int64_t)sizeof(T));
+  const __amdgpu_buffer_rsrc_t rA = buf_rsrc((const T*)a.A + (int64_t)b * a.sab, row_bytes);
+  const __amdgpu_buffer_rsrc_t rB = buf_rsrc((const T*)a.B + (int64_t)b * a.sab, row_bytes);
+  const uint32_t aoff = (uint32_t)(((int64_t)tc * a.sat + g * M::KL) * (int64_t)sizeof(T));
 
   int lv[LG];
-  const T* Brow[LG];
-  uint32_t keep[LG];
+  uint32_t boff[LG];
   float mv[LG];
 #pragma unroll
   for (int j = 0; j < LG; ++j) {
@@ -155,8 +190,9 @@ __global__ __launch_bounds__(kThreads) void gate_preacts_fwd_kernel(FwdArgs a) {
 #pragma unroll
   for (int j = 0; j < LG; ++j) {
     const int src = tc - (1 << lv[j]);             // rows past T use the clamped row: always < T
-    Brow[j] = Bb + (int64_t)(src > 0 ? src : 0) * a.sat + g * M::KL;
-    keep[j] = (t_ok && src >= 0 && l0 + j < a.n_lv && mv[j] > 0.f) ? 0xffffffffu : 0u;
+    const bool keep = t_ok && src >= 0 && l0 + j < a.n_lv && mv[j] > 0.f;
+    // a row without a source reads past the descriptor's range, which returns zeros (B = 0)
+    boff[j] = keep ? (uint32_t)(((int64_t)src * a.sat + g * M::KL) * (int64_t)sizeof(T)) : 0x80000000u;
   }
 
   const int NT = (a.H + 15) >> 4;
@@ -164,53 +200,52 @@ __global__ __launch_bounds__(kThreads) void gate_preacts_fwd_kernel(FwdArgs a) {
   for (int nt = 0; nt < NT; ++nt) {
     const int n = nt * 16 + r;                  // head whose weights this lane feeds
     const int nc = n < a.H ? n : a.H - 1;
-    const T* W[LG][3];
+    const uint32_t woff = (uint32_t)(((int64_t)nc * a.swh + g * M::KL) * (int64_t)sizeof(T));
+    const uint32_t w_bytes = (uint32_t)((int64_t)a.n_lv * a.swl * (int64_t)sizeof(T));
+    const __amdgpu_buffer_rsrc_t rW[3] = {buf_rsrc(a.Wi, w_bytes), buf_rsrc(a.Wf, w_bytes), buf_rsrc(a.Wr, w_bytes)};
+    uint32_t wlo[LG];
 #pragma unroll
-    for (int j = 0; j < LG; ++j) {
-      const int64_t off = (int64_t)lv[j] * a.swl + (int64_t)nc * a.swh + g * M::KL;
-      W[j][0] = (const T*)a.Wi + off;
-      W[j][1] = (const T*)a.Wf + off;
-      W[j][2] = (const T*)a.Wr + off;
-    }
+    for (int j = 0; j < LG; ++j) wlo[j] = (uint32_t)((int64_t)lv[j] * a.swl * (int64_t)sizeof(T));
     f32x4 acc[LG][3];
 #pragma unroll
     for (int j = 0; j < LG; ++j)
 #pragma unroll
       for (int x = 0; x < 3; ++x) acc[j][x] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    uint4 cA[KU], cB[KU][LG], cW[KU][LG][3];
+    // two fragment buffers in ping-pong (no register copies, so a prefetch is never waited for
+    // before the MFMAs of the other buffer have been issued). The host makes GH a multiple of
+    // 2*STEP, so both halves of every iteration are real work (no branch the loads could sink
+    // into); the fetch after the last step is clamped to a valid chunk and never used.
+    uint4 xA[KU], xB[KU][LG], xW[KU][LG][3];
+    uint4 yA[KU], yB[KU][LG], yW[KU][LG][3];
     auto fetch = [&](int k0, uint4 (&fA)[KU], uint4 (&fB)[KU][LG], uint4 (&fW)[KU][LG][3]) {
 #pragma unroll
       for (int u = 0; u < KU; ++u) {
-        const int kk = k0 + u * M::KC;
-        fA[u] = ld16(Arow + kk);
+        const uint32_t kb = (uint32_t)((k0 + u * M::KC) * (int)sizeof(T));   // uniform byte offset
+        fA[u] = bld16(rA, aoff, kb);
 #pragma unroll
-        for (int j = 0; j < LG; ++j) fB[u][j] = ld16(Brow[j] + kk);
+        for (int j = 0; j < LG; ++j) fB[u][j] = bld16(rB, boff[j], kb);
 #pragma unroll
         for (int j = 0; j < LG; ++j)
 #pragma unroll
-          for (int x = 0; x < 3; ++x) fW[u][j][x] = ld16(W[j][x] + kk);
+          for (int x = 0; x < 3; ++x) fW[u][j][x] = bld16(rW[x], woff, wlo[j] + kb);
       }
     };
-    fetch(0, cA, cB, cW);
-    for (int k0 = 0; k0 < a.GH; k0 += STEP) {
-      uint4 nA[KU], nB[KU][LG], nW[KU][LG][3];
-      const int kn = k0 + STEP < a.GH ? k0 + STEP : k0;     // last step re-reads its own chunk
-      fetch(kn, nA, nB, nW);
-#pragma unroll
-      for (int u = 0; u < KU; ++u)
-#pragma unroll
-        for (int j = 0; j < LG; ++j) M::mma3(acc[j], cA[u], cB[u][j], keep[j], cW[u][j]);
+    auto compute = [&](const uint4 (&fA)[KU], const uint4 (&fB)[KU][LG], const uint4 (&fW)[KU][LG][3]) {
 #pragma unroll
       for (int u = 0; u < KU; ++u) {
-        cA[u] = nA[u];
+        float af[M::KL];
+        M::unpack_a(fA[u], af);
 #pragma unroll
-        for (int j = 0; j < LG; ++j) {
-          cB[u][j] = nB[u][j];
-#pragma unroll
-          for (int x = 0; x < 3; ++x) cW[u][j][x] = nW[u][j][x];
-        }
+        for (int j = 0; j < LG; ++j) M::mma3(acc[j], af, fB[u][j], fW[u][j]);
       }
+    };
+    fetch(0, xA, xB, xW);
+    for (int k0 = 0; k0 < a.GH; k0 += 2 * STEP) {
+      fetch(k0 + STEP, yA, yB, yW);
+      compute(xA, xB, xW);
+      fetch(k0 + 2 * STEP < a.GH ? k0 + 2 * STEP : k0, xA, xB, xW);
+      compute(yA, yB, yW);
     }
     // C fragment: column (head) lane%16, rows 4*(lane/16) + i
     const int tb = blockIdx.x * kTileT + wave * 16 + g * 4;
@@ -452,6 +487,10 @@ extern "C" int dh_gate_preacts_fwd(int dtype, const void* A, const void* B, int6
              "%s: strides overlap rows", who);
   DH_REQUIRE(stride_ob >= 0 && stride_ot >= 0 && stride_ol >= 0 && stride_oh >= 0, DH_ERR_INVALID_ARG,
              "%s: negative output stride", who);
+  const int64_t esz_in = dtype == DH_BF16 ? 2 : 4;
+  DH_REQUIRE((int64_t)T * stride_at * esz_in < ((int64_t)1 << 31) &&
+                 (int64_t)n_lv * stride_wl * esz_in < ((int64_t)1 << 31),
+             DH_ERR_UNSUPPORTED_SHAPE, "%s: one batch row of A/B or the weights exceed 2 GiB", who);
   const size_t esz = dtype == DH_BF16 ? 2 : 4;
   const bool vec_out = stride_ot == 1 && stride_ob % 4 == 0 && stride_ol % 4 == 0 && stride_oh % 4 == 0 &&
                        aligned(out_i, 4 * esz) && aligned(out_f, 4 * esz) && aligned(out_r, 4 * esz);
@@ -467,7 +506,8 @@ extern "C" int dh_gate_preacts_fwd(int dtype, const void* A, const void* B, int6
   const int ngroups = (n_lv + LG - 1) / LG;
   const int kc = dtype == DH_BF16 ? 32 : 16;
   int KU = LG == 1 ? 4 : (LG == 2 ? 2 : 1);
-  if (GH % (kc * KU) != 0) KU = 1;
+  while (KU > 1 && GH % (2 * kc * KU) != 0) KU /= 2;       // GH % 64 == 0 covers 2*kc*1
+  if (KU == 2 && LG == 1) KU = 1;                            // no <1, 2> instantiation
   dim3 grid(tiles, ngroups, b);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DH_BF16)

@@ -52,6 +52,65 @@ template <> struct Raw<float> {
   __device__ __forceinline__ static float f(uint32_t r) { return __uint_as_float(r); }
 };
 
+// The C columns of one position as ONE unconditional vector access (C*sizeof(T) bytes, aligned to
+// that size: the host checks row strides and base pointers).
+template <typename T, int C>
+__device__ __forceinline__ void load_cols(const T* p, float (&v)[C]) {
+  if constexpr (sizeof(T) == 2 && C == 1) {
+    v[0] = bf16_to_f32(*p);
+  } else {
+    constexpr int NW = C * (int)sizeof(T) / 4;
+    uint32_t w[NW];
+    if constexpr (NW >= 4) {
+#pragma unroll
+      for (int q = 0; q < NW / 4; ++q) {
+        const uint4 x = reinterpret_cast<const uint4*>(p)[q];
+        w[4 * q] = x.x; w[4 * q + 1] = x.y; w[4 * q + 2] = x.z; w[4 * q + 3] = x.w;
+      }
+    } else if constexpr (NW == 2) {
+      const uint2 x = *reinterpret_cast<const uint2*>(p);
+      w[0] = x.x; w[1] = x.y;
+    } else {
+      w[0] = *reinterpret_cast<const uint32_t*>(p);
+    }
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      if constexpr (sizeof(T) == 2) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      } else {
+        v[i] = __uint_as_float(w[i]);
+      }
+    }
+  }
+}
+
+template <typename T, int C>
+__device__ __forceinline__ void store_cols(T* p, const float (&v)[C]) {
+  if constexpr (sizeof(T) == 2 && C == 1) {
+    *p = f32_to_bf16(v[0]);
+  } else {
+    constexpr int NW = C * (int)sizeof(T) / 4;
+    uint32_t w[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      if constexpr (sizeof(T) == 2)
+        w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+      else
+        w[i] = __float_as_uint(v[i]);
+    }
+    if constexpr (NW >= 4) {
+#pragma unroll
+      for (int q = 0; q < NW / 4; ++q)
+        reinterpret_cast<uint4*>(p)[q] = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+    } else if constexpr (NW == 2) {
+      *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+    } else {
+      *reinterpret_cast<uint32_t*>(p) = w[0];
+    }
+  }
+}
+
 template <typename T, int C, int PPT, int MODE>
 __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
   __shared__ float rv[C * PPT * kThreads];
@@ -74,28 +133,43 @@ __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
   const T* pr = (const T*)a.pre_r + gb;
   const T* mk = (const T*)a.mask + (MODE == kPreMask ? (int64_t)b * a.smb : 0);
 
+  // V0: one unconditional vector load per position from the clamped row, zeroed past T afterwards
   float V[PPT][C];
 #pragma unroll
   for (int j = 0; j < PPT; ++j) {
     const int t = tid + j * kThreads;
     const int tc = t < a.T ? t : a.T - 1;
-    const T* src = (const T*)a.V0 + (int64_t)b * a.svb + (int64_t)tc * a.svt + col0;
+    load_cols<T, C>((const T*)a.V0 + (int64_t)b * a.svb + (int64_t)tc * a.svt + col0, V[j]);
+  }
 #pragma unroll
-    for (int cc = 0; cc < C; ++cc) V[j][cc] = t < a.T ? Elem<T>::load(src + cc) : 0.f;
+  for (int j = 0; j < PPT; ++j) {
+    const bool live = tid + j * kThreads < a.T;
+#pragma unroll
+    for (int cc = 0; cc < C; ++cc) V[j][cc] = live ? V[j][cc] : 0.f;
   }
 
+  // per-position element offsets along t, shared by the three gates (32-bit: the host checks
+  // (T-1)*stride fits); the per-level part of each address is a uniform base
+  uint32_t goff[PPT], moff[PPT];
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    const int t = tid + j * kThreads;
+    const uint32_t tc = t < a.T ? t : a.T - 1;
+    goff[j] = tc * (uint32_t)a.spt;
+    moff[j] = tc * (uint32_t)a.smt;
+  }
   uint32_t ri[PPT], rf[PPT], rr[PPT], rm[PPT];
   auto fetch = [&](int l) {
-    const int64_t lo = (int64_t)l * a.spl, ml = (int64_t)l * a.sml;
+    const T* li = pi + (int64_t)l * a.spl;
+    const T* lf = pf + (int64_t)l * a.spl;
+    const T* lr = pr + (int64_t)l * a.spl;
+    const T* lm = mk + (int64_t)l * a.sml;
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-      const int t = tid + j * kThreads;
-      const int64_t tc = t < a.T ? t : a.T - 1;
-      const int64_t go = tc * a.spt + lo;
-      ri[j] = Raw<T>::load(pi + go);
-      rf[j] = Raw<T>::load(pf + go);
-      rr[j] = Raw<T>::load(pr + go);
-      if (MODE == kPreMask) rm[j] = Raw<T>::load(mk + tc * a.smt + ml);
+      ri[j] = Raw<T>::load(li + goff[j]);
+      rf[j] = Raw<T>::load(lf + goff[j]);
+      rr[j] = Raw<T>::load(lr + goff[j]);
+      if (MODE == kPreMask) rm[j] = Raw<T>::load(lm + moff[j]);
     }
   };
   if (kPrefetch) fetch(0);
@@ -103,8 +177,9 @@ __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
   for (int l = 0; l < a.n_lv; ++l) {
     const int shift = 1 << l;
     if (!kPrefetch) fetch(l);
+    // a position that takes no update at this level gets a = 0, f = 1 (as the activated inputs
+    // already have it), so the update below runs unpredicated: f*V + 0*msg = V for finite data
     float rg[PPT], ad[PPT], fg[PPT];
-    bool up[PPT];
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
       const int t = tid + j * kThreads;
@@ -112,12 +187,11 @@ __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
         ad[j] = Raw<T>::f(ri[j]);
         fg[j] = Raw<T>::f(rf[j]);
         rg[j] = Raw<T>::f(rr[j]);
-        up[j] = true;
       } else {
-        ad[j] = dh_sigmoid(Raw<T>::f(ri[j]));
-        fg[j] = dh_sigmoid(Raw<T>::f(rf[j]));
+        const bool up = t >= shift && (MODE != kPreMask || Raw<T>::f(rm[j]) > 0.f);
+        ad[j] = up ? dh_sigmoid(Raw<T>::f(ri[j])) : 0.f;
+        fg[j] = up ? dh_sigmoid(Raw<T>::f(rf[j])) : 1.f;
         rg[j] = dh_sigmoid(Raw<T>::f(rr[j]));
-        up[j] = t >= shift && (MODE != kPreMask || Raw<T>::f(rm[j]) > 0.f);
       }
     }
     if (kPrefetch) fetch(l + 1 < a.n_lv ? l + 1 : l);   // next level's gates fly during the exchange
@@ -135,10 +209,7 @@ __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
       const int t = tid + j * kThreads;
       const int s = t >= shift ? t - shift : 0;
 #pragma unroll
-      for (int cc = 0; cc < C; ++cc) {
-        const float nv = fg[j] * V[j][cc] + ad[j] * rv[s * C + cc];
-        V[j][cc] = up[j] ? nv : V[j][cc];
-      }
+      for (int cc = 0; cc < C; ++cc) V[j][cc] = fg[j] * V[j][cc] + ad[j] * rv[s * C + cc];
     }
     __syncthreads();
   }
@@ -146,11 +217,7 @@ __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
 #pragma unroll
   for (int j = 0; j < PPT; ++j) {
     const int t = tid + j * kThreads;
-    if (t < a.T) {
-      T* o = (T*)a.V + ((int64_t)b * a.T + t) * ((int64_t)a.H * a.hd) + col0;
-#pragma unroll
-      for (int cc = 0; cc < C; ++cc) Elem<T>::store(o + cc, V[j][cc]);
-    }
+    if (t < a.T) store_cols<T, C>((T*)a.V + ((int64_t)b * a.T + t) * ((int64_t)a.H * a.hd) + col0, V[j]);
   }
 }
 
@@ -199,6 +266,12 @@ extern "C" int dh_level_scan_fwd(int dtype, const void* pre_i, const void* pre_f
              (long long)stride_vt);
   DH_REQUIRE(stride_pb >= 0 && stride_pt >= 0 && stride_pl >= 0 && stride_ph >= 0, DH_ERR_INVALID_ARG,
              "%s: negative gate stride", who);
+  DH_REQUIRE((int64_t)(T - 1) * stride_pt < ((int64_t)1 << 31) && (int64_t)(T - 1) * stride_mt < ((int64_t)1 << 31),
+             DH_ERR_UNSUPPORTED_SHAPE, "%s: (T-1) * gate/mask t-stride exceeds 2^31 elements", who);
+  const int64_t esz = dtype == DH_BF16 ? 2 : 4;
+  DH_REQUIRE((uintptr_t)V0 % 16 == 0 && (uintptr_t)V % 16 == 0 && (stride_vt * esz) % 16 == 0 &&
+                 (stride_vb * esz) % 16 == 0,
+             DH_ERR_INVALID_ARG, "%s: V0/V need 16-byte aligned rows", who);
   ScanArgs a{pre_i, pre_f, pre_r, stride_pb, stride_pt, stride_pl, stride_ph, mask, stride_mb, stride_mt,
              stride_ml, V0, stride_vb, stride_vt, V, b, T, H, hd, n_lv};
   const int mode = activated ? kActivated : (mask ? kPreMask : kPreNoMask);
