@@ -76,7 +76,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // bf16-valued fp32 from fp32 in ONE instruction: v_cvt_pk_bf16_f32(0, x) puts bf16(x) in the high
 // half and bf16(0) = 0 in the low half, which are exactly the fp32 bits of the rounded value
 // (written as the instruction itself: the compiler otherwise converts into the low half and then
-// permutes, two instructions)
+// permutes, two instructions). PRECONDITION: x must not come straight from a transcendental
+// instruction (v_exp/v_rcp/...): gfx950 needs a wait state before a VALU reads a transcendental
+// result and the compiler's hazard pass does not look into inline assembly. The hot loop feeds it
+// v_max results only; everything else rounds with round_bf16_sw.
+__device__ __forceinline__ float round_bf16_sw(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 __device__ __forceinline__ float round_bf16(float x) {
   float r;
   asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(x));
@@ -120,7 +124,7 @@ struct MathBf16 {
     acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hid, wr, acc[2], 0, 0, 0);
   }
   __device__ __forceinline__ static T out(float v) { return f32_to_bf16(v); }
-  __device__ __forceinline__ static float rnd(float v) { return round_bf16(v); }
+  __device__ __forceinline__ static float rnd(float v) { return round_bf16_sw(v); }
   __device__ __forceinline__ static void store4(T* p, const float (&v)[4]) {
     *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
   }

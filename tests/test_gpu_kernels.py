@@ -176,6 +176,42 @@ def test_gate_scan_matches_oracle(case, dtype):
     assert err < (1e-5 if dtype == torch.float32 else 2e-2), f"rel {err:.3e}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("b", [8, 5, 3, 1])
+def test_activated_gates_release_widths(b, dtype):
+    """The activated, masked, head-major gates (activate mode) against torch's sigmoid of the op's
+    own pre-activations, at the released widths (GH 1024, 16 heads, 12 levels, T 4096) and batch
+    sizes that select level groups of 4, 3, 2 and 1, then the full gate_scan against the two-op
+    route. bf16 allows one rounding step of the sigmoid output."""
+    from dispatcher_hybrid import fused_gates as fg
+    print(f"activated gates b={b} {dtype}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(40 + b)
+    T, GH, H, hd, L = 4096, 1024, 16, 64, 12
+    A = torch.randn(b, T, GH, device=DEV, generator=g).to(dtype)
+    B = torch.randn(b, T, GH, device=DEV, generator=g).to(dtype)
+    W = [(torch.randn(L, H, GH, device=DEV, generator=g) / GH ** 0.5).to(dtype) for _ in range(3)]
+    bs = [torch.randn(L, H, device=DEV, generator=g) for _ in range(3)]
+    mask = (torch.rand(b, T, L, device=DEV, generator=g) > 0.1).to(dtype)
+    V0 = torch.randn(b, T, H * hd, device=DEV, generator=g).to(dtype)
+    pre = fg.fused_gate_preacts(A, B, *W, *bs, L, mask)
+    t = torch.arange(T, device=DEV).view(1, T, 1)
+    M = ((t >= (1 << torch.arange(L, device=DEV)).view(1, 1, L)) & (mask > 0)).float().unsqueeze(-1)
+    refs = (torch.sigmoid(pre[0].float()) * M, torch.sigmoid(pre[1].float()) * M + (1 - M),
+            torch.sigmoid(pre[2].float()))
+    ins = fg._prep_gate_inputs(A, B, *W, *bs, L)
+    buf = torch.full((3, b, H, L, T), float("nan"), device=DEV, dtype=ins[0].dtype)
+    gates = [buf[i].permute(0, 3, 2, 1) for i in range(3)]
+    fg._preacts_launch(*ins, mask, gates, gates[0].stride(), 1, L, "test")
+    torch.cuda.synchronize()
+    tol = 1e-6 if dtype == torch.float32 else 2.0 ** -8
+    for got, ref in zip(gates, refs):
+        assert not bool(torch.isnan(got).any()), "unwritten gate entries"
+        assert float((got.float() - ref).abs().max()) <= tol
+    V1 = fg.fused_gate_scan(A, B, *W, *bs, L, mask, V0, H)
+    V2 = fg.fused_level_scan(*pre, mask, V0, H, L)
+    assert rel_err(V1, V2) < (1e-5 if dtype == torch.float32 else 2e-2)
+
+
 def test_gate_scan_equals_two_op_path_fp32():
     """The head-major activated route and the reference-layout op route agree in fp32."""
     from dispatcher_hybrid.fused_gates import fused_gate_preacts, fused_gate_scan, fused_level_scan
