@@ -1,0 +1,268 @@
+// One decode step of a windowed RoPE attention layer, for gfx950: the rotation of the new query and
+// key, the key/value cache write at the device position t, the scores over the window, the softmax
+// and the value average, in one launch.
+//
+// Semantics (reference dispatcher_hybrid/decoding.py:411-435 graph step and :247-266 eager step;
+// modeling_dispatcher.py:163-166 rope):
+//   (q', k')   = rope(q[b,h], t), rope(k[b,h], t)     interleaved pairs: (x0 c - x1 s, x0 s + x1 c)
+//   K[b,h,t]   = k' ; V[b,h,t] = v[b,h]
+//   s_j        = (q' . K[b,h,j]) / sqrt(hd)            j in [lo, t], lo = max(0, t+1-window) (window > 0)
+//   p          = softmax_j(s)                          (fp32 softmax, as the eager step computes it)
+//   y[b,h]     = sum_j p_j V[b,h,j]
+// bf16 mode rounds where the eager bf16 step rounds: each rope product and sum, the q'.K matmul
+// output, its division by sqrt(hd), the softmax output and the value average.
+//
+// Work decomposition: one workgroup (16 wave64s) per (head, batch row). Pass 1 gives every thread
+// one window position at a time and the thread computes that position's full dot product from its
+// key row (hd elements, contiguous in the head-major cache); the scores stay in LDS. A block
+// reduction gives the maximum and the sum of exponentials. Pass 2 splits the window over the 16
+// waves and gives each lane one head dimension (a wave reads whole value rows, 64 lanes x 2 bytes),
+// accumulating p_j V[j] in fp32; the 16 partial sums meet in LDS. The new position t is read from
+// LDS (the rotated key and the value computed in this launch), never from the cache the same
+// launch writes.
+#include "dh_common.h"
+
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxHd = 128;
+constexpr int kMaxWindow = 16384;   // scores held in LDS (64 KB)
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t qkv_bstride;
+  const void* cos;
+  const void* sin;
+  void* K;
+  void* V;
+  const int64_t* t_dev;
+  void* y;
+  int64_t y_bstride;
+  int H, Tmax, window;
+  float scale;            // sqrt(hd): scores are divided by it
+};
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_move<0xb1, 0xf>(v));
+  v = fmaxf(v, dpp_move<0x4e, 0xf>(v));
+  v = fmaxf(v, dpp_move<0x141, 0xf>(v));
+  v = fmaxf(v, dpp_move<0x140, 0xf>(v));
+  // row broadcasts fill the other rows' lanes with 0 (bound_ctrl): take max with the lane itself
+  // only where the source row exists, which the row masks select
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x142, 0xa, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x143, 0xc, 0xf, false)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// q . row for one cache row of hd elements: the row is read in groups of up to 8 16-byte chunks
+// (all loads of a group issued before any is used), q comes from LDS as broadcast reads
+template <typename T, int HD>
+__device__ __forceinline__ float row_dot(const T* p, const float* q) {
+  constexpr int V = 16 / sizeof(T);                    // elements per chunk
+  constexpr int NC = HD / V;
+  constexpr int G = NC < 8 ? NC : 8;
+  float dot = 0.f;
+#pragma unroll
+  for (int c0 = 0; c0 < NC; c0 += G) {
+    uint4 w[G];
+#pragma unroll
+    for (int c = 0; c < G; ++c) w[c] = reinterpret_cast<const uint4*>(p)[c0 + c];
+#pragma unroll
+    for (int c = 0; c < G; ++c) {
+      const uint32_t ws[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+      const int e = (c0 + c) * V;
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          dot += q[e + 2 * j] * __uint_as_float(ws[j] << 16) + q[e + 2 * j + 1] * __uint_as_float(ws[j] & 0xffff0000u);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dot += q[e + j] * __uint_as_float(ws[j]);
+      }
+    }
+  }
+  return dot;
+}
+
+template <typename T, int HD>
+__global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) {
+  extern __shared__ float sc[];                       // scores / probabilities of the window
+  __shared__ float qs[kMaxHd], ks[kMaxHd], vs[kMaxHd];
+  __shared__ float red[kWaves];
+  __shared__ float part[kWaves][64];
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t = *a.t_dev;
+  if (t < 0 || t >= a.Tmax) return;                   // workgroup-uniform: nothing to do
+  const int lo = a.window > 0 ? (int)max((int64_t)0, t + 1 - a.window) : 0;
+  const int n = (int)t - lo + 1;
+  const int64_t head_off = ((int64_t)b * a.H + h) * a.Tmax * HD;  // (b, h) rows of the caches
+  T* Kh = (T*)a.K + head_off;
+  T* Vh = (T*)a.V + head_off;
+
+  // ---- rope of q and k at position t, cache write of (k', v) at t
+  if (tid < HD / 2) {
+    const int64_t base = (int64_t)b * a.qkv_bstride + (int64_t)h * HD;
+    const T* qp = (const T*)a.q + base;
+    const T* kp = (const T*)a.k + base;
+    const T* vp = (const T*)a.v + base;
+    const float c = Elem<T>::load((const T*)a.cos + t * (HD / 2) + tid);
+    const float s = Elem<T>::load((const T*)a.sin + t * (HD / 2) + tid);
+    const float q0 = Elem<T>::load(qp + 2 * tid), q1 = Elem<T>::load(qp + 2 * tid + 1);
+    const float k0 = Elem<T>::load(kp + 2 * tid), k1 = Elem<T>::load(kp + 2 * tid + 1);
+    const float v0 = Elem<T>::load(vp + 2 * tid), v1 = Elem<T>::load(vp + 2 * tid + 1);
+    typedef Elem<T> E;
+    float qr0, qr1, kr0, kr1;
+    {
+      // every product rounded on its own (torch evaluates them as separate tensor ops): no FMA
+#pragma clang fp contract(off)
+      qr0 = E::round(E::round(q0 * c) - E::round(q1 * s));
+      qr1 = E::round(E::round(q0 * s) + E::round(q1 * c));
+      kr0 = E::round(E::round(k0 * c) - E::round(k1 * s));
+      kr1 = E::round(E::round(k0 * s) + E::round(k1 * c));
+    }
+    qs[2 * tid] = qr0; qs[2 * tid + 1] = qr1;
+    ks[2 * tid] = kr0; ks[2 * tid + 1] = kr1;
+    vs[2 * tid] = v0; vs[2 * tid + 1] = v1;
+    E::store(Kh + t * HD + 2 * tid, kr0);
+    E::store(Kh + t * HD + 2 * tid + 1, kr1);
+    E::store(Vh + t * HD + 2 * tid, v0);
+    E::store(Vh + t * HD + 2 * tid + 1, v1);
+  }
+  __syncthreads();
+
+  // ---- pass 1: scores, one position per thread per sweep. Position t (index n-1) is scored from
+  // the rotated key in LDS by thread 0; the cache row this launch writes is never read back.
+  float mx = -INFINITY;
+  for (int i0 = 0; i0 < n - 1; i0 += kThreads) {
+    const int i = i0 + tid;
+    const int j = lo + min(i, n - 2);                  // clamped: every load is a cached position
+    const float dot = row_dot<T, HD>(Kh + (int64_t)j * HD, qs);
+    const float s = Elem<T>::round(Elem<T>::round(dot) / a.scale);
+    if (i < n - 1) {
+      sc[i] = s;
+      mx = fmaxf(mx, s);
+    }
+  }
+  if (tid == 0) {
+    float dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < HD; ++e) dot += qs[e] * ks[e];
+    const float s = Elem<T>::round(Elem<T>::round(dot) / a.scale);
+    sc[n - 1] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  float M = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) M = fmaxf(M, red[w]);
+  __syncthreads();                                     // red is reused below
+  float sum = 0.f;
+  for (int i = tid; i < n; i += kThreads) {
+    const float p = __expf(sc[i] - M);
+    sc[i] = p;
+    sum += p;
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) L += red[w];
+
+  // ---- pass 2: y = sum_j p_j V[j]; wave w takes a contiguous block of the window, lane -> dims
+  constexpr int PPW = HD >= 64 ? 1 : 64 / HD;          // positions per wave iteration
+  constexpr int DPL = HD > 64 ? HD / 64 : 1;           // dims per lane
+  const int nc = n - 1;                                // cached positions; index n-1 is t
+  const int per = (nc + kWaves - 1) / kWaves;
+  const int j0 = wave * per, j1 = min(nc, j0 + per);
+  const int sub = HD >= 64 ? 0 : lane / HD;            // which of the PPW positions
+  const int e0 = HD >= 64 ? lane : lane % HD;
+  float acc[DPL];
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) acc[d] = 0.f;
+  constexpr int U = 8 / DPL;                           // positions in flight per lane
+  for (int i0 = j0; i0 < j1; i0 += PPW * U) {
+    float vv[U][DPL], pp[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * PPW + sub;
+      const int ic = min(i, nc - 1);
+      const int j = lo + ic;
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) vv[u][d] = Elem<T>::load(Vh + (int64_t)j * HD + e0 + 64 * d);
+      pp[u] = i < j1 ? Elem<T>::round(sc[ic] / L) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int d = 0; d < DPL; ++d) acc[d] += pp[u] * vv[u][d];
+  }
+  // lanes of one wave that hold the same dimension (HD < 64) are summed first
+#pragma unroll
+  for (int d = 0; d < DPL; ++d) {
+    float v = acc[d];
+    if (HD < 64) {
+#pragma unroll
+      for (int off = HD; off < 64; off <<= 1) v += __shfl_xor(v, off);
+    }
+    acc[d] = v;
+  }
+  for (int d = 0; d < DPL; ++d) {
+    __syncthreads();
+    if (lane < HD || HD > 64) part[wave][lane] = acc[d];
+    __syncthreads();
+    if (wave == 0 && (HD >= 64 || lane < HD)) {
+      float s = Elem<T>::round(sc[n - 1] / L) * vs[lane + 64 * d];      // position t
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) s += part[w][lane];
+      Elem<T>::store((T*)a.y + (int64_t)b * a.y_bstride + (int64_t)h * HD + lane + 64 * d, s);
+    }
+  }
+}
+
+template <typename T>
+int launch(const AttnArgs& a, int B, int hd, hipStream_t s) {
+  const int nmax = a.window > 0 ? min(a.window, a.Tmax) : a.Tmax;
+  const size_t lds = (size_t)nmax * sizeof(float);
+  dim3 grid(a.H, B), block(kThreads);
+  switch (hd) {
+    case 16: decode_attention_kernel<T, 16><<<grid, block, lds, s>>>(a); break;
+    case 32: decode_attention_kernel<T, 32><<<grid, block, lds, s>>>(a); break;
+    case 64: decode_attention_kernel<T, 64><<<grid, block, lds, s>>>(a); break;
+    default: decode_attention_kernel<T, 128><<<grid, block, lds, s>>>(a); break;
+  }
+  return dh_check_launch("dh_decode_attention");
+}
+
+bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
+
+}  // namespace
+
+extern "C" int dh_decode_attention(int dtype, const void* q, const void* k, const void* v, int64_t qkv_bstride,
+                                   const void* rope_cos, const void* rope_sin, void* K_cache, void* V_cache,
+                                   const int64_t* t_dev, void* y, int64_t y_bstride, int B, int H, int hd,
+                                   int Tmax, int window, void* stream) {
+  const char* who = "dh_decode_attention";
+  DH_REQUIRE(dtype == DH_F32 || dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d", who, dtype);
+  DH_REQUIRE(B >= 1 && H >= 1 && Tmax >= 1 && window >= 0, DH_ERR_INVALID_ARG,
+             "%s: B=%d H=%d Tmax=%d window=%d", who, B, H, Tmax, window);
+  DH_REQUIRE(hd == 16 || hd == 32 || hd == 64 || hd == 128, DH_ERR_UNSUPPORTED_SHAPE,
+             "%s: hd=%d not in {16,32,64,128}", who, hd);
+  const int nmax = window > 0 ? (window < Tmax ? window : Tmax) : Tmax;
+  DH_REQUIRE(nmax <= kMaxWindow, DH_ERR_UNSUPPORTED_SHAPE, "%s: attention span %d exceeds %d", who, nmax,
+             kMaxWindow);
+  DH_REQUIRE(q && k && v && rope_cos && rope_sin && K_cache && V_cache && t_dev && y, DH_ERR_INVALID_ARG,
+             "%s: null pointer argument", who);
+  DH_REQUIRE(aligned(K_cache, 16) && aligned(V_cache, 16), DH_ERR_INVALID_ARG, "%s: caches need 16-byte alignment",
+             who);
+  AttnArgs a{q, k, v, qkv_bstride, rope_cos, rope_sin, K_cache, V_cache, t_dev, y, y_bstride, H, Tmax, window,
+             sqrtf((float)hd)};
+  hipStream_t s = (hipStream_t)stream;
+  return dtype == DH_BF16 ? launch<bf16_t>(a, B, hd, s) : launch<float>(a, B, hd, s);
+}

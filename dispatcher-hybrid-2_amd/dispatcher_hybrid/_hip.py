@@ -64,6 +64,8 @@ def _load():
         "dh_decode_gemv": ([i32, vp, i64, vp, vp, ctypes.c_float, i32, vp, vp, vp, vp, vp,
                             vp, i64, vp, i32, vp, i32, i32, vp], i32),
         "dh_step_scan": ([i32] + [vp] * 7 + [i32] * 6 + [vp], i32),
+        "dh_decode_attention": ([i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, i64,
+                                 i32, i32, i32, i32, i32, vp], i32),
     }
     for name, (argtypes, restype) in sigs.items():
         fn = getattr(lib, name)

@@ -388,8 +388,9 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         dh_decode_gemv       linear_down + residual
 
     in place of ~17 torch ops, the embedding gather folded into the first launch and RMSNorm_out +
-    lm_head as one launch. Attention layers use dh_decode_gemv for their projections and torch for
-    RoPE and the windowed softmax. Same caches, same graph harness; raises ImportError when the
+    lm_head as one launch. An attention layer is the same chain with dh_decode_gemv for its
+    projections and one dh_decode_attention launch (RoPE, cache write, windowed softmax, value
+    average) in place of the mixer. Same caches, same graph harness; raises ImportError when the
     kernel library is missing.
     """
 
@@ -458,19 +459,8 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         fs.decode_gemv(x_in, [(at.linear_q.weight, self.q_buf, d, 0), (at.linear_k.weight, self.k_buf, d, 0),
                               (at.linear_v.weight, self.v_buf, d, 0)], self.t_buf,
                        norm_weight=blk.norm1.weight, eps=self._eps(blk.norm1, self.dtype), x_rows=rows)
-        cos = cache.rope_cos.index_select(0, self.t_buf)[0]
-        sin = cache.rope_sin.index_select(0, self.t_buf)[0]
-        H, hd = at.num_heads, at.head_dim
-        q = rope_rotate(self.q_buf.view(Bb, H, hd), cos, sin)
-        cache.k.index_copy_(2, self.t_buf, rope_rotate(self.k_buf.view(Bb, H, hd), cos, sin).unsqueeze(2))
-        cache.v.index_copy_(2, self.t_buf, self.v_buf.view(Bb, H, hd).unsqueeze(2))
-        valid = self.arangeT <= self.t_buf
-        if at.window > 0:
-            valid = valid & (self.arangeT > self.t_buf - at.window)
-        scores = torch.matmul(cache.k, q.unsqueeze(-1)).squeeze(-1) / math.sqrt(hd)
-        scores = scores.masked_fill(~valid.view(1, 1, -1), float("-inf"))
-        att = torch.softmax(scores.float(), dim=-1).to(self.dtype)
-        self.y_buf.copy_(torch.matmul(att.unsqueeze(2), cache.v).squeeze(2).reshape(Bb, -1))
+        fs.decode_attention(self.q_buf, self.k_buf, self.v_buf, cache.rope_cos, cache.rope_sin,
+                            cache.k, cache.v, self.t_buf, self.y_buf, at.window)
         fs.decode_gemv(self.y_buf, [(at.linear_out.weight, self.x_buf, d, 0)], self.t_buf,
                        resid=x_in, resid_rows=rows)
         self._ffn_g(blk)

@@ -153,3 +153,37 @@ def _step_scan(grid, V0, IG, FG, RG_hist, V_ring, T_buf, Y, T_max, S, L=None, HD
 
 step_gates_kernel = _Launcher(_step_gates, "step_gates_kernel")
 step_scan_kernel = _Launcher(_step_scan, "step_scan_kernel")
+
+
+def decode_attention(q, k, v, rope_cos, rope_sin, K_cache, V_cache, t_buf, y, window):
+    """One decode step of a windowed RoPE attention layer (``dh_decode_attention``).
+
+    q, k, v: (B, H*hd) projections at the device position t = t_buf[0]; K_cache/V_cache:
+    (B, H, Tmax, hd) head-major caches (row t written here); rope_cos/rope_sin: (>= Tmax, hd/2)
+    tables; y: (B, H*hd) receives softmax((q' . K) / sqrt(hd)) . V over [max(0, t+1-window), t]
+    (the whole prefix when window is 0). One launch; same rounding points as the eager step
+    (reference dispatcher_hybrid/decoding.py:247-266, :411-435).
+    """
+    _hip.require_gpu(q, "decode_attention")
+    B, H, Tmax, hd = K_cache.shape
+    dt = q.dtype
+    for name, x in (("k", k), ("v", v), ("rope_cos", rope_cos), ("rope_sin", rope_sin),
+                    ("K_cache", K_cache), ("V_cache", V_cache), ("y", y)):
+        if x.dtype != dt:
+            raise TypeError(f"decode_attention: {name} is {x.dtype}, expected {dt}")
+    for name, x in (("q", q), ("k", k), ("v", v), ("y", y)):
+        if x.shape[0] != B or x.shape[-1] != H * hd or x.stride(-1) != 1:
+            raise ValueError(f"decode_attention: {name} must be ({B}, {H * hd}) with unit inner stride")
+    if not (q.stride(0) == k.stride(0) == v.stride(0)):
+        raise ValueError("decode_attention: q, k and v need one row stride")
+    if not (K_cache.is_contiguous() and V_cache.is_contiguous() and V_cache.shape == K_cache.shape):
+        raise ValueError("decode_attention: caches must be contiguous (B, H, Tmax, hd)")
+    if not (rope_cos.is_contiguous() and rope_sin.is_contiguous()) or rope_cos.shape[0] < Tmax \
+            or rope_cos.shape[-1] != hd // 2:
+        raise ValueError("decode_attention: rope tables must be contiguous (>= Tmax, hd/2)")
+    p = _hip.ptr
+    st = _hip.lib.dh_decode_attention(
+        _hip.dtype_code(dt), p(q), p(k), p(v), q.stride(0), p(rope_cos), p(rope_sin),
+        p(K_cache), p(V_cache), p(t_buf), p(y), y.stride(0), B, H, hd, Tmax, int(window),
+        _hip.stream_handle(q.device))
+    _hip.check(st, "dh_decode_attention")

@@ -161,6 +161,25 @@ int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const int64_t* x
                    const int64_t* t_dev, int B, int K, void* stream);
 
 /*
+ * One decode step of a windowed RoPE attention layer: rotation of the new query and key at the
+ * device position t, the cache write of (k', v) at t, the scores over the window [lo, t]
+ * (lo = max(0, t+1-window), window 0 = the whole prefix), softmax and the value average, as ONE
+ * launch. Replaces the torch ops of FusedGraphedHybridDecoder._attn_step_g (reference
+ * dispatcher_hybrid/decoding.py:411-435) and matches the eager step (decoding.py:247-266).
+ *   q, k, v          (B, H*hd) projections at t, rows qkv_bstride elements apart.
+ *   rope_cos/sin     (>= Tmax, hd/2) tables in `dtype`.
+ *   K_cache/V_cache  (B, H, Tmax, hd) head-major caches, updated in place at t.
+ *   y                (B, H*hd) output rows y_bstride apart.
+ * bf16 rounds at the eager step's points (rope products and sums, scores, scaled scores, softmax
+ * output, value average); t = *t_dev outside [0, Tmax) writes nothing. hd in {16,32,64,128};
+ * the attention span min(window, Tmax) (Tmax when window is 0) at most 16384.
+ */
+int dh_decode_attention(int dtype, const void* q, const void* k, const void* v, int64_t qkv_bstride,
+                        const void* rope_cos, const void* rope_sin, void* K_cache, void* V_cache,
+                        const int64_t* t_dev, void* y, int64_t y_bstride, int B, int H, int hd, int Tmax,
+                        int window, void* stream);
+
+/*
  * The two halves of dh_decode_mixer_step as separate launches, with the reference's own buffer
  * contract, for callers that drive the Triton kernels by name.
  * dh_step_gates replaces `step_gates_kernel` (reference dispatcher_hybrid/fused_step.py:26-59):
