@@ -12,19 +12,20 @@
 // bf16 mode rounds where the eager bf16 step rounds: each rope product and sum, the q'.K matmul
 // output, its division by sqrt(hd), the softmax output and the value average.
 //
-// Work decomposition: one workgroup (16 wave64s) per (head, batch row). Pass 1 gives every thread
-// one window position at a time and the thread computes that position's full dot product from its
+// Work decomposition: one workgroup (8 wave64s) per (head, batch row). Pass 1 gives every thread
+// one window position per sweep and the thread computes that position's full dot product from its
 // key row (hd elements, contiguous in the head-major cache); the scores stay in LDS. A block
-// reduction gives the maximum and the sum of exponentials. Pass 2 splits the window over the 16
-// waves and gives each lane one head dimension (a wave reads whole value rows, 64 lanes x 2 bytes),
-// accumulating p_j V[j] in fp32; the 16 partial sums meet in LDS. The new position t is read from
-// LDS (the rotated key and the value computed in this launch), never from the cache the same
-// launch writes.
+// reduction gives the maximum and the sum of exponentials. Pass 2 splits the window over the 8
+// waves; a wave's 16-byte loads cover whole value rows (lane -> row slot, chunk of the row) and
+// accumulate p_j V[j] in fp32, then the row slots and the waves are summed. The key rows of the
+// first two sweeps and the first block of value rows are requested as soon as t is known, so the
+// launch waits for memory about twice. The new position t is taken from LDS (the rotated key and
+// the value computed in this launch), never read back from the cache the same launch writes.
 #include "dh_common.h"
 
 namespace {
 
-constexpr int kThreads = 1024;
+constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxHd = 128;
 constexpr int kMaxWindow = 16384;   // scores held in LDS (64 KB)
@@ -57,51 +58,49 @@ __device__ __forceinline__ float wave_max(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// q . row for one cache row of hd elements: the row is read in groups of up to 8 16-byte chunks
-// (all loads of a group issued before any is used), q comes from LDS as broadcast reads
-template <typename T, int HD>
-__device__ __forceinline__ float row_dot(const T* p, const float* q) {
-  constexpr int V = 16 / sizeof(T);                    // elements per chunk
-  constexpr int NC = HD / V;
-  constexpr int G = NC < 8 ? NC : 8;
-  float dot = 0.f;
-#pragma unroll
-  for (int c0 = 0; c0 < NC; c0 += G) {
-    uint4 w[G];
-#pragma unroll
-    for (int c = 0; c < G; ++c) w[c] = reinterpret_cast<const uint4*>(p)[c0 + c];
-#pragma unroll
-    for (int c = 0; c < G; ++c) {
-      const uint32_t ws[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
-      const int e = (c0 + c) * V;
-      if constexpr (sizeof(T) == 2) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          dot += q[e + 2 * j] * __uint_as_float(ws[j] << 16) + q[e + 2 * j + 1] * __uint_as_float(ws[j] & 0xffff0000u);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) dot += q[e + j] * __uint_as_float(ws[j]);
-      }
-    }
-  }
-  return dot;
-}
-
 template <typename T, int HD>
 __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) {
   extern __shared__ float sc[];                       // scores / probabilities of the window
   __shared__ float qs[kMaxHd], ks[kMaxHd], vs[kMaxHd];
   __shared__ float red[kWaves];
-  __shared__ float part[kWaves][64];
+  __shared__ float part[kWaves][kMaxHd];
+  constexpr int VE = 16 / (int)sizeof(T);             // elements per 16-byte chunk
+  constexpr int LPR = HD / VE;                        // lanes per cache row in pass 2
+  constexpr int RPI = 64 / LPR;                       // rows per wave load instruction
+  constexpr int KCH = HD / VE;                        // 16-byte chunks per cache row
+  constexpr int KP = KCH <= 8 ? 2 : 1;                // pass-1 sweeps whose key rows are prefetched
+  constexpr int CH = KCH <= 8 ? 16 : 8;               // pass-2 loads in flight per lane
   const int h = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t t = *a.t_dev;
   if (t < 0 || t >= a.Tmax) return;                   // workgroup-uniform: nothing to do
   const int lo = a.window > 0 ? (int)max((int64_t)0, t + 1 - a.window) : 0;
   const int n = (int)t - lo + 1;
+  const int nc = n - 1;                               // cached positions; index n-1 is t itself
   const int64_t head_off = ((int64_t)b * a.H + h) * a.Tmax * HD;  // (b, h) rows of the caches
   T* Kh = (T*)a.K + head_off;
   T* Vh = (T*)a.V + head_off;
+
+  // ---- requests that need only t: this thread's first key row (pass 1) and its first block of
+  // value chunks (pass 2); they fly while the new key is rotated. Rows are clamped into the cached
+  // range, so every load reads a written cache row (results past the range are discarded).
+  const int ck = nc > 0 ? nc - 1 : 0;
+  uint4 krow[KP][KCH];
+#pragma unroll
+  for (int q = 0; q < KP; ++q) {
+    const int j = lo + min(tid + q * kThreads, ck);
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) krow[q][c] = reinterpret_cast<const uint4*>(Kh + (int64_t)j * HD)[c];
+  }
+  const int per = (nc + kWaves - 1) / kWaves;
+  const int j0 = wave * per, j1 = min(nc, j0 + per);
+  const int slot = lane / LPR, dg = lane % LPR;       // row within an instruction, 16-byte chunk of the row
+  uint4 vrow[CH];
+#pragma unroll
+  for (int u = 0; u < CH; ++u) {
+    const int i = min(j0 + u * RPI + slot, ck);
+    vrow[u] = reinterpret_cast<const uint4*>(Vh + (int64_t)(lo + i) * HD)[dg];
+  }
 
   // ---- rope of q and k at position t, cache write of (k', v) at t
   if (tid < HD / 2) {
@@ -136,24 +135,47 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
 
   // ---- pass 1: scores, one position per thread per sweep. Position t (index n-1) is scored from
   // the rotated key in LDS by thread 0; the cache row this launch writes is never read back.
-  float mx = -INFINITY;
-  for (int i0 = 0; i0 < n - 1; i0 += kThreads) {
-    const int i = i0 + tid;
-    const int j = lo + min(i, n - 2);                  // clamped: every load is a cached position
-    const float dot = row_dot<T, HD>(Kh + (int64_t)j * HD, qs);
-    const float s = Elem<T>::round(Elem<T>::round(dot) / a.scale);
-    if (i < n - 1) {
-      sc[i] = s;
-      mx = fmaxf(mx, s);
+  auto score = [&](const uint4 (&w)[KCH]) {
+    float dot = 0.f;
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const uint32_t ws[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+      const int e = c * VE;
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          dot += qs[e + 2 * j] * __uint_as_float(ws[j] << 16) + qs[e + 2 * j + 1] * __uint_as_float(ws[j] & 0xffff0000u);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dot += qs[e + j] * __uint_as_float(ws[j]);
+      }
     }
+    return Elem<T>::round(Elem<T>::round(dot) / a.scale);
+  };
+  float mx = -INFINITY;
+#pragma unroll
+  for (int q = 0; q < KP; ++q) {
+    const int i = tid + q * kThreads;
+    const float s0 = score(krow[q]);
+    if (i < nc) {
+      sc[i] = s0;
+      mx = fmaxf(mx, s0);
+    }
+  }
+  for (int i = tid + KP * kThreads; i < nc; i += kThreads) {   // spans longer than the prefetch
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) krow[0][c] = reinterpret_cast<const uint4*>(Kh + (int64_t)(lo + i) * HD)[c];
+    const float s1 = score(krow[0]);
+    sc[i] = s1;
+    mx = fmaxf(mx, s1);
   }
   if (tid == 0) {
     float dot = 0.f;
 #pragma unroll
     for (int e = 0; e < HD; ++e) dot += qs[e] * ks[e];
-    const float s = Elem<T>::round(Elem<T>::round(dot) / a.scale);
-    sc[n - 1] = s;
-    mx = fmaxf(mx, s);
+    const float s2 = Elem<T>::round(Elem<T>::round(dot) / a.scale);
+    sc[n - 1] = s2;
+    mx = fmaxf(mx, s2);
   }
   mx = wave_max(mx);
   if (lane == 0) red[wave] = mx;
@@ -175,54 +197,53 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) L += red[w];
 
-  // ---- pass 2: y = sum_j p_j V[j]; wave w takes a contiguous block of the window, lane -> dims
-  constexpr int PPW = HD >= 64 ? 1 : 64 / HD;          // positions per wave iteration
-  constexpr int DPL = HD > 64 ? HD / 64 : 1;           // dims per lane
-  const int nc = n - 1;                                // cached positions; index n-1 is t
-  const int per = (nc + kWaves - 1) / kWaves;
-  const int j0 = wave * per, j1 = min(nc, j0 + per);
-  const int sub = HD >= 64 ? 0 : lane / HD;            // which of the PPW positions
-  const int e0 = HD >= 64 ? lane : lane % HD;
-  float acc[DPL];
+  // ---- pass 2: y = sum_j p_j V[j]. Wave w owns cached positions [j0, j1); a load instruction
+  // covers RPI whole rows, lane -> (row slot, 16-byte chunk); the first CH chunks are in flight.
+  float acc[VE];
 #pragma unroll
-  for (int d = 0; d < DPL; ++d) acc[d] = 0.f;
-  constexpr int U = 8 / DPL;                           // positions in flight per lane
-  for (int i0 = j0; i0 < j1; i0 += PPW * U) {
-    float vv[U][DPL], pp[U];
+  for (int e = 0; e < VE; ++e) acc[e] = 0.f;
+  auto accumulate = [&](const uint4& w, int i) {
+    if (i >= j1) return;                               // a clamped row: never folded in, even as 0 * x
+    const float p = Elem<T>::round(sc[i] / L);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    if constexpr (sizeof(T) == 2) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = i0 + u * PPW + sub;
-      const int ic = min(i, nc - 1);
-      const int j = lo + ic;
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] += p * __uint_as_float(ws[j] << 16);
+        acc[2 * j + 1] += p * __uint_as_float(ws[j] & 0xffff0000u);
+      }
+    } else {
 #pragma unroll
-      for (int d = 0; d < DPL; ++d) vv[u][d] = Elem<T>::load(Vh + (int64_t)j * HD + e0 + 64 * d);
-      pp[u] = i < j1 ? Elem<T>::round(sc[ic] / L) : 0.f;
+      for (int j = 0; j < 4; ++j) acc[j] += p * __uint_as_float(ws[j]);
     }
+  };
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+  for (int u = 0; u < CH; ++u) accumulate(vrow[u], j0 + u * RPI + slot);
+  for (int i0 = j0 + CH * RPI; i0 < j1; i0 += CH * RPI) {   // blocks longer than CH instructions
 #pragma unroll
-      for (int d = 0; d < DPL; ++d) acc[d] += pp[u] * vv[u][d];
+    for (int u = 0; u < CH; ++u)
+      vrow[u] = reinterpret_cast<const uint4*>(Vh + (int64_t)(lo + min(i0 + u * RPI + slot, ck)) * HD)[dg];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) accumulate(vrow[u], i0 + u * RPI + slot);
   }
-  // lanes of one wave that hold the same dimension (HD < 64) are summed first
+  // sum the RPI row slots of the wave (lanes dg, dg + LPR, ...), then the 16 waves in LDS
 #pragma unroll
-  for (int d = 0; d < DPL; ++d) {
-    float v = acc[d];
-    if (HD < 64) {
+  for (int e = 0; e < VE; ++e) {
+    float v = acc[e];
 #pragma unroll
-      for (int off = HD; off < 64; off <<= 1) v += __shfl_xor(v, off);
-    }
-    acc[d] = v;
+    for (int off = LPR; off < 64; off <<= 1) v += __shfl_xor(v, off);
+    acc[e] = v;
   }
-  for (int d = 0; d < DPL; ++d) {
-    __syncthreads();
-    if (lane < HD || HD > 64) part[wave][lane] = acc[d];
-    __syncthreads();
-    if (wave == 0 && (HD >= 64 || lane < HD)) {
-      float s = Elem<T>::round(sc[n - 1] / L) * vs[lane + 64 * d];      // position t
+  if (slot == 0) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) s += part[w][lane];
-      Elem<T>::store((T*)a.y + (int64_t)b * a.y_bstride + (int64_t)h * HD + lane + 64 * d, s);
-    }
+    for (int e = 0; e < VE; ++e) part[wave][dg * VE + e] = acc[e];
+  }
+  __syncthreads();
+  if (tid < HD) {
+    float s = Elem<T>::round(sc[n - 1] / L) * vs[tid];      // position t
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) s += part[w][tid];
+    Elem<T>::store((T*)a.y + (int64_t)b * a.y_bstride + (int64_t)h * HD + tid, s);
   }
 }
 
