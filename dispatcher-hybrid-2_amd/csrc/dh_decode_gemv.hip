@@ -12,13 +12,16 @@
 // of the eager torch step (reference dispatcher_hybrid/decoding.py:473-476 and :487-488,
 // dispatcher_hybrid/modeling_dispatcher.py:196-197, 207-212, 348-351).
 //
-// Work decomposition: 256-thread workgroups (4 wave64s); each wave owns R consecutive output rows
-// and every lane owns the same CG 16-byte chunks of K in each of them, so all of a wave's weight
-// bytes are requested by one burst of loads issued before anything else (no load is guarded by a
-// divergent branch: addresses are clamped and predicates applied to values). The activations x are
-// staged once per workgroup in LDS, the RMSNorm scale comes from one wave-level reduction per row,
-// and each (row, batch row) dot product is finished with a butterfly shuffle reduction, after which
-// every lane holds every sum and lane j writes output j.
+// Work decomposition: every wave works alone (no LDS, no barriers). A wave owns R consecutive
+// output rows; lane l owns the 16-byte chunks l, l+64, ... of K in each of them and loads its
+// weight chunks, the matching chunks of the activation rows and of the RMSNorm weight straight
+// from memory, all before any arithmetic (no load is guarded by a divergent branch: addresses are
+// clamped and predicates applied to values). Since the wave's lanes cover the whole row, the wave
+// computes the RMSNorm sum of squares itself with one DPP wave reduction, then each (row, batch
+// row) dot product with another; every lane then holds every sum and lane j writes output j. R is
+// 1 except for very tall matrices, so a launch keeps several thousand waves, and their loads, in
+// flight: for these small matrices the time is set by how many loads are outstanding, not by the
+// bytes.
 #include "dh_common.h"
 
 namespace {
@@ -26,10 +29,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxSeg = 3;
-constexpr int kBP = 4;          // batch rows per accumulation pass
-constexpr int kMaxBch = 64;     // batch rows staged in LDS at once
-constexpr int kLdsBytes = 64 * 1024;
-constexpr int kXU = 4;          // activation chunks in flight per thread while staging
 
 struct Seg {
   const void* W;
@@ -51,7 +50,7 @@ struct GemvArgs {
   const int64_t* t_dev;         // device position (always a valid pointer)
   Seg seg[kMaxSeg];
   int nseg;
-  int B, K, Nrows, bch;
+  int B, K, Nrows;
 };
 
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
@@ -91,20 +90,18 @@ template <> struct Raw<float> {
   __device__ __forceinline__ static float f(uint32_t r) { return __uint_as_float(r); }
 };
 
-template <typename T, int R, int CG, bool SW>
+template <typename T, int R, int CG, int BG, bool SW>
 __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  T* xs = reinterpret_cast<T*>(smem);                 // staged activations [bch][K]
-  __shared__ float rscale[kMaxBch];
   constexpr int V = Vec<T>::N;
   constexpr int NW = SW ? 2 : 1;                      // weight rows per output row
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int K = a.K, B = a.B;
   const int nchunk = K / V;
   const bool has_norm = a.g != nullptr;
+  const int rbase = (blockIdx.x * kWaves + wave) * R;
+  if (rbase >= a.Nrows) return;                       // wave-uniform, and no barrier follows
 
   // ---- weights: every load of the wave in one burst
-  const int rbase = (blockIdx.x * kWaves + wave) * R;
   const T* wrow[R][NW];
   int segi[R];
   int local[R];
@@ -137,139 +134,116 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
     for (int c = 0; c < CG; ++c) gv[c] = ld16((const T*)a.g + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
   }
   const int64_t t = *a.t_dev;
-  // residual operand of the output this lane writes in the first pass (output j = lane: row j % R,
-  // batch row j / R), fetched with the weights; later passes (B > kBP) load theirs in the epilogue
   const bool has_resid = a.resid != nullptr;
-  uint32_t resid_raw = 0;
-  if (has_resid) {                                     // uniform
-    const int b = min(lane / R, B - 1);
-    const int n = min(rbase + lane % R, a.Nrows - 1);
-    const int64_t rrow = a.resid_rows ? a.resid_rows[b] : (int64_t)b;
-    resid_raw = Raw<T>::load((const T*)a.resid + rrow * a.resid_bstride + n);
-  }
 
-  for (int bb = 0; bb < B; bb += a.bch) {
-    const int nb = min(a.bch, B - bb);
-    // ---- stage x rows [bb, bb + nb) in LDS (gathered through x_rows when given)
-    for (int i0 = 0; i0 < nb * nchunk; i0 += kThreads * kXU) {
-      uint4 xr[kXU];
+  for (int b0 = 0; b0 < B; b0 += BG) {
+    // ---- activation chunks of BG batch rows (gathered through x_rows when given) and the residual
+    // operand of the output this lane writes (output j = lane: row j % R, batch row b0 + j / R)
+    uint4 xv[BG][CG];
 #pragma unroll
-      for (int u = 0; u < kXU; ++u) {
-        const int i = min(i0 + tid + u * kThreads, nb * nchunk - 1);
-        const int rr = i / nchunk, kc = i % nchunk;
-        const int64_t xrow = a.x_rows ? a.x_rows[bb + rr] : (int64_t)(bb + rr);
-        xr[u] = ld16((const T*)a.x + xrow * a.x_bstride + (int64_t)kc * V);
-      }
+    for (int bp = 0; bp < BG; ++bp) {
+      const int b = min(b0 + bp, B - 1);
+      const int64_t xrow = a.x_rows ? a.x_rows[b] : (int64_t)b;
+      const T* xp = (const T*)a.x + xrow * a.x_bstride;
 #pragma unroll
-      for (int u = 0; u < kXU; ++u) {
-        const int i = i0 + tid + u * kThreads;
-        if (i < nb * nchunk) *reinterpret_cast<uint4*>(xs + (int64_t)i * V) = xr[u];
-      }
+      for (int c = 0; c < CG; ++c) xv[bp][c] = ld16(xp + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
     }
-    __syncthreads();
-    // ---- RMSNorm scale per staged row: one wave per row
-    if (has_norm) {
-      for (int rr = wave; rr < nb; rr += kWaves) {
+    uint32_t resid_raw = 0;
+    if (has_resid) {                                   // uniform
+      const int b = min(b0 + lane / R, B - 1);
+      const int n = min(rbase + lane % R, a.Nrows - 1);
+      const int64_t rrow = a.resid_rows ? a.resid_rows[b] : (int64_t)b;
+      resid_raw = Raw<T>::load((const T*)a.resid + rrow * a.resid_bstride + n);
+    }
+    // ---- RMSNorm scale of each batch row: the wave's lanes cover the whole row
+    float rs[BG];
+#pragma unroll
+    for (int bp = 0; bp < BG; ++bp) {
+      rs[bp] = 1.f;
+      if (has_norm) {
         float ss = 0.f;
-        for (int k = lane; k < K; k += 64) {
-          const float v = Elem<T>::load(xs + (int64_t)rr * K + k);
-          ss += v * v;
+#pragma unroll
+        for (int c = 0; c < CG; ++c) {
+          float xf[V];
+          Vec<T>::unpack(xv[bp][c], xf);
+          float part = 0.f;
+#pragma unroll
+          for (int e = 0; e < V; ++e) part += xf[e] * xf[e];
+          ss += lane + 64 * c < nchunk ? part : 0.f;
         }
-        ss = wave_sum(ss);
-        if (lane == 0) rscale[rr] = rsqrtf(ss / (float)K + a.eps);
-      }
-      __syncthreads();
-    }
-    // ---- dot products, kBP batch rows per pass
-    for (int b0 = 0; b0 < nb; b0 += kBP) {
-      float acc[R][NW][kBP];
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int q = 0; q < NW; ++q)
-#pragma unroll
-          for (int bp = 0; bp < kBP; ++bp) acc[r][q][bp] = 0.f;
-#pragma unroll
-      for (int c = 0; c < CG; ++c) {
-        const int chr = lane + 64 * c;
-        const bool live = chr < nchunk;
-        const int ch = min(chr, nchunk - 1);
-        float gw[V];
-        if (has_norm) Vec<T>::unpack(gv[c], gw);
-#pragma unroll
-        for (int bp = 0; bp < kBP; ++bp) {
-          if (b0 + bp < nb) {                          // uniform
-            float hv[V];
-            Vec<T>::unpack(*reinterpret_cast<const uint4*>(xs + ((int64_t)(b0 + bp) * K) + (int64_t)ch * V), hv);
-            if (has_norm) {
-              const float rs = rscale[b0 + bp];
-#pragma unroll
-              for (int e = 0; e < V; ++e) hv[e] = Elem<T>::round(hv[e] * rs * gw[e]);
-            }
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-              for (int q = 0; q < NW; ++q) {
-                float wv[V];
-                Vec<T>::unpack(w[r][q][c], wv);
-                float s = 0.f;
-#pragma unroll
-                for (int e = 0; e < V; ++e) s += wv[e] * hv[e];
-                acc[r][q][bp] += live ? s : 0.f;
-              }
-          }
-        }
-      }
-      // butterfly reduction: every lane ends with every (row, batch row) sum
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int q = 0; q < NW; ++q)
-#pragma unroll
-          for (int bp = 0; bp < kBP; ++bp) acc[r][q][bp] = wave_sum(acc[r][q][bp]);
-      // epilogue: lane j writes output (row j % R, batch row b0 + j / R)
-      const int r = lane % R, bp = lane / R;
-      if (bp < kBP && b0 + bp < nb && rbase + r < a.Nrows) {
-        float v0 = 0.f, v1 = 0.f;
-#pragma unroll
-        for (int rr = 0; rr < R; ++rr)
-#pragma unroll
-          for (int pp = 0; pp < kBP; ++pp)
-            if (rr == r && pp == bp) {
-              v0 = acc[rr][0][pp];
-              v1 = acc[rr][NW - 1][pp];
-            }
-        float out;
-        if (SW) {
-          out = Elem<T>::round(Elem<T>::round(silu(Elem<T>::round(v0))) * Elem<T>::round(v1));
-        } else {
-          out = Elem<T>::round(v0);
-          if (has_resid) {
-            const int64_t b = bb + b0 + bp;
-            float rv;
-            if (bb == 0 && b0 == 0) {
-              rv = Raw<T>::f(resid_raw);
-            } else {
-              const int64_t rrow = a.resid_rows ? a.resid_rows[b] : b;
-              rv = Elem<T>::load((const T*)a.resid + rrow * a.resid_bstride + rbase + r);
-            }
-            out = Elem<T>::round(out + rv);
-          }
-        }
-        int s = 0;
-        int loc = 0;
-#pragma unroll
-        for (int rr = 0; rr < R; ++rr)
-          if (rr == r) {
-            s = segi[rr];
-            loc = local[rr];
-          }
-        const Seg& sg = a.seg[s];
-        const int64_t b = bb + b0 + bp;
-        Elem<T>::store((T*)sg.out + b * sg.out_bstride + t * sg.t_stride + loc, out);
+        rs[bp] = rsqrtf(wave_sum(ss) / (float)K + a.eps);
       }
     }
-    __syncthreads();                                   // xs / rscale reused by the next chunk
+    // ---- dot products
+    float acc[R][NW][BG];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int q = 0; q < NW; ++q)
+#pragma unroll
+        for (int bp = 0; bp < BG; ++bp) acc[r][q][bp] = 0.f;
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+      const bool live = lane + 64 * c < nchunk;
+      float gw[V];
+      if (has_norm) Vec<T>::unpack(gv[c], gw);
+#pragma unroll
+      for (int bp = 0; bp < BG; ++bp) {
+        float hv[V];
+        Vec<T>::unpack(xv[bp][c], hv);
+        if (has_norm) {
+#pragma unroll
+          for (int e = 0; e < V; ++e) hv[e] = Elem<T>::round(hv[e] * rs[bp] * gw[e]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int q = 0; q < NW; ++q) {
+            float wv[V];
+            Vec<T>::unpack(w[r][q][c], wv);
+            float sdot = 0.f;
+#pragma unroll
+            for (int e = 0; e < V; ++e) sdot += wv[e] * hv[e];
+            acc[r][q][bp] += live ? sdot : 0.f;
+          }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int q = 0; q < NW; ++q)
+#pragma unroll
+        for (int bp = 0; bp < BG; ++bp) acc[r][q][bp] = wave_sum(acc[r][q][bp]);
+    // ---- epilogue: lane j writes output (row j % R, batch row b0 + j / R)
+    const int r = lane % R, bp = lane / R;
+    if (bp < BG && b0 + bp < B && rbase + r < a.Nrows) {
+      float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+      for (int rr = 0; rr < R; ++rr)
+#pragma unroll
+        for (int pp = 0; pp < BG; ++pp)
+          if (rr == r && pp == bp) {
+            v0 = acc[rr][0][pp];
+            v1 = acc[rr][NW - 1][pp];
+          }
+      float out;
+      if (SW) {
+        out = Elem<T>::round(Elem<T>::round(silu(Elem<T>::round(v0))) * Elem<T>::round(v1));
+      } else {
+        out = Elem<T>::round(v0);
+        if (has_resid) out = Elem<T>::round(out + Raw<T>::f(resid_raw));
+      }
+      int s = 0, loc = 0;
+#pragma unroll
+      for (int rr = 0; rr < R; ++rr)
+        if (rr == r) {
+          s = segi[rr];
+          loc = local[rr];
+        }
+      const Seg& sg = a.seg[s];
+      const int64_t b = b0 + bp;
+      Elem<T>::store((T*)sg.out + b * sg.out_bstride + t * sg.t_stride + loc, out);
+    }
   }
 }
 
@@ -277,15 +251,23 @@ template <typename T, int R, int CG, bool SW>
 void launch(const GemvArgs& a, hipStream_t s) {
   const int rows_per_block = kWaves * R;
   const int grid = (a.Nrows + rows_per_block - 1) / rows_per_block;
-  const size_t lds = (size_t)a.bch * a.K * sizeof(T);
-  decode_gemv_kernel<T, R, CG, SW><<<dim3(grid), dim3(kThreads), lds, s>>>(a);
+  // batch rows per pass: as many as the activation chunks' registers allow
+  constexpr int BG = CG <= 2 ? 8 : (CG <= 6 ? 4 : 2);
+  if (a.B == 1)
+    decode_gemv_kernel<T, R, CG, 1, SW><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
+  else
+    decode_gemv_kernel<T, R, CG, BG, SW><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
 }
 
 template <typename T, int CG, bool SW>
 void pick_r(const GemvArgs& a, int R, hipStream_t s) {
-  if (R >= 4 && !SW) launch<T, 4, CG, SW>(a, s);
-  else if (R >= 2) launch<T, 2, CG, SW>(a, s);
-  else launch<T, 1, CG, SW>(a, s);
+  if constexpr (!SW) {
+    if (R >= 4) {
+      launch<T, 4, CG, SW>(a, s);
+      return;
+    }
+  }
+  launch<T, 1, CG, SW>(a, s);
 }
 
 template <typename T, bool SW>
@@ -344,15 +326,11 @@ extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const
     total = N[0];
   }
   a.Nrows = total;
-  const size_t esz = dtype == DH_BF16 ? 2 : 4;
-  int bch = (int)(kLdsBytes / ((size_t)K * esz));
-  bch = bch > kMaxBch ? kMaxBch : bch;
-  DH_REQUIRE(bch >= 1, DH_ERR_UNSUPPORTED_SHAPE, "%s: K=%d too large to stage one row in LDS", who, K);
-  a.bch = bch < B ? bch : B;
   const int C = (K / vec + 63) / 64;
   DH_REQUIRE(C <= 12, DH_ERR_UNSUPPORTED_SHAPE, "%s: K=%d exceeds %d elements per row", who, K, 12 * 64 * vec);
-  // rows per wave: enough workgroups to cover the chip, more bytes per wave when rows abound
-  const int R = a.Nrows >= 16384 ? 4 : (a.Nrows >= 2048 ? 2 : 1);
+  // one output row per wave, except for very tall matrices (the vocabulary head), where four rows
+  // per wave still leave > 12k waves
+  const int R = a.Nrows >= 16384 ? 4 : 1;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DH_BF16) {
     if (swiglu) pick_cg<bf16_t, true>(a, C, R, s); else pick_cg<bf16_t, false>(a, C, R, s);
