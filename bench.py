@@ -79,9 +79,11 @@ def time_decode(torch, model, batch, prompt, warmup, steps, sample):
     logits = dec.prefill(ids)[:, -1]
     torch.manual_seed(5)
 
+    from dispatcher_hybrid import fused_step
+
     def next_tok(lg):
         if not sample:
-            return lg.argmax(-1)
+            return fused_step.argmax_tokens(lg)           # device argmax (same token as torch's)
         lg = lg.float() / 0.8
         kth = torch.topk(lg, 50, dim=-1).values[:, -1:]
         lg = lg.masked_fill(lg < kth, float("-inf"))

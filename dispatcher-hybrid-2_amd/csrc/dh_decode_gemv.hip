@@ -136,25 +136,39 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
   const int64_t t = *a.t_dev;
   const bool has_resid = a.resid != nullptr;
 
-  for (int b0 = 0; b0 < B; b0 += BG) {
-    // ---- activation chunks of BG batch rows (gathered through x_rows when given) and the residual
-    // operand of the output this lane writes (output j = lane: row j % R, batch row b0 + j / R)
-    uint4 xv[BG][CG];
+  // activation chunks of BG batch rows (gathered through x_rows when given) and the residual
+  // operand of the output this lane writes (output j = lane: row j % R, batch row b0 + j / R).
+  // The first group is requested in the same burst as the weights and each later group while the
+  // previous one is computed, so no load waits for another one (the weight unpacking, which the
+  // compiler hoists out of the batch loop, comes after these requests).
+  uint4 xv[BG][CG];
+  uint32_t resid_raw = 0;
+  auto fetch_group = [&](int g0) {
 #pragma unroll
     for (int bp = 0; bp < BG; ++bp) {
-      const int b = min(b0 + bp, B - 1);
+      const int b = min(g0 + bp, B - 1);
       const int64_t xrow = a.x_rows ? a.x_rows[b] : (int64_t)b;
       const T* xp = (const T*)a.x + xrow * a.x_bstride;
 #pragma unroll
       for (int c = 0; c < CG; ++c) xv[bp][c] = ld16(xp + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
     }
-    uint32_t resid_raw = 0;
     if (has_resid) {                                   // uniform
-      const int b = min(b0 + lane / R, B - 1);
+      const int b = min(g0 + lane / R, B - 1);
       const int n = min(rbase + lane % R, a.Nrows - 1);
       const int64_t rrow = a.resid_rows ? a.resid_rows[b] : (int64_t)b;
       resid_raw = Raw<T>::load((const T*)a.resid + rrow * a.resid_bstride + n);
     }
+  };
+  fetch_group(0);
+
+  for (int b0 = 0; b0 < B; b0 += BG) {
+    uint4 xc[BG][CG];
+#pragma unroll
+    for (int bp = 0; bp < BG; ++bp)
+#pragma unroll
+      for (int c = 0; c < CG; ++c) xc[bp][c] = xv[bp][c];
+    const uint32_t rc = resid_raw;
+    if (b0 + BG < B) fetch_group(b0 + BG);             // uniform; used in the next iteration
     // ---- RMSNorm scale of each batch row: the wave's lanes cover the whole row
     float rs[BG];
 #pragma unroll
@@ -165,7 +179,7 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int c = 0; c < CG; ++c) {
           float xf[V];
-          Vec<T>::unpack(xv[bp][c], xf);
+          Vec<T>::unpack(xc[bp][c], xf);
           float part = 0.f;
 #pragma unroll
           for (int e = 0; e < V; ++e) part += xf[e] * xf[e];
@@ -190,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int bp = 0; bp < BG; ++bp) {
         float hv[V];
-        Vec<T>::unpack(xv[bp][c], hv);
+        Vec<T>::unpack(xc[bp][c], hv);
         if (has_norm) {
 #pragma unroll
           for (int e = 0; e < V; ++e) hv[e] = Elem<T>::round(hv[e] * rs[bp] * gw[e]);
@@ -231,7 +245,7 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
         out = Elem<T>::round(Elem<T>::round(silu(Elem<T>::round(v0))) * Elem<T>::round(v1));
       } else {
         out = Elem<T>::round(v0);
-        if (has_resid) out = Elem<T>::round(out + Raw<T>::f(resid_raw));
+        if (has_resid) out = Elem<T>::round(out + Raw<T>::f(rc));
       }
       int s = 0, loc = 0;
 #pragma unroll

@@ -187,3 +187,21 @@ def decode_attention(q, k, v, rope_cos, rope_sin, K_cache, V_cache, t_buf, y, wi
         p(K_cache), p(V_cache), p(t_buf), p(y), y.stride(0), B, H, hd, Tmax, int(window),
         _hip.stream_handle(q.device))
     _hip.check(st, "dh_decode_attention")
+
+
+def argmax_tokens(logits, out=None):
+    """Greedy next tokens on the device (``dh_argmax``): out[b] = logits[b].argmax() as int64,
+    first index on ties, NaN above every number (torch.argmax's rule). logits: (B, V) fp32 or bf16
+    with a unit inner stride; returns `out` (allocated when None)."""
+    _hip.require_gpu(logits, "argmax_tokens")
+    if logits.dim() != 2 or logits.stride(-1) != 1:
+        raise ValueError("argmax_tokens: logits must be (B, V) with a unit inner stride")
+    B, V = logits.shape
+    if out is None:
+        out = torch.empty(B, dtype=torch.long, device=logits.device)
+    if out.dtype != torch.long or out.numel() != B or not out.is_contiguous():
+        raise ValueError("argmax_tokens: out must be a contiguous int64 tensor of B elements")
+    st = _hip.lib.dh_argmax(_hip.dtype_code(logits.dtype), _hip.ptr(logits), logits.stride(0), B, V,
+                            _hip.ptr(out), _hip.stream_handle(logits.device))
+    _hip.check(st, "dh_argmax")
+    return out

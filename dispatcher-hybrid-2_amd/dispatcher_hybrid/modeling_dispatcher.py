@@ -442,15 +442,23 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
         logits = dec.prefill(ids)[:, -1]                     # ids is 2-D: (B, T, V) -> (B, V)
         finished = torch.zeros(Bb, dtype=torch.bool, device=ids.device)
         out = [ids]
+        # greedy picks through the fused decoder take the device argmax kernel: a positive
+        # temperature and top-k masking never move the maximum, so the tokens are the same
+        device_argmax = None
+        if not do_sample and isinstance(dec, FusedGraphedHybridDecoder):
+            device_argmax = dec._fused_step.argmax_tokens
         for _ in range(max_new_tokens):
-            logits = logits.float() / max(temperature, 1e-6)
-            if top_k is not None:
-                kth = torch.topk(logits, top_k, dim=-1).values[:, -1:]
-                logits = logits.masked_fill(logits < kth, float("-inf"))
-            if do_sample:
-                nxt = torch.multinomial(F.softmax(logits, dim=-1), 1)[:, 0]
+            if device_argmax is not None:
+                nxt = device_argmax(logits)
             else:
-                nxt = logits.argmax(-1)
+                logits = logits.float() / max(temperature, 1e-6)
+                if top_k is not None:
+                    kth = torch.topk(logits, top_k, dim=-1).values[:, -1:]
+                    logits = logits.masked_fill(logits < kth, float("-inf"))
+                if do_sample:
+                    nxt = torch.multinomial(F.softmax(logits, dim=-1), 1)[:, 0]
+                else:
+                    nxt = logits.argmax(-1)
             if eos_token_id is not None:
                 nxt = torch.where(finished, torch.full_like(nxt, eos_token_id), nxt)
                 finished = finished | (nxt == eos_token_id)

@@ -180,6 +180,14 @@ int dh_decode_attention(int dtype, const void* q, const void* k, const void* v, 
                         int window, void* stream);
 
 /*
+ * Greedy next token: out[b] = argmax over row b of logits (B rows of V, rows row_stride elements
+ * apart), as torch.argmax: first index of the maximum, NaN above every number. Replaces the
+ * torch argmax of fast_generate's greedy branch (reference dispatcher_hybrid/modeling_dispatcher.py
+ * :426-441) with one launch whose output can be fed back as the decoder's next tokens. V <= 65536.
+ */
+int dh_argmax(int dtype, const void* logits, int64_t row_stride, int B, int V, int64_t* out, void* stream);
+
+/*
  * The two halves of dh_decode_mixer_step as separate launches, with the reference's own buffer
  * contract, for callers that drive the Triton kernels by name.
  * dh_step_gates replaces `step_gates_kernel` (reference dispatcher_hybrid/fused_step.py:26-59):
