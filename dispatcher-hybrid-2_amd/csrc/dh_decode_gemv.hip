@@ -58,6 +58,12 @@ __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<
 template <typename T> struct Vec;
 template <> struct Vec<bf16_t> {
   static constexpr int N = 8;
+  __device__ __forceinline__ static uint4 pack(const float (&o)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = (uint32_t)f32_to_bf16(o[2 * j]) | ((uint32_t)f32_to_bf16(o[2 * j + 1]) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
   __device__ __forceinline__ static void unpack(const uint4& v, float (&o)[8]) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -69,6 +75,9 @@ template <> struct Vec<bf16_t> {
 };
 template <> struct Vec<float> {
   static constexpr int N = 4;
+  __device__ __forceinline__ static uint4 pack(const float (&o)[4]) {
+    return make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3]));
+  }
   __device__ __forceinline__ static void unpack(const uint4& v, float (&o)[4]) {
     o[0] = __uint_as_float(v.x);
     o[1] = __uint_as_float(v.y);
@@ -261,10 +270,188 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
   }
 }
 
+// Batched variant (B > 1): the workgroup normalises each activation row ONCE into LDS (wave w takes
+// rows w, w + 4, ...; one barrier), then every wave runs its rows' dot products against the staged
+// rows. Same loads-first order: the weight burst is issued before the staging.
+template <typename T, int R, int CG, bool SW>
+__global__ __launch_bounds__(kThreads) void decode_gemv_staged_kernel(GemvArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* hs = reinterpret_cast<T*>(smem);                 // [B][nchunk * V] staged (normalised) rows
+  constexpr int V = Vec<T>::N;
+  constexpr int NW = SW ? 2 : 1;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int K = a.K, B = a.B;
+  const int nchunk = K / V;
+  const bool has_norm = a.g != nullptr;
+  const int rbase = (blockIdx.x * kWaves + wave) * R;
+
+  const T* wrow[R][NW];
+  int segi[R];
+  int local[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = min(rbase + r, a.Nrows - 1);
+    int s = 0, n0 = 0;
+    if (!SW) {
+#pragma unroll
+      for (int q = 0; q < kMaxSeg - 1; ++q)
+        if (q + 1 < a.nseg && n - n0 >= a.seg[s].N) { n0 += a.seg[s].N; ++s; }
+    }
+    segi[r] = s;
+    local[r] = n - n0;
+    wrow[r][0] = (const T*)a.seg[s].W + (int64_t)local[r] * K;
+    if (SW) wrow[r][NW - 1] = (const T*)a.seg[1].W + (int64_t)local[r] * K;
+  }
+  uint4 w[R][NW][CG];
+#pragma unroll
+  for (int c = 0; c < CG; ++c) {
+    const int ch = min(lane + 64 * c, nchunk - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int q = 0; q < NW; ++q) w[r][q][c] = ld16(wrow[r][q] + (int64_t)ch * V);
+  }
+  uint4 gv[CG];
+  if (has_norm) {
+#pragma unroll
+    for (int c = 0; c < CG; ++c) gv[c] = ld16((const T*)a.g + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
+  }
+  const int64_t t = *a.t_dev;
+
+  // ---- staging: wave w normalises rows w, w + 4, ... (its lanes cover the row's chunks)
+  for (int b = wave; b < B; b += kWaves) {
+    const int64_t xrow = a.x_rows ? a.x_rows[b] : (int64_t)b;
+    const T* xp = (const T*)a.x + xrow * a.x_bstride;
+    uint4 xv[CG];
+#pragma unroll
+    for (int c = 0; c < CG; ++c) xv[c] = ld16(xp + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
+    float rs = 1.f;
+    if (has_norm) {
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < CG; ++c) {
+        float xf[V];
+        Vec<T>::unpack(xv[c], xf);
+        float part = 0.f;
+#pragma unroll
+        for (int e = 0; e < V; ++e) part += xf[e] * xf[e];
+        ss += lane + 64 * c < nchunk ? part : 0.f;
+      }
+      rs = rsqrtf(wave_sum(ss) / (float)K + a.eps);
+    }
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+      const int ch = lane + 64 * c;
+      if (ch < nchunk) {
+        uint4 hv = xv[c];
+        if (has_norm) {
+          float xf[V], gw[V];
+          Vec<T>::unpack(xv[c], xf);
+          Vec<T>::unpack(gv[c], gw);
+#pragma unroll
+          for (int e = 0; e < V; ++e) xf[e] = xf[e] * rs * gw[e];
+          hv = Vec<T>::pack(xf);
+        }
+        *reinterpret_cast<uint4*>(hs + ((int64_t)b * nchunk + ch) * V) = hv;
+      }
+    }
+  }
+  __syncthreads();
+  if (rbase >= a.Nrows) return;                       // after the barrier: every wave staged its rows
+
+  // ---- dot products from the staged rows, four batch rows at a time
+  constexpr int BG = 4;
+  for (int b0 = 0; b0 < B; b0 += BG) {
+    const bool has_resid = a.resid != nullptr;
+    uint32_t rc = 0;
+    if (has_resid) {
+      const int b = min(b0 + lane / R, B - 1);
+      const int n = min(rbase + lane % R, a.Nrows - 1);
+      const int64_t rrow = a.resid_rows ? a.resid_rows[b] : (int64_t)b;
+      rc = Raw<T>::load((const T*)a.resid + rrow * a.resid_bstride + n);
+    }
+    float acc[R][NW][BG];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int q = 0; q < NW; ++q)
+#pragma unroll
+        for (int bp = 0; bp < BG; ++bp) acc[r][q][bp] = 0.f;
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+      const int chr = lane + 64 * c;
+      const bool live = chr < nchunk;
+      const int ch = min(chr, nchunk - 1);
+#pragma unroll
+      for (int bp = 0; bp < BG; ++bp) {
+        const int b = min(b0 + bp, B - 1);
+        float hv[V];
+        Vec<T>::unpack(*reinterpret_cast<const uint4*>(hs + ((int64_t)b * nchunk + ch) * V), hv);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int q = 0; q < NW; ++q) {
+            float wv[V];
+            Vec<T>::unpack(w[r][q][c], wv);
+            float sdot = 0.f;
+#pragma unroll
+            for (int e = 0; e < V; ++e) sdot += wv[e] * hv[e];
+            acc[r][q][bp] += live ? sdot : 0.f;
+          }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int q = 0; q < NW; ++q)
+#pragma unroll
+        for (int bp = 0; bp < BG; ++bp) acc[r][q][bp] = wave_sum(acc[r][q][bp]);
+    const int r = lane % R, bp = lane / R;
+    if (bp < BG && b0 + bp < B && rbase + r < a.Nrows) {
+      float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+      for (int rr = 0; rr < R; ++rr)
+#pragma unroll
+        for (int pp = 0; pp < BG; ++pp)
+          if (rr == r && pp == bp) {
+            v0 = acc[rr][0][pp];
+            v1 = acc[rr][NW - 1][pp];
+          }
+      float out;
+      if (SW) {
+        out = Elem<T>::round(Elem<T>::round(silu(Elem<T>::round(v0))) * Elem<T>::round(v1));
+      } else {
+        out = Elem<T>::round(v0);
+        if (has_resid) out = Elem<T>::round(out + Raw<T>::f(rc));
+      }
+      int s = 0, loc = 0;
+#pragma unroll
+      for (int rr = 0; rr < R; ++rr)
+        if (rr == r) {
+          s = segi[rr];
+          loc = local[rr];
+        }
+      const Seg& sg = a.seg[s];
+      const int64_t b = b0 + bp;
+      Elem<T>::store((T*)sg.out + b * sg.out_bstride + t * sg.t_stride + loc, out);
+    }
+  }
+}
+
+constexpr int kStageBytes = 96 * 1024;                 // LDS for staged batch rows
+
 template <typename T, int R, int CG, bool SW>
 void launch(const GemvArgs& a, hipStream_t s) {
   const int rows_per_block = kWaves * R;
   const int grid = (a.Nrows + rows_per_block - 1) / rows_per_block;
+  const size_t stage = (size_t)a.B * a.K * sizeof(T);
+  if (a.B > 1 && stage <= (size_t)kStageBytes) {
+    if (stage > 64 * 1024)   // past the default dynamic LDS limit (gfx950 has 160 KB per CU)
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_gemv_staged_kernel<T, R, CG, SW>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kStageBytes);
+    decode_gemv_staged_kernel<T, R, CG, SW><<<dim3(grid), dim3(kThreads), stage, s>>>(a);
+    return;
+  }
   // batch rows per pass: as many as the activation chunks' registers allow
   constexpr int BG = CG <= 2 ? 8 : (CG <= 6 ? 4 : 2);
   if (a.B == 1)
@@ -281,14 +468,15 @@ void pick_r(const GemvArgs& a, int R, hipStream_t s) {
       return;
     }
   }
-  launch<T, 1, CG, SW>(a, s);
+  if (R >= 2) launch<T, 2, CG, SW>(a, s);
+  else launch<T, 1, CG, SW>(a, s);
 }
 
 template <typename T, bool SW>
 void pick_cg(const GemvArgs& a, int C, int R, hipStream_t s) {
   if (C <= 2) pick_r<T, 2, SW>(a, R, s);
   else if (C <= 4) pick_r<T, 4, SW>(a, R, s);
-  else if (C <= 6) pick_r<T, 6, SW>(a, 1, s);
+  else if (C <= 6) pick_r<T, 6, SW>(a, R < 2 ? R : 2, s);
   else pick_r<T, 12, SW>(a, 1, s);
 }
 
@@ -344,7 +532,9 @@ extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const
   DH_REQUIRE(C <= 12, DH_ERR_UNSUPPORTED_SHAPE, "%s: K=%d exceeds %d elements per row", who, K, 12 * 64 * vec);
   // one output row per wave, except for very tall matrices (the vocabulary head), where four rows
   // per wave still leave > 12k waves
-  const int R = a.Nrows >= 16384 ? 4 : 1;
+  // batched calls stage the rows once per workgroup and reuse each weight chunk across all of
+  // them, so more rows per wave pay off there
+  const int R = a.Nrows >= 16384 || (B > 1 && a.Nrows >= 2048) ? 4 : (B > 1 ? 2 : 1);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DH_BF16) {
     if (swiglu) pick_cg<bf16_t, true>(a, C, R, s); else pick_cg<bf16_t, false>(a, C, R, s);

@@ -136,7 +136,7 @@ def test_embedding_gather_rows(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("B", [1, 16])
+@pytest.mark.parametrize("B", [1, 2, 16])
 def test_down_projection_release_shape(B, dtype):
     """linear_down of the released model: K = 2816 (the widest K per lane), residual in place."""
     from dispatcher_hybrid import fused_step
