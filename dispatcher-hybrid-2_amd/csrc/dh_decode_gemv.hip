@@ -108,7 +108,8 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
   const int nchunk = K / V;
   const bool has_norm = a.g != nullptr;
   const int rbase = (blockIdx.x * kWaves + wave) * R;
-  if (rbase >= a.Nrows) return;                       // wave-uniform, and no barrier follows
+  // (no early exit for waves past the last row: a branch here would make every wave wait for the
+  // row count before requesting anything; their loads are clamped and their stores predicated)
 
   // ---- weights: every load of the wave in one burst
   const T* wrow[R][NW];
