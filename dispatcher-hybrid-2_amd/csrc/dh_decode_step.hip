@@ -379,6 +379,142 @@ __global__ __launch_bounds__(kFusedThreads) void decode_mixer_step_kernel(StepAr
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Two-launch form for the graphed decoder: the gate readouts spread over one wave per
+// (level, head, group of RB rows) -- the gate weights stream through ~H*L compute units instead of
+// H -- and a small recurrence launch per (head, row). The first launch also gathers everything
+// the recurrence reads at position-dependent addresses (the level-l ring value and transmit gate
+// of position t - 2^l) into a staging buffer, so the second reads only fixed addresses.
+// Staging record per (b, h, l): {ig, fg, r_src, 0, V_src[hd]} in fp32 (kStageHead + hd floats).
+// Same arithmetic as decode_mixer_step_kernel.
+// ---------------------------------------------------------------------------------------------
+constexpr int kStageHead = 4;
+
+template <typename T, int C, int RB>
+__global__ __launch_bounds__(64) void decode_gates_kernel(StepArgs a, float* stage) {
+  constexpr int V = Chunk<T>::N;
+  const int lane = threadIdx.x;
+  const int H = a.H, L = a.L, GH = a.GH, hd = a.hd;
+  const int h = blockIdx.x % H, l = blockIdx.x / H;
+  const int b0 = blockIdx.y * RB;
+  const int nchunk = GH / V;
+  const int64_t d = (int64_t)H * hd;
+  const int sw = kStageHead + hd;
+
+  // ---- position-independent operands and t, in one burst
+  const int64_t t = *a.t_dev;
+  const int64_t wrow = ((int64_t)l * H + h) * GH;
+  uint4 w[3][C], av[RB][C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int64_t k = (int64_t)min(lane + 64 * c, nchunk - 1) * V;
+    w[0][c] = ld16((const T*)a.Wi + wrow + k);
+    w[1][c] = ld16((const T*)a.Wf + wrow + k);
+    w[2][c] = ld16((const T*)a.Wr + wrow + k);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) av[r][c] = ld16((const T*)a.A + (int64_t)min(b0 + r, a.B - 1) * GH + k);
+  }
+  const int64_t gi = (int64_t)l * H + h;
+  const uint32_t bir = Raw<T>::load((const T*)a.bi + gi);
+  const uint32_t bfr = Raw<T>::load((const T*)a.bf + gi);
+  const uint32_t brr = Raw<T>::load((const T*)a.br + gi);
+  if (t < 0 || t >= a.Tmax) return;                    // uniform
+
+  // ---- operands addressed through t: source row of B_hist, ring value and transmit gate
+  const int64_t src = t - ((int64_t)1 << l);
+  const bool ok = src >= 0;
+  const int64_t sc = ok ? src : 0;
+  uint4 bv[RB][C];
+  uint32_t vraw[RB][2], rraw[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const int64_t b = min(b0 + r, a.B - 1);
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      bv[r][c] = ld16((const T*)a.B_hist + (b * a.Tmax + sc) * GH + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
+    const T* ring = (const T*)a.V_ring + (b * a.S + ring_offset(l) + (sc & ring_mask(l))) * d + (int64_t)h * hd;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) vraw[r][q] = Raw<T>::load(ring + min(lane + 64 * q, hd - 1));
+    rraw[r] = Raw<T>::load((const T*)a.rg_hist + ((b * a.Tmax + sc) * L + l) * H + h);
+  }
+
+  // ---- the three dot products of each row, gates, staging
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      float wi[V], wf[V], wr[V], x1[V], x2[V];
+      Chunk<T>::unpack(w[0][c], wi);
+      Chunk<T>::unpack(w[1][c], wf);
+      Chunk<T>::unpack(w[2][c], wr);
+      Chunk<T>::unpack(av[r][c], x1);
+      Chunk<T>::unpack(bv[r][c], x2);
+      const float live = (lane + 64 * c) < nchunk ? 1.f : 0.f;
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        float x = fmaxf(x1[e] + (ok ? x2[e] : 0.f), 0.f);
+        x = x * x * live;
+        s0 += wi[e] * x;
+        s1 += wf[e] * x;
+        s2 += wr[e] * x;
+      }
+    }
+    s0 = wave_sum(s0);
+    s1 = wave_sum(s1);
+    s2 = wave_sum(s2);
+    const int b = b0 + r;
+    if (b < a.B) {                                     // uniform
+      float* st = stage + (((int64_t)b * H + h) * L + l) * sw;
+      if (lane == 0) {
+        const float okf = ok ? 1.f : 0.f;
+        st[0] = dh_sigmoid(s0 + Raw<T>::f(bir)) * okf;
+        st[1] = dh_sigmoid(s1 + Raw<T>::f(bfr)) * okf + (1.f - okf);
+        st[2] = ok ? Raw<T>::f(rraw[r]) : 0.f;
+        Elem<T>::store((T*)a.rg_hist + (((int64_t)b * a.Tmax + t) * L + l) * H + h, dh_sigmoid(s2 + Raw<T>::f(brr)));
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int e = lane + 64 * q;
+        if (e < hd) st[kStageHead + e] = ok ? Raw<T>::f(vraw[r][q]) : 0.f;
+      }
+    }
+  }
+}
+
+// The level recurrence of one (head, row) from the staged gates and sources: one thread per element.
+template <typename T, int LMAX>
+__global__ __launch_bounds__(kMaxHd) void decode_scan_kernel(StepArgs a, const float* stage) {
+  const int h = blockIdx.x, b = blockIdx.y, e = threadIdx.x;
+  const int H = a.H, L = a.L, hd = a.hd;
+  const int64_t d = (int64_t)H * hd;
+  const int sw = kStageHead + hd;
+  const int64_t t = *a.t_dev;
+  const float* st = stage + ((int64_t)b * H + h) * L * sw;
+  float ig[LMAX], fg[LMAX], rs[LMAX], vs[LMAX];
+#pragma unroll
+  for (int l = 0; l < LMAX; ++l) {                     // levels past L re-read level L-1 (unused)
+    const float* sl = st + (int64_t)min(l, L - 1) * sw;
+    ig[l] = sl[0];
+    fg[l] = sl[1];
+    rs[l] = sl[2];
+    vs[l] = sl[kStageHead + e];
+  }
+  const uint32_t v0raw = Raw<T>::load((const T*)a.V0 + (int64_t)b * d + (int64_t)h * hd + e);
+  if (t < 0 || t >= a.Tmax) return;                    // uniform
+  T* ring = (T*)a.V_ring + (int64_t)b * a.S * d + (int64_t)h * hd + e;
+  float v = Raw<T>::f(v0raw);
+  Elem<T>::store(ring + (t & 1) * d, v);
+#pragma unroll
+  for (int l = 0; l < LMAX; ++l) {
+    if (l < L) {
+      v = fg[l] * v + ig[l] * rs[l] * vs[l];
+      if (l + 1 < L) Elem<T>::store(ring + (ring_offset(l + 1) + (t & ring_mask(l + 1))) * d, v);
+    }
+  }
+  Elem<T>::store((T*)a.Y + (int64_t)b * d + (int64_t)h * hd + e, v);
+}
+
 template <typename T, int RPB, int C, int LMAX>
 void launch_fused(const StepArgs& a, hipStream_t s) {
   dim3 grid(a.H, (a.B + RPB - 1) / RPB), block(kFusedThreads);
@@ -462,6 +598,74 @@ extern "C" int dh_decode_mixer_step(int dtype, const void* A, const void* B_hist
     dispatch_fused<float>(a, rpb, C, s);
   else
     dispatch_fused<bf16_t>(a, rpb, C, s);
+  return dh_check_launch(who);
+}
+
+template <typename T, int C>
+void launch_gates(const StepArgs& a, float* stage, hipStream_t s) {
+  if (a.B >= 4) {
+    dim3 grid(a.H * a.L, (a.B + 3) / 4);
+    decode_gates_kernel<T, C, 4><<<grid, dim3(64), 0, s>>>(a, stage);
+  } else {
+    dim3 grid(a.H * a.L, a.B);
+    decode_gates_kernel<T, C, 1><<<grid, dim3(64), 0, s>>>(a, stage);
+  }
+}
+
+template <typename T>
+void launch_scan(const StepArgs& a, const float* stage, hipStream_t s) {
+  dim3 grid(a.H, a.B), block(a.hd);
+  if (a.L <= 8) decode_scan_kernel<T, 8><<<grid, block, 0, s>>>(a, stage);
+  else if (a.L <= 12) decode_scan_kernel<T, 12><<<grid, block, 0, s>>>(a, stage);
+  else decode_scan_kernel<T, 16><<<grid, block, 0, s>>>(a, stage);
+}
+
+extern "C" int dh_decode_gates(int dtype, const void* A, const void* B_hist, const void* Wi, const void* Wf,
+                               const void* Wr, const void* bi, const void* bf, const void* br, const int64_t* t_dev,
+                               void* rg_hist, const void* V_ring, float* stage, int B, int Tmax, int S, int GH,
+                               int H, int hd, int L, void* stream) {
+  const char* who = "dh_decode_gates";
+  int st = check_common(who, dtype, B, Tmax, GH, H, hd, L);
+  if (st) return st;
+  DH_REQUIRE(S == (int)ring_offset(L), DH_ERR_INVALID_ARG, "%s: S=%d but L=%d needs %lld ring slots", who, S, L,
+             (long long)ring_offset(L));
+  DH_REQUIRE(A && B_hist && Wi && Wf && Wr && bi && bf && br && t_dev && rg_hist && V_ring && stage,
+             DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
+  DH_REQUIRE(aligned(A, 16) && aligned(B_hist, 16) && aligned(Wi, 16) && aligned(Wf, 16) && aligned(Wr, 16),
+             DH_ERR_INVALID_ARG, "%s: A/B_hist/W need 16-byte alignment", who);
+  const int vec = dtype == DH_BF16 ? 8 : 4;
+  const int C = (GH / vec + 63) / 64;
+  DH_REQUIRE(C <= 4, DH_ERR_UNSUPPORTED_SHAPE, "%s: GH=%d exceeds %d elements per gate row", who, GH, 4 * 64 * vec);
+  StepArgs a{A, B_hist, Wi, Wf, Wr, bi, bf, br, t_dev, rg_hist, (void*)V_ring, nullptr, nullptr, nullptr, nullptr,
+             B, Tmax, S, GH, H, hd, L, 0};
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == DH_F32) {
+    if (C <= 1) launch_gates<float, 1>(a, stage, s);
+    else if (C == 2) launch_gates<float, 2>(a, stage, s);
+    else launch_gates<float, 4>(a, stage, s);
+  } else {
+    if (C <= 1) launch_gates<bf16_t, 1>(a, stage, s);
+    else if (C == 2) launch_gates<bf16_t, 2>(a, stage, s);
+    else launch_gates<bf16_t, 4>(a, stage, s);
+  }
+  return dh_check_launch(who);
+}
+
+extern "C" int dh_decode_scan(int dtype, const void* V0, const float* stage, const int64_t* t_dev, void* V_ring,
+                              void* Y, int B, int Tmax, int S, int H, int hd, int L, void* stream) {
+  const char* who = "dh_decode_scan";
+  int st = check_common(who, dtype, B, Tmax, 64, H, hd, L);
+  if (st) return st;
+  DH_REQUIRE(S == (int)ring_offset(L), DH_ERR_INVALID_ARG, "%s: S=%d but L=%d needs %lld ring slots", who, S, L,
+             (long long)ring_offset(L));
+  DH_REQUIRE(V0 && stage && t_dev && V_ring && Y, DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
+  StepArgs a{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, t_dev, nullptr, V_ring, V0, Y,
+             nullptr, nullptr, B, Tmax, S, 64, H, hd, L, 0};
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == DH_F32)
+    launch_scan<float>(a, stage, s);
+  else
+    launch_scan<bf16_t>(a, stage, s);
   return dh_check_launch(who);
 }
 

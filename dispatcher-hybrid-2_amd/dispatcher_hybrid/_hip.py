@@ -67,6 +67,8 @@ def _load():
         "dh_decode_attention": ([i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, i64,
                                  i32, i32, i32, i32, i32, vp], i32),
         "dh_argmax": ([i32, vp, i64, i32, i32, vp, vp], i32),
+        "dh_decode_gates": ([i32] + [vp] * 12 + [i32] * 7 + [vp], i32),
+        "dh_decode_scan": ([i32] + [vp] * 5 + [i32] * 6 + [vp], i32),
     }
     for name, (argtypes, restype) in sigs.items():
         fn = getattr(lib, name)

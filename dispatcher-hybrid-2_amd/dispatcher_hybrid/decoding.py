@@ -379,10 +379,11 @@ class GraphedHybridDecoder(_GraphedBase):
 
 
 class FusedGraphedHybridDecoder(GraphedHybridDecoder):
-    """Graphed decoder whose step runs on gfx950 kernels: per tree layer five launches
+    """Graphed decoder whose step runs on gfx950 kernels: per tree layer six launches
 
         dh_decode_gemv       RMSNorm1 + [W_in; W1x; W1s] -> V0, A, B_hist[t]
-        dh_decode_mixer_step gate readouts of all L levels + the level recurrence over the rings
+        dh_decode_gates      gate readouts of all L levels, one wave per (level, head)
+        dh_decode_scan       the level recurrence over the rings
         dh_decode_gemv       linear_out + residual
         dh_decode_gemv       RMSNorm2 + [W_gate; W_up] + SwiGLU
         dh_decode_gemv       linear_down + residual
@@ -412,6 +413,9 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         self.a_buf = z(gh)
         self.h_buf = z(cfg.dim_feedforward)
         self.q_buf, self.k_buf, self.v_buf = z(cfg.d_model), z(cfg.d_model), z(cfg.d_model)
+        # staging of the two-launch mixer step, shared by every tree layer (same shapes)
+        self.stage = torch.zeros(self._fused_step.stage_floats(Bb, mix0.num_heads, mix0.levels,
+                                                               mix0.head_dim), device=dev)
 
     @staticmethod
     def _eps(norm, dtype):
@@ -444,9 +448,9 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
                               (mx.gate_hidden_src.weight, cache.B_hist, cache.B_hist.stride(0), gh)],
                        self.t_buf, norm_weight=blk.norm1.weight, eps=self._eps(blk.norm1, self.dtype),
                        x_rows=rows)
-        fs.decode_mixer_step(self.a_buf, cache.B_hist, mx.gate_out, mx.forget_out, mx.reset_out,
+        fs.decode_gates_scan(self.a_buf, cache.B_hist, mx.gate_out, mx.forget_out, mx.reset_out,
                              mx.gate_out_bias, mx.forget_out_bias, mx.reset_out_bias, self.t_buf,
-                             cache.rg_hist, cache.V_ring, self.v0_buf, self.y_buf)
+                             cache.rg_hist, cache.V_ring, self.v0_buf, self.y_buf, self.stage)
         fs.decode_gemv(self.y_buf, [(mx.linear_out.weight, self.x_buf, d, 0)], self.t_buf,
                        resid=x_in, resid_rows=rows)
         self._ffn_g(blk)

@@ -38,19 +38,12 @@ def _check_contig(name, t):
         raise ValueError(f"{name} must be contiguous")
 
 
-def decode_mixer_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring, V0, Y):
-    """One tree layer's decode step at the position held in the device tensor `t_buf`.
-
-    A (B, GH) current destination features; B_hist (B, Tmax, GH) with row t written;
-    Wi/Wf/Wr (L, H, GH); bi/bf/br (L, H); rg_hist (B, Tmax, L, H) (row t written);
-    V_ring (B, S, H*hd) (slots of position t written); V0 (B, H*hd) linear_in output;
-    Y (B, H*hd) output. Everything in the model dtype (fp32 or bf16), on one GPU.
-    """
+def _check_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring, V0, Y):
     _hip.require_gpu(A, "decode_mixer_step")
-    Bb, GH = A.shape
+    Bb = A.shape[0]
     Tmax = B_hist.shape[1]
     L, H = Wi.shape[0], Wi.shape[1]
-    S, d = V_ring.shape[1], V_ring.shape[2]
+    d = V_ring.shape[2]
     dt = A.dtype
     for name, t in (("A", A), ("B_hist", B_hist), ("Wi", Wi), ("Wf", Wf), ("Wr", Wr), ("bi", bi),
                     ("bf", bf), ("br", br), ("rg_hist", rg_hist), ("V_ring", V_ring), ("V0", V0),
@@ -62,6 +55,22 @@ def decode_mixer_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring,
         raise TypeError("t_buf must be an int64 device tensor")
     if tuple(rg_hist.shape) != (Bb, Tmax, L, H) or tuple(V0.shape) != (Bb, d) or tuple(Y.shape) != (Bb, d):
         raise ValueError("decode_mixer_step: inconsistent cache / buffer shapes")
+
+
+def decode_mixer_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring, V0, Y):
+    """One tree layer's decode step at the position held in the device tensor `t_buf`.
+
+    A (B, GH) current destination features; B_hist (B, Tmax, GH) with row t written;
+    Wi/Wf/Wr (L, H, GH); bi/bf/br (L, H); rg_hist (B, Tmax, L, H) (row t written);
+    V_ring (B, S, H*hd) (slots of position t written); V0 (B, H*hd) linear_in output;
+    Y (B, H*hd) output. Everything in the model dtype (fp32 or bf16), on one GPU.
+    """
+    _check_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring, V0, Y)
+    Bb, GH = A.shape
+    Tmax = B_hist.shape[1]
+    L, H = Wi.shape[0], Wi.shape[1]
+    S, d = V_ring.shape[1], V_ring.shape[2]
+    dt = A.dtype
     p = _hip.ptr
     st = _hip.lib.dh_decode_mixer_step(
         _hip.dtype_code(dt), p(A), p(B_hist), p(Wi), p(Wf), p(Wr), p(bi), p(bf), p(br), p(t_buf),
@@ -104,6 +113,37 @@ def decode_gemv(x, segments, t_buf, norm_weight=None, eps=None, resid=None, swig
         Ws, outs, obs, ots, Ns, p(resid), resid.stride(0) if resid is not None else 0, p(resid_rows),
         int(bool(swiglu)), p(t_buf), B, K, _hip.stream_handle(x.device))
     _hip.check(st, "dh_decode_gemv")
+
+
+def stage_floats(B, H, L, hd):
+    """Size (in fp32 elements) of the staging buffer decode_gates_scan needs."""
+    return B * H * L * (4 + hd)
+
+
+def decode_gates_scan(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring, V0, Y, stage):
+    """decode_mixer_step as two launches (``dh_decode_gates`` then ``dh_decode_scan``): the gate
+    readouts run one wave per (level, head, row group) so the gate weights stream through many
+    compute units, and the recurrence reads its position-dependent sources from the fp32 staging
+    buffer `stage` (``stage_floats(B, H, L, hd)`` elements) the first launch fills. Same arguments,
+    state updates and arithmetic as decode_mixer_step."""
+    _check_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring, V0, Y)
+    Bb, Tmax, GH = B_hist.shape
+    S, d = V_ring.shape[1], V_ring.shape[2]
+    L, H = Wi.shape[0], Wi.shape[1]
+    hd = d // H
+    if stage.dtype != torch.float32 or not stage.is_contiguous() or stage.numel() < stage_floats(Bb, H, L, hd):
+        raise ValueError(f"decode_gates_scan: stage must be a contiguous fp32 buffer of >= "
+                         f"{stage_floats(Bb, H, L, hd)} elements")
+    p = _hip.ptr
+    code = _hip.dtype_code(A.dtype)
+    stream = _hip.stream_handle(A.device)
+    st = _hip.lib.dh_decode_gates(code, p(A), p(B_hist), p(Wi), p(Wf), p(Wr), p(bi), p(bf), p(br),
+                                  p(t_buf), p(rg_hist), p(V_ring), p(stage), Bb, Tmax, S, GH, H, hd, L,
+                                  stream)
+    _hip.check(st, "dh_decode_gates")
+    st = _hip.lib.dh_decode_scan(code, p(V0), p(stage), p(t_buf), p(V_ring), p(Y), Bb, Tmax, S, H, hd,
+                                 L, stream)
+    _hip.check(st, "dh_decode_scan")
 
 
 class _Launcher:

@@ -180,6 +180,25 @@ int dh_decode_attention(int dtype, const void* q, const void* k, const void* v, 
                         int window, void* stream);
 
 /*
+ * dh_decode_mixer_step as two launches with a wider first one, for the graphed decoder:
+ * dh_decode_gates runs one wave per (level, head, group of rows) -- the gate weights stream through
+ * H*L compute units -- writes rg_hist[:, t] and a staging record per (b, h, l):
+ *   stage[((b*H + h)*L + l)*(4 + hd) + ...] = {ig, fg, r_src, 0, V_src[0..hd)}   (fp32)
+ * with ig/fg the admit/forget gates of level l at t and r_src, V_src the level-l transmit gate and
+ * ring value of position t - 2^l (zeros before the sequence start). dh_decode_scan then runs the
+ * L-level recurrence from the staging buffer (one workgroup per (head, row)), writing the ring
+ * slots of position t and Y. Same arguments and arithmetic as dh_decode_mixer_step; `stage` holds
+ * B*H*L*(4 + hd) floats of caller-provided device memory. Replaces the same Triton pair as
+ * dh_decode_mixer_step (reference dispatcher_hybrid/fused_step.py:26-88, decoding.py:477-486).
+ */
+int dh_decode_gates(int dtype, const void* A, const void* B_hist, const void* Wi, const void* Wf,
+                    const void* Wr, const void* bi, const void* bf, const void* br, const int64_t* t_dev,
+                    void* rg_hist, const void* V_ring, float* stage, int B, int Tmax, int S, int GH, int H,
+                    int hd, int L, void* stream);
+int dh_decode_scan(int dtype, const void* V0, const float* stage, const int64_t* t_dev, void* V_ring, void* Y,
+                   int B, int Tmax, int S, int H, int hd, int L, void* stream);
+
+/*
  * Greedy next token: out[b] = argmax over row b of logits (B rows of V, rows row_stride elements
  * apart), as torch.argmax: first index of the maximum, NaN above every number. Replaces the
  * torch argmax of fast_generate's greedy branch (reference dispatcher_hybrid/modeling_dispatcher.py
