@@ -47,7 +47,9 @@ struct GemvArgs {
   const void* resid;            // nullable residual (B, N0)
   int64_t resid_bstride;
   const int64_t* resid_rows;    // nullable: residual row of batch b is resid_rows[b]
-  const int64_t* t_dev;         // device position (always a valid pointer)
+  const int64_t* t_dev;         // device position (read only when some segment has a t_stride)
+  int64_t* t_advance;           // nullable: incremented by one by this launch
+  int uses_t;
   Seg seg[kMaxSeg];
   int nseg;
   int B, K, Nrows;
@@ -108,6 +110,7 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
   const int nchunk = K / V;
   const bool has_norm = a.g != nullptr;
   const int rbase = (blockIdx.x * kWaves + wave) * R;
+  if (a.t_advance && blockIdx.x == 0 && threadIdx.x == 0) *a.t_advance += 1;   // host: uses_t == 0
   // (no early exit for waves past the last row: a branch here would make every wave wait for the
   // row count before requesting anything; their loads are clamped and their stores predicated)
 
@@ -143,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int c = 0; c < CG; ++c) gv[c] = ld16((const T*)a.g + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
   }
-  const int64_t t = *a.t_dev;
+  const int64_t t = a.uses_t ? *a.t_dev : 0;
   const bool has_resid = a.resid != nullptr;
 
   // activation chunks of BG batch rows (gathered through x_rows when given) and the residual
@@ -285,6 +288,7 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_staged_kernel(GemvArgs a
   const int nchunk = K / V;
   const bool has_norm = a.g != nullptr;
   const int rbase = (blockIdx.x * kWaves + wave) * R;
+  if (a.t_advance && blockIdx.x == 0 && threadIdx.x == 0) *a.t_advance += 1;   // host: uses_t == 0
 
   const T* wrow[R][NW];
   int segi[R];
@@ -317,7 +321,7 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_staged_kernel(GemvArgs a
 #pragma unroll
     for (int c = 0; c < CG; ++c) gv[c] = ld16((const T*)a.g + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
   }
-  const int64_t t = *a.t_dev;
+  const int64_t t = a.uses_t ? *a.t_dev : 0;
 
   // ---- staging: wave w normalises rows w, w + 4, ... (its lanes cover the row's chunks)
   for (int b = wave; b < B; b += kWaves) {
@@ -489,8 +493,8 @@ extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const
                               const void* norm_w, float eps, int nseg, const void* const* W,
                               void* const* out, const int64_t* out_bstride, const int64_t* out_t_stride,
                               const int* N, const void* resid, int64_t resid_bstride,
-                              const int64_t* resid_rows, int swiglu, const int64_t* t_dev, int B, int K,
-                              void* stream) {
+                              const int64_t* resid_rows, int swiglu, const int64_t* t_dev, int64_t* t_advance,
+                              int B, int K, void* stream) {
   const char* who = "dh_decode_gemv";
   DH_REQUIRE(dtype == DH_F32 || dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d", who, dtype);
   const int vec = dtype == DH_BF16 ? 8 : 4;             // elements per 16-byte chunk
@@ -514,6 +518,7 @@ extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const
   a.resid_bstride = resid_bstride;
   a.resid_rows = resid_rows;
   a.t_dev = t_dev;
+  a.t_advance = t_advance;
   a.nseg = nseg;
   a.B = B;
   a.K = K;
@@ -522,8 +527,11 @@ extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const
     DH_REQUIRE(W[s] && out[s] && N[s] >= 1, DH_ERR_INVALID_ARG, "%s: segment %d incomplete", who, s);
     DH_REQUIRE(aligned(W[s], 16), DH_ERR_INVALID_ARG, "%s: segment %d weights need 16-byte alignment", who, s);
     a.seg[s] = Seg{W[s], out[s], out_bstride[s], out_t_stride[s], N[s]};
+    a.uses_t |= out_t_stride[s] != 0;
     total += N[s];
   }
+  DH_REQUIRE(!t_advance || !a.uses_t, DH_ERR_INVALID_ARG,
+             "%s: a launch that advances the position cannot also address its outputs through it", who);
   if (swiglu) {
     DH_REQUIRE(N[0] == N[1], DH_ERR_INVALID_ARG, "%s: gate and up rows differ (%d, %d)", who, N[0], N[1]);
     total = N[0];

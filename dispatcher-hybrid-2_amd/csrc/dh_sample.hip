@@ -4,16 +4,15 @@
 // dispatcher_hybrid/modeling_dispatcher.py:426-441): the index of the largest value, the first
 // such index on ties, and NaN counts as larger than every number (the first NaN wins).
 //
-// Work decomposition: one workgroup (16 wave64s) per row. Every thread requests all of its
-// elements (index tid + 1024*k) before comparing any, keeps its best (value, index), then DPP wave
-// reductions and one LDS step across the waves pick the row's winner.
+// Work decomposition: two launches. The first splits every row into slices of kSlice elements, one
+// workgroup (4 wave64s) per (slice, row): each thread requests all of its elements before
+// comparing any, keeps its best (value, index), and DPP wave reductions plus one LDS step give the
+// slice's candidate. The second launch reduces each row's candidates with the same ordering. A
+// row of a 50k vocabulary thus streams through ~25 compute units instead of one.
 #include "dh_common.h"
 
 namespace {
 
-constexpr int kThreads = 1024;
-constexpr int kWaves = kThreads / 64;
-constexpr int kMaxPerThread = 64;        // V <= 65536
 
 // a beats b: larger value, NaN above all numbers, lower index on ties
 __device__ __forceinline__ bool beats(float va, int ia, float vb, int ib) {
@@ -33,73 +32,97 @@ __device__ __forceinline__ void dpp_pair(float& v, int& i) {
   }
 }
 
-template <typename T, int PT>
-__global__ __launch_bounds__(kThreads) void argmax_kernel(const T* logits, int64_t row_stride, int V, int64_t* out) {
-  __shared__ float bv[kWaves];
-  __shared__ int bi[kWaves];
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const T* row = logits + (int64_t)b * row_stride;
-  float x[PT];
-#pragma unroll
-  for (int k = 0; k < PT; ++k) x[k] = Elem<T>::load(row + min(tid + k * kThreads, V - 1));   // clamped
-  float best = x[0];
-  int bidx = tid < V ? tid : V - 1;
-#pragma unroll
-  for (int k = 1; k < PT; ++k) {
-    const int i = tid + k * kThreads;
-    if (i < V && beats(x[k], i, best, bidx)) {
-      best = x[k];
-      bidx = i;
-    }
-  }
+constexpr int kSlice = 2048;              // elements per first-pass workgroup
+constexpr int kT1 = 256;                  // first-pass threads: kSlice / kT1 = 8 elements each
+
+struct Cand {
+  float v;
+  int i;
+};
+
+// best (value, index) of a wave, in lane 63
+__device__ __forceinline__ void wave_best(float& best, int& bidx) {
   dpp_pair<0xb1, 0xf>(best, bidx);      // quad_perm(1,0,3,2)
   dpp_pair<0x4e, 0xf>(best, bidx);      // quad_perm(2,3,0,1)
   dpp_pair<0x141, 0xf>(best, bidx);     // row_half_mirror
   dpp_pair<0x140, 0xf>(best, bidx);     // row_mirror
   dpp_pair<0x142, 0xa>(best, bidx);     // row_bcast:15 into rows 1, 3
   dpp_pair<0x143, 0xc>(best, bidx);     // row_bcast:31 into rows 2, 3
-  if (lane == 63) {
-    bv[wave] = best;
-    bi[wave] = bidx;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float v = bv[0];
-    int i = bi[0];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w)
-      if (beats(bv[w], bi[w], v, i)) {
-        v = bv[w];
-        i = bi[w];
-      }
-    out[b] = i;
-  }
 }
 
 template <typename T>
-void launch_argmax(const T* logits, int64_t row_stride, int B, int V, int64_t* out, hipStream_t s) {
-  const int pt = (V + kThreads - 1) / kThreads;
-  if (pt <= 8) argmax_kernel<T, 8><<<B, kThreads, 0, s>>>(logits, row_stride, V, out);
-  else if (pt <= 16) argmax_kernel<T, 16><<<B, kThreads, 0, s>>>(logits, row_stride, V, out);
-  else if (pt <= 32) argmax_kernel<T, 32><<<B, kThreads, 0, s>>>(logits, row_stride, V, out);
-  else argmax_kernel<T, kMaxPerThread><<<B, kThreads, 0, s>>>(logits, row_stride, V, out);
+__global__ __launch_bounds__(kT1) void argmax_slices(const T* logits, int64_t row_stride, int V, Cand* cand) {
+  __shared__ Cand wb[kT1 / 64];
+  const int s = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const T* row = logits + (int64_t)b * row_stride;
+  constexpr int PT = kSlice / kT1;
+  const int base = s * kSlice;
+  float x[PT];
+#pragma unroll
+  for (int k = 0; k < PT; ++k) x[k] = Elem<T>::load(row + min(base + tid + k * kT1, V - 1));   // clamped
+  float best = x[0];
+  int bidx = min(base + tid, V - 1);
+#pragma unroll
+  for (int k = 1; k < PT; ++k) {
+    const int i = base + tid + k * kT1;
+    if (i < V && beats(x[k], i, best, bidx)) {
+      best = x[k];
+      bidx = i;
+    }
+  }
+  wave_best(best, bidx);
+  if (lane == 63) wb[wave] = Cand{best, bidx};
+  __syncthreads();
+  if (tid == 0) {
+    Cand c = wb[0];
+#pragma unroll
+    for (int w = 1; w < kT1 / 64; ++w)
+      if (beats(wb[w].v, wb[w].i, c.v, c.i)) c = wb[w];
+    cand[(int64_t)b * gridDim.x + s] = c;
+  }
+}
+
+__global__ __launch_bounds__(64) void argmax_final(const Cand* cand, int nslice, int64_t* out) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  const Cand* cb = cand + (int64_t)b * nslice;
+  float best = -INFINITY;
+  int bidx = 0x7fffffff;
+  for (int j = lane; j < nslice; j += 64) {
+    const Cand c = cb[j];
+    if (beats(c.v, c.i, best, bidx)) {
+      best = c.v;
+      bidx = c.i;
+    }
+  }
+  wave_best(best, bidx);
+  if (lane == 63) out[b] = bidx;
 }
 
 }  // namespace
 
+extern "C" int64_t dh_argmax_workspace_bytes(int B, int V) {
+  return (int64_t)B * ((V + kSlice - 1) / kSlice) * (int64_t)sizeof(Cand);
+}
+
 extern "C" int dh_argmax(int dtype, const void* logits, int64_t row_stride, int B, int V, int64_t* out,
-                         void* stream) {
+                         void* workspace, int64_t workspace_bytes, void* stream) {
   const char* who = "dh_argmax";
   DH_REQUIRE(dtype == DH_F32 || dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d", who, dtype);
-  DH_REQUIRE(B >= 1 && V >= 1 && row_stride >= V, DH_ERR_INVALID_ARG, "%s: B=%d V=%d row_stride=%lld", who, B, V,
-             (long long)row_stride);
-  DH_REQUIRE(V <= kThreads * kMaxPerThread, DH_ERR_UNSUPPORTED_SHAPE, "%s: V=%d exceeds %d", who, V,
-             kThreads * kMaxPerThread);
-  DH_REQUIRE(logits && out, DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
+  DH_REQUIRE(B >= 1 && B <= 65535 && V >= 1 && row_stride >= V, DH_ERR_INVALID_ARG, "%s: B=%d V=%d row_stride=%lld",
+             who, B, V, (long long)row_stride);
+  DH_REQUIRE(logits && out && workspace, DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
+  DH_REQUIRE(workspace_bytes >= dh_argmax_workspace_bytes(B, V), DH_ERR_INVALID_ARG,
+             "%s: workspace of %lld bytes, needs %lld", who, (long long)workspace_bytes,
+             (long long)dh_argmax_workspace_bytes(B, V));
+  DH_REQUIRE((uintptr_t)workspace % 8 == 0, DH_ERR_INVALID_ARG, "%s: workspace needs 8-byte alignment", who);
+  const int nslice = (V + kSlice - 1) / kSlice;
+  Cand* cand = (Cand*)workspace;
   hipStream_t s = (hipStream_t)stream;
+  dim3 g1(nslice, B);
   if (dtype == DH_BF16)
-    launch_argmax<bf16_t>((const bf16_t*)logits, row_stride, B, V, out, s);
+    argmax_slices<bf16_t><<<g1, kT1, 0, s>>>((const bf16_t*)logits, row_stride, V, cand);
   else
-    launch_argmax<float>((const float*)logits, row_stride, B, V, out, s);
+    argmax_slices<float><<<g1, kT1, 0, s>>>((const float*)logits, row_stride, V, cand);
+  argmax_final<<<B, 64, 0, s>>>(cand, nslice, out);
   return dh_check_launch(who);
 }

@@ -15,7 +15,7 @@ import os
 
 import torch
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 _LIB_NAME = "libdh_mixer.so"
 
 DH_F32, DH_BF16 = 0, 1
@@ -62,11 +62,12 @@ def _load():
         "dh_decode_mixer_step": ([i32] + [vp] * 13 + [i32] * 7 + [vp], i32),
         "dh_step_gates": ([i32] + [vp] * 12 + [i32] * 5 + [vp], i32),
         "dh_decode_gemv": ([i32, vp, i64, vp, vp, ctypes.c_float, i32, vp, vp, vp, vp, vp,
-                            vp, i64, vp, i32, vp, i32, i32, vp], i32),
+                            vp, i64, vp, i32, vp, vp, i32, i32, vp], i32),
         "dh_step_scan": ([i32] + [vp] * 7 + [i32] * 6 + [vp], i32),
         "dh_decode_attention": ([i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, i64,
                                  i32, i32, i32, i32, i32, vp], i32),
-        "dh_argmax": ([i32, vp, i64, i32, i32, vp, vp], i32),
+        "dh_argmax": ([i32, vp, i64, i32, i32, vp, vp, i64, vp], i32),
+        "dh_argmax_workspace_bytes": ([i32, i32], i64),
         "dh_decode_gates": ([i32] + [vp] * 12 + [i32] * 7 + [vp], i32),
         "dh_decode_scan": ([i32] + [vp] * 5 + [i32] * 6 + [vp], i32),
     }

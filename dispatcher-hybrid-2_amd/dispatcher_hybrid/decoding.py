@@ -476,7 +476,7 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
             else:
                 self._tree_step_f(blk, cache, i == 0)
         V = self.logits_out.shape[1]
+        # the last launch also advances the device position (no separate add kernel)
         self._fused_step.decode_gemv(self.x_buf, [(self.m.lm_head.weight, self.logits_out, V, 0)],
                                      self.t_buf, norm_weight=self.m.norm_out.weight,
-                                     eps=self._eps(self.m.norm_out, self.dtype))
-        self.t_buf.add_(1)
+                                     eps=self._eps(self.m.norm_out, self.dtype), t_advance=self.t_buf)

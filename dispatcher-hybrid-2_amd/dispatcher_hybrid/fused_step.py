@@ -81,7 +81,7 @@ def decode_mixer_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring,
 
 
 def decode_gemv(x, segments, t_buf, norm_weight=None, eps=None, resid=None, swiglu=False,
-                x_rows=None, resid_rows=None):
+                x_rows=None, resid_rows=None, t_advance=None):
     """Fused matrix-vector products of the decode step (``dh_decode_gemv``).
 
     x: (B, K) activations (or the embedding table with ``x_rows`` = token ids: row b is
@@ -90,7 +90,9 @@ def decode_gemv(x, segments, t_buf, norm_weight=None, eps=None, resid=None, swig
     norm_weight: RMSNorm weight applied to x first (eps defaults to the fp32 epsilon 2^-23, which
     nn.RMSNorm(eps=None) takes from torch's fp32 math type for fp32 and bf16 inputs alike). resid: (B, N) added to segment 0's result (rows through
     ``resid_rows`` when given); swiglu: segments are (gate, up) and silu(gate) * up goes to the
-    gate segment's destination. Everything in one dtype (fp32 or bf16) on one GPU.
+    gate segment's destination. t_advance: an int64 device tensor the launch adds one to (the
+    decode step's position advance, folded into its last launch; outputs may then not use
+    t_stride). Everything in one dtype (fp32 or bf16) on one GPU.
     """
     _hip.require_gpu(x, "decode_gemv")
     dt = x.dtype
@@ -111,7 +113,7 @@ def decode_gemv(x, segments, t_buf, norm_weight=None, eps=None, resid=None, swig
     st = _hip.lib.dh_decode_gemv(
         _hip.dtype_code(dt), p(x), x.stride(0), p(x_rows), p(norm_weight), float(eps or 0.0), n,
         Ws, outs, obs, ots, Ns, p(resid), resid.stride(0) if resid is not None else 0, p(resid_rows),
-        int(bool(swiglu)), p(t_buf), B, K, _hip.stream_handle(x.device))
+        int(bool(swiglu)), p(t_buf), p(t_advance), B, K, _hip.stream_handle(x.device))
     _hip.check(st, "dh_decode_gemv")
 
 
@@ -241,7 +243,15 @@ def argmax_tokens(logits, out=None):
         out = torch.empty(B, dtype=torch.long, device=logits.device)
     if out.dtype != torch.long or out.numel() != B or not out.is_contiguous():
         raise ValueError("argmax_tokens: out must be a contiguous int64 tensor of B elements")
+    nbytes = int(_hip.lib.dh_argmax_workspace_bytes(B, V))
+    ws = _ARGMAX_WS.get(logits.device)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 4096), dtype=torch.uint8, device=logits.device)
+        _ARGMAX_WS[logits.device] = ws
     st = _hip.lib.dh_argmax(_hip.dtype_code(logits.dtype), _hip.ptr(logits), logits.stride(0), B, V,
-                            _hip.ptr(out), _hip.stream_handle(logits.device))
+                            _hip.ptr(out), _hip.ptr(ws), ws.numel(), _hip.stream_handle(logits.device))
     _hip.check(st, "dh_argmax")
     return out
+
+
+_ARGMAX_WS = {}           # per-device candidate buffer of argmax_tokens, grown on demand

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 2
+#define DH_ABI_VERSION 3
 
 enum dh_status {
   DH_OK = 0,
@@ -149,7 +149,10 @@ int dh_decode_mixer_step(int dtype, const void* A, const void* B_hist, const voi
  *         round(W[s][n].h)                                     plain
  *       | round(round(W[0][n].h) + resid[b, n])               resid != NULL (nseg == 1); resid[b] as x
  *       | round(round(silu(round(W[0][n].h))) * round(W[1][n].h)) into out[0]   swiglu (nseg == 2)
- *   t = *t_dev (device position; e.g. the B_hist row of the source projection).
+ *   t = *t_dev (device position; e.g. the B_hist row of the source projection), read only when
+ *   some out_t_stride is non-zero. t_advance (nullable): the launch adds one to *t_advance (the
+ *   decode step's position advance folded into its last launch); not allowed together with a
+ *   non-zero out_t_stride.
  * All activations and weights in dtype; fp32 accumulation. The array arguments W, out, out_bstride,
  * out_t_stride and N are host arrays of nseg entries. K must be a multiple of 8 (bf16) or 4 (fp32):
  * rows are read in 16-byte chunks.
@@ -158,7 +161,7 @@ int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const int64_t* x
                    const void* norm_w, float eps, int nseg, const void* const* W, void* const* out,
                    const int64_t* out_bstride, const int64_t* out_t_stride, const int* N,
                    const void* resid, int64_t resid_bstride, const int64_t* resid_rows, int swiglu,
-                   const int64_t* t_dev, int B, int K, void* stream);
+                   const int64_t* t_dev, int64_t* t_advance, int B, int K, void* stream);
 
 /*
  * One decode step of a windowed RoPE attention layer: rotation of the new query and key at the
@@ -202,9 +205,13 @@ int dh_decode_scan(int dtype, const void* V0, const float* stage, const int64_t*
  * Greedy next token: out[b] = argmax over row b of logits (B rows of V, rows row_stride elements
  * apart), as torch.argmax: first index of the maximum, NaN above every number. Replaces the
  * torch argmax of fast_generate's greedy branch (reference dispatcher_hybrid/modeling_dispatcher.py
- * :426-441) with one launch whose output can be fed back as the decoder's next tokens. V <= 65536.
+ * :426-441) with two short launches whose output can be fed back as the decoder's next tokens.
+ * workspace: device memory of at least dh_argmax_workspace_bytes(B, V) bytes (per-slice
+ * candidates); its contents on entry do not matter.
  */
-int dh_argmax(int dtype, const void* logits, int64_t row_stride, int B, int V, int64_t* out, void* stream);
+int64_t dh_argmax_workspace_bytes(int B, int V);
+int dh_argmax(int dtype, const void* logits, int64_t row_stride, int B, int V, int64_t* out, void* workspace,
+              int64_t workspace_bytes, void* stream);
 
 /*
  * The two halves of dh_decode_mixer_step as separate launches, with the reference's own buffer
