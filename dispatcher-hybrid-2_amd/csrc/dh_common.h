@@ -83,5 +83,18 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// A uniform value no thread of the launch writes (a decode position, a token row index), read
+// through the constant address space: the compiler emits a scalar load, so waiting for it never
+// waits for vector loads already in flight (those return in issue order), and it lands in an SGPR.
+template <typename T>
+__device__ __forceinline__ T load_uniform(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+
+// Scheduling fence: nothing moves across it. Placed after a burst of loads, every request of the
+// burst is issued before the first wait for any of them (the scheduler otherwise interleaves
+// arithmetic on early arrivals, with its waits, between the requests).
+#define DH_ISSUE_FENCE() __builtin_amdgcn_sched_barrier(0)
+
 __host__ __device__ __forceinline__ int64_t ring_offset(int j) { return ((int64_t)2 << j) - 2; }
 __host__ __device__ __forceinline__ int64_t ring_mask(int j) { return ((int64_t)2 << j) - 1; }

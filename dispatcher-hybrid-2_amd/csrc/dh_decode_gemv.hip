@@ -101,18 +101,47 @@ template <> struct Raw<float> {
   __device__ __forceinline__ static float f(uint32_t r) { return __uint_as_float(r); }
 };
 
+// Segment of concatenated output row n, from uniform selects over the argument fields (indexing
+// the argument array with a runtime value makes the compiler read it with vector loads, and wait
+// for them, before the weight requests).
+struct RowSeg {
+  int s, local;
+};
+__device__ __forceinline__ RowSeg row_segment(const GemvArgs& a, int n) {
+  const int N0 = a.seg[0].N, N1 = a.seg[1].N;
+  const bool in1 = a.nseg > 1 && n >= N0;
+  const bool in2 = a.nseg > 2 && n >= N0 + N1;
+  return RowSeg{in2 ? 2 : (in1 ? 1 : 0), n - (in2 ? N0 + N1 : (in1 ? N0 : 0))};
+}
+template <typename P>
+__device__ __forceinline__ P pick_seg(int s, P p0, P p1, P p2) {
+  return s == 0 ? p0 : (s == 1 ? p1 : p2);
+}
+// destination of output `loc` of segment s for batch row b at position t
+template <typename T>
+__device__ __forceinline__ T* out_ptr(const GemvArgs& a, int s, int64_t b, int64_t t, int loc) {
+  T* o = (T*)pick_seg(s, a.seg[0].out, a.seg[1].out, a.seg[2].out);
+  return o + b * pick_seg(s, a.seg[0].out_bstride, a.seg[1].out_bstride, a.seg[2].out_bstride) +
+         t * pick_seg(s, a.seg[0].t_stride, a.seg[1].t_stride, a.seg[2].t_stride) + loc;
+}
+
+// the launch's position advance (block 0, thread 0), placed after the launch's requests
+__device__ __forceinline__ void advance_position(const GemvArgs& a) {
+  if (a.t_advance && blockIdx.x == 0 && threadIdx.x == 0) *a.t_advance += 1;   // host: uses_t == 0
+}
+
 template <typename T, int R, int CG, int BG, bool SW>
 __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
   constexpr int V = Vec<T>::N;
   constexpr int NW = SW ? 2 : 1;                      // weight rows per output row
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int K = a.K, B = a.B;
   const int nchunk = K / V;
   const bool has_norm = a.g != nullptr;
   const int rbase = (blockIdx.x * kWaves + wave) * R;
-  if (a.t_advance && blockIdx.x == 0 && threadIdx.x == 0) *a.t_advance += 1;   // host: uses_t == 0
   // (no early exit for waves past the last row: a branch here would make every wave wait for the
-  // row count before requesting anything; their loads are clamped and their stores predicated)
+  // row count before requesting anything; their loads are clamped and their stores predicated;
+  // the position advance, when asked for, comes last for the same reason)
 
   // ---- weights: every load of the wave in one burst
   const T* wrow[R][NW];
@@ -121,16 +150,11 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int n = min(rbase + r, a.Nrows - 1);
-    int s = 0, n0 = 0;
-    if (!SW) {
-#pragma unroll
-      for (int q = 0; q < kMaxSeg - 1; ++q)
-        if (q + 1 < a.nseg && n - n0 >= a.seg[s].N) { n0 += a.seg[s].N; ++s; }
-    }
-    segi[r] = s;
-    local[r] = n - n0;
-    wrow[r][0] = (const T*)a.seg[s].W + (int64_t)local[r] * K;
-    if (SW) wrow[r][NW - 1] = (const T*)a.seg[1].W + (int64_t)local[r] * K;
+    const RowSeg rw = SW ? RowSeg{0, n} : row_segment(a, n);
+    segi[r] = rw.s;
+    local[r] = rw.local;
+    wrow[r][0] = (const T*)pick_seg(rw.s, a.seg[0].W, a.seg[1].W, a.seg[2].W) + (int64_t)rw.local * K;
+    if (SW) wrow[r][NW - 1] = (const T*)a.seg[1].W + (int64_t)rw.local * K;
   }
   uint4 w[R][NW][CG];
 #pragma unroll
@@ -146,7 +170,7 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int c = 0; c < CG; ++c) gv[c] = ld16((const T*)a.g + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
   }
-  const int64_t t = a.uses_t ? *a.t_dev : 0;
+  const int64_t t = a.uses_t ? load_uniform(a.t_dev) : 0;
   const bool has_resid = a.resid != nullptr;
 
   // activation chunks of BG batch rows (gathered through x_rows when given) and the residual
@@ -160,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int bp = 0; bp < BG; ++bp) {
       const int b = min(g0 + bp, B - 1);
-      const int64_t xrow = a.x_rows ? a.x_rows[b] : (int64_t)b;
+      const int64_t xrow = a.x_rows ? load_uniform(a.x_rows + b) : (int64_t)b;
       const T* xp = (const T*)a.x + xrow * a.x_bstride;
 #pragma unroll
       for (int c = 0; c < CG; ++c) xv[bp][c] = ld16(xp + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
@@ -267,11 +291,173 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
           s = segi[rr];
           loc = local[rr];
         }
-      const Seg& sg = a.seg[s];
-      const int64_t b = b0 + bp;
-      Elem<T>::store((T*)sg.out + b * sg.out_bstride + t * sg.t_stride + loc, out);
+      Elem<T>::store(out_ptr<T>(a, s, b0 + bp, t, loc), out);
     }
   }
+  advance_position(a);
+}
+
+// Single-row variant (B == 1). Every lane of the per-wave kernel above requests its own copy of
+// the activation row and of the RMSNorm weight: three requests per weight request, all through
+// the compute unit's vector memory path, which bounds these short launches. Here each workgroup
+// requests the two rows once, one 16-byte load per thread, stages them in LDS behind one barrier,
+// and each wave reads its chunks from LDS. The small requests (activation, norm weight, residual)
+// go out BEFORE the weight burst: loads return in issue order, so they arrive first and the
+// staging never waits for the weights. When a row is gathered through x_rows or resid_rows (the
+// embedding), its address waits on a scalar load, so the weights go first instead (GATHER).
+// Same arithmetic as the per-wave kernel.
+template <typename T, int R, int CG, bool SW, int NT, bool GATHER>
+__global__ __launch_bounds__(NT) void decode_gemv_row_kernel(GemvArgs a) {
+  __shared__ uint4 sx[2 * CG * 64];                   // x chunks [0, nchunk), norm weight after
+  constexpr int V = Vec<T>::N;
+  constexpr int NW = SW ? 2 : 1;
+  constexpr int NWV = NT / 64;
+  constexpr int XCH = (2 * CG * 64 + NT - 1) / NT;     // staged chunks per thread
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int K = a.K;
+  const int nchunk = K / V;
+  const bool has_norm = a.g != nullptr;
+  const bool has_resid = a.resid != nullptr;
+  const int nst = has_norm ? 2 * nchunk : nchunk;
+  const int rbase = (blockIdx.x * NWV + wave) * R;
+
+  uint4 st[XCH];
+  uint32_t rc = 0;
+  auto small_loads = [&]() {
+    const int64_t xrow = GATHER && a.x_rows ? load_uniform(a.x_rows) : 0;
+    const T* xp = (const T*)a.x + xrow * a.x_bstride;
+    const T* gp = has_norm ? (const T*)a.g : xp;
+#pragma unroll
+    for (int j = 0; j < XCH; ++j) {
+      const int i = min((int)threadIdx.x + j * NT, nst - 1);
+      st[j] = ld16(i < nchunk ? xp + (int64_t)i * V : gp + (int64_t)(i - nchunk) * V);
+    }
+    // the residual of output `lane`; without one, a harmless read of x keeps the load unconditional
+    // (a branch around it makes the no-residual path wait for the staging loads)
+    const int n = min(rbase + lane % R, a.Nrows - 1);
+    const int64_t rrow = GATHER && a.resid_rows ? load_uniform(a.resid_rows) : 0;
+    rc = Raw<T>::load(has_resid ? (const T*)a.resid + rrow * a.resid_bstride + n : xp);
+  };
+  if constexpr (!GATHER) {
+    small_loads();
+    DH_ISSUE_FENCE();
+  }
+
+  // ---- weights: every load of the wave in one burst
+  const T* wrow[R][NW];
+  int segi[R];
+  int local[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = min(rbase + r, a.Nrows - 1);
+    const RowSeg rw = SW ? RowSeg{0, n} : row_segment(a, n);
+    segi[r] = rw.s;
+    local[r] = rw.local;
+    wrow[r][0] = (const T*)pick_seg(rw.s, a.seg[0].W, a.seg[1].W, a.seg[2].W) + (int64_t)rw.local * K;
+    if (SW) wrow[r][NW - 1] = (const T*)a.seg[1].W + (int64_t)rw.local * K;
+  }
+  uint4 w[R][NW][CG];
+#pragma unroll
+  for (int c = 0; c < CG; ++c) {
+    const int ch = min(lane + 64 * c, nchunk - 1);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int q = 0; q < NW; ++q) w[r][q][c] = ld16(wrow[r][q] + (int64_t)ch * V);
+  }
+  if constexpr (GATHER) small_loads();
+  const int64_t t = a.uses_t ? load_uniform(a.t_dev) : 0;
+  DH_ISSUE_FENCE();
+
+  // ---- stage the activation row and the norm weight
+#pragma unroll
+  for (int j = 0; j < XCH; ++j) {
+    const int i = threadIdx.x + j * NT;
+    if (i < nst) sx[i] = st[j];
+  }
+  __syncthreads();
+  uint4 xc[CG], gv[CG];
+#pragma unroll
+  for (int c = 0; c < CG; ++c) {
+    const int ch = min(lane + 64 * c, nchunk - 1);
+    xc[c] = sx[ch];
+    if (has_norm) gv[c] = sx[nchunk + ch];
+  }
+
+  // ---- RMSNorm scale: the wave's lanes cover the whole row
+  float rs = 1.f;
+  if (has_norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+      float xf[V];
+      Vec<T>::unpack(xc[c], xf);
+      float part = 0.f;
+#pragma unroll
+      for (int e = 0; e < V; ++e) part += xf[e] * xf[e];
+      ss += lane + 64 * c < nchunk ? part : 0.f;
+    }
+    rs = rsqrtf(wave_sum(ss) / (float)K + a.eps);
+  }
+  // ---- dot products
+  float acc[R][NW];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int q = 0; q < NW; ++q) acc[r][q] = 0.f;
+#pragma unroll
+  for (int c = 0; c < CG; ++c) {
+    const bool live = lane + 64 * c < nchunk;
+    float hv[V];
+    Vec<T>::unpack(xc[c], hv);
+    if (has_norm) {
+      float gw[V];
+      Vec<T>::unpack(gv[c], gw);
+#pragma unroll
+      for (int e = 0; e < V; ++e) hv[e] = Elem<T>::round(hv[e] * rs * gw[e]);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        float wv[V];
+        Vec<T>::unpack(w[r][q][c], wv);
+        float sdot = 0.f;
+#pragma unroll
+        for (int e = 0; e < V; ++e) sdot += wv[e] * hv[e];
+        acc[r][q] += live ? sdot : 0.f;
+      }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int q = 0; q < NW; ++q) acc[r][q] = wave_sum(acc[r][q]);
+  // ---- epilogue: lane r < R writes output row rbase + r
+  if (lane < R && rbase + lane < a.Nrows) {
+    float v0 = 0.f, v1 = 0.f;
+    int s = 0, loc = 0;
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr)
+      if (rr == lane) {
+        v0 = acc[rr][0];
+        v1 = acc[rr][NW - 1];
+        s = segi[rr];
+        loc = local[rr];
+      }
+    float out;
+    if (SW) {
+      out = Elem<T>::round(Elem<T>::round(silu(Elem<T>::round(v0))) * Elem<T>::round(v1));
+    } else {
+      out = Elem<T>::round(v0);
+      if (has_resid) {
+        uint32_t rv = rc;
+        asm volatile("" : "+v"(rv));                    // convert here, not beside the load
+        out = Elem<T>::round(out + Raw<T>::f(rv));
+      }
+    }
+    Elem<T>::store(out_ptr<T>(a, s, 0, t, loc), out);
+  }
+  advance_position(a);
 }
 
 // Batched variant (B > 1): the workgroup normalises each activation row ONCE into LDS (wave w takes
@@ -283,12 +469,11 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_staged_kernel(GemvArgs a
   T* hs = reinterpret_cast<T*>(smem);                 // [B][nchunk * V] staged (normalised) rows
   constexpr int V = Vec<T>::N;
   constexpr int NW = SW ? 2 : 1;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int K = a.K, B = a.B;
   const int nchunk = K / V;
   const bool has_norm = a.g != nullptr;
   const int rbase = (blockIdx.x * kWaves + wave) * R;
-  if (a.t_advance && blockIdx.x == 0 && threadIdx.x == 0) *a.t_advance += 1;   // host: uses_t == 0
 
   const T* wrow[R][NW];
   int segi[R];
@@ -296,16 +481,11 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_staged_kernel(GemvArgs a
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int n = min(rbase + r, a.Nrows - 1);
-    int s = 0, n0 = 0;
-    if (!SW) {
-#pragma unroll
-      for (int q = 0; q < kMaxSeg - 1; ++q)
-        if (q + 1 < a.nseg && n - n0 >= a.seg[s].N) { n0 += a.seg[s].N; ++s; }
-    }
-    segi[r] = s;
-    local[r] = n - n0;
-    wrow[r][0] = (const T*)a.seg[s].W + (int64_t)local[r] * K;
-    if (SW) wrow[r][NW - 1] = (const T*)a.seg[1].W + (int64_t)local[r] * K;
+    const RowSeg rw = SW ? RowSeg{0, n} : row_segment(a, n);
+    segi[r] = rw.s;
+    local[r] = rw.local;
+    wrow[r][0] = (const T*)pick_seg(rw.s, a.seg[0].W, a.seg[1].W, a.seg[2].W) + (int64_t)rw.local * K;
+    if (SW) wrow[r][NW - 1] = (const T*)a.seg[1].W + (int64_t)rw.local * K;
   }
   uint4 w[R][NW][CG];
 #pragma unroll
@@ -321,11 +501,11 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_staged_kernel(GemvArgs a
 #pragma unroll
     for (int c = 0; c < CG; ++c) gv[c] = ld16((const T*)a.g + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
   }
-  const int64_t t = a.uses_t ? *a.t_dev : 0;
+  const int64_t t = a.uses_t ? load_uniform(a.t_dev) : 0;
 
   // ---- staging: wave w normalises rows w, w + 4, ... (its lanes cover the row's chunks)
   for (int b = wave; b < B; b += kWaves) {
-    const int64_t xrow = a.x_rows ? a.x_rows[b] : (int64_t)b;
+    const int64_t xrow = a.x_rows ? load_uniform(a.x_rows + b) : (int64_t)b;
     const T* xp = (const T*)a.x + xrow * a.x_bstride;
     uint4 xv[CG];
 #pragma unroll
@@ -362,6 +542,7 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_staged_kernel(GemvArgs a
     }
   }
   __syncthreads();
+  advance_position(a);
   if (rbase >= a.Nrows) return;                       // after the barrier: every wave staged its rows
 
   // ---- dot products from the staged rows, four batch rows at a time
@@ -436,14 +617,16 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_staged_kernel(GemvArgs a
           s = segi[rr];
           loc = local[rr];
         }
-      const Seg& sg = a.seg[s];
-      const int64_t b = b0 + bp;
-      Elem<T>::store((T*)sg.out + b * sg.out_bstride + t * sg.t_stride + loc, out);
+      Elem<T>::store(out_ptr<T>(a, s, b0 + bp, t, loc), out);
     }
   }
 }
 
 constexpr int kStageBytes = 96 * 1024;                 // LDS for staged batch rows
+#ifndef DH_GEMV_ROW_THREADS
+#define DH_GEMV_ROW_THREADS 256
+#endif
+constexpr int kRowThreads = DH_GEMV_ROW_THREADS;      // workgroup of the single-row kernel
 
 template <typename T, int R, int CG, bool SW>
 void launch(const GemvArgs& a, hipStream_t s) {
@@ -457,12 +640,18 @@ void launch(const GemvArgs& a, hipStream_t s) {
     decode_gemv_staged_kernel<T, R, CG, SW><<<dim3(grid), dim3(kThreads), stage, s>>>(a);
     return;
   }
+  if (a.B == 1) {
+    constexpr int NT = kRowThreads;
+    const int grid1 = (a.Nrows + (NT / 64) * R - 1) / ((NT / 64) * R);
+    if (a.x_rows || a.resid_rows)
+      decode_gemv_row_kernel<T, R, CG, SW, NT, true><<<dim3(grid1), dim3(NT), 0, s>>>(a);
+    else
+      decode_gemv_row_kernel<T, R, CG, SW, NT, false><<<dim3(grid1), dim3(NT), 0, s>>>(a);
+    return;
+  }
   // batch rows per pass: as many as the activation chunks' registers allow
   constexpr int BG = CG <= 2 ? 8 : (CG <= 6 ? 4 : 2);
-  if (a.B == 1)
-    decode_gemv_kernel<T, R, CG, 1, SW><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
-  else
-    decode_gemv_kernel<T, R, CG, BG, SW><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
+  decode_gemv_kernel<T, R, CG, BG, SW><<<dim3(grid), dim3(kThreads), 0, s>>>(a);
 }
 
 template <typename T, int CG, bool SW>

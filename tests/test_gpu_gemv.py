@@ -111,14 +111,15 @@ def test_norm_swiglu(B, K, ff, dtype):
     assert rel_err(out, ref) < (1e-5 if dtype == torch.float32 else 1.5e-2)
 
 
+@pytest.mark.parametrize("B", [1, 5])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_embedding_gather_rows(dtype):
+def test_embedding_gather_rows(dtype, B):
     """x_rows / resid_rows: the first decode launch reads the token rows of the embedding."""
     from dispatcher_hybrid import fused_step
     g = torch.Generator(device=DEV).manual_seed(11)
-    V, K, N, B = 300, 256, 256, 5
+    V, K, N = 300, 256, 256
     emb = torch.randn(V, K, device=DEV, generator=g).to(dtype)
-    tok = torch.tensor([3, 299, 0, 3, 150], device=DEV)
+    tok = torch.tensor([299, 3, 0, 3, 150], device=DEV)[:B]
     W = (torch.randn(N, K, device=DEV, generator=g) / K ** 0.5).to(dtype)
     w = torch.rand(K, device=DEV, generator=g).add(0.5).to(dtype)
     out = torch.empty(B, N, device=DEV, dtype=dtype)
@@ -153,17 +154,36 @@ def test_down_projection_release_shape(B, dtype):
     assert rel_err(x, ref) < (1e-5 if dtype == torch.float32 else 1e-2)
 
 
-def test_lm_head_shape():
+@pytest.mark.parametrize("B", [1, 2])
+def test_lm_head_shape(B):
     """A vocabulary-sized output (N = 50257, not a multiple of the row tiling)."""
     from dispatcher_hybrid import fused_step
     g = torch.Generator(device=DEV).manual_seed(5)
     V, K = 50257, 1024
     W = (torch.randn(V, K, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
-    x = torch.randn(2, K, device=DEV, generator=g).to(torch.bfloat16)
-    w = torch.ones(K, device=DEV, dtype=torch.bfloat16)
-    out = torch.full((2, V), 9.0, device=DEV, dtype=torch.bfloat16)
+    x = torch.randn(B, K, device=DEV, generator=g).to(torch.bfloat16)
+    w = torch.rand(K, device=DEV, generator=g).add(0.5).to(torch.bfloat16)
+    out = torch.full((B, V), 9.0, device=DEV, dtype=torch.bfloat16)
     t_buf = torch.zeros(1, dtype=torch.long, device=DEV)
     fused_step.decode_gemv(x, [(W, out, V, 0)], t_buf, norm_weight=w)
     torch.cuda.synchronize()
     ref = _rnd(_norm(x, w, torch.bfloat16) @ W.double().T, torch.bfloat16)
     assert rel_err(out, ref) < 1e-2
+
+
+@pytest.mark.parametrize("B", [1, 3, 64])
+def test_position_advance(B):
+    """t_advance: each launch adds exactly one to the position (the decode step's last launch)."""
+    from dispatcher_hybrid import fused_step
+    g = torch.Generator(device=DEV).manual_seed(21)
+    K, N = 512, 1000                   # B = 64: 128 KB of fp32 rows, past the LDS staging limit
+    x = torch.randn(B, K, device=DEV, generator=g)
+    W = torch.randn(N, K, device=DEV, generator=g) / K ** 0.5
+    out = torch.empty(B, N, device=DEV)
+    t_buf = torch.full((1,), 41, dtype=torch.long, device=DEV)
+    pos = torch.full((1,), 7, dtype=torch.long, device=DEV)
+    for _ in range(3):
+        fused_step.decode_gemv(x, [(W, out, N, 0)], t_buf, t_advance=pos)
+    torch.cuda.synchronize()
+    assert int(pos.item()) == 10 and int(t_buf.item()) == 41
+    assert rel_err(out, x.double() @ W.double().T) < 1e-5
