@@ -58,6 +58,13 @@ __device__ __forceinline__ float wave_max(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// an element's raw bits (bf16 zero-extended), converted to fp32 separately
+__device__ __forceinline__ uint32_t raw_load(const bf16_t* p) { return *p; }
+__device__ __forceinline__ uint32_t raw_load(const float* p) { return __float_as_uint(*p); }
+template <typename T> __device__ __forceinline__ float raw_f(uint32_t r);
+template <> __device__ __forceinline__ float raw_f<bf16_t>(uint32_t r) { return __uint_as_float(r << 16); }
+template <> __device__ __forceinline__ float raw_f<float>(uint32_t r) { return __uint_as_float(r); }
+
 template <typename T, int HD>
 __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) {
   extern __shared__ float sc[];                       // scores / probabilities of the window
@@ -72,7 +79,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
   constexpr int CH = KCH <= 8 ? 16 : 8;               // pass-2 loads in flight per lane
   const int h = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t t = *a.t_dev;
+  const int64_t t = load_uniform(a.t_dev);
   if (t < 0 || t >= a.Tmax) return;                   // workgroup-uniform: nothing to do
   const int lo = a.window > 0 ? (int)max((int64_t)0, t + 1 - a.window) : 0;
   const int n = (int)t - lo + 1;
@@ -80,6 +87,27 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
   const int64_t head_off = ((int64_t)b * a.H + h) * a.Tmax * HD;  // (b, h) rows of the caches
   T* Kh = (T*)a.K + head_off;
   T* Vh = (T*)a.V + head_off;
+
+  // ---- the rotation's operands first (q, k, v pairs of this thread and the angle at t): loads
+  // return in issue order, so the rotation and the cache write below wait only for these while the
+  // key and value requests behind them are in flight
+  // (raw bits, loaded by every thread at a clamped index: a branch or a conversion here would put
+  // a wait for them ahead of the key and value requests)
+  const bool roper = tid < HD / 2;
+  uint32_t rop[8];
+  {
+    const int pt = min(tid, HD / 2 - 1);
+    const int64_t base = (int64_t)b * a.qkv_bstride + (int64_t)h * HD + 2 * pt;
+    rop[0] = raw_load((const T*)a.cos + t * (HD / 2) + pt);
+    rop[1] = raw_load((const T*)a.sin + t * (HD / 2) + pt);
+    rop[2] = raw_load((const T*)a.q + base);
+    rop[3] = raw_load((const T*)a.q + base + 1);
+    rop[4] = raw_load((const T*)a.k + base);
+    rop[5] = raw_load((const T*)a.k + base + 1);
+    rop[6] = raw_load((const T*)a.v + base);
+    rop[7] = raw_load((const T*)a.v + base + 1);
+  }
+  DH_ISSUE_FENCE();
 
   // ---- requests that need only t: this thread's first key row (pass 1) and its first block of
   // value chunks (pass 2); they fly while the new key is rotated. Rows are clamped into the cached
@@ -101,18 +129,16 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
     const int i = min(j0 + u * RPI + slot, ck);
     vrow[u] = reinterpret_cast<const uint4*>(Vh + (int64_t)(lo + i) * HD)[dg];
   }
+  DH_ISSUE_FENCE();
 
   // ---- rope of q and k at position t, cache write of (k', v) at t
-  if (tid < HD / 2) {
-    const int64_t base = (int64_t)b * a.qkv_bstride + (int64_t)h * HD;
-    const T* qp = (const T*)a.q + base;
-    const T* kp = (const T*)a.k + base;
-    const T* vp = (const T*)a.v + base;
-    const float c = Elem<T>::load((const T*)a.cos + t * (HD / 2) + tid);
-    const float s = Elem<T>::load((const T*)a.sin + t * (HD / 2) + tid);
-    const float q0 = Elem<T>::load(qp + 2 * tid), q1 = Elem<T>::load(qp + 2 * tid + 1);
-    const float k0 = Elem<T>::load(kp + 2 * tid), k1 = Elem<T>::load(kp + 2 * tid + 1);
-    const float v0 = Elem<T>::load(vp + 2 * tid), v1 = Elem<T>::load(vp + 2 * tid + 1);
+  if (roper) {
+    asm volatile("" : "+v"(rop[0]), "+v"(rop[1]), "+v"(rop[2]), "+v"(rop[3]), "+v"(rop[4]), "+v"(rop[5]),
+                 "+v"(rop[6]), "+v"(rop[7]));           // converted here, after the key/value requests
+    const float c = raw_f<T>(rop[0]), s = raw_f<T>(rop[1]);
+    const float q0 = raw_f<T>(rop[2]), q1 = raw_f<T>(rop[3]);
+    const float k0 = raw_f<T>(rop[4]), k1 = raw_f<T>(rop[5]);
+    const float v0 = raw_f<T>(rop[6]), v1 = raw_f<T>(rop[7]);
     typedef Elem<T> E;
     float qr0, qr1, kr0, kr1;
     {

@@ -253,7 +253,7 @@ __global__ __launch_bounds__(kFusedThreads) void decode_mixer_step_kernel(StepAr
   __shared__ float src_r[RPB][LMAX];           // rg_hist[t - 2^l, l, h] per (row, level)
 
   // ---- load wave 1: t and the position-independent operands
-  const int64_t t = *a.t_dev;
+  const int64_t t = load_uniform(a.t_dev);
   uint4 w[3][C];
   uint4 av[RPB][C];
   const int64_t wrow = ((int64_t)gl * H + h) * GH;
@@ -401,8 +401,10 @@ __global__ __launch_bounds__(64) void decode_gates_kernel(StepArgs a, float* sta
   const int64_t d = (int64_t)H * hd;
   const int sw = kStageHead + hd;
 
-  // ---- position-independent operands and t, in one burst
-  const int64_t t = *a.t_dev;
+  // ---- t (a scalar load, so the position-dependent requests below go out as soon as it arrives,
+  // while the weights are in flight), then the position-independent operands in one burst
+  const int64_t t = load_uniform(a.t_dev);
+  DH_ISSUE_FENCE();
   const int64_t wrow = ((int64_t)l * H + h) * GH;
   uint4 w[3][C], av[RB][C];
 #pragma unroll
@@ -418,12 +420,15 @@ __global__ __launch_bounds__(64) void decode_gates_kernel(StepArgs a, float* sta
   const uint32_t bir = Raw<T>::load((const T*)a.bi + gi);
   const uint32_t bfr = Raw<T>::load((const T*)a.bf + gi);
   const uint32_t brr = Raw<T>::load((const T*)a.br + gi);
-  if (t < 0 || t >= a.Tmax) return;                    // uniform
+  DH_ISSUE_FENCE();
+  // out-of-range t: addresses clamped, nothing stored (no early exit: a branch before the loads
+  // would make every request wait for t)
+  const bool live = t >= 0 && t < a.Tmax;             // uniform
 
   // ---- operands addressed through t: source row of B_hist, ring value and transmit gate
   const int64_t src = t - ((int64_t)1 << l);
   const bool ok = src >= 0;
-  const int64_t sc = ok ? src : 0;
+  const int64_t sc = ok && live ? src : 0;
   uint4 bv[RB][C];
   uint32_t vraw[RB][2], rraw[RB];
 #pragma unroll
@@ -437,6 +442,7 @@ __global__ __launch_bounds__(64) void decode_gates_kernel(StepArgs a, float* sta
     for (int q = 0; q < 2; ++q) vraw[r][q] = Raw<T>::load(ring + min(lane + 64 * q, hd - 1));
     rraw[r] = Raw<T>::load((const T*)a.rg_hist + ((b * a.Tmax + sc) * L + l) * H + h);
   }
+  DH_ISSUE_FENCE();
 
   // ---- the three dot products of each row, gates, staging
 #pragma unroll
@@ -464,7 +470,7 @@ __global__ __launch_bounds__(64) void decode_gates_kernel(StepArgs a, float* sta
     s1 = wave_sum(s1);
     s2 = wave_sum(s2);
     const int b = b0 + r;
-    if (b < a.B) {                                     // uniform
+    if (b < a.B && live) {                             // uniform
       float* st = stage + (((int64_t)b * H + h) * L + l) * sw;
       if (lane == 0) {
         const float okf = ok ? 1.f : 0.f;
@@ -489,7 +495,8 @@ __global__ __launch_bounds__(kMaxHd) void decode_scan_kernel(StepArgs a, const f
   const int H = a.H, L = a.L, hd = a.hd;
   const int64_t d = (int64_t)H * hd;
   const int sw = kStageHead + hd;
-  const int64_t t = *a.t_dev;
+  const int64_t t = load_uniform(a.t_dev);             // requested first, waited for last
+  DH_ISSUE_FENCE();
   const float* st = stage + ((int64_t)b * H + h) * L * sw;
   float ig[LMAX], fg[LMAX], rs[LMAX], vs[LMAX];
 #pragma unroll
@@ -501,18 +508,21 @@ __global__ __launch_bounds__(kMaxHd) void decode_scan_kernel(StepArgs a, const f
     vs[l] = sl[kStageHead + e];
   }
   const uint32_t v0raw = Raw<T>::load((const T*)a.V0 + (int64_t)b * d + (int64_t)h * hd + e);
-  if (t < 0 || t >= a.Tmax) return;                    // uniform
+  DH_ISSUE_FENCE();
+  // out-of-range t: nothing stored (no early exit: a branch here lets the compiler move the staged
+  // loads behind the wait for t)
+  const bool live = t >= 0 && t < a.Tmax;             // uniform
   T* ring = (T*)a.V_ring + (int64_t)b * a.S * d + (int64_t)h * hd + e;
   float v = Raw<T>::f(v0raw);
-  Elem<T>::store(ring + (t & 1) * d, v);
+  if (live) Elem<T>::store(ring + (t & 1) * d, v);
 #pragma unroll
   for (int l = 0; l < LMAX; ++l) {
     if (l < L) {
       v = fg[l] * v + ig[l] * rs[l] * vs[l];
-      if (l + 1 < L) Elem<T>::store(ring + (ring_offset(l + 1) + (t & ring_mask(l + 1))) * d, v);
+      if (live && l + 1 < L) Elem<T>::store(ring + (ring_offset(l + 1) + (t & ring_mask(l + 1))) * d, v);
     }
   }
-  Elem<T>::store((T*)a.Y + (int64_t)b * d + (int64_t)h * hd + e, v);
+  if (live) Elem<T>::store((T*)a.Y + (int64_t)b * d + (int64_t)h * hd + e, v);
 }
 
 template <typename T, int RPB, int C, int LMAX>
@@ -541,7 +551,7 @@ void dispatch_fused(const StepArgs& a, int rpb, int C, hipStream_t s) {
 
 template <typename T>
 __global__ __launch_bounds__(kThreads) void step_gates_kernel(StepArgs a) {
-  const int64_t t = *a.t_dev;
+  const int64_t t = load_uniform(a.t_dev);
   if (t < 0 || t >= a.Tmax) return;
   int h, l;
   block_coords(blockIdx.x, a.H, a.L, h, l);
@@ -550,7 +560,7 @@ __global__ __launch_bounds__(kThreads) void step_gates_kernel(StepArgs a) {
 
 template <typename T>
 __global__ __launch_bounds__(kThreads) void step_scan_kernel(StepArgs a) {
-  const int64_t t = *a.t_dev;
+  const int64_t t = load_uniform(a.t_dev);
   if (t < 0 || t >= a.Tmax) return;
   scan_phase<T>(a, blockIdx.x, t);
 }
