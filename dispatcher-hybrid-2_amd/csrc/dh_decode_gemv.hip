@@ -301,7 +301,8 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_kernel(GemvArgs a) {
 // the activation row and of the RMSNorm weight: three requests per weight request, all through
 // the compute unit's vector memory path, which bounds these short launches. Here each workgroup
 // requests the two rows once, one 16-byte load per thread, stages them in LDS behind one barrier,
-// and each wave reads its chunks from LDS. The small requests (activation, norm weight, residual)
+// normalises the row once (block sum of squares, then the scaled row written back in place), and
+// each wave reads its chunks from LDS. The small requests (activation, norm weight, residual)
 // go out BEFORE the weight burst: loads return in issue order, so they arrive first and the
 // staging never waits for the weights. When a row is gathered through x_rows or resid_rows (the
 // embedding), its address waits on a scalar load, so the weights go first instead (GATHER).
@@ -369,36 +370,43 @@ __global__ __launch_bounds__(NT) void decode_gemv_row_kernel(GemvArgs a) {
   const int64_t t = a.uses_t ? load_uniform(a.t_dev) : 0;
   DH_ISSUE_FENCE();
 
-  // ---- stage the activation row and the norm weight
+  // ---- stage the activation row; with a norm, the workgroup normalises it once, in place
 #pragma unroll
   for (int j = 0; j < XCH; ++j) {
     const int i = threadIdx.x + j * NT;
     if (i < nst) sx[i] = st[j];
   }
   __syncthreads();
-  uint4 xc[CG], gv[CG];
-#pragma unroll
-  for (int c = 0; c < CG; ++c) {
-    const int ch = min(lane + 64 * c, nchunk - 1);
-    xc[c] = sx[ch];
-    if (has_norm) gv[c] = sx[nchunk + ch];
-  }
-
-  // ---- RMSNorm scale: the wave's lanes cover the whole row
-  float rs = 1.f;
-  if (has_norm) {
+  if (has_norm) {                                      // uniform
+    __shared__ float red[NWV];
     float ss = 0.f;
-#pragma unroll
-    for (int c = 0; c < CG; ++c) {
+    for (int i = threadIdx.x; i < nchunk; i += NT) {
       float xf[V];
-      Vec<T>::unpack(xc[c], xf);
-      float part = 0.f;
+      Vec<T>::unpack(sx[i], xf);
 #pragma unroll
-      for (int e = 0; e < V; ++e) part += xf[e] * xf[e];
-      ss += lane + 64 * c < nchunk ? part : 0.f;
+      for (int e = 0; e < V; ++e) ss += xf[e] * xf[e];
     }
-    rs = rsqrtf(wave_sum(ss) / (float)K + a.eps);
+    ss = wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < NWV; ++w2) tot += red[w2];
+    const float rs = rsqrtf(tot / (float)K + a.eps);
+    for (int i = threadIdx.x; i < nchunk; i += NT) {
+      float xf[V], gw[V];
+      Vec<T>::unpack(sx[i], xf);
+      Vec<T>::unpack(sx[nchunk + i], gw);
+#pragma unroll
+      for (int e = 0; e < V; ++e) xf[e] = Elem<T>::round(xf[e] * rs * gw[e]);
+      sx[i] = Vec<T>::pack(xf);
+    }
+    __syncthreads();
   }
+  uint4 xc[CG];
+#pragma unroll
+  for (int c = 0; c < CG; ++c) xc[c] = sx[min(lane + 64 * c, nchunk - 1)];
+
   // ---- dot products
   float acc[R][NW];
 #pragma unroll
@@ -410,12 +418,6 @@ __global__ __launch_bounds__(NT) void decode_gemv_row_kernel(GemvArgs a) {
     const bool live = lane + 64 * c < nchunk;
     float hv[V];
     Vec<T>::unpack(xc[c], hv);
-    if (has_norm) {
-      float gw[V];
-      Vec<T>::unpack(gv[c], gw);
-#pragma unroll
-      for (int e = 0; e < V; ++e) hv[e] = Elem<T>::round(hv[e] * rs * gw[e]);
-    }
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -728,11 +730,18 @@ extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const
   a.Nrows = total;
   const int C = (K / vec + 63) / 64;
   DH_REQUIRE(C <= 12, DH_ERR_UNSUPPORTED_SHAPE, "%s: K=%d exceeds %d elements per row", who, K, 12 * 64 * vec);
-  // one output row per wave, except for very tall matrices (the vocabulary head), where four rows
-  // per wave still leave > 12k waves
-  // batched calls stage the rows once per workgroup and reuse each weight chunk across all of
-  // them, so more rows per wave pay off there
-  const int R = a.Nrows >= 16384 || (B > 1 && a.Nrows >= 2048) ? 4 : (B > 1 ? 2 : 1);
+  // Rows per wave. Single row (measured on MI355X, weights streamed from HBM): about 4 KB of
+  // weights per wave while the launch keeps >= ~1.5k waves -- two rows of K = 1024 bf16 for the
+  // 3072-row projection, one row for 1024-row outputs, for SwiGLU (whose wave already reads a gate
+  // and an up row) and for K = 2816; four rows for the vocabulary head (> 12k waves). Batched calls
+  // stage the rows once per workgroup and reuse each weight chunk across all of them, so more rows
+  // per wave pay off there.
+  const int esz = dtype == DH_BF16 ? 2 : 4;
+  int R;
+  if (B == 1)
+    R = a.Nrows >= 16384 ? 4 : (!swiglu && K * esz <= 2048 && a.Nrows >= 3072 ? 2 : 1);
+  else
+    R = a.Nrows >= 2048 ? 4 : 2;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DH_BF16) {
     if (swiglu) pick_cg<bf16_t, true>(a, C, R, s); else pick_cg<bf16_t, false>(a, C, R, s);
