@@ -4,15 +4,17 @@
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 
 Headline (`value`): steady-state batch-1 bf16 greedy decode tok/s of the 292M model at 3840-4096
-context through FusedGraphedHybridDecoder (one HIP-graph replay per token; five gfx950 launches
-per tree layer: fused RMSNorm/projections, the mixer step, out-projection + residual, RMSNorm +
-SwiGLU, down-projection + residual). A step is one decode token; prefill and graph capture are outside the timed region
+context through FusedGraphedHybridDecoder (one HIP-graph replay per token; six gfx950 launches per tree
+layer: fused RMSNorm/projections, the mixer step's gate readouts and its recurrence,
+out-projection + residual, RMSNorm + SwiGLU, down-projection + residual). A step is one decode token; prefill and graph capture are outside the timed region
 (reference scripts/benchmark_decode.py:21-28 protocol). Also reported in the same JSON line:
   decode_b16_*      lockstep batch-16 decode with temperature 0.8 / top-k 50 sampling
   prefill_*         C2: 292M bf16 forward at B=1, T=1024, fused gates vs eager
   forward_c5_*      C5: 292M bf16 forward at B=8, T=4096, fused gates vs eager (+ peak HBM)
   gate_path_c5_*    one mixer layer at the C5 shape, fused vs eager
-  roofline          dh_decode_mixer_step: algorithmic bytes / HIP-event-timed launch duration
+  roofline          dh_decode_gemv, the dominant kernel (73 of the 111 launches of a step, ~60% of
+                    its time): algorithmic bytes / HIP-event-timed launch duration
+  mixer_step        the decoder's mixer step (dh_decode_gates + dh_decode_scan) per tree layer
   step_roofline     whole decode step: bf16 weight bytes per token x tok/s vs 8 TB/s
   cpu_baseline      the oracle's eager torch decoder (reference algorithm) on the host CPU, fp32
 All inputs are synthetic (uniform token ids) and the weights are a random init of the released
@@ -35,10 +37,10 @@ HBM_PEAK_GBS = 8000.0                  # MI355X HBM3E
 MFMA_BF16_TFLOPS = 2500.0              # MI355X dense bf16
 REF_DECODE_TOK_S = 525.1               # reference FusedGraphedHybridDecoder @3900 ctx (A6000, README.md:76-81)
 EOT = 50256
-# HBM bytes per dh_decode_mixer_step launch (bf16, B=1, 12 levels): rocprofv3 --pmc FETCH_SIZE
-# (1,613,665 B after scaling by the 256 MiB copy probe's reading, x1.9997) + WRITE_SIZE (29,696 B,
-# x1.0), from profiles/decode_c3_b1_kernels.md
-TRAFFIC_MIXER_STEP = 1_643_361
+# HBM bytes per dh_decode_gemv launch, averaged over the decode step's 73 launches: rocprofv3 --pmc
+# FETCH_SIZE (3832.1 KiB x 1.99975, the factor a 256 MiB copy's reading gives) + WRITE_SIZE
+# (13.67 KiB x 1.0), from profiles/decode_c3_b1_kernels.md
+TRAFFIC_GEMV_LAUNCH = 7_861_186
 
 
 def parse():
@@ -129,12 +131,86 @@ def time_mixer(torch, mixer, x, mask, fused, reps=5):
     return (time.perf_counter() - t0) / reps * 1e3
 
 
-def decode_kernel_roofline(torch, model, dec, copies=400, reps=5):
-    """Average duration of dh_decode_mixer_step at B=1, t=4000 (all 12 levels live). The launches
-    run as they do inside the decode step: captured back to back in one HIP graph on the launch
-    stream, the graph replayed between two HIP events on that stream. The gate weights cycle
-    through `copies` distinct copies (> 256 MB in total, more than the MI355X last-level cache) so
-    every launch streams its weights from HBM. The figure includes the graph's inter-node gap."""
+def _graph_time(torch, launch, n, reps):
+    """Capture launch(0..n-1) back to back in one HIP graph on the current stream, replay it `reps`
+    times between two HIP events recorded on that stream; average microseconds per launch. The
+    figure includes the graph's inter-node gap (the per-launch floor a decode step pays)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(min(n, 8)):
+            launch(i)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(n):
+            launch(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    del graph
+    return 1e3 * e0.elapsed_time(e1) / (reps * n)
+
+
+def gemv_chain_roofline(torch, model, reps=20):
+    """dh_decode_gemv over the launches of one batch-1 decode step: the same 73 launches, shapes and
+    weights as FusedGraphedHybridDecoder's step -- per tree layer RMSNorm + [W_in; W1x; W1s],
+    linear_out + residual, RMSNorm + SwiGLU, linear_down + residual; per attention layer the same
+    with [Wq; Wk; Wv]; RMSNorm + lm_head -- on random activations, in one HIP graph. The model's
+    584 MB of weights exceed the 256 MB last-level cache, so every launch streams its weights from
+    HBM as in decode. Returns (algorithmic bytes per step, microseconds per launch, launches)."""
+    from dispatcher_hybrid import fused_step
+    from dispatcher_hybrid.modeling_dispatcher import AttentionBlock
+    dev = next(model.parameters()).device
+    dt = torch.bfloat16
+    cfg = model.config
+    d, ff = cfg.d_model, cfg.dim_feedforward
+    t_buf = torch.zeros(1, dtype=torch.long, device=dev)
+    x = torch.randn(1, d, device=dev, dtype=dt)
+    xr = torch.randn(1, d, device=dev, dtype=dt)
+    h = torch.randn(1, ff, device=dev, dtype=dt) * 0.1
+    o = torch.empty(1, 3 * d + ff, device=dev, dtype=dt)
+    logits = torch.empty(1, model.lm_head.weight.shape[0], device=dev, dtype=dt)
+    calls, nbytes = [], 0
+
+    def add(xin, segs, **kw):
+        nonlocal nbytes
+        K = xin.shape[1]
+        rows = sum(w.shape[0] for w, _, _, _ in segs)
+        nbytes += 2 * (rows * K + K + (K if kw.get("norm_weight") is not None else 0)
+                       + (rows // 2 if kw.get("swiglu") else rows) + (rows if kw.get("resid") is not None else 0))
+        calls.append(lambda: fused_step.decode_gemv(xin, segs, t_buf, **kw))
+
+    for blk in model.blocks:
+        if isinstance(blk, AttentionBlock):
+            at = blk.attn
+            ws = [at.linear_q.weight, at.linear_k.weight, at.linear_v.weight]
+            wo = at.linear_out.weight
+        else:
+            mx = blk.mixer
+            ws = [mx.linear_in.weight, mx.gate_hidden.weight, mx.gate_hidden_src.weight]
+            wo = mx.linear_out.weight
+        add(x, [(w, o[:, i * d:], o.shape[1], 0) for i, w in enumerate(ws)], norm_weight=blk.norm1.weight)
+        add(x, [(wo, xr, d, 0)], resid=xr)
+        f = blk.ffn
+        add(x, [(f.linear_gate.weight, o, ff, 0), (f.linear_up.weight, o, ff, 0)],
+            norm_weight=blk.norm2.weight, swiglu=True)
+        add(h, [(f.linear_down.weight, xr, d, 0)], resid=xr)
+    add(x, [(model.lm_head.weight, logits, logits.shape[1], 0)], norm_weight=model.norm_out.weight)
+    us = _graph_time(torch, lambda i: calls[i](), len(calls), reps)
+    return nbytes, us, len(calls)
+
+
+def mixer_step_time(torch, model, dec, copies=400, reps=5):
+    """The decoder's mixer step (dh_decode_gates + dh_decode_scan, two launches) at B=1, t=4000 (all
+    12 levels live), the gate weights cycling through `copies` distinct copies (> 256 MB, more than
+    the last-level cache). Returns (algorithmic bytes per step, microseconds per step)."""
     from dispatcher_hybrid import fused_step
     dev = next(model.parameters()).device
     mx = next(b.mixer for b in model.blocks if hasattr(b, "mixer"))
@@ -149,36 +225,16 @@ def decode_kernel_roofline(torch, model, dec, copies=400, reps=5):
     B_hist = torch.zeros(1, 4096, GH, device=dev, dtype=torch.bfloat16)
     rg = torch.zeros(1, 4096, L, H, device=dev, dtype=torch.bfloat16)
     ring = torch.zeros(1, cache.S, d, device=dev, dtype=torch.bfloat16)
+    stage = torch.zeros(fused_step.stage_floats(1, H, L, d // H), device=dev)
 
     def launch(i):
         W = Ws[i % copies]
-        fused_step.decode_mixer_step(A, B_hist, W[0], W[1], W[2], bi, bf, br, t_buf, rg, ring, V0, Y)
+        fused_step.decode_gates_scan(A, B_hist, W[0], W[1], W[2], bi, bf, br, t_buf, rg, ring, V0, Y, stage)
 
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for i in range(8):
-            launch(i)
-    torch.cuda.current_stream().wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(copies):
-            launch(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
-        graph.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    avg_us = 1e3 * e0.elapsed_time(e1) / (reps * copies)
-    del graph
+    us = 2 * _graph_time(torch, launch, copies, reps)       # per step: two launches
     s = 2
-    B = 1
-    nbytes = 3 * L * H * GH * s + 3 * L * H * s + B * (L * GH + GH + 2 * L * H + 2 * L * d + 2 * d) * s
-    return nbytes, avg_us, reps * copies
+    nbytes = 3 * L * H * GH * s + 3 * L * H * s + (L * GH + GH + 2 * L * H + 2 * L * d + 2 * d) * s
+    return nbytes, us
 
 
 def copy_probe(torch, dev, mib=256):
@@ -260,13 +316,20 @@ def main():
                             "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4),
                             "what": "bf16 weight bytes per decode token (584,316,928 B) x tok/s"}
 
-    nbytes, avg_us, nl = decode_kernel_roofline(torch, model, dec1)
-    achieved = nbytes / (avg_us * 1e-6) / 1e9
-    out["roofline"] = {"kernel": "dh_decode_mixer_step (decode_mixer_step_kernel<bf16,1,2,12>)",
+    mb, mus = mixer_step_time(torch, model, dec1)
+    out["mixer_step"] = {"kernels": "dh_decode_gates + dh_decode_scan (one tree layer, B=1, t=4000)",
+                         "us": round(mus, 3), "bytes": mb,
+                         "achieved_gbs": round(mb / (mus * 1e-6) / 1e9, 1)}
+    log(f"mixer step (gates + scan): {mus:.2f} us per layer")
+    nbytes, avg_us, nl = gemv_chain_roofline(torch, model)
+    achieved = nbytes / nl / (avg_us * 1e-6) / 1e9
+    out["roofline"] = {"kernel": "dh_decode_gemv: the 73 launches of one batch-1 decode step "
+                                 "(decode_gemv_row_kernel instantiations)",
                        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_MIXER_STEP,
-                       "bytes_per_launch": nbytes, "avg_launch_us": round(avg_us, 3), "launches_timed": nl}
-    log(f"decode mixer kernel: {avg_us:.2f} us/launch, {achieved:.0f} GB/s")
+                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_GEMV_LAUNCH,
+                       "bytes_per_launch": round(nbytes / nl), "bytes_per_step": nbytes,
+                       "avg_launch_us": round(avg_us, 3), "launches_per_step": nl}
+    log(f"decode GEMV chain: {nl} launches, {avg_us:.2f} us/launch, {achieved:.0f} GB/s")
     del dec1
     torch.cuda.empty_cache()
 
