@@ -8,7 +8,7 @@ context through FusedGraphedHybridDecoder (one HIP-graph replay per token; six g
 layer: fused RMSNorm/projections, the mixer step's gate readouts and its recurrence,
 out-projection + residual, RMSNorm + SwiGLU, down-projection + residual). A step is one decode token; prefill and graph capture are outside the timed region
 (reference scripts/benchmark_decode.py:21-28 protocol). Also reported in the same JSON line:
-  decode_b16_*      lockstep batch-16 decode with temperature 0.8 / top-k 50 sampling
+  decode_b16_*      lockstep batch-16 decode with temperature 0.8 / top-k 50 sampling (dh_sample_topk)
   prefill_*         C2: 292M bf16 forward at B=1, T=1024, fused gates vs eager
   forward_c5_*      C5: 292M bf16 forward at B=8, T=4096, fused gates vs eager (+ peak HBM)
   gate_path_c5_*    one mixer layer at the C5 shape, fused vs eager
@@ -86,10 +86,8 @@ def time_decode(torch, model, batch, prompt, warmup, steps, sample):
     def next_tok(lg):
         if not sample:
             return fused_step.argmax_tokens(lg)           # device argmax (same token as torch's)
-        lg = lg.float() / 0.8
-        kth = torch.topk(lg, 50, dim=-1).values[:, -1:]
-        lg = lg.masked_fill(lg < kth, float("-inf"))
-        return torch.multinomial(torch.softmax(lg, dim=-1), 1)[:, 0]
+        # temperature 0.8 / top-k 50 sampling on the device, draws keyed by (seed, position, row)
+        return fused_step.sample_tokens(lg, 0.8, 50, 5, dec.t_buf)
 
     for _ in range(warmup):
         logits = dec.step(next_tok(logits))

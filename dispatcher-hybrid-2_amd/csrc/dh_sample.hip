@@ -98,7 +98,261 @@ __global__ __launch_bounds__(64) void argmax_final(const Cand* cand, int nslice,
   if (lane == 63) out[b] = bidx;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Temperature / top-k sampling (reference modeling_dispatcher.py:426-441, the do_sample branch):
+//   l   = float(logits[b]) / temperature
+//   l_i = -inf where l_i < kth, kth = the top_k-th largest l (every element equal to kth stays)
+//   out[b] ~ Categorical(softmax(l))
+// One workgroup (16 wave64s) per row, the row held in registers (thread t owns elements
+// [64t, 64t + 64), kept as order-preserving 32-bit keys; slots past V hold key 0, below every number).
+// kth, exactly: tau = the top_k-th largest of the 1024 per-thread maxima is a lower bound (at least
+// top_k elements are >= tau), so kth is the top_k-th largest of the elements >= tau; those are
+// compacted into LDS (usually a few hundred) and bitonic-sorted as order-preserving 32-bit keys.
+// When they exceed the LDS buffer (or top_k > 1024), a binary search over the key space with
+// block-wide counts finds kth instead. Then weights exp(l_i - max) on the kept elements, a block
+// prefix scan of the per-thread sums, and one uniform draw u in [0, 1) per row from Philox4x32-10
+// (Salmon et al., SC'11) keyed by the seed with counter (offset, row): the token is the element
+// whose cumulative weight interval, in index order, holds u * sum.
+// ---------------------------------------------------------------------------------------------
+constexpr int kST = 1024;                 // threads per row
+constexpr int kSPT = 64;                  // elements per thread: V <= 65536
+constexpr int kCap = 4096;                // candidate keys sorted in LDS
+
+__device__ __forceinline__ uint32_t order_key(float f) {   // a < b  <=>  key(a) < key(b)
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Philox4x32-10: first output word for key `seed` and counter (ctr_lo, ctr_hi, c2, 0)
+__device__ __forceinline__ uint32_t philox4x32_10(uint64_t seed, uint64_t ctr, uint32_t c2) {
+  uint32_t x0 = (uint32_t)ctr, x1 = (uint32_t)(ctr >> 32), x2 = c2, x3 = 0u;
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = (uint64_t)0xD2511F53u * x0;
+    const uint64_t p1 = (uint64_t)0xCD9E8D57u * x2;
+    const uint32_t y0 = (uint32_t)(p1 >> 32) ^ x1 ^ k0;
+    const uint32_t y2 = (uint32_t)(p0 >> 32) ^ x3 ^ k1;
+    x1 = (uint32_t)p1;
+    x3 = (uint32_t)p0;
+    x0 = y0;
+    x2 = y2;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return x0;
+}
+
+// block-wide helpers over the kST threads; `red` holds kST / 64 entries; every thread gets the result
+__device__ __forceinline__ float block_max(float v, float* red) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int w = 1; w < kST / 64; ++w) m = fmaxf(m, red[w]);
+  return m;
+}
+// exclusive prefix (in thread order) and total of a per-thread value
+template <typename V>
+__device__ __forceinline__ V block_scan(V v, V* red, V& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  V incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const V u = __shfl_up(incl, o);
+    if (lane >= o) incl += u;
+  }
+  __syncthreads();
+  if (lane == 63) red[wave] = incl;
+  __syncthreads();
+  V base = 0;
+  total = 0;
+#pragma unroll
+  for (int w = 0; w < kST / 64; ++w) {
+    base += w < wave ? red[w] : (V)0;
+    total += red[w];
+  }
+  return base + incl - v;
+}
+
+// descending bitonic sort of buf[0, n), n a power of two; callers synchronise before
+__device__ __forceinline__ void bitonic_desc(uint32_t* buf, int n) {
+  for (int size = 2; size <= n; size <<= 1)
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < (n >> 1); i += kST) {
+        const int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1));
+        const int hi = lo + stride;
+        const uint32_t a = buf[lo], b = buf[hi];
+        const bool desc = (lo & size) == 0;
+        if (desc ? (a < b) : (a > b)) {
+          buf[lo] = b;
+          buf[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kST) void sample_topk_kernel(const T* logits, int64_t row_stride, int V,
+                                                          float temperature, int top_k, uint64_t seed,
+                                                          const int64_t* offset_dev, int64_t* out) {
+  __shared__ uint32_t buf[kCap + 1];                   // + a slot for unselected writes
+  __shared__ float fred[kST / 64];
+  __shared__ uint32_t ured[kST / 64];
+  __shared__ int chosen, fallback;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const T* row = logits + (int64_t)b * row_stride;
+  const int i0 = tid * kSPT;                           // this thread's elements: [i0, i0 + kSPT)
+  const int nv = min(max(V - i0, 0), kSPT);
+  const int64_t off = offset_dev ? load_uniform(offset_dev) : 0;
+
+  // ---- the chunk as order keys of l = float(x) / temperature (key 0, below every number, past V).
+  // Raw buffer loads: reads past the row's V elements return zero without touching memory.
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(row), (short)0, (int)(V * (int)sizeof(T)), 0x00020000);
+  constexpr int EPC = 16 / (int)sizeof(T);             // elements per 16-byte load
+  uint32_t xk[kSPT];
+#pragma unroll
+  for (int c = 0; c < kSPT / EPC; ++c) {
+    const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   rsrc, (uint32_t)(i0 * (int)sizeof(T)) + c * 16, 0, 0));
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      if constexpr (sizeof(T) == 2)
+        xk[c * EPC + e] = (e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16);
+      else
+        xk[c * EPC + e] = w[e];
+    }
+  }
+  uint32_t kmax = 0u;
+#pragma unroll
+  for (int j = 0; j < kSPT; ++j) {
+    xk[j] = j < nv ? order_key(__uint_as_float(xk[j]) / temperature) : 0u;
+    kmax = max(kmax, xk[j]);
+  }
+  if (tid == 0) {
+    chosen = 0x7fffffff;
+    fallback = -1;
+  }
+  uint32_t bm = kmax;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) bm = max(bm, (uint32_t)__shfl_xor((int)bm, o));
+  if ((tid & 63) == 0) ured[tid >> 6] = bm;
+  __syncthreads();
+  uint32_t mkey = ured[0];
+#pragma unroll
+  for (int w = 1; w < kST / 64; ++w) mkey = max(mkey, ured[w]);
+  const float M = key_value(mkey);
+
+  // ---- kth largest (exact), as a key
+  uint32_t kkey = 0u;                                  // 0: keep every element
+  if (top_k > 0 && top_k < V) {                        // uniform
+    bool found = false;
+    if (top_k <= kST) {
+      buf[tid] = kmax;
+      __syncthreads();
+      bitonic_desc(buf, kST);
+      const uint32_t tau = buf[top_k - 1];
+      uint32_t c = 0;
+#pragma unroll
+      for (int j = 0; j < kSPT; ++j) c += (xk[j] >= tau && xk[j] != 0u) ? 1u : 0u;
+      uint32_t C;
+      uint32_t r = block_scan(c, ured, C);             // (its barriers also end the reads of buf)
+      if (C <= (uint32_t)kCap) {
+#pragma unroll
+        for (int j = 0; j < kSPT; ++j) {              // branch-free: unselected keys go to buf[kCap]
+          const bool take = xk[j] >= tau && xk[j] != 0u;
+          buf[take ? r : kCap] = xk[j];
+          r += take ? 1u : 0u;
+        }
+        int n = 64;
+        while (n < (int)C) n <<= 1;
+        for (int i = (int)C + tid; i < n; i += kST) buf[i] = 0u;
+        __syncthreads();
+        bitonic_desc(buf, n);
+        kkey = buf[top_k - 1];
+        found = true;
+      }
+    }
+    if (!found) {                                      // uniform: the largest v with count(key >= v) >= top_k
+      uint32_t lo = 1u, hi = mkey;
+      while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo + 1u) >> 1);
+        uint32_t c = 0;
+#pragma unroll
+        for (int j = 0; j < kSPT; ++j) c += xk[j] >= mid ? 1u : 0u;
+        uint32_t cnt;
+        (void)block_scan(c, ured, cnt);
+        if (cnt >= (uint32_t)top_k) lo = mid; else hi = mid - 1u;
+      }
+      kkey = lo;
+    }
+  }
+  // kept: l >= kth as floats (the reference's mask; -0.0 and +0.0 compare equal), weights in place
+  const float kth = kkey ? key_value(kkey) : -INFINITY;
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kSPT; ++j) {
+    const float l = key_value(xk[j]);
+    const float w = (xk[j] != 0u && l >= kth && l > -INFINITY) ? __expf(l - M) : 0.f;
+    xk[j] = __float_as_uint(w);
+    s += w;
+  }
+  float total;
+  const float excl = block_scan(s, fred, total);
+
+  // ---- the draw: the element whose cumulative interval (index order) holds u * total
+  const uint32_t rnd = philox4x32_10(seed, (uint64_t)off, (uint32_t)b);
+  const float target = (float)(rnd >> 8) * 0x1.0p-24f * total;
+  if (s > 0.f) {
+    int hit = 0x7fffffff, last = -1;
+    float c = excl;
+#pragma unroll
+    for (int j = 0; j < kSPT; ++j) {
+      const float w = __uint_as_float(xk[j]);
+      const bool pos = w > 0.f;
+      if (pos && hit == 0x7fffffff && target >= c && target < c + w) hit = i0 + j;
+      last = pos ? i0 + j : last;
+      c += w;
+    }
+    if (hit != 0x7fffffff) atomicMin(&chosen, hit);
+    atomicMax(&fallback, last);
+  }
+  __syncthreads();
+  if (tid == 0) out[b] = chosen != 0x7fffffff ? chosen : (fallback >= 0 ? fallback : 0);
+}
+
 }  // namespace
+
+extern "C" int dh_sample_topk(int dtype, const void* logits, int64_t row_stride, int B, int V, float temperature,
+                              int top_k, uint64_t seed, const int64_t* offset_dev, int64_t* out, void* stream) {
+  const char* who = "dh_sample_topk";
+  DH_REQUIRE(dtype == DH_F32 || dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d", who, dtype);
+  DH_REQUIRE(B >= 1 && B <= 65535 && V >= 1 && row_stride >= V, DH_ERR_INVALID_ARG, "%s: B=%d V=%d row_stride=%lld",
+             who, B, V, (long long)row_stride);
+  DH_REQUIRE(V <= kST * kSPT, DH_ERR_UNSUPPORTED_SHAPE, "%s: V=%d exceeds %d", who, V, kST * kSPT);
+  DH_REQUIRE(top_k >= 0 && top_k <= V, DH_ERR_INVALID_ARG, "%s: top_k=%d not in [0, V=%d] (0: no top-k)", who,
+             top_k, V);
+  DH_REQUIRE(temperature > 0.f && temperature < INFINITY, DH_ERR_INVALID_ARG, "%s: temperature %g must be positive",
+             who, (double)temperature);
+  DH_REQUIRE(logits && out, DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == DH_BF16)
+    sample_topk_kernel<bf16_t><<<B, kST, 0, s>>>((const bf16_t*)logits, row_stride, V, temperature, top_k, seed,
+                                                  offset_dev, out);
+  else
+    sample_topk_kernel<float><<<B, kST, 0, s>>>((const float*)logits, row_stride, V, temperature, top_k, seed,
+                                                 offset_dev, out);
+  return dh_check_launch(who);
+}
 
 extern "C" int64_t dh_argmax_workspace_bytes(int B, int V) {
   return (int64_t)B * ((V + kSlice - 1) / kSlice) * (int64_t)sizeof(Cand);

@@ -255,3 +255,32 @@ def argmax_tokens(logits, out=None):
 
 
 _ARGMAX_WS = {}           # per-device candidate buffer of argmax_tokens, grown on demand
+
+
+def sample_tokens(logits, temperature=1.0, top_k=None, seed=0, offset=None, out=None):
+    """Temperature / top-k sampling on the device (``dh_sample_topk``), the do_sample branch of
+    fast_generate (reference modeling_dispatcher.py:426-441): logits.float() / temperature, every
+    element below the top_k-th largest masked out (ties with it kept), one draw per row from
+    softmax. The draw of row b comes from Philox4x32-10 keyed by `seed` with counter (offset[0], b):
+    pass the decoder's device position as `offset` so each step draws afresh (also under graph
+    replay). logits: (B, V) fp32 or bf16, unit inner stride, V <= 65536. Returns int64 `out`."""
+    _hip.require_gpu(logits, "sample_tokens")
+    if logits.dim() != 2 or logits.stride(-1) != 1:
+        raise ValueError("sample_tokens: logits must be (B, V) with a unit inner stride")
+    B, V = logits.shape
+    k = 0 if top_k is None else int(top_k)
+    if not 0 < k <= V and top_k is not None:
+        raise ValueError(f"sample_tokens: top_k={top_k} out of range for {V} logits")
+    if not temperature > 0:
+        raise ValueError(f"sample_tokens: temperature {temperature} must be positive")
+    if offset is not None and (offset.dtype != torch.long or offset.device != logits.device):
+        raise ValueError("sample_tokens: offset must be an int64 tensor on the logits' device")
+    if out is None:
+        out = torch.empty(B, dtype=torch.long, device=logits.device)
+    if out.dtype != torch.long or out.numel() != B or not out.is_contiguous():
+        raise ValueError("sample_tokens: out must be a contiguous int64 tensor of B elements")
+    st = _hip.lib.dh_sample_topk(_hip.dtype_code(logits.dtype), _hip.ptr(logits), logits.stride(0), B, V,
+                                 ctypes.c_float(float(temperature)), k, ctypes.c_uint64(int(seed) & (2 ** 64 - 1)),
+                                 _hip.ptr(offset), _hip.ptr(out), _hip.stream_handle(logits.device))
+    _hip.check(st, "dh_sample_topk")
+    return out

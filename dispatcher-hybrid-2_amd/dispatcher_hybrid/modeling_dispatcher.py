@@ -442,14 +442,23 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
         logits = dec.prefill(ids)[:, -1]                     # ids is 2-D: (B, T, V) -> (B, V)
         finished = torch.zeros(Bb, dtype=torch.bool, device=ids.device)
         out = [ids]
-        # greedy picks through the fused decoder take the device argmax kernel: a positive
-        # temperature and top-k masking never move the maximum, so the tokens are the same
-        device_argmax = None
-        if not do_sample and isinstance(dec, FusedGraphedHybridDecoder):
-            device_argmax = dec._fused_step.argmax_tokens
+        # Through the fused decoder the next token is picked on the device. Greedy: the argmax
+        # kernel (a positive temperature and top-k masking never move the maximum, so the tokens
+        # are the same). Sampling: the top-k sampler, its draws keyed by a seed taken from torch's
+        # generator (torch.manual_seed reproduces a run) and the decoder's device position; the
+        # stream of draws is not torch.multinomial's.
+        device_pick = None
+        if isinstance(dec, FusedGraphedHybridDecoder):
+            fs = dec._fused_step
+            if not do_sample:
+                device_pick = fs.argmax_tokens
+            else:
+                seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+                temp = max(temperature, 1e-6)
+                device_pick = lambda lg: fs.sample_tokens(lg, temp, top_k, seed, dec.t_buf)
         for _ in range(max_new_tokens):
-            if device_argmax is not None:
-                nxt = device_argmax(logits)
+            if device_pick is not None:
+                nxt = device_pick(logits)
             else:
                 logits = logits.float() / max(temperature, 1e-6)
                 if top_k is not None:

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 3
+#define DH_ABI_VERSION 4
 
 enum dh_status {
   DH_OK = 0,
@@ -212,6 +212,20 @@ int dh_decode_scan(int dtype, const void* V0, const float* stage, const int64_t*
 int64_t dh_argmax_workspace_bytes(int B, int V);
 int dh_argmax(int dtype, const void* logits, int64_t row_stride, int B, int V, int64_t* out, void* workspace,
               int64_t workspace_bytes, void* stream);
+
+/*
+ * Temperature / top-k sampling of the next token, on the device. Replaces the do_sample branch of
+ * fast_generate (reference dispatcher_hybrid/modeling_dispatcher.py:426-441):
+ *   l = float(logits[b]) / temperature;  l_i = -inf where l_i < kth (kth = the top_k-th largest l;
+ *   every element equal to kth stays; top_k 0 = no top-k);  out[b] ~ Categorical(softmax(l)).
+ * The uniform draw of row b comes from Philox4x32-10 keyed by `seed` with counter
+ * (*offset_dev, b) (offset_dev nullable: counter 0), so a captured graph that advances the offset
+ * draws afresh on every replay; the stream of draws is not torch's. One workgroup per row;
+ * V <= 65536, 0 <= top_k <= V, temperature > 0; logits must be finite or -inf (a row with no
+ * finite logit yields token 0).
+ */
+int dh_sample_topk(int dtype, const void* logits, int64_t row_stride, int B, int V, float temperature, int top_k,
+                   uint64_t seed, const int64_t* offset_dev, int64_t* out, void* stream);
 
 /*
  * The two halves of dh_decode_mixer_step as separate launches, with the reference's own buffer

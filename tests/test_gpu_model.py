@@ -168,6 +168,35 @@ def test_fast_generate_fused_equals_eager_greedy():
     assert torch.equal(auto, eager)
 
 
+def test_fast_generate_fused_sampling_support_and_reproducibility():
+    """do_sample through the fused decoder draws on the device (dh_sample_topk): every generated
+    token lies in the top-k set of the logits at its position (teacher-forced fp32 oracle forward
+    over the generated sequence), torch.manual_seed reproduces a run, and eos freezes rows."""
+    cfgd, sd = tiny("tiny_a")
+    m = product_model(cfgd, sd, device=DEV)
+    spec = te.Spec(m.config)
+    prompt = torch.randint(0, cfgd["vocab_size"] - 1, (1, 12), generator=torch.Generator().manual_seed(1))
+    k, T, n = 5, 0.7, 20
+    torch.manual_seed(42)
+    out = m.fast_generate(prompt.to(DEV), max_new_tokens=n, do_sample=True, temperature=T, top_k=k,
+                          num_return_sequences=4, decoder="fused")
+    torch.manual_seed(42)
+    again = m.fast_generate(prompt.to(DEV), max_new_tokens=n, do_sample=True, temperature=T, top_k=k,
+                            num_return_sequences=4, decoder="fused")
+    assert torch.equal(out, again)
+    assert out.shape == (4, 12 + n)
+    logits = te.forward(sd, spec, out.cpu())                            # (4, 32, V) fp32
+    live = torch.ones(4, dtype=torch.bool)     # a generated EOT is doc-masked only by the forward
+    for t in range(12, 12 + n):
+        l = logits[:, t - 1] / T
+        kth = torch.topk(l, k, dim=-1).values[:, -1]
+        tok = out[:, t].cpu()
+        inside = l.gather(1, tok[:, None])[:, 0] >= kth - 1e-5
+        assert bool((inside | ~live).all()), t
+        live &= tok != cfgd["eot_token"]
+    assert len({tuple(r) for r in out[:, 12:].tolist()}) > 1           # rows diverge
+
+
 def test_fused_decoder_context_exhausted_raises():
     from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder
     cfgd, sd = tiny("tiny_b")

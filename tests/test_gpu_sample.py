@@ -1,6 +1,14 @@
-"""dh_argmax (greedy next token on the device) against torch.argmax, the call it replaces in
-fast_generate's greedy branch (reference dispatcher_hybrid/modeling_dispatcher.py:426-441):
-same index bit for bit, including ties (first index) and NaN (first NaN)."""
+"""Next-token selection on the device, against the calls it replaces in fast_generate (reference
+dispatcher_hybrid/modeling_dispatcher.py:426-441).
+
+dh_argmax vs torch.argmax: same index bit for bit, including ties (first index) and NaN (first NaN).
+dh_sample_topk vs logits.float() / T, torch.topk masking, softmax, multinomial: its random stream
+is not torch's, so it is checked by (1) support -- every draw lies in the set torch's own top-k
+mask keeps, ties at the k-th value included -- and (2) distribution -- a chi-square test of many
+draws against the float64 softmax of the masked logits (6-sigma bound; the draws are a fixed
+function of the seeds, so the outcome is deterministic)."""
+
+import math
 
 import pytest
 import torch
@@ -53,3 +61,153 @@ def test_argmax_large_vocabulary():
     x = torch.randn(3, 200003, device=DEV, generator=g)
     x[1, 199999] = 100.0
     assert torch.equal(fused_step.argmax_tokens(x), x.argmax(-1))
+
+
+def _kept_and_probs(logits, temperature, top_k):
+    """The reference's masking and softmax (modeling_dispatcher.py:454-459) on the same device."""
+    l = logits.float() / temperature
+    if top_k is not None:
+        kth = torch.topk(l, top_k, dim=-1).values[:, -1:]
+        l = l.masked_fill(l < kth, float("-inf"))
+    return torch.isfinite(l), torch.softmax(l.double(), dim=-1)
+
+
+def _chi2_ok(draws, p, label):
+    """draws: int64 tokens of one distribution p (V,) float64. Categories with expected count < 5
+    are pooled. Passes when chi2 < df + 6 sqrt(2 df)."""
+    n = draws.numel()
+    obs = torch.bincount(draws.cpu(), minlength=p.numel()).double()
+    exp = p.cpu() * n
+    big = exp >= 5
+    o = torch.cat([obs[big], obs[~big].sum().view(1)])
+    e = torch.cat([exp[big], exp[~big].sum().view(1)])
+    keep = e > 0
+    o, e = o[keep], e[keep]
+    chi2 = float(((o - e) ** 2 / e).sum())
+    df = max(int(keep.sum()) - 1, 1)
+    bound = df + 6 * math.sqrt(2 * df)
+    print(f"{label}: n={n} categories={df + 1} chi2={chi2:.1f} bound={bound:.1f}", flush=True)
+    assert chi2 < bound, (label, chi2, bound)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sample_topk_distribution_with_ties(dtype):
+    """top_k = 50 of 1000 at T = 0.8, with four logits tied at the 50th value: every draw is kept by
+    torch's mask (all four ties included) and the frequencies follow its softmax."""
+    from dispatcher_hybrid import fused_step
+    g = torch.Generator(device=DEV).manual_seed(7)
+    V, k, T, rows = 1000, 50, 0.8, 8192
+    base = torch.randn(V, device=DEV, generator=g) * 2
+    order = base.argsort(descending=True)
+    base[order[k - 2:k + 2]] = float(base[order[k - 2]])               # ties across the boundary
+    logits = base.to(dtype).expand(rows, V).contiguous()
+    kept, p = _kept_and_probs(logits[:1], T, k)
+    assert int(kept.sum()) >= k + 2
+    off = torch.zeros(1, dtype=torch.long, device=DEV)
+    draws = []
+    for step in range(4):
+        off.fill_(1000 + step)
+        draws.append(fused_step.sample_tokens(logits, T, k, seed=123, offset=off))
+    d = torch.cat(draws)
+    torch.cuda.synchronize()
+    assert bool(kept[0, d].all()), "a draw outside the top-k set"
+    tied = order[k - 2:k + 2]
+    assert all(int((d == i).sum()) > 0 for i in tied.tolist())       # every tie can be drawn
+    _chi2_ok(d, p[0], f"top-k {dtype}")
+
+
+def test_sample_full_softmax_and_temperature():
+    """No top-k (every logit kept) at T = 1.3 over 300 logits."""
+    from dispatcher_hybrid import fused_step
+    g = torch.Generator(device=DEV).manual_seed(8)
+    V, T, rows = 300, 1.3, 16384
+    base = torch.randn(V, device=DEV, generator=g) * 1.5
+    logits = base.expand(rows, V).contiguous()
+    _, p = _kept_and_probs(logits[:1], T, None)
+    d = fused_step.sample_tokens(logits, T, None, seed=99, offset=None)
+    torch.cuda.synchronize()
+    assert int(d.min()) >= 0 and int(d.max()) < V
+    _chi2_ok(d, p[0], "full softmax")
+
+
+@pytest.mark.parametrize("V,k", [(5000, 2000), (50257, 50)])
+def test_sample_wide_top_k_and_all_ties(V, k):
+    """top_k > 1024 (the kth found by the exact key-space search) and a row of one repeated value
+    (every element ties with the kth: all of them kept, drawn uniformly)."""
+    from dispatcher_hybrid import fused_step
+    g = torch.Generator(device=DEV).manual_seed(V)
+    rows = 4096
+    if V == 5000:
+        base = torch.randn(V, device=DEV, generator=g)
+    else:
+        base = torch.full((V,), 0.75, device=DEV)
+    logits = base.to(torch.bfloat16).expand(rows, V).contiguous()
+    kept, p = _kept_and_probs(logits[:1], 1.0, k)
+    d = fused_step.sample_tokens(logits, 1.0, k, seed=5, offset=None)
+    torch.cuda.synchronize()
+    assert bool(kept[0, d].all())
+    if V == 5000:
+        _chi2_ok(d, p[0], "top-k 2000")
+    else:
+        assert int(kept.sum()) == V
+        assert d.unique().numel() > rows * 0.9                           # ~uniform over 50257
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sample_release_vocab_support(dtype):
+    """The C4 setting: 16 rows of 50257 logits, T = 0.8, top-k 50, 32 steps keyed by an advancing
+    device position: every draw inside its row's top-k set, and the draws vary."""
+    from dispatcher_hybrid import fused_step
+    g = torch.Generator(device=DEV).manual_seed(3)
+    logits = (torch.randn(16, 50257, device=DEV, generator=g) * 3).to(dtype)
+    kept, _ = _kept_and_probs(logits, 0.8, 50)
+    pos = torch.full((1,), 3840, dtype=torch.long, device=DEV)
+    seen = []
+    for _ in range(32):
+        d = fused_step.sample_tokens(logits, 0.8, 50, seed=2024, offset=pos)
+        seen.append(d.clone())
+        pos += 1
+    d = torch.stack(seen)
+    torch.cuda.synchronize()
+    assert bool(kept.gather(1, d.T).all())
+    assert d.unique().numel() > 50
+
+
+def test_sample_deterministic_and_keyed():
+    from dispatcher_hybrid import fused_step
+    g = torch.Generator(device=DEV).manual_seed(4)
+    logits = torch.randn(64, 4000, device=DEV, generator=g)
+    o1 = torch.full((1,), 11, dtype=torch.long, device=DEV)
+    o2 = torch.full((1,), 12, dtype=torch.long, device=DEV)
+    a = fused_step.sample_tokens(logits, 1.0, 100, seed=1, offset=o1)
+    b = fused_step.sample_tokens(logits, 1.0, 100, seed=1, offset=o1)
+    c = fused_step.sample_tokens(logits, 1.0, 100, seed=1, offset=o2)
+    e = fused_step.sample_tokens(logits, 1.0, 100, seed=2, offset=o1)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert not torch.equal(a, c) and not torch.equal(a, e)
+
+
+def test_sample_top1_and_tiny_temperature_are_argmax():
+    from dispatcher_hybrid import fused_step
+    g = torch.Generator(device=DEV).manual_seed(6)
+    logits = torch.randn(32, 50257, device=DEV, generator=g).to(torch.bfloat16)
+    ref = logits.argmax(-1)
+    top1 = fused_step.sample_tokens(logits, 0.9, 1, seed=3)
+    cold = fused_step.sample_tokens(logits, 1e-6, None, seed=3)
+    torch.cuda.synchronize()
+    uniq = [(logits[r] == logits[r].max()).sum().item() == 1 for r in range(32)]
+    for r in range(32):
+        if uniq[r]:
+            assert int(top1[r]) == int(ref[r]) and int(cold[r]) == int(ref[r])
+
+
+def test_sample_rejects_bad_arguments():
+    from dispatcher_hybrid import fused_step
+    x = torch.zeros(2, 10, device=DEV)
+    with pytest.raises(ValueError, match="top_k"):
+        fused_step.sample_tokens(x, 1.0, 11)
+    with pytest.raises(ValueError, match="temperature"):
+        fused_step.sample_tokens(x, 0.0, 5)
+    with pytest.raises(ValueError, match="65536"):
+        fused_step.sample_tokens(torch.zeros(1, 70000, device=DEV), 1.0, 5)
