@@ -9,6 +9,7 @@ layer: fused RMSNorm/projections, the mixer step's gate readouts and its recurre
 out-projection + residual, RMSNorm + SwiGLU, down-projection + residual). A step is one decode token; prefill and graph capture are outside the timed region
 (reference scripts/benchmark_decode.py:21-28 protocol). Also reported in the same JSON line:
   decode_b16_*      lockstep batch-16 decode with temperature 0.8 / top-k 50 sampling (dh_sample_topk)
+  decoder_prefill_* the decoders' C3 prefill (3840 tokens, all decode state): fused vs eager
   prefill_*         C2: 292M bf16 forward at B=1, T=1024, fused gates vs eager
   forward_c5_*      C5: 292M bf16 forward at B=8, T=4096, fused gates vs eager (+ peak HBM)
   gate_path_c5_*    one mixer layer at the C5 shape, fused vs eager
@@ -98,6 +99,29 @@ def time_decode(torch, model, batch, prompt, warmup, steps, sample):
     sync_barrier(torch)
     dt = time.perf_counter() - t0
     return batch * steps / dt, 1e3 * dt / steps, dec
+
+
+def time_decoder_prefill(torch, model, prompt, reps=3):
+    """The decoders' prefill of a C3 prompt (state for every layer plus the logits): the fused
+    decoder's (parallel gate kernels fill the tree state) against the eager one the reference's
+    fused decoder runs (decoding.py:143-185, 353-356). Graph capture is not included."""
+    from dispatcher_hybrid.decoding import IncrementalDecoder, _FusedPrefillDecoder
+    dev = next(model.parameters()).device
+    g = torch.Generator(device=dev).manual_seed(7)
+    ids = torch.randint(0, EOT, (1, prompt), device=dev, generator=g)
+    res = []
+    for cls in (_FusedPrefillDecoder, IncrementalDecoder):
+        dec = cls(model)
+        dec.prefill(ids)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            dec.prefill(ids)
+        torch.cuda.synchronize()
+        res.append((time.perf_counter() - t0) / reps * 1e3)
+        del dec
+        torch.cuda.empty_cache()
+    return res[0], res[1]
 
 
 def time_forward(torch, model, ids, fused, reps=3):
@@ -340,6 +364,12 @@ def main():
         out["decode_b16_tok_s"] = round(tok16, 1)
         out["decode_b16_ms_per_step"] = round(ms16, 4)
         out["decode_b16_step_roofline_frac"] = round(W_BYTES * tok16 / 16 / 1e9 / HBM_PEAK_GBS, 4)
+
+        pf_ms, pe_ms = time_decoder_prefill(torch, model, prompt)
+        out["decoder_prefill_c3_fused_ms"] = round(pf_ms, 3)
+        out["decoder_prefill_c3_eager_ms"] = round(pe_ms, 3)
+        out["decoder_prefill_c3_speedup"] = round(pe_ms / pf_ms, 2)
+        log(f"C3 decoder prefill ({prompt} tokens): fused {pf_ms:.1f} ms, eager {pe_ms:.1f} ms")
 
         g = torch.Generator(device=dev).manual_seed(2)
         ids = torch.randint(0, 50257, (1, 1024), device=dev, generator=g)

@@ -38,7 +38,8 @@ struct ScanArgs {
   const void* V0;
   int64_t svb, svt;
   void* V;
-  int b, T, H, hd, n_lv;
+  void* ring;              // nullable decoder ring buffer (b, S, H*hd), S = 2^(ring_L+1) - 2
+  int b, T, H, hd, n_lv, ring_L;
 };
 
 // raw element bits, converted after the loads of a burst have all been issued
@@ -174,6 +175,22 @@ __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
   };
   if (kPrefetch) fetch(0);
 
+  // decoder prefill: the state entering level j of the positions ring j still holds (the last
+  // 2^(j+1)), at slot 2^(j+1) - 2 + (t & (2^(j+1) - 1)) (reference decoding.py:50-76, 143-185)
+  const int64_t d = (int64_t)a.H * a.hd;
+  auto write_slab = [&](int j) {
+    if (a.ring == nullptr || j >= a.ring_L) return;   // uniform
+    const int p0 = a.T - (2 << j);
+    const int msk = (2 << j) - 1;
+    T* rb = (T*)a.ring + (int64_t)b * ((int64_t)(2 << a.ring_L) - 2) * d + (int64_t)((2 << j) - 2) * d + col0;
+#pragma unroll
+    for (int jj = 0; jj < PPT; ++jj) {
+      const int t = tid + jj * kThreads;
+      if (t < a.T && t >= p0) store_cols<T, C>(rb + (int64_t)(t & msk) * d, V[jj]);
+    }
+  };
+  write_slab(0);
+
   for (int l = 0; l < a.n_lv; ++l) {
     const int shift = 1 << l;
     if (!kPrefetch) fetch(l);
@@ -211,8 +228,10 @@ __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
 #pragma unroll
       for (int cc = 0; cc < C; ++cc) V[j][cc] = fg[j] * V[j][cc] + ad[j] * rv[s * C + cc];
     }
+    write_slab(l + 1);
     __syncthreads();
   }
+  for (int j = a.n_lv + 1; j < a.ring_L; ++j) write_slab(j);   // beyond the horizon: passed through
 
 #pragma unroll
   for (int j = 0; j < PPT; ++j) {
@@ -252,7 +271,8 @@ extern "C" int dh_level_scan_fwd(int dtype, const void* pre_i, const void* pre_f
                                  int64_t stride_pb, int64_t stride_pt, int64_t stride_pl, int64_t stride_ph,
                                  const void* mask, int64_t stride_mb, int64_t stride_mt, int64_t stride_ml,
                                  const void* V0, int64_t stride_vb, int64_t stride_vt, void* V, int b, int T,
-                                 int H, int hd, int n_lv, int activated, void* stream) {
+                                 int H, int hd, int n_lv, int activated, void* ring, int ring_L,
+                                 void* stream) {
   const char* who = "dh_level_scan_fwd";
   DH_REQUIRE(dtype == DH_F32 || dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d", who, dtype);
   DH_REQUIRE(b >= 1 && T >= 1, DH_ERR_INVALID_ARG, "%s: b=%d T=%d must be >= 1", who, b, T);
@@ -272,8 +292,10 @@ extern "C" int dh_level_scan_fwd(int dtype, const void* pre_i, const void* pre_f
   DH_REQUIRE((uintptr_t)V0 % 16 == 0 && (uintptr_t)V % 16 == 0 && (stride_vt * esz) % 16 == 0 &&
                  (stride_vb * esz) % 16 == 0,
              DH_ERR_INVALID_ARG, "%s: V0/V need 16-byte aligned rows", who);
+  DH_REQUIRE(!ring || (ring_L >= n_lv && ring_L <= 16 && (uintptr_t)ring % 16 == 0), DH_ERR_INVALID_ARG,
+             "%s: ring needs ring_L in [n_lv, 16] (got %d, n_lv %d) and 16-byte alignment", who, ring_L, n_lv);
   ScanArgs a{pre_i, pre_f, pre_r, stride_pb, stride_pt, stride_pl, stride_ph, mask, stride_mb, stride_mt,
-             stride_ml, V0, stride_vb, stride_vt, V, b, T, H, hd, n_lv};
+             stride_ml, V0, stride_vb, stride_vt, V, ring, b, T, H, hd, n_lv, ring ? ring_L : 0};
   const int mode = activated ? kActivated : (mask ? kPreMask : kPreNoMask);
   hipStream_t s = (hipStream_t)stream;
   return dtype == DH_F32 ? dispatch<float>(a, mode, s) : dispatch<bf16_t>(a, mode, s);

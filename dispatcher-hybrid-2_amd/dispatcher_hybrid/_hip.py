@@ -15,7 +15,7 @@ import os
 
 import torch
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 _LIB_NAME = "libdh_mixer.so"
 
 DH_F32, DH_BF16 = 0, 1
@@ -58,7 +58,7 @@ def _load():
                                  vp, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp,
                                  i32, i32, i32, i32, i32, vp], i32),
         "dh_level_scan_fwd": ([i32, vp, vp, vp, i64, i64, i64, i64, vp, i64, i64, i64,
-                               vp, i64, i64, vp, i32, i32, i32, i32, i32, i32, vp], i32),
+                               vp, i64, i64, vp, i32, i32, i32, i32, i32, i32, vp, i32, vp], i32),
         "dh_decode_mixer_step": ([i32] + [vp] * 13 + [i32] * 7 + [vp], i32),
         "dh_step_gates": ([i32] + [vp] * 12 + [i32] * 5 + [vp], i32),
         "dh_decode_gemv": ([i32, vp, i64, vp, vp, ctypes.c_float, i32, vp, vp, vp, vp, vp,

@@ -253,6 +253,30 @@ class IncrementalDecoder:
 # ==============================================================================================
 
 
+class _FusedPrefillDecoder(IncrementalDecoder):
+    """The fused decoder's prefill: each tree layer runs the parallel gfx950 kernels -- activated
+    gates of all L levels in one launch, the level scan over the active levels in a second, which
+    also stores the ring slabs -- instead of the eager roll/level loop, and fills the same state
+    (B_hist, rg_hist for every level, V_ring; reference decoding.py:143-185). Attention layers and
+    the steps stay those of IncrementalDecoder."""
+
+    def _tree_prefill(self, blk, cache, x):
+        from .fused_gates import prefill_gate_scan
+        mx = blk.mixer
+        T = x.shape[1]
+        dt = cache.V_ring.dtype
+        h1 = blk.norm1(x)
+        A = mx.gate_hidden(h1)
+        Bs = mx.gate_hidden_src(h1)
+        cache.B_hist[:, :T] = Bs
+        V0 = mx.linear_in(h1)
+        (Wi, bi), (Wf, bf), (Wr, br) = mx._gate_params()
+        V = prefill_gate_scan(A.to(dt), Bs.to(dt), Wi, Wf, Wr, bi, bf, br, V0.to(dt), cache.H,
+                              cache.rg_hist, cache.V_ring)
+        x = x + mx.linear_out(V.to(x.dtype))
+        return x + blk.ffn(blk.norm2(x))
+
+
 class _GraphedBase:
     def _capture(self, step_fn):
         g = torch.cuda.CUDAGraph()
@@ -282,10 +306,12 @@ class _GraphedBase:
 class GraphedHybridDecoder(_GraphedBase):
     """Eager prefill, then one HIP-graph replay per generated token."""
 
+    _prefill_cls = IncrementalDecoder
+
     def __init__(self, model, max_len=None, dtype=None):
         if not torch.cuda.is_available():
             raise RuntimeError("GraphedHybridDecoder requires a GPU")
-        self.inner = IncrementalDecoder(model, max_len, dtype=dtype)
+        self.inner = self._prefill_cls(model, max_len, dtype=dtype)
         self.m = model
         self.max_len = self.inner.max_len
         self.dtype = self.inner.dtype
@@ -379,7 +405,8 @@ class GraphedHybridDecoder(_GraphedBase):
 
 
 class FusedGraphedHybridDecoder(GraphedHybridDecoder):
-    """Graphed decoder whose step runs on gfx950 kernels: per tree layer six launches
+    """Graphed decoder on gfx950 kernels. Prefill: the parallel gate kernels fill the tree state
+    (_FusedPrefillDecoder). Step: per tree layer six launches
 
         dh_decode_gemv       RMSNorm1 + [W_in; W1x; W1s] -> V0, A, B_hist[t]
         dh_decode_gates      gate readouts of all L levels, one wave per (level, head)
@@ -394,6 +421,8 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
     average) in place of the mixer. Same caches, same graph harness; raises ImportError when the
     kernel library is missing.
     """
+
+    _prefill_cls = _FusedPrefillDecoder
 
     def __init__(self, model, max_len=None, dtype=None):
         from . import fused_step                          # loads libdh_mixer.so

@@ -197,7 +197,7 @@ def _level_scan_fwd_op(pre_i: torch.Tensor, pre_f: torch.Tensor, pre_r: torch.Te
     return out
 
 
-def _scan_launch(pre_i, pre_f, pre_r, mask, V0, out, num_heads, n_lv, activated, what):
+def _scan_launch(pre_i, pre_f, pre_r, mask, V0, out, num_heads, n_lv, activated, what, ring=None, ring_L=0):
     b, T, d = V0.shape
     cd = V0.dtype
     V0_ = V0 if V0.stride(-1) == 1 else V0.contiguous()
@@ -209,7 +209,7 @@ def _scan_launch(pre_i, pre_f, pre_r, mask, V0, out, num_heads, n_lv, activated,
     st = _hip.lib.dh_level_scan_fwd(
         _hip.dtype_code(cd), p(pi), p(pf), p(pr), *pi.stride(), p(m_), smb, smt, sml,
         p(V0_), V0_.stride(0), V0_.stride(1), p(out), b, T, num_heads, d // num_heads, n_lv,
-        int(activated), _hip.stream_handle(V0.device))
+        int(activated), p(ring), int(ring_L), _hip.stream_handle(V0.device))
     _hip.check(st, what)
 
 
@@ -270,3 +270,31 @@ def fused_gate_scan(A, B, Wi, Wf, Wr, bi, bf, br, n_lv, mask, V0, num_heads):
     of the activated gates, which follows the eager path (reference
     dispatcher_hybrid/modeling_dispatcher.py:86-88, 100-121)."""
     return torch.ops.dispatcher.gate_scan_fwd(A, B, Wi, Wf, Wr, bi, bf, br, mask, V0, num_heads, n_lv)
+
+
+def prefill_gate_scan(A, B, Wi, Wf, Wr, bi, bf, br, V0, num_heads, rg_hist, V_ring):
+    """Decoder prefill of one tree layer through the parallel kernels: the scanned state (b, T, d)
+    plus the decode state the eager prefill fills (reference dispatcher_hybrid/decoding.py:143-185)
+    -- rg_hist[:, :T] for every one of the layer's L levels (beyond the prompt's horizon the wrap
+    mask is zero, so the transmit gate is sigmoid(relu(A)^2 . W_r + b_r), the eager prefill's
+    formula) and, in V_ring, the state entering each level of the last 2^(j+1) positions. Two
+    launches: dh_gate_preacts_fwd (activated, all L levels, head-major) and dh_level_scan_fwd over
+    the active levels with the ring output; one strided copy moves the transmit gates into
+    rg_hist. A, B, V0: (b, T, .) in the state's dtype; no doc-reset mask (a decoder prompt is one
+    document)."""
+    b, T, d = V0.shape
+    L = Wi.shape[0]
+    H = num_heads
+    cd = _compute_dtype(A)
+    if rg_hist.dtype != cd or V_ring.dtype != cd or rg_hist.shape[2] != L:
+        raise ValueError("prefill_gate_scan: rg_hist / V_ring must be (b, Tmax, L, H) / (b, S, d) in the compute dtype")
+    ins = _prep_gate_inputs(A, B, Wi, Wf, Wr, bi, bf, br, L)
+    g = torch.empty(3, b, H, L, T, device=V0.device, dtype=cd)
+    gates = [g[i].permute(0, 3, 2, 1) for i in range(3)]              # logical (b, T, L, H)
+    _preacts_launch(*ins, None, gates, gates[0].stride(), 1, L, "prefill_gate_scan")
+    rg_hist[:, :T].copy_(gates[2])
+    n_lv = min(L, T.bit_length())                                       # levels with a source
+    out = torch.empty(b, T, d, device=V0.device, dtype=cd)
+    _scan_launch(gates[0], gates[1], gates[2], None, V0.to(cd), out, H, n_lv, 1, "prefill_gate_scan",
+                 ring=V_ring, ring_L=L)
+    return out

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 4
+#define DH_ABI_VERSION 5
 
 enum dh_status {
   DH_OK = 0,
@@ -106,12 +106,18 @@ int dh_gate_preacts_bwd(int dtype, const void* A, const void* B, int64_t stride_
  *             activated, masked gates a, f, r that dh_gate_preacts_fwd writes with `activate`.
  *   V0        (b, T, H*hd): V0[b,t,h*hd+e] at b*stride_vb + t*stride_vt + h*hd + e (linear_in output).
  *   V         (b, T, H*hd) contiguous output, the scanned state in the layout linear_out consumes.
+ *   ring      nullable: the decoder prefill's ring buffer V_ring (b, S, H*hd), S = 2^(ring_L+1)-2,
+ *             ring_L >= n_lv (the layer's level count). For every level j < ring_L the state
+ *             entering level j (V0 for j = 0; the final state for j > n_lv) of the last 2^(j+1)
+ *             positions is stored at slot 2^(j+1)-2 + (t & (2^(j+1)-1)), as the reference's
+ *             eager prefill stores it (dispatcher_hybrid/decoding.py:143-185); other slots are
+ *             left untouched.
  */
 int dh_level_scan_fwd(int dtype, const void* pre_i, const void* pre_f, const void* pre_r,
                       int64_t stride_pb, int64_t stride_pt, int64_t stride_pl, int64_t stride_ph,
                       const void* mask, int64_t stride_mb, int64_t stride_mt, int64_t stride_ml,
                       const void* V0, int64_t stride_vb, int64_t stride_vt, void* V, int b, int T, int H,
-                      int hd, int n_lv, int activated, void* stream);
+                      int hd, int n_lv, int activated, void* ring, int ring_L, void* stream);
 
 /*
  * One decode step of one tree layer: all L levels' gate readouts plus the L-level recurrence over

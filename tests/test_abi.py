@@ -53,9 +53,9 @@ def test_status_codes_without_device_work():
     st = lib.dh_gate_preacts_fwd(0, *([S] * 2), 0, 0, *([S] * 3), 0, 0, *([S] * 4), 0, 0, 0,
                                  *([S] * 3), 0, 0, 0, 0, 0, 1, 8, 60, 2, 3, S)
     assert st == 2 and b"GH=60" in lib.dh_last_error()
-    st = lib.dh_level_scan_fwd(1, *([S] * 3), 0, 0, 0, 0, S, 0, 0, 0, S, 0, 0, S, 1, 40000, 2, 64, 3, 0, S)
+    st = lib.dh_level_scan_fwd(1, *([S] * 3), 0, 0, 0, 0, S, 0, 0, 0, S, 0, 0, S, 1, 40000, 2, 64, 3, 0, S, 0, S)
     assert st == 2 and b"32768" in lib.dh_last_error()
-    st = lib.dh_level_scan_fwd(1, *([S] * 3), 0, 0, 0, 0, S, 0, 0, 0, S, 0, 0, S, 1, 64, 2, 64, 3, 1, S)
+    st = lib.dh_level_scan_fwd(1, *([S] * 3), 0, 0, 0, 0, S, 0, 0, 0, S, 0, 0, S, 1, 64, 2, 64, 3, 1, S, 0, S)
     assert st == 1 and b"null" in lib.dh_last_error()
 
 

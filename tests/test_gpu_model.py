@@ -130,6 +130,31 @@ def test_fused_decoder_state_equals_eager_decoder_state():
             assert max_abs(cf.B_hist, ce.B_hist) < 1e-5
 
 
+@pytest.mark.parametrize("T", [1, 2, 3, 5, 17, 40, 63])
+def test_fused_prefill_state_equals_eager_prefill(T):
+    """The fused decoder's prefill (parallel gate kernels + the scan's ring output) leaves the same
+    tree state as the eager prefill (reference decoding.py:143-185) for prompts that fill the rings
+    partly or fully and reach 1 .. all 6 levels: B_hist, rg_hist for every level (beyond the
+    horizon too), every V_ring slot (written or untouched) and the prefill logits (fp32)."""
+    # (the prefill decoder itself: the graphed decoder's capture warm-ups then write position T)
+    from dispatcher_hybrid.decoding import IncrementalDecoder, _FusedPrefillDecoder
+    cfgd, sd = tiny("tiny_a")
+    m = product_model(cfgd, sd, device=DEV)
+    prompts = torch.randint(0, 250, (2, T), device=DEV, generator=torch.Generator(device=DEV).manual_seed(T))
+    eager, fused = IncrementalDecoder(m), _FusedPrefillDecoder(m)
+    le = eager.prefill(prompts)
+    lf = fused.prefill(prompts)
+    assert rel_err(lf, le) < 1e-5
+    n = 0
+    for ce, cf in zip(eager.caches, fused.caches):
+        if hasattr(ce, "V_ring"):
+            n += 1
+            assert max_abs(cf.B_hist, ce.B_hist) < 1e-5        # layer 2 on: inputs differ by ulps
+            assert max_abs(cf.rg_hist, ce.rg_hist) < 1e-5      # sigmoid: a few fp32 ulps
+            assert max_abs(cf.V_ring, ce.V_ring) < 1e-5
+    assert n == 2
+
+
 def test_batched_graphed_and_fused_bf16():
     """reference tests/test_decoding.py:156-178 (bf16, 4 rows)."""
     from dispatcher_hybrid.decoding import (FusedGraphedHybridDecoder, GraphedHybridDecoder,
