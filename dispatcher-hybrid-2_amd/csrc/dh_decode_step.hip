@@ -385,10 +385,16 @@ __global__ __launch_bounds__(kFusedThreads) void decode_mixer_step_kernel(StepAr
 // H -- and a small recurrence launch per (head, row). The first launch also gathers everything
 // the recurrence reads at position-dependent addresses (the level-l ring value and transmit gate
 // of position t - 2^l) into a staging buffer, so the second reads only fixed addresses.
-// Staging record per (b, h, l): {ig, fg, r_src, 0, V_src[hd]} in fp32 (kStageHead + hd floats).
-// Same arithmetic as decode_mixer_step_kernel.
+// Staging buffer (caller-provided device memory of at least B*H*L*(4 + hd) floats), two regions:
+//   coef[(b*H + h)*L + l]            = {fg, ig * r_src}     float2, from byte 0
+//   vsrc[((b*H + h)*L + l)*hd + e]   = V_src[e]             model dtype, from byte vsrc_offset(B, H, L)
+// with ig/fg the admit/forget gates of level l at t and r_src, V_src the level-l transmit gate and
+// ring value of position t - 2^l (zeros before the sequence start). The recurrence is then
+// V <- fg * V + (ig * r_src) * V_src: the same products as decode_mixer_step_kernel.
 // ---------------------------------------------------------------------------------------------
-constexpr int kStageHead = 4;
+__host__ __device__ __forceinline__ int64_t vsrc_offset(int B, int H, int L) {
+  return (((int64_t)B * H * L * 8) + 15) & ~(int64_t)15;
+}
 
 template <typename T, int C, int RB>
 __global__ __launch_bounds__(64) void decode_gates_kernel(StepArgs a, float* stage) {
@@ -399,7 +405,8 @@ __global__ __launch_bounds__(64) void decode_gates_kernel(StepArgs a, float* sta
   const int b0 = blockIdx.y * RB;
   const int nchunk = GH / V;
   const int64_t d = (int64_t)H * hd;
-  const int sw = kStageHead + hd;
+  float2* coef = reinterpret_cast<float2*>(stage);
+  T* vsrc = reinterpret_cast<T*>(reinterpret_cast<char*>(stage) + vsrc_offset(a.B, H, L));
 
   // ---- t (a scalar load, so the position-dependent requests below go out as soon as it arrives,
   // while the weights are in flight), then the position-independent operands in one burst
@@ -471,18 +478,25 @@ __global__ __launch_bounds__(64) void decode_gates_kernel(StepArgs a, float* sta
     s2 = wave_sum(s2);
     const int b = b0 + r;
     if (b < a.B && live) {                             // uniform
-      float* st = stage + (((int64_t)b * H + h) * L + l) * sw;
+      const int64_t rec = ((int64_t)b * H + h) * L + l;
       if (lane == 0) {
         const float okf = ok ? 1.f : 0.f;
-        st[0] = dh_sigmoid(s0 + Raw<T>::f(bir)) * okf;
-        st[1] = dh_sigmoid(s1 + Raw<T>::f(bfr)) * okf + (1.f - okf);
-        st[2] = ok ? Raw<T>::f(rraw[r]) : 0.f;
+        const float ig = dh_sigmoid(s0 + Raw<T>::f(bir)) * okf;
+        const float fg = dh_sigmoid(s1 + Raw<T>::f(bfr)) * okf + (1.f - okf);
+        const float rs = ok ? Raw<T>::f(rraw[r]) : 0.f;
+        coef[rec] = make_float2(fg, ig * rs);
         Elem<T>::store((T*)a.rg_hist + (((int64_t)b * a.Tmax + t) * L + l) * H + h, dh_sigmoid(s2 + Raw<T>::f(brr)));
       }
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int e = lane + 64 * q;
-        if (e < hd) st[kStageHead + e] = ok ? Raw<T>::f(vraw[r][q]) : 0.f;
+        if (e < hd) {                                  // the ring value's own bits (exact)
+          const uint32_t bits = ok ? vraw[r][q] : 0u;
+          if constexpr (sizeof(T) == 2)
+            vsrc[rec * hd + e] = (T)bits;
+          else
+            vsrc[rec * hd + e] = __uint_as_float(bits);
+        }
       }
     }
   }
@@ -494,18 +508,18 @@ __global__ __launch_bounds__(kMaxHd) void decode_scan_kernel(StepArgs a, const f
   const int h = blockIdx.x, b = blockIdx.y, e = threadIdx.x;
   const int H = a.H, L = a.L, hd = a.hd;
   const int64_t d = (int64_t)H * hd;
-  const int sw = kStageHead + hd;
   const int64_t t = load_uniform(a.t_dev);             // requested first, waited for last
   DH_ISSUE_FENCE();
-  const float* st = stage + ((int64_t)b * H + h) * L * sw;
-  float ig[LMAX], fg[LMAX], rs[LMAX], vs[LMAX];
+  const float2* coef = reinterpret_cast<const float2*>(stage) + ((int64_t)b * H + h) * L;
+  const T* vsrc = reinterpret_cast<const T*>(reinterpret_cast<const char*>(stage) + vsrc_offset(a.B, H, L)) +
+                  ((int64_t)b * H + h) * L * hd + e;
+  float2 cf[LMAX];
+  uint32_t vr[LMAX];
 #pragma unroll
   for (int l = 0; l < LMAX; ++l) {                     // levels past L re-read level L-1 (unused)
-    const float* sl = st + (int64_t)min(l, L - 1) * sw;
-    ig[l] = sl[0];
-    fg[l] = sl[1];
-    rs[l] = sl[2];
-    vs[l] = sl[kStageHead + e];
+    const int lc = min(l, L - 1);
+    cf[l] = coef[lc];
+    vr[l] = Raw<T>::load(vsrc + (int64_t)lc * hd);
   }
   const uint32_t v0raw = Raw<T>::load((const T*)a.V0 + (int64_t)b * d + (int64_t)h * hd + e);
   DH_ISSUE_FENCE();
@@ -518,7 +532,7 @@ __global__ __launch_bounds__(kMaxHd) void decode_scan_kernel(StepArgs a, const f
 #pragma unroll
   for (int l = 0; l < LMAX; ++l) {
     if (l < L) {
-      v = fg[l] * v + ig[l] * rs[l] * vs[l];
+      v = cf[l].x * v + cf[l].y * Raw<T>::f(vr[l]);
       if (live && l + 1 < L) Elem<T>::store(ring + (ring_offset(l + 1) + (t & ring_mask(l + 1))) * d, v);
     }
   }
@@ -577,6 +591,180 @@ int check_common(const char* who, int dtype, int B, int Tmax, int GH, int H, int
              "%s: hd=%d not in {16,32,64,128}", who, hd);
   DH_REQUIRE(GH >= 64 && GH % 64 == 0, DH_ERR_UNSUPPORTED_SHAPE, "%s: GH=%d not a multiple of 64", who, GH);
   return DH_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// dh_decode_scan_out (batch 1): the recurrence of dh_decode_scan fused into the out-projection
+// GEMV that consumes its Y (linear_out + residual, reference decoding.py:473-476), saving a launch
+// per tree layer. The out-projection needs all of Y in every workgroup, so every workgroup runs the
+// whole recurrence (d elements, 4 per thread) from the staging record -- copied cooperatively into
+// LDS with 16-byte loads (26 KB at the released shape, L2-resident) -- and workgroup 0 alone writes
+// the ring slots of position t and Y. Order of requests: t (scalar), the staging record and V0,
+// the residual, then the wave's weight row; the LDS copy then waits for the staging loads only
+// (loads return in issue order), Y goes to LDS in the model dtype (rounded where the two-launch path
+// stores it), and each wave's output row is a dot product with DPP reductions, as in dh_decode_gemv.
+// Out-of-range t: nothing is written.
+// ---------------------------------------------------------------------------------------------
+// four consecutive elements as one 8-byte (bf16) or 16-byte (fp32) access
+template <typename T> struct Quad;
+template <> struct Quad<bf16_t> {
+  __device__ __forceinline__ static void load(const bf16_t* p, float (&o)[4]) {
+    const uint2 w = *reinterpret_cast<const uint2*>(p);
+    o[0] = __uint_as_float(w.x << 16);
+    o[1] = __uint_as_float(w.x & 0xffff0000u);
+    o[2] = __uint_as_float(w.y << 16);
+    o[3] = __uint_as_float(w.y & 0xffff0000u);
+  }
+  __device__ __forceinline__ static void store(bf16_t* p, const float (&v)[4]) {
+    *reinterpret_cast<uint2*>(p) = make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                                              (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
+  }
+};
+template <> struct Quad<float> {
+  __device__ __forceinline__ static void load(const float* p, float (&o)[4]) {
+    const float4 w = *reinterpret_cast<const float4*>(p);
+    o[0] = w.x;
+    o[1] = w.y;
+    o[2] = w.z;
+    o[3] = w.w;
+  }
+  __device__ __forceinline__ static void store(float* p, const float (&v)[4]) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+
+struct ScanOutArgs {
+  const void* V0;
+  const float* stage;
+  const int64_t* t_dev;
+  void* V_ring;
+  void* Y;
+  const void* W;              // (N, d) linear_out weight, row-major
+  const void* resid;          // residual row (model dtype)
+  const int64_t* resid_rows;  // nullable: the residual row is resid + resid_rows[0] * resid_stride
+  int64_t resid_stride;
+  void* out;                  // (N) output row; may alias the residual row
+  int Tmax, S, H, hd, L, N;
+};
+constexpr int kSOThreads = 256;
+constexpr int kSOEpt = 4;                  // recurrence elements per thread: d <= 1024
+
+template <typename T, int CG, int LMAX>
+__global__ __launch_bounds__(kSOThreads) void decode_scan_out_kernel(ScanOutArgs a) {
+  constexpr int kMaxD = kSOEpt * kSOThreads;           // 1024
+  constexpr int VCH = kMaxD * LMAX * (int)sizeof(T) / 16 / kSOThreads;   // staged 16-byte chunks per thread
+  __shared__ uint4 svs[kMaxD * LMAX * sizeof(T) / 16];  // ring sources of batch row 0, (h, l, e)
+  __shared__ float2 scf[64 * LMAX];                      // {fg, ig * r_src} of row 0, (h, l)
+  __shared__ uint4 sy[CG * 64];                          // Y in the model dtype
+  constexpr int V = Chunk<T>::N;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int H = a.H, L = a.L, hd = a.hd;
+  const int d = H * hd;
+  const int nchunk = d / V;
+  const int64_t t = load_uniform(a.t_dev);
+  DH_ISSUE_FENCE();
+
+  // ---- batch row 0's staging record (H*L coefficient pairs, H*L*hd sources) and V0, all at fixed
+  // addresses written by the gates launch: one cooperative copy into LDS, 16-byte loads
+  const int ncf = H * L;
+  const int nvs = ncf * hd * (int)sizeof(T) / 16;
+  const float2* gcf = reinterpret_cast<const float2*>(a.stage);
+  const uint4* gvs = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(a.stage) + vsrc_offset(1, H, L));
+  // (four word arrays: an array of uint4 here is kept in private memory by the compiler)
+  uint32_t cvx[VCH], cvy[VCH], cvz[VCH], cvw[VCH];
+#pragma unroll
+  for (int j = 0; j < VCH; ++j) {
+    const uint4 q = gvs[min(tid + j * kSOThreads, nvs - 1)];
+    cvx[j] = q.x; cvy[j] = q.y; cvz[j] = q.z; cvw[j] = q.w;
+  }
+  float2 cc[(64 * LMAX + kSOThreads - 1) / kSOThreads];
+#pragma unroll
+  for (int j = 0; j < (64 * LMAX + kSOThreads - 1) / kSOThreads; ++j) cc[j] = gcf[min(tid + j * kSOThreads, ncf - 1)];
+  const int e0 = min(tid * kSOEpt, d - kSOEpt);
+  uint32_t v0r[kSOEpt];
+#pragma unroll
+  for (int q = 0; q < kSOEpt; ++q) v0r[q] = Raw<T>::load((const T*)a.V0 + e0 + q);
+  // the residual of this wave's output row (every lane reads it; lane 0 uses it)
+  const int n = min((int)blockIdx.x * 4 + wave, a.N - 1);
+  const int64_t rrow = a.resid_rows ? load_uniform(a.resid_rows) : 0;
+  const uint32_t rc = Raw<T>::load((const T*)a.resid + rrow * a.resid_stride + n);
+  DH_ISSUE_FENCE();
+
+  // ---- the wave's weight row, one burst
+  uint4 w[CG];
+#pragma unroll
+  for (int c = 0; c < CG; ++c) w[c] = ld16((const T*)a.W + (int64_t)n * d + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
+  DH_ISSUE_FENCE();
+
+  // ---- stage into LDS (waits for the staging loads only; clamped duplicates rewrite the last slot)
+#pragma unroll
+  for (int j = 0; j < VCH; ++j) svs[min(tid + j * kSOThreads, nvs - 1)] = make_uint4(cvx[j], cvy[j], cvz[j], cvw[j]);
+#pragma unroll
+  for (int j = 0; j < (64 * LMAX + kSOThreads - 1) / kSOThreads; ++j) scf[min(tid + j * kSOThreads, ncf - 1)] = cc[j];
+  __syncthreads();
+
+  // ---- this thread's operands of every level, then the recurrence of elements e0 .. e0+3 (one
+  // head), branch-free; workgroup 0 then writes the ring slots and Y
+  const bool live = t >= 0 && t < a.Tmax;
+  const bool writer = live && blockIdx.x == 0 && tid * kSOEpt < d;
+  const int h = e0 / hd, eh = e0 - h * hd;
+  const T* lvs = reinterpret_cast<const T*>(svs);
+  float2 cf[LMAX];
+  float vs[LMAX][kSOEpt];
+#pragma unroll
+  for (int l = 0; l < LMAX; ++l) {
+    const int lc = min(l, L - 1);
+    cf[l] = scf[h * L + lc];
+    Quad<T>::load(lvs + (int64_t)(h * L + lc) * hd + eh, vs[l]);
+  }
+  float v[kSOEpt];
+#pragma unroll
+  for (int q = 0; q < kSOEpt; ++q) v[q] = Raw<T>::f(v0r[q]);
+  float hist[LMAX][kSOEpt];                              // state entering level l + 1
+#pragma unroll
+  for (int l = 0; l < LMAX; ++l) {
+    const bool on = l < L;                               // uniform
+#pragma unroll
+    for (int q = 0; q < kSOEpt; ++q) {
+      const float nv = cf[l].x * v[q] + cf[l].y * vs[l][q];
+      v[q] = on ? nv : v[q];
+      hist[l][q] = v[q];
+    }
+  }
+  if (writer) {
+    T* ring = (T*)a.V_ring + e0;
+    float v0f[kSOEpt];
+#pragma unroll
+    for (int q = 0; q < kSOEpt; ++q) v0f[q] = Raw<T>::f(v0r[q]);
+    Quad<T>::store(ring + (t & 1) * d, v0f);
+#pragma unroll
+    for (int l = 0; l + 1 < LMAX; ++l)
+      if (l + 1 < L) Quad<T>::store(ring + (ring_offset(l + 1) + (t & ring_mask(l + 1))) * d, hist[l]);
+    Quad<T>::store((T*)a.Y + e0, v);
+  }
+  if (tid * kSOEpt < d) Quad<T>::store(reinterpret_cast<T*>(sy) + e0, v);
+  __syncthreads();
+
+  // ---- out[n] = round(round(W[n] . Y) + resid[n])
+  float acc = 0.f;
+#pragma unroll
+  for (int c = 0; c < CG; ++c) {
+    const int ch = lane + 64 * c;
+    float wv[V], yv[V];
+    Chunk<T>::unpack(w[c], wv);
+    Chunk<T>::unpack(sy[min(ch, nchunk - 1)], yv);
+    float part = 0.f;
+#pragma unroll
+    for (int e = 0; e < V; ++e) part += wv[e] * yv[e];
+    acc += ch < nchunk ? part : 0.f;
+  }
+  acc = wave_sum(acc);
+  if (lane == 0 && live && (int)blockIdx.x * 4 + wave < a.N) {
+    uint32_t rv = rc;
+    asm volatile("" : "+v"(rv));                        // converted here, not beside its load
+    Elem<T>::store((T*)a.out + n, Elem<T>::round(Elem<T>::round(acc) + Raw<T>::f(rv)));
+  }
 }
 
 }  // namespace
@@ -717,5 +905,40 @@ extern "C" int dh_step_scan(int dtype, const void* V0, const float* IG, const fl
     step_scan_kernel<float><<<dim3(H), dim3(kThreads), 0, s>>>(a);
   else
     step_scan_kernel<bf16_t><<<dim3(H), dim3(kThreads), 0, s>>>(a);
+  return dh_check_launch(who);
+}
+
+extern "C" int dh_decode_scan_out(int dtype, const void* V0, const float* stage, const int64_t* t_dev,
+                                  void* V_ring, void* Y, const void* W, const void* resid,
+                                  const int64_t* resid_rows, int64_t resid_stride, void* out, int Tmax, int S,
+                                  int H, int hd, int L, int N, void* stream) {
+  const char* who = "dh_decode_scan_out";
+  int st = check_common(who, dtype, 1, Tmax, 64, H, hd, L);
+  if (st) return st;
+  const int d = H * hd;
+  const int vec = dtype == DH_BF16 ? 8 : 4;
+  DH_REQUIRE(d <= kSOEpt * kSOThreads && d % vec == 0 && (d / vec + 63) / 64 <= 4, DH_ERR_UNSUPPORTED_SHAPE,
+             "%s: d=%d (H*hd) must be <= %d", who, d, kSOEpt * kSOThreads);
+  DH_REQUIRE(S == (int)ring_offset(L), DH_ERR_INVALID_ARG, "%s: S=%d but L=%d needs %lld ring slots", who, S, L,
+             (long long)ring_offset(L));
+  DH_REQUIRE(N >= 1, DH_ERR_INVALID_ARG, "%s: N=%d", who, N);
+  DH_REQUIRE(V0 && stage && t_dev && V_ring && Y && W && resid && out, DH_ERR_INVALID_ARG,
+             "%s: null pointer argument", who);
+  DH_REQUIRE(aligned(stage, 16) && aligned(W, 16), DH_ERR_INVALID_ARG, "%s: stage/W need 16-byte alignment", who);
+  ScanOutArgs a{V0, stage, t_dev, V_ring, Y, W, resid, resid_rows, resid_stride, out, Tmax, S, H, hd, L, N};
+  hipStream_t s = (hipStream_t)stream;
+  const int grid = (N + 3) / 4;
+  const int C = (d / vec + 63) / 64;
+#define DH_SO(TT, CC, LL) decode_scan_out_kernel<TT, CC, LL><<<dim3(grid), dim3(kSOThreads), 0, s>>>(a)
+  if (dtype == DH_BF16) {
+    if (L <= 8) { if (C <= 2) DH_SO(bf16_t, 2, 8); else DH_SO(bf16_t, 4, 8); }
+    else if (L <= 12) { if (C <= 2) DH_SO(bf16_t, 2, 12); else DH_SO(bf16_t, 4, 12); }
+    else { if (C <= 2) DH_SO(bf16_t, 2, 16); else DH_SO(bf16_t, 4, 16); }
+  } else {
+    if (L <= 8) { if (C <= 2) DH_SO(float, 2, 8); else DH_SO(float, 4, 8); }
+    else if (L <= 12) { if (C <= 2) DH_SO(float, 2, 12); else DH_SO(float, 4, 12); }
+    else { if (C <= 2) DH_SO(float, 2, 16); else DH_SO(float, 4, 16); }
+  }
+#undef DH_SO
   return dh_check_launch(who);
 }

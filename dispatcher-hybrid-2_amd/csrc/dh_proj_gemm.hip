@@ -1,0 +1,235 @@
+// The mixer's input projections as one MFMA GEMM, for gfx950:
+//   out_s[m, n] = sum_k X[m, k] * W_s[n, k]        s < nseg <= 3, W_s (N_s, K) row-major (nn.Linear)
+// (reference dispatcher_hybrid/modeling_dispatcher.py:63-74: V0 = linear_in(x), A = gate_hidden(x),
+// B = gate_hidden_src(x) -- three GEMMs over the same rows, done here as one launch over the
+// concatenated N = N_0 + N_1 + N_2 columns). fp32 accumulation; bf16 outputs rounded once.
+//
+// Work decomposition: a workgroup (4 wave64s) computes a 128 x 128 output tile; each wave a 64 x 64
+// quadrant as 4 x 4 MFMA tiles of 16 x 16 (v_mfma_f32_16x16x32_bf16; fp32 models use
+// v_mfma_f32_16x16x4f32). K advances in tiles of 128 bytes per row (64 bf16 / 32 fp32): both operand
+// tiles (128 rows each) are staged in LDS with a 16-byte row pad (conflict-free 16-byte fragment
+// reads), double-buffered, the next tile's global loads in flight in registers while the current one
+// is multiplied; one barrier per K tile. The weight tile is the MFMA's A operand and the activation
+// tile its B operand, so the accumulator of a lane holds four consecutive output columns of one
+// output row: the epilogue writes 8 (bf16) or 16 (fp32) contiguous bytes per lane and tile.
+// Block order is XCD-aware: with round-robin dispatch over the 8 XCDs, block id % 8 picks the XCD,
+// and every column tile of a row tile goes to the same XCD, so the row tile's activations are
+// fetched once into that XCD's L2.
+#include "dh_common.h"
+
+namespace {
+
+constexpr int kBM = 128;                  // output rows (activation rows) per workgroup
+constexpr int kBN = 128;                  // output columns (weight rows) per workgroup
+constexpr int kThreads = 256;
+constexpr int kRowBytes = 128;            // K bytes of a staged row
+constexpr int kPad = 16;
+constexpr int kRS = kRowBytes + kPad;     // LDS row stride
+constexpr int kTileBytes = 128 * kRS;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+struct GemmArgs {
+  const void* X;
+  int64_t ldx;
+  const void* W[3];
+  void* out[3];
+  int64_t ldo[3];
+  int N[3];
+  int nseg, M, K, Ntot;
+  int mtiles, ntiles;
+};
+
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// segment and local column of concatenated column n (uniform selects over the argument fields)
+__device__ __forceinline__ int seg_of(const GemmArgs& a, int n, int& local) {
+  const int N0 = a.N[0], N1 = a.N[1];
+  const bool in1 = a.nseg > 1 && n >= N0;
+  const bool in2 = a.nseg > 2 && n >= N0 + N1;
+  local = n - (in2 ? N0 + N1 : (in1 ? N0 : 0));
+  return in2 ? 2 : (in1 ? 1 : 0);
+}
+template <typename P>
+__device__ __forceinline__ P pick(int s, P p0, P p1, P p2) {
+  return s == 0 ? p0 : (s == 1 ? p1 : p2);
+}
+
+template <typename T> struct Frag;
+template <> struct Frag<bf16_t> {
+  static constexpr int VE = 8;            // elements per 16-byte chunk
+  static constexpr int KSTEPS = 2;        // MFMA k-steps of 32 per staged tile
+  // one 16x16x32 step: lane (r, g) holds k = 8g .. 8g+7 of the step for row / column r
+  __device__ __forceinline__ static void mma(f32x4& acc, const uint4& w, const uint4& x) {
+    bf16x8 a, b;
+    __builtin_memcpy(&a, &w, 16);
+    __builtin_memcpy(&b, &x, 16);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+  }
+  __device__ __forceinline__ static void store4(bf16_t* p, const f32x4& v) {
+    const uint32_t lo = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+    const uint32_t hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+    *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
+  }
+};
+template <> struct Frag<float> {
+  static constexpr int VE = 4;
+  static constexpr int KSTEPS = 2;        // steps of 16 k: lane group g holds k = 4g .. 4g+3
+  // four 16x16x4 MFMAs; MFMA j takes k = 4g + j on both operands
+  __device__ __forceinline__ static void mma(f32x4& acc, const uint4& w, const uint4& x) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(w.x), __uint_as_float(x.x), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(w.y), __uint_as_float(x.y), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(w.z), __uint_as_float(x.z), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(w.w), __uint_as_float(x.w), acc, 0, 0, 0);
+  }
+  __device__ __forceinline__ static void store4(float* p, const f32x4& v) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void proj_gemm_kernel(GemmArgs a) {
+  __shared__ __align__(16) unsigned char smem[2][2][kTileBytes];   // [buffer][weights | activations]
+  typedef Frag<T> F;
+  constexpr int VE = F::VE;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int wm = wave & 1, wn = wave >> 1;             // the wave's 64 x 64 quadrant
+
+  // tile of this workgroup: XCD x = id % 8 takes row tiles x, x + 8, ..., each with all its
+  // column tiles in a row
+  const int id = blockIdx.x;
+  const int xcd = id & 7, slot = id >> 3;
+  const int mt = (slot / a.ntiles) * 8 + xcd, nt = slot % a.ntiles;
+  if (mt >= a.mtiles) return;                          // uniform
+  const int m0 = mt * kBM, n0 = nt * kBN;
+
+  // global -> LDS mapping: chunk c = tid + 256 q is row c / 8, 16-byte chunk c % 8 of the row
+  const T* xp[4];
+  const T* wp[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c = tid + kThreads * q;
+    const int row = c >> 3, cc = c & 7;
+    const int m = min(m0 + row, a.M - 1);
+    xp[q] = (const T*)a.X + (int64_t)m * a.ldx + cc * VE;
+    int loc;
+    const int n = min(n0 + row, a.Ntot - 1);
+    const int s = seg_of(a, n, loc);
+    wp[q] = (const T*)pick(s, a.W[0], a.W[1], a.W[2]) + (int64_t)loc * a.K + cc * VE;
+  }
+  uint4 px[4], pw[4];
+  auto fetch = [&](int kt) {
+    const int k0 = kt * (kRowBytes / (int)sizeof(T));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      pw[q] = ld16(wp[q] + k0);
+      px[q] = ld16(xp[q] + k0);
+    }
+  };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = tid + kThreads * q;
+      const int off = (c >> 3) * kRS + (c & 7) * 16;
+      *reinterpret_cast<uint4*>(&smem[buf][0][off]) = pw[q];
+      *reinterpret_cast<uint4*>(&smem[buf][1][off]) = px[q];
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = a.K / (kRowBytes / (int)sizeof(T));
+  fetch(0);
+  stage(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) fetch(kt + 1);                    // in flight during the multiply
+#pragma unroll
+    for (int ks = 0; ks < F::KSTEPS; ++ks) {
+      uint4 wf[4], xf[4];
+      const int kb = ks * 64 + g * 16;                 // byte offset of this lane's k chunk
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        wf[j] = *reinterpret_cast<const uint4*>(&smem[cur][0][(wn * 64 + j * 16 + r) * kRS + kb]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xf[i] = *reinterpret_cast<const uint4*>(&smem[cur][1][(wm * 64 + i * 16 + r) * kRS + kb]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) F::mma(acc[j][i], wf[j], xf[i]);
+    }
+    if (kt + 1 < nk) stage(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: acc[j][i] = out[m][n .. n+3], m = m0 + wm*64 + i*16 + r, n = n0 + wn*64 + j*16 + 4g
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + wn * 64 + j * 16 + 4 * g;
+    int loc;
+    const int s = seg_of(a, n, loc);
+    T* o = (T*)pick(s, a.out[0], a.out[1], a.out[2]);
+    const int64_t ld = pick(s, a.ldo[0], a.ldo[1], a.ldo[2]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + wm * 64 + i * 16 + r;
+      if (m < a.M && n < a.Ntot) F::store4(o + (int64_t)m * ld + loc, acc[j][i]);
+    }
+  }
+}
+
+bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
+
+}  // namespace
+
+extern "C" int dh_proj_gemm(int dtype, const void* X, int64_t ldx, int M, int K, int nseg, const void* const* W,
+                            const int* N, void* const* out, const int64_t* ldo, void* stream) {
+  const char* who = "dh_proj_gemm";
+  DH_REQUIRE(dtype == DH_F32 || dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d", who, dtype);
+  DH_REQUIRE(nseg >= 1 && nseg <= 3, DH_ERR_INVALID_ARG, "%s: nseg=%d not in [1,3]", who, nseg);
+  DH_REQUIRE(X && W && N && out && ldo, DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
+  const int esz = dtype == DH_BF16 ? 2 : 4;
+  const int kt = kRowBytes / esz;
+  DH_REQUIRE(M >= 1 && K >= kt && K % kt == 0, DH_ERR_UNSUPPORTED_SHAPE,
+             "%s: M=%d K=%d (K must be a positive multiple of %d)", who, M, K, kt);
+  DH_REQUIRE(ldx >= K && aligned(X, 16) && (ldx * esz) % 16 == 0, DH_ERR_INVALID_ARG,
+             "%s: X rows need ldx >= K and 16-byte alignment", who);
+  GemmArgs a{};
+  a.X = X;
+  a.ldx = ldx;
+  a.nseg = nseg;
+  a.M = M;
+  a.K = K;
+  int total = 0;
+  for (int s = 0; s < nseg; ++s) {
+    DH_REQUIRE(W[s] && out[s] && N[s] >= 4 && N[s] % 4 == 0, DH_ERR_INVALID_ARG,
+               "%s: segment %d needs weights, an output and N a positive multiple of 4", who, s);
+    DH_REQUIRE(aligned(W[s], 16) && aligned(out[s], 4 * esz) && ldo[s] >= N[s] && ldo[s] % 4 == 0,
+               DH_ERR_INVALID_ARG, "%s: segment %d alignment / leading dimension", who, s);
+    a.W[s] = W[s];
+    a.out[s] = out[s];
+    a.ldo[s] = ldo[s];
+    a.N[s] = N[s];
+    total += N[s];
+  }
+  a.Ntot = total;
+  a.mtiles = (M + kBM - 1) / kBM;
+  a.ntiles = (total + kBN - 1) / kBN;
+  const int64_t grid = (int64_t)((a.mtiles + 7) / 8) * 8 * a.ntiles;
+  DH_REQUIRE(grid < (1ll << 31), DH_ERR_UNSUPPORTED_SHAPE, "%s: M=%d too large", who, M);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == DH_BF16)
+    proj_gemm_kernel<bf16_t><<<dim3((unsigned)grid), dim3(kThreads), 0, s>>>(a);
+  else
+    proj_gemm_kernel<float><<<dim3((unsigned)grid), dim3(kThreads), 0, s>>>(a);
+  return dh_check_launch(who);
+}

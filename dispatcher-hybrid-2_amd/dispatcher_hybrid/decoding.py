@@ -406,7 +406,8 @@ class GraphedHybridDecoder(_GraphedBase):
 
 class FusedGraphedHybridDecoder(GraphedHybridDecoder):
     """Graphed decoder on gfx950 kernels. Prefill: the parallel gate kernels fill the tree state
-    (_FusedPrefillDecoder). Step: per tree layer six launches
+    (_FusedPrefillDecoder). Step: per tree layer six launches (five at batch 1, where the
+    recurrence runs inside the out-projection launch, dh_decode_scan_out)
 
         dh_decode_gemv       RMSNorm1 + [W_in; W1x; W1s] -> V0, A, B_hist[t]
         dh_decode_gates      gate readouts of all L levels, one wave per (level, head)
@@ -477,11 +478,16 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
                               (mx.gate_hidden_src.weight, cache.B_hist, cache.B_hist.stride(0), gh)],
                        self.t_buf, norm_weight=blk.norm1.weight, eps=self._eps(blk.norm1, self.dtype),
                        x_rows=rows)
-        fs.decode_gates_scan(self.a_buf, cache.B_hist, mx.gate_out, mx.forget_out, mx.reset_out,
-                             mx.gate_out_bias, mx.forget_out_bias, mx.reset_out_bias, self.t_buf,
-                             cache.rg_hist, cache.V_ring, self.v0_buf, self.y_buf, self.stage)
-        fs.decode_gemv(self.y_buf, [(mx.linear_out.weight, self.x_buf, d, 0)], self.t_buf,
-                       resid=x_in, resid_rows=rows)
+        gate_args = (self.a_buf, cache.B_hist, mx.gate_out, mx.forget_out, mx.reset_out, mx.gate_out_bias,
+                     mx.forget_out_bias, mx.reset_out_bias, self.t_buf, cache.rg_hist, cache.V_ring,
+                     self.v0_buf, self.y_buf, self.stage)
+        if fs.scan_out_supported(self.x_buf.shape[0], d):
+            # batch 1: the recurrence runs inside the out-projection launch
+            fs.decode_gates_scan_out(*gate_args, mx.linear_out.weight, x_in, self.x_buf, resid_rows=rows)
+        else:
+            fs.decode_gates_scan(*gate_args)
+            fs.decode_gemv(self.y_buf, [(mx.linear_out.weight, self.x_buf, d, 0)], self.t_buf,
+                           resid=x_in, resid_rows=rows)
         self._ffn_g(blk)
 
     def _attn_step_f(self, blk, cache, first):

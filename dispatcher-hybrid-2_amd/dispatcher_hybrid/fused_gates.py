@@ -21,6 +21,7 @@ mixer (``dh_level_scan_fwd``), which the reference runs as eager torch ops
 Importing this module loads the kernel library and raises ImportError if it is missing.
 """
 
+import ctypes
 from typing import List, Optional
 
 import torch
@@ -298,3 +299,31 @@ def prefill_gate_scan(A, B, Wi, Wf, Wr, bi, bf, br, V0, num_heads, rg_hist, V_ri
     _scan_launch(gates[0], gates[1], gates[2], None, V0.to(cd), out, H, n_lv, 1, "prefill_gate_scan",
                  ring=V_ring, ring_L=L)
     return out
+
+
+def fused_projections(x, weights):
+    """[x . W_s^T for W_s in weights] as ONE MFMA GEMM launch (``dh_proj_gemm``) over the
+    concatenated weights: the mixer's V0 = linear_in(x), A = gate_hidden(x), B = gate_hidden_src(x)
+    (reference dispatcher_hybrid/modeling_dispatcher.py:63-74). x: (..., K) in fp32 or bf16,
+    weights: up to three (N_s, K) tensors of x's dtype. Inference only (no autograd)."""
+    _hip.require_gpu(x, "fused_projections")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    n = len(weights)
+    for w in weights:
+        if w.dtype != x.dtype or w.dim() != 2 or w.shape[1] != K or not w.is_contiguous():
+            raise ValueError("fused_projections: weights must be contiguous (N, K) tensors of x's dtype")
+    outs = [torch.empty(*x.shape[:-1], w.shape[0], device=x.device, dtype=x.dtype) for w in weights]
+    if M == 0:
+        return outs
+    Ws = (ctypes.c_void_p * n)(*[w.data_ptr() for w in weights])
+    Ns = (ctypes.c_int * n)(*[w.shape[0] for w in weights])
+    Os = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    Ls = (ctypes.c_int64 * n)(*[w.shape[0] for w in weights])
+    st = _hip.lib.dh_proj_gemm(_hip.dtype_code(x.dtype), _hip.ptr(x2), x2.stride(0), M, K, n, Ws, Ns, Os, Ls,
+                               _hip.stream_handle(x.device))
+    _hip.check(st, "dh_proj_gemm")
+    return outs

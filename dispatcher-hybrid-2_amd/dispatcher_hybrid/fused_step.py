@@ -148,6 +148,46 @@ def decode_gates_scan(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring,
     _hip.check(st, "dh_decode_scan")
 
 
+def scan_out_supported(B, d):
+    """dh_decode_scan_out covers batch 1 with d = H*hd <= 1024."""
+    return B == 1 and d <= 1024
+
+
+def decode_gates_scan_out(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring, V0, Y, stage,
+                          W_out, resid, out, resid_rows=None):
+    """decode_gates_scan followed by the layer's out-projection + residual, out = round(round(
+    W_out . Y) + resid) (reference decoding.py:473-476), in two launches at batch 1:
+    ``dh_decode_gates`` and ``dh_decode_scan_out``, which runs the recurrence in every workgroup of
+    the out-projection GEMV (workgroup 0 writes the ring slots and Y). resid: rows of N elements
+    (row resid_rows[0] when given, else row 0); out: (1, N), may be the residual row itself."""
+    _check_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring, V0, Y)
+    Bb, Tmax, GH = B_hist.shape
+    S, d = V_ring.shape[1], V_ring.shape[2]
+    L, H = Wi.shape[0], Wi.shape[1]
+    hd = d // H
+    if not scan_out_supported(Bb, d):
+        raise ValueError(f"decode_gates_scan_out: batch {Bb}, d {d} (needs batch 1, d <= 1024)")
+    if stage.dtype != torch.float32 or not stage.is_contiguous() or stage.numel() < stage_floats(Bb, H, L, hd):
+        raise ValueError("decode_gates_scan_out: stage too small or not contiguous fp32")
+    N = W_out.shape[0]
+    for name, t in (("W_out", W_out), ("resid", resid), ("out", out)):
+        if t.dtype != A.dtype or t.stride(-1) != 1:
+            raise ValueError(f"decode_gates_scan_out: {name} must be {A.dtype} with a unit inner stride")
+    if tuple(W_out.shape) != (N, d) or not W_out.is_contiguous() or resid.shape[-1] != N or out.numel() < N:
+        raise ValueError("decode_gates_scan_out: W_out (N, d), resid rows of N and out of N elements expected")
+    p = _hip.ptr
+    code = _hip.dtype_code(A.dtype)
+    stream = _hip.stream_handle(A.device)
+    st = _hip.lib.dh_decode_gates(code, p(A), p(B_hist), p(Wi), p(Wf), p(Wr), p(bi), p(bf), p(br),
+                                  p(t_buf), p(rg_hist), p(V_ring), p(stage), Bb, Tmax, S, GH, H, hd, L,
+                                  stream)
+    _hip.check(st, "dh_decode_gates")
+    rstride = resid.stride(0) if resid.dim() > 1 else N
+    st = _hip.lib.dh_decode_scan_out(code, p(V0), p(stage), p(t_buf), p(V_ring), p(Y), p(W_out), p(resid),
+                                     p(resid_rows), rstride, p(out), Tmax, S, H, hd, L, N, stream)
+    _hip.check(st, "dh_decode_scan_out")
+
+
 class _Launcher:
     """`kernel[grid](*args, **meta)` call syntax of a Triton kernel, mapped onto a HIP entry."""
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 5
+#define DH_ABI_VERSION 7
 
 enum dh_status {
   DH_OK = 0,
@@ -76,6 +76,18 @@ int dh_gate_preacts_fwd(int dtype, const void* A, const void* B, int64_t stride_
                         void* out_i, void* out_f, void* out_r, int64_t stride_ob, int64_t stride_ot,
                         int64_t stride_ol, int64_t stride_oh, int activate, int b, int T, int GH, int H,
                         int n_lv, void* stream);
+
+/*
+ * The mixer's input projections as one MFMA GEMM over the concatenated weights:
+ *   out[s][m*ldo[s] + n] = sum_k X[m*ldx + k] * W[s][n*K + k]      s < nseg <= 3, n < N[s], m < M
+ * Replaces the three nn.Linear calls V0 = linear_in(x), A = gate_hidden(x), B = gate_hidden_src(x)
+ * of the parallel forward (reference dispatcher_hybrid/modeling_dispatcher.py:63-74) with one
+ * launch. W[s] (N[s], K) row-major (nn.Linear weight layout), N[s] a multiple of 4; K a multiple
+ * of 64 (bf16) / 32 (fp32); fp32 accumulation, one rounding per bf16 output. W, N, out, ldo are
+ * host arrays of nseg entries.
+ */
+int dh_proj_gemm(int dtype, const void* X, int64_t ldx, int M, int K, int nseg, const void* const* W,
+                 const int* N, void* const* out, const int64_t* ldo, void* stream);
 
 /*
  * Backward of dh_gate_preacts_fwd (autograd of the fused op).
@@ -206,6 +218,20 @@ int dh_decode_gates(int dtype, const void* A, const void* B_hist, const void* Wi
                     int hd, int L, void* stream);
 int dh_decode_scan(int dtype, const void* V0, const float* stage, const int64_t* t_dev, void* V_ring, void* Y,
                    int B, int Tmax, int S, int H, int hd, int L, void* stream);
+
+/*
+ * Batch 1: dh_decode_scan fused into the out-projection + residual that consumes its Y (replaces,
+ * with dh_decode_gates, the step kernels and the linear_out + residual of _tree_step_g, reference
+ * dispatcher_hybrid/fused_step.py:62-88 and decoding.py:473-476):
+ *   Y = the L-level recurrence of dh_decode_scan (ring slots of t written, Y written)
+ *   out[n] = round(round(W[n] . Y) + resid[rrow*resid_stride + n])   n < N, rrow = resid_rows ? *resid_rows : 0
+ * W (N, H*hd) row-major; out may alias the residual row. Every workgroup of the GEMV runs the
+ * recurrence from the staging buffer; one writes the state. H*hd <= 1024; t = *t_dev outside
+ * [0, Tmax) writes nothing.
+ */
+int dh_decode_scan_out(int dtype, const void* V0, const float* stage, const int64_t* t_dev, void* V_ring, void* Y,
+                       const void* W, const void* resid, const int64_t* resid_rows, int64_t resid_stride, void* out,
+                       int Tmax, int S, int H, int hd, int L, int N, void* stream);
 
 /*
  * Greedy next token: out[b] = argmax over row b of logits (B rows of V, rows row_stride elements

@@ -252,7 +252,7 @@ DECODE_CASES = [
 
 
 def _run_decode(case, dtype, seed, split=False, W_zero=False, bias=None, V0_onehot=False, sentinel=0.0,
-                two=False):
+                two=False, out_proj=None):
     from dispatcher_hybrid import fused_step
     Bb, T, Tmax, GH, H, hd, L = case
     d = H * hd
@@ -282,6 +282,11 @@ def _run_decode(case, dtype, seed, split=False, W_zero=False, bias=None, V0_oneh
                                                   IG, FG, st.rg_hist, Tmax, GH=GH, H=H, L=L, BK=128)
             fused_step.step_scan_kernel[(Bb, H)](tV0[:, t].contiguous(), IG, FG, st.rg_hist, st.V_ring,
                                                  st.t_buf, st.Y, Tmax, st.S, L=L, HD=hd, H=H)
+        elif out_proj is not None:
+            W_out, resid, outs = out_proj
+            fused_step.decode_gates_scan_out(tA[:, t].contiguous(), st.B_hist, *tW, *tb, st.t_buf,
+                                             st.rg_hist, st.V_ring, tV0[:, t].contiguous(), st.Y, stage,
+                                             W_out, resid[t:t + 1], outs[t:t + 1])
         elif two:
             fused_step.decode_gates_scan(tA[:, t].contiguous(), st.B_hist, *tW, *tb, st.t_buf,
                                          st.rg_hist, st.V_ring, tV0[:, t].contiguous(), st.Y, stage)
@@ -390,3 +395,74 @@ def test_decode_wrapper_rejects_mixed_dtypes():
         fused_step.decode_mixer_step(torch.randn(Bb, GH, device=DEV), st.B_hist, W, W, W, bias, bias,
                                      bias, st.t_buf, st.rg_hist, st.V_ring,
                                      torch.randn(Bb, H * hd, device=DEV), st.Y)
+
+
+SCAN_OUT_CASES = [
+    # B, T(steps), Tmax, GH, H, hd, L -- batch 1 (the fused recurrence + out-projection launch)
+    (1, 40, 64, 64, 2, 64, 6),
+    (1, 70, 128, 128, 4, 16, 7),
+    (1, 24, 4096, 1024, 16, 64, 12),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", SCAN_OUT_CASES)
+def test_scan_out_matches_two_launches_and_oracle(case, dtype):
+    """dh_decode_gates + dh_decode_scan_out (the recurrence inside the out-projection launch) over T
+    steps: Y, rg_hist and every ring slot equal the two-launch path's (same arithmetic, compared to
+    one fp32 rounding), Y matches the oracle, and out = round(round(W_out . Y) + resid) matches a
+    float64 product of the kernel's own Y (reference decoding.py:473-476)."""
+    Bb, T, Tmax, GH, H, hd, L = case
+    d = H * hd
+    print(f"scan_out case={case} {dtype}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(T)
+    W_out = (torch.randn(d, d, device=DEV, generator=g) / d ** 0.5).to(dtype)
+    resid = torch.randn(T, d, device=DEV, generator=g).to(dtype)
+    outs = torch.full((T, d), 5.0, device=DEV, dtype=dtype)
+    a, Ya, inp = _run_decode(case, dtype, seed=13, two=True)
+    b, Yb, _ = _run_decode(case, dtype, seed=13, out_proj=(W_out, resid, outs))
+    tol = 1e-6 if dtype == torch.float32 else 1e-2
+    assert rel_err(_np(Yb), _np(Ya)) < tol
+    assert rel_err(_np(b.V_ring), _np(a.V_ring)) < tol
+    assert torch.equal(b.rg_hist, a.rg_hist)
+    Yo, _, _ = _oracle_decode(case, inp)
+    assert rel_err(_np(Yb), Yo) < (1e-4 if dtype == torch.float32 else 2e-2)
+    rnd = (lambda x: x.to(dtype).double()) if dtype == torch.bfloat16 else (lambda x: x)
+    ref = rnd(rnd(Yb[0].double() @ W_out.double().T) + resid.double())
+    assert rel_err(outs.double(), ref) < (1e-5 if dtype == torch.float32 else 1e-2)
+
+
+def test_scan_out_residual_rows_in_place_and_range():
+    """The residual read through resid_rows (the first layer's embedding row), `out` aliasing the
+    residual row, and a position outside [0, Tmax) writing nothing."""
+    from dispatcher_hybrid import fused_step
+    Bb, Tmax, GH, H, hd, L = 1, 64, 64, 2, 64, 6
+    d = H * hd
+    g = torch.Generator(device=DEV).manual_seed(31)
+    st = _DecodeState(Bb, Tmax, GH, H, hd, L, torch.float32, 0.0)
+    A = torch.randn(1, GH, device=DEV, generator=g)
+    V0 = torch.randn(1, d, device=DEV, generator=g)
+    Ws = [torch.randn(L, H, GH, device=DEV, generator=g) / 8 for _ in range(3)]
+    bs = [torch.randn(L, H, device=DEV, generator=g) for _ in range(3)]
+    W_out = torch.randn(d, d, device=DEV, generator=g) / d ** 0.5
+    emb = torch.randn(50, d, device=DEV, generator=g)
+    rows = torch.tensor([37], device=DEV)
+    x = torch.zeros(1, d, device=DEV)
+    stage = torch.zeros(fused_step.stage_floats(1, H, L, hd), device=DEV)
+    st.B_hist[:, 5] = torch.randn(GH, device=DEV, generator=g)
+    st.t_buf.fill_(5)
+    fused_step.decode_gates_scan_out(A, st.B_hist, *Ws, *bs, st.t_buf, st.rg_hist, st.V_ring, V0, st.Y, stage,
+                                      W_out, emb, x, resid_rows=rows)
+    torch.cuda.synchronize()
+    assert rel_err(x, st.Y.double() @ W_out.double().T + emb[37].double()) < 1e-5
+    x2 = emb[3:4].clone()
+    fused_step.decode_gates_scan_out(A, st.B_hist, *Ws, *bs, st.t_buf, st.rg_hist, st.V_ring, V0, st.Y, stage,
+                                      W_out, x2, x2)                     # in place
+    torch.cuda.synchronize()
+    assert rel_err(x2, st.Y.double() @ W_out.double().T + emb[3].double()) < 1e-5
+    ring0, Y0, x3 = st.V_ring.clone(), st.Y.clone(), x.clone()
+    st.t_buf.fill_(Tmax)
+    fused_step.decode_gates_scan_out(A, st.B_hist, *Ws, *bs, st.t_buf, st.rg_hist, st.V_ring, V0, st.Y, stage,
+                                      W_out, emb, x, resid_rows=rows)
+    torch.cuda.synchronize()
+    assert torch.equal(st.V_ring, ring0) and torch.equal(st.Y, Y0) and torch.equal(x, x3)

@@ -1,0 +1,57 @@
+"""dh_proj_gemm (the mixer's three input projections as one MFMA GEMM) against a float64 matmul
+of the same operands (reference dispatcher_hybrid/modeling_dispatcher.py:63-74 computes them as
+three nn.Linear calls). Bars: fp32 1e-5 relative (accumulation order only); bf16 one output
+rounding (2^-8 relative to each element's magnitude) plus fp32 accumulation order."""
+
+import pytest
+import torch
+
+from helpers import rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+CASES = [
+    # M, K, segment widths
+    (1, 64, [64]),
+    (130, 128, [128, 128, 128]),          # ragged M, three segments
+    (1000, 256, [64, 192, 128]),          # segments that straddle the 128-column tiles
+    (4096, 1024, [1024, 1024, 1024]),     # the released mixer (d = gh = 1024)
+    (257, 1024, [1024]),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", CASES)
+def test_proj_gemm_matches_matmul(case, dtype):
+    from dispatcher_hybrid.fused_gates import fused_projections
+    M, K, Ns = case
+    print(f"proj_gemm M={M} K={K} N={Ns} {dtype}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(M + K)
+    x = torch.randn(M, K, device=DEV, generator=g).to(dtype)
+    Ws = [(torch.randn(n, K, device=DEV, generator=g) / K ** 0.5).to(dtype) for n in Ns]
+    outs = fused_projections(x, Ws)
+    torch.cuda.synchronize()
+    for o, w in zip(outs, Ws):
+        ref = x.double() @ w.double().T
+        assert o.shape == (M, w.shape[0]) and o.dtype == dtype
+        if dtype == torch.float32:
+            assert rel_err(o, ref) < 1e-5
+        else:
+            err = (o.double() - ref).abs()
+            assert bool((err <= ref.abs() * 2.0 ** -8 + 2e-3).all()), err.max().item()
+
+
+def test_proj_gemm_batched_view_and_rejects():
+    from dispatcher_hybrid.fused_gates import fused_projections
+    g = torch.Generator(device=DEV).manual_seed(9)
+    x = torch.randn(2, 300, 128, device=DEV, generator=g)
+    W = torch.randn(96, 128, device=DEV, generator=g)
+    (o,) = fused_projections(x, [W])
+    torch.cuda.synchronize()
+    assert o.shape == (2, 300, 96)
+    assert rel_err(o, x.double() @ W.double().T) < 1e-5
+    with pytest.raises(ValueError):
+        fused_projections(torch.zeros(4, 100, device=DEV), [torch.zeros(8, 100, device=DEV)])   # K % 32
+    with pytest.raises(ValueError):
+        fused_projections(x, [torch.zeros(6, 128, device=DEV)])                                  # N % 4
