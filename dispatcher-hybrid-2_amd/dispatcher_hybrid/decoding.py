@@ -261,15 +261,13 @@ class _FusedPrefillDecoder(IncrementalDecoder):
     the steps stay those of IncrementalDecoder."""
 
     def _tree_prefill(self, blk, cache, x):
-        from .fused_gates import prefill_gate_scan
+        from .fused_gates import input_projections, prefill_gate_scan
         mx = blk.mixer
         T = x.shape[1]
         dt = cache.V_ring.dtype
         h1 = blk.norm1(x)
-        A = mx.gate_hidden(h1)
-        Bs = mx.gate_hidden_src(h1)
+        V0, A, Bs = input_projections(h1, mx)
         cache.B_hist[:, :T] = Bs
-        V0 = mx.linear_in(h1)
         (Wi, bi), (Wf, bf), (Wr, br) = mx._gate_params()
         V = prefill_gate_scan(A.to(dt), Bs.to(dt), Wi, Wf, Wr, bi, bf, br, V0.to(dt), cache.H,
                               cache.rg_hist, cache.V_ring)

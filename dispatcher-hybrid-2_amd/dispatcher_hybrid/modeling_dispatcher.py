@@ -134,16 +134,17 @@ class DispatcherMixer(nn.Module):
         if not x.is_cuda:
             raise RuntimeError("fused gates are enabled but the input is on the CPU; move the model "
                                "to the GPU or call enable_fused_gates(False)")
-        from .fused_gates import fused_gate_preacts, fused_gate_scan
+        from .fused_gates import fused_gate_preacts, fused_gate_scan, input_projections
         Bb, T = x.shape[0], x.shape[1]
         H, hd = self.num_heads, self.head_dim
-        V0 = self.linear_in(x)
-        A = self.gate_hidden(x)
-        Bs = self.gate_hidden_src(x)
-        m3 = mask[..., :n_lv] if mask.dim() == 3 else None
-        (Wi, bi), (Wf, bf), (Wr, br) = self._gate_params()
         needs_grad = torch.is_grad_enabled() and (
             x.requires_grad or any(p.requires_grad for p in self.parameters()))
+        if needs_grad:
+            V0, A, Bs = self.linear_in(x), self.gate_hidden(x), self.gate_hidden_src(x)
+        else:
+            V0, A, Bs = input_projections(x, self)
+        m3 = mask[..., :n_lv] if mask.dim() == 3 else None
+        (Wi, bi), (Wf, bf), (Wr, br) = self._gate_params()
         if needs_grad:
             # differentiable: the fused pre-activations (custom op with autograd) + torch scan
             pre_i, pre_f, pre_r = fused_gate_preacts(A, Bs, Wi, Wf, Wr, bi, bf, br, n_lv, m3)
