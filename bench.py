@@ -4,8 +4,8 @@
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 
 Headline (`value`): steady-state batch-1 bf16 greedy decode tok/s of the 292M model at 3840-4096
-context through FusedGraphedHybridDecoder (one HIP-graph replay per token; six gfx950 launches per tree
-layer: fused RMSNorm/projections, the mixer step's gate readouts and its recurrence,
+context through FusedGraphedHybridDecoder (one HIP-graph replay per token; five gfx950 launches per tree
+layer: fused RMSNorm/projections, the mixer step's gate readouts, its recurrence fused with the
 out-projection + residual, RMSNorm + SwiGLU, down-projection + residual). A step is one decode token; prefill and graph capture are outside the timed region
 (reference scripts/benchmark_decode.py:21-28 protocol). Also reported in the same JSON line:
   decode_b16_*      lockstep batch-16 decode with temperature 0.8 / top-k 50 sampling (dh_sample_topk)
@@ -13,7 +13,7 @@ out-projection + residual, RMSNorm + SwiGLU, down-projection + residual). A step
   prefill_*         C2: 292M bf16 forward at B=1, T=1024, fused gates vs eager
   forward_c5_*      C5: 292M bf16 forward at B=8, T=4096, fused gates vs eager (+ peak HBM)
   gate_path_c5_*    one mixer layer at the C5 shape, fused vs eager
-  roofline          dh_decode_gemv, the dominant kernel (73 of the 111 launches of a step, ~60% of
+  roofline          dh_decode_gemv, the dominant kernel (57 of the 95 launches of a step, ~55% of
                     its time): algorithmic bytes / HIP-event-timed launch duration
   mixer_step        the decoder's mixer step (dh_decode_gates + dh_decode_scan) per tree layer
   step_roofline     whole decode step: bf16 weight bytes per token x tok/s vs 8 TB/s
@@ -38,10 +38,10 @@ HBM_PEAK_GBS = 8000.0                  # MI355X HBM3E
 MFMA_BF16_TFLOPS = 2500.0              # MI355X dense bf16
 REF_DECODE_TOK_S = 525.1               # reference FusedGraphedHybridDecoder @3900 ctx (A6000, README.md:76-81)
 EOT = 50256
-# HBM bytes per dh_decode_gemv launch, averaged over the decode step's 73 launches: rocprofv3 --pmc
-# FETCH_SIZE (3832.1 KiB x 1.99975, the factor a 256 MiB copy's reading gives) + WRITE_SIZE
-# (13.67 KiB x 1.0), from profiles/decode_c3_b1_kernels.md
-TRAFFIC_GEMV_LAUNCH = 7_861_186
+# HBM bytes per dh_decode_gemv launch, averaged over the decode step's 57 launches: rocprofv3 --pmc
+# FETCH_SIZE (x 1.99974, the factor a 256 MiB copy's reading gives) + WRITE_SIZE (x 1.0), from
+# profiles/decode_c3_b1_kernels.md
+TRAFFIC_GEMV_LAUNCH = 9_453_519
 
 
 def parse():
@@ -181,12 +181,13 @@ def _graph_time(torch, launch, n, reps):
 
 
 def gemv_chain_roofline(torch, model, reps=20):
-    """dh_decode_gemv over the launches of one batch-1 decode step: the same 73 launches, shapes and
+    """dh_decode_gemv over the launches of one batch-1 decode step: the same 57 launches, shapes and
     weights as FusedGraphedHybridDecoder's step -- per tree layer RMSNorm + [W_in; W1x; W1s],
-    linear_out + residual, RMSNorm + SwiGLU, linear_down + residual; per attention layer the same
-    with [Wq; Wk; Wv]; RMSNorm + lm_head -- on random activations, in one HIP graph. The model's
-    584 MB of weights exceed the 256 MB last-level cache, so every launch streams its weights from
-    HBM as in decode. Returns (algorithmic bytes per step, microseconds per launch, launches)."""
+    RMSNorm + SwiGLU, linear_down + residual (its linear_out runs inside dh_decode_scan_out); per
+    attention layer RMSNorm + [Wq; Wk; Wv], linear_out + residual, RMSNorm + SwiGLU, linear_down +
+    residual; RMSNorm + lm_head -- on random activations, in one HIP graph. The model's 584 MB of
+    weights exceed the 256 MB last-level cache, so every launch streams its weights from HBM as in
+    decode. Returns (algorithmic bytes per step, microseconds per launch, launches)."""
     from dispatcher_hybrid import fused_step
     from dispatcher_hybrid.modeling_dispatcher import AttentionBlock
     dev = next(model.parameters()).device
@@ -219,7 +220,8 @@ def gemv_chain_roofline(torch, model, reps=20):
             ws = [mx.linear_in.weight, mx.gate_hidden.weight, mx.gate_hidden_src.weight]
             wo = mx.linear_out.weight
         add(x, [(w, o[:, i * d:], o.shape[1], 0) for i, w in enumerate(ws)], norm_weight=blk.norm1.weight)
-        add(x, [(wo, xr, d, 0)], resid=xr)
+        if isinstance(blk, AttentionBlock):
+            add(x, [(wo, xr, d, 0)], resid=xr)
         f = blk.ffn
         add(x, [(f.linear_gate.weight, o, ff, 0), (f.linear_up.weight, o, ff, 0)],
             norm_weight=blk.norm2.weight, swiglu=True)
@@ -345,7 +347,7 @@ def main():
     log(f"mixer step (gates + scan): {mus:.2f} us per layer")
     nbytes, avg_us, nl = gemv_chain_roofline(torch, model)
     achieved = nbytes / nl / (avg_us * 1e-6) / 1e9
-    out["roofline"] = {"kernel": "dh_decode_gemv: the 73 launches of one batch-1 decode step "
+    out["roofline"] = {"kernel": "dh_decode_gemv: the 57 launches of one batch-1 decode step "
                                  "(decode_gemv_row_kernel instantiations)",
                        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_GEMV_LAUNCH,
