@@ -287,6 +287,272 @@ int launch(const AttnArgs& a, int B, int hd, hipStream_t s) {
   return dh_check_launch("dh_decode_attention");
 }
 
+// ---------------------------------------------------------------------------------------------
+// Split-window form for small batches (dh_decode_attention_split): the window is cut into S
+// segments and each (segment, head, row) gets its own workgroup, so a head's keys and values
+// stream through S compute units instead of one (the single-workgroup kernel above is bound by one
+// CU's request rate at batch 1). Segment s computes, over its positions, the rounded scores, their
+// maximum m_s, l_s = sum exp(s_j - m_s) and the unnormalised value sum o_s = sum exp(s_j - m_s)
+// V_j (fp32), into a caller-provided workspace; a second launch combines the S records of a head:
+//   M = max_s m_s,  y = round( sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s ).
+// Same scores (rounded where the eager step rounds them) and the same softmax; the probabilities
+// enter the value sum in fp32 (the single-workgroup kernel rounds them to the model dtype first,
+// as the eager bf16 step does). The segment holding t rotates k, writes the cache row of t and
+// takes position t from LDS, never from the cache.
+// ---------------------------------------------------------------------------------------------
+constexpr int kSThreads = 128;
+constexpr int kSplits = 16;
+constexpr int kMaxSplitPos = kMaxWindow / kSplits;    // positions per segment (LDS scores)
+
+template <typename T, int HD>
+__global__ __launch_bounds__(kSThreads) void decode_attention_split_kernel(AttnArgs a, int S, float* ws) {
+  __shared__ float qs[HD], ks[HD], vsh[HD];
+  __shared__ float sc[kMaxSplitPos];
+  __shared__ float red[kSThreads / 64];
+  __shared__ float part[kSThreads / 64][HD];
+  constexpr int VE = 16 / (int)sizeof(T);             // elements per 16-byte chunk
+  constexpr int KCH = HD / VE;                        // chunks per cache row
+  constexpr int RPI = 64 / KCH;                       // rows per wave instruction in the value pass
+  constexpr int NW = kSThreads / 64;
+  constexpr int VCH = 8;                              // value instructions in flight per lane
+  const int sg = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t = load_uniform(a.t_dev);
+  if (t < 0 || t >= a.Tmax) return;                   // workgroup-uniform: nothing to do
+  const int lo = a.window > 0 ? (int)max((int64_t)0, t + 1 - a.window) : 0;
+  const int n = (int)t - lo + 1;                      // positions lo .. t; index n-1 is t itself
+  const int P = (n + S - 1) / S;
+  const int j0 = min(sg * P, n), j1 = min(n, j0 + P); // this segment's indices [j0, j1)
+  const bool has_t = j0 <= n - 1 && n - 1 < j1;
+  const int jc1 = min(j1, n - 1);                     // cached indices [j0, jc1)
+  const int cmax = max(n - 2, 0);                     // clamp: a written cache row (results discarded)
+  const int64_t head_off = ((int64_t)b * a.H + h) * a.Tmax * HD;
+  T* Kh = (T*)a.K + head_off;
+  T* Vh = (T*)a.V + head_off;
+
+  // ---- rotation operands first (raw bits, every thread, clamped index), then the first key row of
+  // this thread and the first value block, then the rotation
+  const bool roper = tid < HD / 2;
+  uint32_t rop[8];
+  {
+    const int pt = min(tid, HD / 2 - 1);
+    const int64_t base = (int64_t)b * a.qkv_bstride + (int64_t)h * HD + 2 * pt;
+    rop[0] = raw_load((const T*)a.cos + t * (HD / 2) + pt);
+    rop[1] = raw_load((const T*)a.sin + t * (HD / 2) + pt);
+    rop[2] = raw_load((const T*)a.q + base);
+    rop[3] = raw_load((const T*)a.q + base + 1);
+    rop[4] = raw_load((const T*)a.k + base);
+    rop[5] = raw_load((const T*)a.k + base + 1);
+    rop[6] = raw_load((const T*)a.v + base);
+    rop[7] = raw_load((const T*)a.v + base + 1);
+  }
+  DH_ISSUE_FENCE();
+  uint4 krow[KCH];
+  {
+    const int i = min(j0 + tid, cmax);
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) krow[c] = reinterpret_cast<const uint4*>(Kh + (int64_t)(lo + i) * HD)[c];
+  }
+  const int slot = lane / KCH, dg = lane % KCH;
+  uint4 vrow[VCH];
+#pragma unroll
+  for (int u = 0; u < VCH; ++u) {
+    const int i = min(j0 + (u * NW + wave) * RPI + slot, cmax);
+    vrow[u] = reinterpret_cast<const uint4*>(Vh + (int64_t)(lo + i) * HD)[dg];
+  }
+  DH_ISSUE_FENCE();
+  if (roper) {
+    asm volatile("" : "+v"(rop[0]), "+v"(rop[1]), "+v"(rop[2]), "+v"(rop[3]), "+v"(rop[4]), "+v"(rop[5]),
+                 "+v"(rop[6]), "+v"(rop[7]));           // converted here, after the key/value requests
+    const float c = raw_f<T>(rop[0]), s = raw_f<T>(rop[1]);
+    const float q0 = raw_f<T>(rop[2]), q1 = raw_f<T>(rop[3]);
+    const float k0 = raw_f<T>(rop[4]), k1 = raw_f<T>(rop[5]);
+    const float v0 = raw_f<T>(rop[6]), v1 = raw_f<T>(rop[7]);
+    typedef Elem<T> E;
+    float qr0, qr1, kr0, kr1;
+    {
+#pragma clang fp contract(off)
+      qr0 = E::round(E::round(q0 * c) - E::round(q1 * s));
+      qr1 = E::round(E::round(q0 * s) + E::round(q1 * c));
+      kr0 = E::round(E::round(k0 * c) - E::round(k1 * s));
+      kr1 = E::round(E::round(k0 * s) + E::round(k1 * c));
+    }
+    qs[2 * tid] = qr0; qs[2 * tid + 1] = qr1;
+    ks[2 * tid] = kr0; ks[2 * tid + 1] = kr1;
+    vsh[2 * tid] = v0; vsh[2 * tid + 1] = v1;
+    if (has_t) {
+      E::store(Kh + t * HD + 2 * tid, kr0);
+      E::store(Kh + t * HD + 2 * tid + 1, kr1);
+      E::store(Vh + t * HD + 2 * tid, v0);
+      E::store(Vh + t * HD + 2 * tid + 1, v1);
+    }
+  }
+  __syncthreads();
+
+  // ---- scores of the cached positions (one per thread per sweep) and of t (thread 0, from LDS)
+  auto score = [&](const uint4 (&w)[KCH]) {
+    float dot = 0.f;
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const uint32_t wsd[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+      const int e = c * VE;
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          dot += qs[e + 2 * j] * __uint_as_float(wsd[j] << 16) + qs[e + 2 * j + 1] * __uint_as_float(wsd[j] & 0xffff0000u);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dot += qs[e + j] * __uint_as_float(wsd[j]);
+      }
+    }
+    return Elem<T>::round(Elem<T>::round(dot) / a.scale);
+  };
+  float mx = -INFINITY;
+  for (int i0 = j0; i0 < jc1; i0 += kSThreads) {
+    const int i = i0 + tid;
+    if (i0 > j0) {                                     // sweeps past the first (long segments)
+#pragma unroll
+      for (int c = 0; c < KCH; ++c) krow[c] = reinterpret_cast<const uint4*>(Kh + (int64_t)(lo + min(i, cmax)) * HD)[c];
+    }
+    const float s0 = score(krow);
+    if (i < jc1) {
+      sc[i - j0] = s0;
+      mx = fmaxf(mx, s0);
+    }
+  }
+  if (has_t && tid == 0) {
+    float dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < HD; ++e) dot += qs[e] * ks[e];
+    const float s2 = Elem<T>::round(Elem<T>::round(dot) / a.scale);
+    sc[n - 1 - j0] = s2;
+    mx = fmaxf(mx, s2);
+  }
+  mx = wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  float M = red[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, red[w]);
+  __syncthreads();                                     // red is reused below
+  float sum = 0.f;
+  for (int i = j0 + tid; i < j1; i += kSThreads) {
+    const float p = __expf(sc[i - j0] - M);
+    sc[i - j0] = p;
+    sum += p;
+  }
+  sum = wave_sum(sum);
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  float Ls = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) Ls += red[w];
+
+  // ---- o = sum_i p_i V_i over the cached positions (lane -> (row slot, chunk)), then position t
+  float acc[VE];
+#pragma unroll
+  for (int e = 0; e < VE; ++e) acc[e] = 0.f;
+  auto accumulate = [&](const uint4& w, int i) {
+    if (i >= jc1) return;                              // a clamped row: never folded in
+    const float p = sc[i - j0];
+    const uint32_t wsd[4] = {w.x, w.y, w.z, w.w};
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] += p * __uint_as_float(wsd[j] << 16);
+        acc[2 * j + 1] += p * __uint_as_float(wsd[j] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] += p * __uint_as_float(wsd[j]);
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < VCH; ++u) accumulate(vrow[u], j0 + (u * NW + wave) * RPI + slot);
+  for (int i0 = j0 + VCH * NW * RPI; i0 < jc1; i0 += VCH * NW * RPI) {   // segments past the prefetch
+#pragma unroll
+    for (int u = 0; u < VCH; ++u)
+      vrow[u] = reinterpret_cast<const uint4*>(Vh + (int64_t)(lo + min(i0 + (u * NW + wave) * RPI + slot, cmax)) * HD)[dg];
+#pragma unroll
+    for (int u = 0; u < VCH; ++u) accumulate(vrow[u], i0 + (u * NW + wave) * RPI + slot);
+  }
+#pragma unroll
+  for (int e = 0; e < VE; ++e) {
+    float v = acc[e];
+#pragma unroll
+    for (int off = KCH; off < 64; off <<= 1) v += __shfl_xor(v, off);
+    acc[e] = v;
+  }
+  if (slot == 0) {
+#pragma unroll
+    for (int e = 0; e < VE; ++e) part[wave][dg * VE + e] = acc[e];
+  }
+  __syncthreads();
+  float* rec = ws + (((int64_t)b * a.H + h) * S + sg) * (2 + HD);
+  if (tid < HD) {
+    float o = has_t ? sc[n - 1 - j0] * vsh[tid] : 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) o += part[w][tid];
+    rec[2 + tid] = o;
+  }
+  if (tid == 0) {
+    rec[0] = M;                                         // -inf for an empty segment
+    rec[1] = Ls;
+  }
+}
+
+template <typename T, int HD>
+__global__ __launch_bounds__(HD) void decode_attention_combine_kernel(AttnArgs a, int S, const float* ws) {
+  const int h = blockIdx.x, b = blockIdx.y, e = threadIdx.x;
+  const int64_t t = load_uniform(a.t_dev);
+  if (t < 0 || t >= a.Tmax) return;
+  const float* rec = ws + ((int64_t)b * a.H + h) * S * (2 + HD);
+  // every record requested before any is used (a loop over S would wait once per record)
+  float m[kSplits], l[kSplits], o[kSplits];
+#pragma unroll
+  for (int s = 0; s < kSplits; ++s) {
+    const float* r = rec + min(s, S - 1) * (2 + HD);
+    m[s] = r[0];
+    l[s] = r[1];
+    o[s] = r[2 + e];
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kSplits; ++s) M = s < S ? fmaxf(M, m[s]) : M;
+  float L = 0.f, y = 0.f;
+#pragma unroll
+  for (int s = 0; s < kSplits; ++s) {
+    const float w = (s < S && m[s] > -INFINITY) ? __expf(m[s] - M) : 0.f;
+    L += w * l[s];
+    y += w * o[s];
+  }
+  Elem<T>::store((T*)a.y + (int64_t)b * a.y_bstride + (int64_t)h * HD + e, y / L);
+}
+
+template <typename T>
+int launch_split(const AttnArgs& a, int B, int hd, int S, float* ws, hipStream_t s) {
+  dim3 g1(S, a.H, B), g2(a.H, B);
+  switch (hd) {
+    case 16:
+      decode_attention_split_kernel<T, 16><<<g1, kSThreads, 0, s>>>(a, S, ws);
+      decode_attention_combine_kernel<T, 16><<<g2, 16, 0, s>>>(a, S, ws);
+      break;
+    case 32:
+      decode_attention_split_kernel<T, 32><<<g1, kSThreads, 0, s>>>(a, S, ws);
+      decode_attention_combine_kernel<T, 32><<<g2, 32, 0, s>>>(a, S, ws);
+      break;
+    case 64:
+      decode_attention_split_kernel<T, 64><<<g1, kSThreads, 0, s>>>(a, S, ws);
+      decode_attention_combine_kernel<T, 64><<<g2, 64, 0, s>>>(a, S, ws);
+      break;
+    default:
+      decode_attention_split_kernel<T, 128><<<g1, kSThreads, 0, s>>>(a, S, ws);
+      decode_attention_combine_kernel<T, 128><<<g2, 128, 0, s>>>(a, S, ws);
+      break;
+  }
+  return dh_check_launch("dh_decode_attention_split");
+}
+
 bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
 
 }  // namespace
@@ -312,4 +578,37 @@ extern "C" int dh_decode_attention(int dtype, const void* q, const void* k, cons
              sqrtf((float)hd)};
   hipStream_t s = (hipStream_t)stream;
   return dtype == DH_BF16 ? launch<bf16_t>(a, B, hd, s) : launch<float>(a, B, hd, s);
+}
+
+extern "C" int64_t dh_decode_attention_workspace_bytes(int B, int H, int hd) {
+  return (int64_t)B * H * kSplits * (2 + hd) * (int64_t)sizeof(float);
+}
+
+extern "C" int dh_decode_attention_split(int dtype, const void* q, const void* k, const void* v, int64_t qkv_bstride,
+                                         const void* rope_cos, const void* rope_sin, void* K_cache, void* V_cache,
+                                         const int64_t* t_dev, void* y, int64_t y_bstride, int B, int H, int hd,
+                                         int Tmax, int window, void* workspace, int64_t workspace_bytes,
+                                         void* stream) {
+  const char* who = "dh_decode_attention_split";
+  DH_REQUIRE(dtype == DH_F32 || dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d", who, dtype);
+  DH_REQUIRE(B >= 1 && B <= 65535 && H >= 1 && H <= 65535 && Tmax >= 1 && window >= 0, DH_ERR_INVALID_ARG,
+             "%s: B=%d H=%d Tmax=%d window=%d", who, B, H, Tmax, window);
+  DH_REQUIRE(hd == 16 || hd == 32 || hd == 64 || hd == 128, DH_ERR_UNSUPPORTED_SHAPE,
+             "%s: hd=%d not in {16,32,64,128}", who, hd);
+  const int nmax = window > 0 ? (window < Tmax ? window : Tmax) : Tmax;
+  DH_REQUIRE(nmax <= kMaxWindow, DH_ERR_UNSUPPORTED_SHAPE, "%s: attention span %d exceeds %d", who, nmax,
+             kMaxWindow);
+  DH_REQUIRE(q && k && v && rope_cos && rope_sin && K_cache && V_cache && t_dev && y && workspace,
+             DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
+  DH_REQUIRE(aligned(K_cache, 16) && aligned(V_cache, 16) && aligned(workspace, 16), DH_ERR_INVALID_ARG,
+             "%s: caches and workspace need 16-byte alignment", who);
+  DH_REQUIRE(workspace_bytes >= dh_decode_attention_workspace_bytes(B, H, hd), DH_ERR_INVALID_ARG,
+             "%s: workspace of %lld bytes, needs %lld", who, (long long)workspace_bytes,
+             (long long)dh_decode_attention_workspace_bytes(B, H, hd));
+  AttnArgs a{q, k, v, qkv_bstride, rope_cos, rope_sin, K_cache, V_cache, t_dev, y, y_bstride, H, Tmax, window,
+             sqrtf((float)hd)};
+  const int S = nmax < kSplits ? nmax : kSplits;
+  hipStream_t s = (hipStream_t)stream;
+  return dtype == DH_BF16 ? launch_split<bf16_t>(a, B, hd, S, (float*)workspace, s)
+                          : launch_split<float>(a, B, hd, S, (float*)workspace, s);
 }

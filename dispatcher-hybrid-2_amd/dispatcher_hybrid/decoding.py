@@ -444,6 +444,11 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         # staging of the two-launch mixer step, shared by every tree layer (same shapes)
         self.stage = torch.zeros(self._fused_step.stage_floats(Bb, mix0.num_heads, mix0.levels,
                                                                mix0.head_dim), device=dev)
+        # small batches split each head's attention window over several workgroups
+        att0 = next((b.attn for b in self.m.blocks if isinstance(b, AttentionBlock)), None)
+        self.attn_ws = None
+        if att0 is not None and Bb * att0.num_heads <= 64:
+            self.attn_ws = self._fused_step.attention_workspace(Bb, att0.num_heads, att0.head_dim, dev)
 
     @staticmethod
     def _eps(norm, dtype):
@@ -497,7 +502,7 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
                               (at.linear_v.weight, self.v_buf, d, 0)], self.t_buf,
                        norm_weight=blk.norm1.weight, eps=self._eps(blk.norm1, self.dtype), x_rows=rows)
         fs.decode_attention(self.q_buf, self.k_buf, self.v_buf, cache.rope_cos, cache.rope_sin,
-                            cache.k, cache.v, self.t_buf, self.y_buf, at.window)
+                            cache.k, cache.v, self.t_buf, self.y_buf, at.window, workspace=self.attn_ws)
         fs.decode_gemv(self.y_buf, [(at.linear_out.weight, self.x_buf, d, 0)], self.t_buf,
                        resid=x_in, resid_rows=rows)
         self._ffn_g(blk)

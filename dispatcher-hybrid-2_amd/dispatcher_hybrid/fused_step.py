@@ -237,14 +237,23 @@ step_gates_kernel = _Launcher(_step_gates, "step_gates_kernel")
 step_scan_kernel = _Launcher(_step_scan, "step_scan_kernel")
 
 
-def decode_attention(q, k, v, rope_cos, rope_sin, K_cache, V_cache, t_buf, y, window):
+def attention_workspace(B, H, hd, device):
+    """Workspace of the split-window attention step (``dh_decode_attention_split``)."""
+    n = int(_hip.lib.dh_decode_attention_workspace_bytes(B, H, hd))
+    return torch.empty((n + 3) // 4, dtype=torch.float32, device=device)
+
+
+def decode_attention(q, k, v, rope_cos, rope_sin, K_cache, V_cache, t_buf, y, window, workspace=None):
     """One decode step of a windowed RoPE attention layer (``dh_decode_attention``).
 
     q, k, v: (B, H*hd) projections at the device position t = t_buf[0]; K_cache/V_cache:
     (B, H, Tmax, hd) head-major caches (row t written here); rope_cos/rope_sin: (>= Tmax, hd/2)
     tables; y: (B, H*hd) receives softmax((q' . K) / sqrt(hd)) . V over [max(0, t+1-window), t]
     (the whole prefix when window is 0). One launch; same rounding points as the eager step
-    (reference dispatcher_hybrid/decoding.py:247-266, :411-435).
+    (reference dispatcher_hybrid/decoding.py:247-266, :411-435). With a `workspace`
+    (attention_workspace(B, H, hd, device)) the window is split over up to 16 workgroups per head
+    and combined in a second launch (``dh_decode_attention_split``), the probabilities then kept in
+    fp32: the small-batch form.
     """
     _hip.require_gpu(q, "decode_attention")
     B, H, Tmax, hd = K_cache.shape
@@ -264,6 +273,15 @@ def decode_attention(q, k, v, rope_cos, rope_sin, K_cache, V_cache, t_buf, y, wi
             or rope_cos.shape[-1] != hd // 2:
         raise ValueError("decode_attention: rope tables must be contiguous (>= Tmax, hd/2)")
     p = _hip.ptr
+    if workspace is not None:
+        if workspace.dtype != torch.float32 or not workspace.is_contiguous():
+            raise ValueError("decode_attention: workspace must be a contiguous fp32 tensor")
+        st = _hip.lib.dh_decode_attention_split(
+            _hip.dtype_code(dt), p(q), p(k), p(v), q.stride(0), p(rope_cos), p(rope_sin),
+            p(K_cache), p(V_cache), p(t_buf), p(y), y.stride(0), B, H, hd, Tmax, int(window),
+            p(workspace), workspace.numel() * 4, _hip.stream_handle(q.device))
+        _hip.check(st, "dh_decode_attention_split")
+        return
     st = _hip.lib.dh_decode_attention(
         _hip.dtype_code(dt), p(q), p(k), p(v), q.stride(0), p(rope_cos), p(rope_sin),
         p(K_cache), p(V_cache), p(t_buf), p(y), y.stride(0), B, H, hd, Tmax, int(window),

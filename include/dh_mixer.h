@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 7
+#define DH_ABI_VERSION 8
 
 enum dh_status {
   DH_OK = 0,
@@ -199,6 +199,21 @@ int dh_decode_attention(int dtype, const void* q, const void* k, const void* v, 
                         const void* rope_cos, const void* rope_sin, void* K_cache, void* V_cache,
                         const int64_t* t_dev, void* y, int64_t y_bstride, int B, int H, int hd, int Tmax,
                         int window, void* stream);
+
+/*
+ * dh_decode_attention for small batches, as two launches over a split window: the window is cut
+ * into min(16, span) segments, one workgroup per (segment, head, row) computes the segment's
+ * rounded scores, maximum m_s, exp-sum l_s and unnormalised value sum o_s into `workspace`
+ * (dh_decode_attention_workspace_bytes(B, H, hd) bytes), and a second launch writes
+ * y = round(sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s). Same arguments, cache update and scores
+ * as dh_decode_attention; the probabilities enter the value sum in fp32 (dh_decode_attention
+ * rounds them to the model dtype first, as the eager bf16 step does).
+ */
+int64_t dh_decode_attention_workspace_bytes(int B, int H, int hd);
+int dh_decode_attention_split(int dtype, const void* q, const void* k, const void* v, int64_t qkv_bstride,
+                              const void* rope_cos, const void* rope_sin, void* K_cache, void* V_cache,
+                              const int64_t* t_dev, void* y, int64_t y_bstride, int B, int H, int hd, int Tmax,
+                              int window, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * dh_decode_mixer_step as two launches with a wider first one, for the graphed decoder:

@@ -55,15 +55,21 @@ CASES = [
     (1, 2, 128, 300, 256, 0),             # first position, hd 128
     (16, 16, 64, 4096, 1024, 1500),       # batch 16
     (1, 1, 64, 2048, 0, 2047),            # 2048 positions: more than one sweep per thread
+    (1, 16, 64, 4096, 0, 4095),           # whole prefix: 256 positions per split segment (2 sweeps)
+    (2, 3, 128, 40, 0, 3),                # fewer positions than segments (empty segments)
 ]
 
 
+@pytest.mark.parametrize("split", [False, True], ids=["one_launch", "split_window"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("case", CASES)
-def test_decode_attention_matches_eager_step(case, dtype):
+def test_decode_attention_matches_eager_step(case, dtype, split):
+    """split_window (dh_decode_attention_split) keeps the probabilities in fp32 where the eager bf16
+    step rounds them: its bf16 bar is the same 1e-2 relative (the rounding moves y by ~2^-9 of the
+    value average's magnitude)."""
     from dispatcher_hybrid import fused_step
     B, H, hd, Tmax, window, t = case
-    print(f"decode_attention case={case} {dtype}", flush=True)
+    print(f"decode_attention case={case} {dtype} split={split}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(hd * 31 + t)
     d = H * hd
     q = torch.randn(B, d, device=DEV, generator=g).to(dtype)
@@ -76,7 +82,10 @@ def test_decode_attention_matches_eager_step(case, dtype):
     K0, V0 = K.clone(), V.clone()
     y = torch.full((B, d), 7.0, device=DEV, dtype=dtype)
     t_buf = torch.full((1,), t, dtype=torch.long, device=DEV)
-    fused_step.decode_attention(q, k, v, cos, sin, K, V, t_buf, y, window)
+    ws = fused_step.attention_workspace(B, H, hd, DEV) if split else None
+    if ws is not None:
+        ws.fill_(float("nan"))                           # every record read is written first
+    fused_step.decode_attention(q, k, v, cos, sin, K, V, t_buf, y, window, workspace=ws)
     torch.cuda.synchronize()
     assert rel_err(y, ref_y) < (1e-5 if dtype == torch.float32 else 1e-2)
     # the cache changes in row t only: the rotated key and the value, bit for bit
@@ -87,7 +96,8 @@ def test_decode_attention_matches_eager_step(case, dtype):
     assert torch.equal(K[:, :, rest], K0[:, :, rest]) and torch.equal(V[:, :, rest], V0[:, :, rest])
 
 
-def test_decode_attention_position_out_of_range_writes_nothing():
+@pytest.mark.parametrize("split", [False, True], ids=["one_launch", "split_window"])
+def test_decode_attention_position_out_of_range_writes_nothing(split):
     from dispatcher_hybrid import fused_step
     B, H, hd, Tmax = 1, 2, 64, 32
     q = torch.randn(B, H * hd, device=DEV)
@@ -97,7 +107,8 @@ def test_decode_attention_position_out_of_range_writes_nothing():
     cos, sin = _rope_tables(Tmax, hd, torch.float32)
     y = torch.full((B, H * hd), 3.0, device=DEV)
     t_buf = torch.full((1,), Tmax, dtype=torch.long, device=DEV)
-    fused_step.decode_attention(q, q, q, cos, sin, K, V, t_buf, y, 0)
+    ws = fused_step.attention_workspace(B, H, hd, DEV) if split else None
+    fused_step.decode_attention(q, q, q, cos, sin, K, V, t_buf, y, 0, workspace=ws)
     torch.cuda.synchronize()
     assert torch.equal(K, K0) and torch.equal(V, V0) and bool((y == 3.0).all())
 
