@@ -647,9 +647,13 @@ struct ScanOutArgs {
   int Tmax, S, H, hd, L, N;
 };
 constexpr int kSOThreads = 256;
+#ifndef DH_SCANOUT_ROWS
+#define DH_SCANOUT_ROWS 1
+#endif
+constexpr int kSORows = DH_SCANOUT_ROWS;   // output rows per wave (each workgroup redoes the recurrence)
 constexpr int kSOEpt = 4;                  // recurrence elements per thread: d <= 1024
 
-template <typename T, int CG, int LMAX>
+template <typename T, int CG, int LMAX, int RW>
 __global__ __launch_bounds__(kSOThreads) void decode_scan_out_kernel(ScanOutArgs a) {
   constexpr int kMaxD = kSOEpt * kSOThreads;           // 1024
   constexpr int VCH = kMaxD * LMAX * (int)sizeof(T) / 16 / kSOThreads;   // staged 16-byte chunks per thread
@@ -685,16 +689,19 @@ __global__ __launch_bounds__(kSOThreads) void decode_scan_out_kernel(ScanOutArgs
   uint32_t v0r[kSOEpt];
 #pragma unroll
   for (int q = 0; q < kSOEpt; ++q) v0r[q] = Raw<T>::load((const T*)a.V0 + e0 + q);
-  // the residual of this wave's output row (every lane reads it; lane 0 uses it)
-  const int n = min((int)blockIdx.x * 4 + wave, a.N - 1);
+  // the residual of output row nbase + lane % RW (lane r < RW uses it)
+  const int nbase = ((int)blockIdx.x * (kSOThreads / 64) + wave) * RW;
   const int64_t rrow = a.resid_rows ? load_uniform(a.resid_rows) : 0;
-  const uint32_t rc = Raw<T>::load((const T*)a.resid + rrow * a.resid_stride + n);
+  const uint32_t rc = Raw<T>::load((const T*)a.resid + rrow * a.resid_stride + min(nbase + lane % RW, a.N - 1));
   DH_ISSUE_FENCE();
 
-  // ---- the wave's weight row, one burst
-  uint4 w[CG];
+  // ---- the wave's RW weight rows, one burst
+  uint4 w[RW][CG];
 #pragma unroll
-  for (int c = 0; c < CG; ++c) w[c] = ld16((const T*)a.W + (int64_t)n * d + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
+  for (int c = 0; c < CG; ++c)
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+      w[r][c] = ld16((const T*)a.W + (int64_t)min(nbase + r, a.N - 1) * d + (int64_t)min(lane + 64 * c, nchunk - 1) * V);
   DH_ISSUE_FENCE();
 
   // ---- stage into LDS (waits for the staging loads only; clamped duplicates rewrite the last slot)
@@ -746,24 +753,34 @@ __global__ __launch_bounds__(kSOThreads) void decode_scan_out_kernel(ScanOutArgs
   if (tid * kSOEpt < d) Quad<T>::store(reinterpret_cast<T*>(sy) + e0, v);
   __syncthreads();
 
-  // ---- out[n] = round(round(W[n] . Y) + resid[n])
-  float acc = 0.f;
+  // ---- out[n] = round(round(W[n] . Y) + resid[n]) for the wave's rows
+  float acc[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) acc[r] = 0.f;
 #pragma unroll
   for (int c = 0; c < CG; ++c) {
     const int ch = lane + 64 * c;
-    float wv[V], yv[V];
-    Chunk<T>::unpack(w[c], wv);
+    float yv[V];
     Chunk<T>::unpack(sy[min(ch, nchunk - 1)], yv);
-    float part = 0.f;
 #pragma unroll
-    for (int e = 0; e < V; ++e) part += wv[e] * yv[e];
-    acc += ch < nchunk ? part : 0.f;
+    for (int r = 0; r < RW; ++r) {
+      float wv[V];
+      Chunk<T>::unpack(w[r][c], wv);
+      float part = 0.f;
+#pragma unroll
+      for (int e = 0; e < V; ++e) part += wv[e] * yv[e];
+      acc[r] += ch < nchunk ? part : 0.f;
+    }
   }
-  acc = wave_sum(acc);
-  if (lane == 0 && live && (int)blockIdx.x * 4 + wave < a.N) {
+#pragma unroll
+  for (int r = 0; r < RW; ++r) acc[r] = wave_sum(acc[r]);
+  if (lane < RW && live && nbase + lane < a.N) {
+    float v0 = 0.f;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) v0 = r == lane ? acc[r] : v0;
     uint32_t rv = rc;
     asm volatile("" : "+v"(rv));                        // converted here, not beside its load
-    Elem<T>::store((T*)a.out + n, Elem<T>::round(Elem<T>::round(acc) + Raw<T>::f(rv)));
+    Elem<T>::store((T*)a.out + nbase + lane, Elem<T>::round(Elem<T>::round(v0) + Raw<T>::f(rv)));
   }
 }
 
@@ -927,9 +944,9 @@ extern "C" int dh_decode_scan_out(int dtype, const void* V0, const float* stage,
   DH_REQUIRE(aligned(stage, 16) && aligned(W, 16), DH_ERR_INVALID_ARG, "%s: stage/W need 16-byte alignment", who);
   ScanOutArgs a{V0, stage, t_dev, V_ring, Y, W, resid, resid_rows, resid_stride, out, Tmax, S, H, hd, L, N};
   hipStream_t s = (hipStream_t)stream;
-  const int grid = (N + 3) / 4;
+  const int grid = (N + (kSOThreads / 64) * kSORows - 1) / ((kSOThreads / 64) * kSORows);
   const int C = (d / vec + 63) / 64;
-#define DH_SO(TT, CC, LL) decode_scan_out_kernel<TT, CC, LL><<<dim3(grid), dim3(kSOThreads), 0, s>>>(a)
+#define DH_SO(TT, CC, LL) decode_scan_out_kernel<TT, CC, LL, kSORows><<<dim3(grid), dim3(kSOThreads), 0, s>>>(a)
   if (dtype == DH_BF16) {
     if (L <= 8) { if (C <= 2) DH_SO(bf16_t, 2, 8); else DH_SO(bf16_t, 4, 8); }
     else if (L <= 12) { if (C <= 2) DH_SO(bf16_t, 2, 12); else DH_SO(bf16_t, 4, 12); }
