@@ -81,6 +81,9 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // result and the compiler's hazard pass does not look into inline assembly. The hot loop feeds it
 // v_max results only; everything else rounds with round_bf16_sw.
 __device__ __forceinline__ float round_bf16_sw(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+// the same through the compiler's own conversion (v_cvt_pk_bf16_f32 + shift; round to nearest
+// even, NaN stays NaN), usable on transcendental results
+__device__ __forceinline__ float round_bf16_cc(float x) { return (float)(__bf16)x; }
 __device__ __forceinline__ float round_bf16(float x) {
   float r;
   asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(x));
@@ -304,6 +307,236 @@ __global__ __launch_bounds__(kThreads) void gate_preacts_fwd_kernel(FwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// bf16 forward with the weights staged in LDS (H <= 16).
+//
+// The kernel above streams every weight fragment from the cache hierarchy into every wave: per
+// k-step a wave reads 3 KB of weights per level for 1 KB of activations, and at C5 sizes
+// (b = 8, T = 4096) the launch is bound by those cache reads (L2 requests ~25x the bytes the
+// launch needs) and by the waits on them. Here a workgroup of 4 waves owns P = 64*MB positions and
+// LG levels; for each 64-wide k-chunk it copies the chunk of W_i/W_f/W_r of its levels
+// (LG x 3 x 16 heads x 64 k, bf16) into LDS once, with rows padded to 144 bytes so the 16-byte
+// reads of the MFMA B operand (lanes = 16 heads x 4 k-groups) hit distinct banks, and every wave
+// reads each fragment once for its MB row blocks of 16 positions. The activation fragments (A
+// rows, lagged B rows) go straight from memory into MFMA A-operand registers, one k-step ahead;
+// the next chunk's weights are requested at the start of a chunk and written to the other LDS
+// buffer at its end (one barrier per chunk). Same arithmetic, rounding points and outputs as the
+// kernel above.
+// ---------------------------------------------------------------------------------------------
+constexpr int kLdsKC = 64;                      // k elements per LDS weight chunk (2 MFMA k-steps)
+constexpr int kLdsRow = kLdsKC * 2 + 16;         // padded LDS row: 144 bytes
+
+// occupancy by register footprint: (levels x row blocks) accumulators plus two chunks of fragments
+template <int LG, int MB> struct LdsOcc { static constexpr int value = LG * MB >= 4 ? 2 : 3; };
+
+template <int LG, int MB, bool HAS_MASK>
+__global__ __launch_bounds__(kThreads, (LdsOcc<LG, MB>::value)) void gate_preacts_fwd_lds_kernel(FwdArgs a) {
+  typedef bf16_t T;
+  constexpr int P = 64 * MB;                     // positions per workgroup
+  constexpr int WBYTES = LG * 3 * 16 * kLdsRow;  // one LDS weight buffer
+  constexpr int PIECES = LG * 3 * 16 * (kLdsKC / 8);   // 16-byte pieces of one chunk
+  constexpr int PPT = (PIECES + kThreads - 1) / kThreads;
+  __shared__ __align__(16) unsigned char wl[2][WBYTES];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int b = blockIdx.z;
+  const int l0 = blockIdx.y * LG;
+  const int tbase = blockIdx.x * P + wave * 16 * MB;   // first position of the wave
+
+  const uint32_t row_bytes = (uint32_t)((int64_t)a.T * a.sat * (int64_t)sizeof(T));
+  const __amdgpu_buffer_rsrc_t rA = buf_rsrc((const T*)a.A + (int64_t)b * a.sab, row_bytes);
+  const __amdgpu_buffer_rsrc_t rB = buf_rsrc((const T*)a.B + (int64_t)b * a.sab, row_bytes);
+  const uint32_t w_bytes = (uint32_t)((int64_t)a.n_lv * a.swl * (int64_t)sizeof(T));
+  const __amdgpu_buffer_rsrc_t rW[3] = {buf_rsrc(a.Wi, w_bytes), buf_rsrc(a.Wf, w_bytes), buf_rsrc(a.Wr, w_bytes)};
+
+  // ---- activation loads. The MFMA A operand wants lane (r, g) = (lane % 16, lane / 16) to hold
+  // 16 bytes of row r; loaded that way, the four lanes of every quad read four different rows and
+  // the texture unit serves the load at a quarter of its rate (measured: the data return path busy
+  // ~80% of the launch). So lane S loads piece S & 3 of row S >> 2 (each quad reads 64 contiguous
+  // bytes of one row) and four ds_bpermute moves per fragment hand lane (r, g) the piece of source
+  // lane 4 r + g.
+  const int crow = lane >> 2, cpiece = lane & 3;
+  const int bperm = 4 * (4 * r + g);                 // byte address of the source lane
+  uint32_t aoff[MB], boff[MB][LG];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int t = tbase + 16 * mb + crow;
+    const bool t_ok = t < a.T;
+    const int tc = t_ok ? t : a.T - 1;
+    aoff[mb] = (uint32_t)(((int64_t)tc * a.sat + cpiece * 8) * (int64_t)sizeof(T));
+#pragma unroll
+    for (int j = 0; j < LG; ++j) {
+      const int lv = min(l0 + j, a.n_lv - 1);
+      float mv = 1.f;
+      if (HAS_MASK)
+        mv = Elem<T>::load((const T*)a.mask + (int64_t)b * a.smb + (int64_t)tc * a.smt + (int64_t)lv * a.sml);
+      const int src = tc - (1 << lv);
+      const bool keep = t_ok && src >= 0 && l0 + j < a.n_lv && mv > 0.f;
+      // a row without a source reads past the descriptor's range, which returns zeros (B = 0)
+      boff[mb][j] = keep ? (uint32_t)(((int64_t)src * a.sat + cpiece * 8) * (int64_t)sizeof(T)) : 0x80000000u;
+    }
+  }
+  auto to_mfma = [&](const uint4& v) {
+    return make_uint4((uint32_t)__builtin_amdgcn_ds_bpermute(bperm, (int)v.x),
+                      (uint32_t)__builtin_amdgcn_ds_bpermute(bperm, (int)v.y),
+                      (uint32_t)__builtin_amdgcn_ds_bpermute(bperm, (int)v.z),
+                      (uint32_t)__builtin_amdgcn_ds_bpermute(bperm, (int)v.w));
+  };
+
+  // ---- weight chunk copy: piece q = tid + 256 i -> (level j, gate x, head n, 16-byte column c).
+  // A (level, gate) block is 16 rows x 8 pieces = 128 pieces = two waves, so the block index
+  // jx = q >> 7 = 2 i + wave / 2 is uniform over a wave: its descriptor is picked with scalar
+  // selects (a per-lane descriptor would make the compiler loop over the lanes' distinct values).
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t wsrc[PPT], wdst[PPT];
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int q = min(tid + i * kThreads, PIECES - 1);
+    const int c = q & 7, n = (q >> 3) & 15;
+    const int jx = min(2 * i + (wave_u >> 1), 3 * LG - 1);   // = q >> 7 (uniform)
+    const int j = jx / 3;
+    const int lv = min(l0 + j, a.n_lv - 1), nc = min(n, a.H - 1);
+    wsrc[i] = (uint32_t)(((int64_t)lv * a.swl + (int64_t)nc * a.swh + c * 8) * (int64_t)sizeof(T));
+    wdst[i] = (uint32_t)((jx * 16 + n) * kLdsRow + c * 16);
+  }
+  uint4 wst[PPT];
+  auto w_fetch = [&](int k0) {
+    const uint32_t kb = (uint32_t)(k0 * (int)sizeof(T));
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int jx = min(2 * i + (wave_u >> 1), 3 * LG - 1);
+      const int x = jx % 3;
+      const __amdgpu_buffer_rsrc_t rw = x == 0 ? rW[0] : (x == 1 ? rW[1] : rW[2]);
+      wst[i] = bld16(rw, wsrc[i], kb);
+    }
+  };
+  auto w_store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i)
+      if (tid + i * kThreads < PIECES) *reinterpret_cast<uint4*>(&wl[buf][wdst[i]]) = wst[i];
+  };
+
+  f32x4 acc[MB][LG][3];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int j = 0; j < LG; ++j)
+#pragma unroll
+      for (int x = 0; x < 3; ++x) acc[mb][j][x] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // activation fragments of one chunk (2 k-steps): A rows and the LG lagged B rows of each row
+  // block. Two chunk buffers in ping-pong: the next chunk's fragments are in flight during the
+  // whole current chunk (the loads' latency under load is several k-steps of arithmetic).
+  uint4 xA[2][MB], xB[2][MB][LG], yA[2][MB], yB[2][MB][LG];
+  auto fetch = [&](int k0, uint4 (&fA)[2][MB], uint4 (&fB)[2][MB][LG]) {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const uint32_t kb = (uint32_t)((k0 + 32 * kk) * (int)sizeof(T));
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        fA[kk][mb] = bld16(rA, aoff[mb], kb);
+#pragma unroll
+        for (int j = 0; j < LG; ++j) fB[kk][mb][j] = bld16(rB, boff[mb][j], kb);
+      }
+    }
+  };
+  // one chunk from the LDS weight buffer `buf`
+  auto compute = [&](const uint4 (&fA)[2][MB], const uint4 (&fB)[2][MB][LG], int buf) {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      float af[MB][8];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) MathBf16::unpack_a(to_mfma(fA[kk][mb]), af[mb]);
+#pragma unroll
+      for (int j = 0; j < LG; ++j) {
+        uint4 w[3];
+#pragma unroll
+        for (int x = 0; x < 3; ++x)
+          w[x] = *reinterpret_cast<const uint4*>(&wl[buf][((j * 3 + x) * 16 + r) * kLdsRow + kk * 64 + g * 16]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) MathBf16::mma3(acc[mb][j], af[mb], to_mfma(fB[kk][mb][j]), w);
+      }
+    }
+  };
+  const int nchunk_ = a.GH / kLdsKC;
+  // chunk c: request chunk c+1 (weights and fragments), compute chunk c, store the weights of c+1
+  auto chunk = [&](int c, const uint4 (&cA)[2][MB], const uint4 (&cB)[2][MB][LG], uint4 (&nA)[2][MB],
+                   uint4 (&nB)[2][MB][LG]) {
+    const bool more = c + 1 < nchunk_;                   // uniform
+    if (more) {
+      w_fetch((c + 1) * kLdsKC);
+      fetch((c + 1) * kLdsKC, nA, nB);
+    }
+    compute(cA, cB, c & 1);
+    if (more) w_store((c + 1) & 1);
+    __syncthreads();
+  };
+
+  w_fetch(0);
+  fetch(0, xA, xB);
+  w_store(0);
+  __syncthreads();
+  int c = 0;
+  for (; c + 1 < nchunk_; c += 2) {
+    chunk(c, xA, xB, yA, yB);
+    chunk(c + 1, yA, yB, xA, xB);
+  }
+  if (c < nchunk_) chunk(c, xA, xB, yA, yB);
+
+  // ---- epilogue: C fragment column (head) r, rows 4g + i of row block mb
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int tb = tbase + 16 * mb + g * 4;
+    const bool vec = a.vec_out && tb + 3 < a.T;
+#pragma unroll
+    for (int j = 0; j < LG; ++j) {
+      const int l = l0 + j;
+      if (l >= a.n_lv || r >= a.H) continue;
+      const float bias[3] = {a.bi[l * a.H + r], a.bf[l * a.H + r], a.br[l * a.H + r]};
+      T* outs[3] = {(T*)a.oi, (T*)a.of, (T*)a.orr};
+      const int64_t base = (int64_t)b * a.sob + (int64_t)l * a.sol + (int64_t)r * a.soh;
+      float v[3][4];
+#pragma unroll
+      for (int x = 0; x < 3; ++x)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[x][i] = acc[mb][j][x][i] + bias[x];
+      if (a.activate) {
+        float mval[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          mval[i] = 1.f;
+          if (HAS_MASK) {
+            const int to = min(tb + i, a.T - 1);
+            mval[i] = Elem<T>::load((const T*)a.mask + (int64_t)b * a.smb + (int64_t)to * a.smt + (int64_t)l * a.sml);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float m = (tb + i >= (1 << l) && mval[i] > 0.f) ? 1.f : 0.f;
+          // compiler-emitted bf16 rounding (hardware conversion, its hazards handled)
+          const float si = round_bf16_cc(dh_sigmoid(round_bf16_cc(v[0][i])));
+          const float sf = round_bf16_cc(dh_sigmoid(round_bf16_cc(v[1][i])));
+          const float sr = round_bf16_cc(dh_sigmoid(round_bf16_cc(v[2][i])));
+          v[0][i] = si * m;
+          v[1][i] = sf * m + (1.f - m);
+          v[2][i] = sr;
+        }
+      }
+#pragma unroll
+      for (int x = 0; x < 3; ++x) {
+        if (vec) {
+          MathBf16::store4(outs[x] + base + tb, v[x]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (tb + i < a.T) outs[x][base + (int64_t)(tb + i) * a.sot] = MathBf16::out(v[x][i]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // backward (reference dispatcher_hybrid/fused_gates.py:96-173)
 //   dh[t,l,k]  = sum_{x,h} dP_x[t,l,h] * W_x[l,h,k]
 //   dx[t,l,k]  = 2 * relu(a + ok*b)[k] * dh[t,l,k]        (a+b rounded as in the forward)
@@ -461,6 +694,25 @@ void launch_fwd(const FwdArgs& a, dim3 grid, hipStream_t s) {
     gate_preacts_fwd_kernel<M, LG, KU, false><<<grid, dim3(kThreads), 0, s>>>(a);
 }
 
+template <int LG, int MB>
+void launch_fwd_lds(const FwdArgs& a, hipStream_t s) {
+  constexpr int P = 64 * MB;
+  dim3 grid((a.T + P - 1) / P, (a.n_lv + LG - 1) / LG, a.b);
+  if (a.mask)
+    gate_preacts_fwd_lds_kernel<LG, MB, true><<<grid, dim3(kThreads), 0, s>>>(a);
+  else
+    gate_preacts_fwd_lds_kernel<LG, MB, false><<<grid, dim3(kThreads), 0, s>>>(a);
+}
+
+// Tile per workgroup (measured on MI355X at the released widths): two levels x 64 positions once
+// the launch has >= 1024 workgroups (b = 8, T = 4096: 154 us, against 169 for 2 x 128 and 172
+// for 1 x 64), else one level x 64 positions, the most workgroups for short prefills.
+void dispatch_fwd_lds(const FwdArgs& a, hipStream_t s) {
+  const int64_t wgs21 = (int64_t)((a.T + 63) / 64) * ((a.n_lv + 1) / 2) * a.b;
+  if (wgs21 >= 1024) launch_fwd_lds<2, 1>(a, s);
+  else launch_fwd_lds<1, 1>(a, s);
+}
+
 template <typename M>
 void dispatch_fwd(const FwdArgs& a, int LG, int KU, dim3 grid, hipStream_t s) {
   if (LG == 1 && KU == 4) launch_fwd<M, 1, 4>(a, grid, s);
@@ -514,7 +766,9 @@ extern "C" int dh_gate_preacts_fwd(int dtype, const void* A, const void* B, int6
   if (KU == 2 && LG == 1) KU = 1;                            // no <1, 2> instantiation
   dim3 grid(tiles, ngroups, b);
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == DH_BF16)
+  if (dtype == DH_BF16 && H <= 16)
+    dispatch_fwd_lds(a, s);
+  else if (dtype == DH_BF16)
     dispatch_fwd<MathBf16>(a, LG, KU, grid, s);
   else
     dispatch_fwd<MathF32>(a, LG, KU, grid, s);

@@ -35,9 +35,12 @@ PREACT_CASES = [
     (1, 256, 512, 8, 8, False),          # C1 shape (d 512, 8 levels, T 256)
     (2, 200, 1024, 16, 12, True),        # release widths
     # level groups: the host gives each workgroup LG levels so that tiles x groups >= 1024
+    # (fp32 streaming kernel: level groups of 2, 3, 4; bf16 LDS kernel: two levels per workgroup
+    # from 1024 workgroups, with a partial last tile and a one-level last group in the second)
     (3, 4096, 128, 4, 12, False),        # 192 tiles -> LG 2, two k-chunks per step
     (11, 1500, 64, 4, 12, True),         # 264 tiles -> LG 3, last group 2 levels, last tile partial
     (6, 4096, 64, 4, 12, True),          # 384 tiles -> LG 4
+    (2, 4096, 128, 8, 12, True),         # bf16: 768 two-level workgroups -> one level per workgroup
 ]
 
 
