@@ -240,6 +240,144 @@ __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
   }
 }
 
+// Contexts up to 4096 positions: 1024 threads (PPT <= 4 positions each, 4 waves per SIMD) and
+// C = 8 columns per workgroup. Each level exchanges the state itself, not r * V: position t
+// publishes V[t] (column pairs as float2, consecutive positions in consecutive 8-byte words, so
+// neither the writes nor the shifted reads conflict on LDS banks) and r[t] once, and the
+// destination forms coef = a[t] * r[t - 2^l] once per position, then V = f * V + coef * V_src:
+// two VALU operations per element and level instead of three. 144 KB of LDS at T = 4096.
+template <typename T, int PPT, int MODE>
+__global__ __launch_bounds__(1024) void level_scan_wide_kernel(ScanArgs a) {
+  constexpr int C = 8, NT = 1024, TC = PPT * NT;
+  __shared__ float2 vs[C / 2][TC];
+  __shared__ float rs[TC];
+  const int nchunks = a.hd / C;
+  const int ngroups = a.b * a.H;
+  const int bid = blockIdx.x;
+  const int x = bid & 7, rem = bid >> 3;
+  const int c = rem % nchunks, g = (rem / nchunks) * 8 + x;
+  if (g >= ngroups) return;
+  const int b = g / a.H, h = g % a.H;
+  const int64_t col0 = (int64_t)h * a.hd + (int64_t)c * C;
+  const int tid = threadIdx.x;
+
+  const int64_t gb = (int64_t)b * a.spb + (int64_t)h * a.sph;
+  const T* pi = (const T*)a.pre_i + gb;
+  const T* pf = (const T*)a.pre_f + gb;
+  const T* pr = (const T*)a.pre_r + gb;
+  const T* mk = (const T*)a.mask + (MODE == kPreMask ? (int64_t)b * a.smb : 0);
+
+  float V[PPT][C];
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    const int t = tid + j * NT;
+    const int tc = t < a.T ? t : a.T - 1;
+    load_cols<T, C>((const T*)a.V0 + (int64_t)b * a.svb + (int64_t)tc * a.svt + col0, V[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    const bool live = tid + j * NT < a.T;
+#pragma unroll
+    for (int cc = 0; cc < C; ++cc) V[j][cc] = live ? V[j][cc] : 0.f;
+  }
+  uint32_t goff[PPT], moff[PPT];
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    const int t = tid + j * NT;
+    const uint32_t tc = t < a.T ? t : a.T - 1;
+    goff[j] = tc * (uint32_t)a.spt;
+    moff[j] = tc * (uint32_t)a.smt;
+  }
+  uint32_t ri[PPT], rf[PPT], rr[PPT], rm[PPT];
+  auto fetch = [&](int l) {
+    const T* li = pi + (int64_t)l * a.spl;
+    const T* lf = pf + (int64_t)l * a.spl;
+    const T* lr = pr + (int64_t)l * a.spl;
+    const T* lm = mk + (int64_t)l * a.sml;
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      ri[j] = Raw<T>::load(li + goff[j]);
+      rf[j] = Raw<T>::load(lf + goff[j]);
+      rr[j] = Raw<T>::load(lr + goff[j]);
+      if (MODE == kPreMask) rm[j] = Raw<T>::load(lm + moff[j]);
+    }
+  };
+  fetch(0);
+
+  const int64_t d = (int64_t)a.H * a.hd;
+  auto write_slab = [&](int j) {
+    if (a.ring == nullptr || j >= a.ring_L) return;   // uniform
+    const int p0 = a.T - (2 << j);
+    const int msk = (2 << j) - 1;
+    T* rb = (T*)a.ring + (int64_t)b * ((int64_t)(2 << a.ring_L) - 2) * d + (int64_t)((2 << j) - 2) * d + col0;
+#pragma unroll
+    for (int jj = 0; jj < PPT; ++jj) {
+      const int t = tid + jj * NT;
+      if (t < a.T && t >= p0) store_cols<T, C>(rb + (int64_t)(t & msk) * d, V[jj]);
+    }
+  };
+  write_slab(0);
+
+  for (int l = 0; l < a.n_lv; ++l) {
+    const int shift = 1 << l;
+    float rg[PPT], ad[PPT], fg[PPT];
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int t = tid + j * NT;
+      if (MODE == kActivated) {
+        ad[j] = Raw<T>::f(ri[j]);
+        fg[j] = Raw<T>::f(rf[j]);
+        rg[j] = Raw<T>::f(rr[j]);
+      } else {
+        const bool up = t >= shift && (MODE != kPreMask || Raw<T>::f(rm[j]) > 0.f);
+        ad[j] = up ? dh_sigmoid(Raw<T>::f(ri[j])) : 0.f;
+        fg[j] = up ? dh_sigmoid(Raw<T>::f(rf[j])) : 1.f;
+        rg[j] = dh_sigmoid(Raw<T>::f(rr[j]));
+      }
+    }
+    fetch(l + 1 < a.n_lv ? l + 1 : l);                 // next level's gates fly during the exchange
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int t = tid + j * NT;
+#pragma unroll
+      for (int q = 0; q < C / 2; ++q) vs[q][t] = make_float2(V[j][2 * q], V[j][2 * q + 1]);
+      rs[t] = rg[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int t = tid + j * NT;
+      const int s = t >= shift ? t - shift : 0;          // a = 0 where there is no source
+      const float coef = ad[j] * rs[s];
+#pragma unroll
+      for (int q = 0; q < C / 2; ++q) {
+        const float2 w = vs[q][s];
+        V[j][2 * q] = fg[j] * V[j][2 * q] + coef * w.x;
+        V[j][2 * q + 1] = fg[j] * V[j][2 * q + 1] + coef * w.y;
+      }
+    }
+    write_slab(l + 1);
+    __syncthreads();
+  }
+  for (int j = a.n_lv + 1; j < a.ring_L; ++j) write_slab(j);
+
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    const int t = tid + j * NT;
+    if (t < a.T) store_cols<T, C>((T*)a.V + ((int64_t)b * a.T + t) * ((int64_t)a.H * a.hd) + col0, V[j]);
+  }
+}
+
+template <typename T, int PPT>
+void launch_wide(const ScanArgs& a, int mode, hipStream_t s) {
+  const int nchunks = a.hd / 8;
+  const int grid = ((a.b * a.H + 7) / 8) * 8 * nchunks;
+  auto go = [&](auto kern) { kern<<<dim3(grid), dim3(1024), 0, s>>>(a); };
+  if (mode == kActivated) go(level_scan_wide_kernel<T, PPT, kActivated>);
+  else if (mode == kPreMask) go(level_scan_wide_kernel<T, PPT, kPreMask>);
+  else go(level_scan_wide_kernel<T, PPT, kPreNoMask>);
+}
+
 template <typename T, int C, int PPT>
 void launch(const ScanArgs& a, int mode, hipStream_t s) {
   const int nchunks = a.hd / C;
@@ -255,10 +393,9 @@ void launch(const ScanArgs& a, int mode, hipStream_t s) {
 
 template <typename T>
 int dispatch(const ScanArgs& a, int mode, hipStream_t s) {
-  if (a.T <= 512) launch<T, 8, 1>(a, mode, s);
-  else if (a.T <= 1024) launch<T, 8, 2>(a, mode, s);
-  else if (a.T <= 2048) launch<T, 8, 4>(a, mode, s);
-  else if (a.T <= 4096) launch<T, 8, 8>(a, mode, s);
+  if (a.T <= 1024) launch_wide<T, 1>(a, mode, s);
+  else if (a.T <= 2048) launch_wide<T, 2>(a, mode, s);
+  else if (a.T <= 4096) launch_wide<T, 4>(a, mode, s);
   else if (a.T <= 8192) launch<T, 4, 16>(a, mode, s);
   else if (a.T <= 16384) launch<T, 2, 32>(a, mode, s);
   else launch<T, 1, 64>(a, mode, s);

@@ -93,7 +93,9 @@ SCAN_CASES = [
     (1, 256, 8, 64, 8, False),           # C1
     (1, 600, 2, 32, 10, True),           # PPT = 2
     (2, 1024, 16, 64, 11, True),         # C2 length
+    (1, 1500, 4, 32, 11, True),          # two positions per thread
     (1, 4096, 2, 128, 12, True),         # full context, hd 128
+    (1, 5000, 2, 64, 12, False),         # past 4096 positions: the 512-thread kernel
 ]
 
 
@@ -115,6 +117,39 @@ def test_level_scan_matches_oracle(case, dtype):
     ref = om.level_scan(*[_np(p) for p in tp], _np(tV0), H, mask)
     err = rel_err(_np(V), ref)
     assert err < (1e-5 if dtype == torch.float32 else 2e-2), f"rel {err:.3e}"
+
+
+@pytest.mark.parametrize("T,n_lv,ring_L", [(3000, 12, 12), (1500, 11, 12), (300, 9, 10)])
+def test_level_scan_ring_output(T, n_lv, ring_L):
+    """The decoder-prefill output of the scan (fp32, pre-activation mode with a mask): ring slab j
+    holds, at slot 2^(j+1) - 2 + (p & (2^(j+1) - 1)), the state entering level j of each of the last
+    2^(j+1) positions p (reference decoding.py:50-76, 143-185): the oracle scan run with j levels;
+    beyond n_lv the final state. Slots of positions before the prompt stay untouched."""
+    from dispatcher_hybrid import fused_gates as fg
+    print(f"level_scan ring T={T} n_lv={n_lv} ring_L={ring_L}", flush=True)
+    b, H, hd = 2, 2, 64
+    rng = np.random.default_rng(T)
+    pres = [rng.normal(size=(b, T, n_lv, H)) * 2 for _ in range(3)]
+    V0 = rng.normal(size=(b, T, H * hd))
+    mask = (rng.random((b, T, n_lv)) > 0.2).astype(np.float64)
+    tp = [_cuda(p, torch.float32) for p in pres]
+    tV0, tm = _cuda(V0, torch.float32), _cuda(mask, torch.float32)
+    S = (2 << ring_L) - 2
+    sentinel = -7.0
+    ring = torch.full((b, S, H * hd), sentinel, device=DEV)
+    out = torch.empty_like(tV0)
+    fg._scan_launch(*tp, tm, tV0, out, H, n_lv, False, "test", ring=ring, ring_L=ring_L)
+    torch.cuda.synchronize()
+    got = ring.cpu().numpy()
+    for j in range(ring_L):
+        jj = min(j, n_lv)
+        ref = V0 if jj == 0 else om.level_scan(*[p[:, :, :jj] for p in pres], V0, H, mask[..., :jj])
+        span = 2 << j
+        p0 = max(0, T - span)
+        slots = (span - 2) + (np.arange(p0, T) & (span - 1))
+        np.testing.assert_allclose(got[:, slots], ref[:, p0:T], rtol=1e-5, atol=1e-5)
+        untouched = np.setdiff1d(np.arange(span - 2, 2 * span - 2), slots)
+        assert np.all(got[:, untouched] == sentinel)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
