@@ -15,7 +15,7 @@ import os
 
 import torch
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 _LIB_NAME = "libdh_mixer.so"
 
 DH_F32, DH_BF16 = 0, 1
@@ -70,6 +70,8 @@ def _load():
         "dh_decode_attention_workspace_bytes": ([i32, i32, i32], i64),
         "dh_decode_attention_split": ([i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, i64, i32, i32, i32, i32, i32,
                                        vp, i64, vp], i32),
+        "dh_window_attention_fwd": ([i32, vp, vp, vp, i64, i64, vp, vp, vp, i64, i64, vp, vp, i64, i64,
+                                     i32, i32, i32, i32, i32, i32, vp], i32),
         "dh_decode_scan_out": ([i32] + [vp] * 8 + [i64, vp] + [i32] * 6 + [vp], i32),
         "dh_proj_gemm": ([i32, vp, i64, i32, i32, i32, vp, vp, vp, vp, vp], i32),
         "dh_sample_topk": ([i32, vp, i64, i32, i32, ctypes.c_float, i32, ctypes.c_uint64, vp, vp, vp], i32),

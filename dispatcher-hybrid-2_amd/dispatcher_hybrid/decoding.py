@@ -257,8 +257,23 @@ class _FusedPrefillDecoder(IncrementalDecoder):
     """The fused decoder's prefill: each tree layer runs the parallel gfx950 kernels -- activated
     gates of all L levels in one launch, the level scan over the active levels in a second, which
     also stores the ring slabs -- instead of the eager roll/level loop, and fills the same state
-    (B_hist, rg_hist for every level, V_ring; reference decoding.py:143-185). Attention layers and
-    the steps stay those of IncrementalDecoder."""
+    (B_hist, rg_hist for every level, V_ring; reference decoding.py:143-185). Attention layers (bf16,
+    head width 32/64/128) run the banded-attention kernel, which also writes rope(k) and v into the
+    caches; the steps stay those of IncrementalDecoder."""
+
+    def _attn_prefill(self, blk, cache, x):
+        from . import fused_attention as fa
+        at = blk.attn
+        if not (fa.supported(x.dtype, at.head_dim) and cache.k.dtype == x.dtype):
+            return super()._attn_prefill(blk, cache, x)
+        T = x.shape[1]
+        h1 = blk.norm1(x)
+        window = at.window if 0 < at.window < T else 0
+        cos, sin = at.rope_tables(T, x.device, x.dtype)
+        y = fa.window_attention(at.linear_q(h1), at.linear_k(h1), at.linear_v(h1), cos, sin, at.num_heads,
+                                window, k_cache=cache.k, v_cache=cache.v)
+        x = x + at.linear_out(y)
+        return x + blk.ffn(blk.norm2(x))
 
     def _tree_prefill(self, blk, cache, x):
         from .fused_gates import input_projections, prefill_gate_scan

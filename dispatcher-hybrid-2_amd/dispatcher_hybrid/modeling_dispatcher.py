@@ -205,6 +205,7 @@ class WindowAttention(nn.Module):
         self.linear_v = nn.Linear(d, d, bias=False)
         self.linear_out = nn.Linear(d, d, bias=False)
         self._rope_key = None
+        self.use_fused = False      # gfx950 banded-attention kernel for inference (enable_fused_gates)
 
     def rope_tables(self, length, device, dtype):
         """cos/sin of angle t * 10000^(-2i/hd), (length, hd/2), cached per (length, device, dtype).
@@ -224,11 +225,19 @@ class WindowAttention(nn.Module):
 
     def forward(self, x):
         Bb, T = x.shape[0], x.shape[1]
+        window = self.window if 0 < self.window < T else 0
+        if self.use_fused and not torch.is_grad_enabled() and x.is_cuda:
+            from . import fused_attention as fa
+            if fa.supported(x.dtype, self.head_dim):
+                # RoPE, banded scores, softmax and the value average in one launch, (B, T, d) in/out
+                cos, sin = self.rope_tables(T, x.device, x.dtype)
+                y = fa.window_attention(self.linear_q(x), self.linear_k(x), self.linear_v(x), cos, sin,
+                                        self.num_heads, window)
+                return self.linear_out(y)
         shape = (Bb, T, self.num_heads, self.head_dim)
         q = self.apply_rope(self.linear_q(x).view(shape).transpose(1, 2), T)
         k = self.apply_rope(self.linear_k(x).view(shape).transpose(1, 2), T)
         v = self.linear_v(x).view(shape).transpose(1, 2)
-        window = self.window if 0 < self.window < T else 0
         y = causal_window_attention(q, k, v, window)
         return self.linear_out(y.transpose(1, 2).reshape(Bb, T, self.embed_dim))
 
@@ -390,16 +399,20 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
         return {"input_ids": input_ids[:, -self.config.max_len:]}
 
     def enable_fused_gates(self, enabled=True):
-        """Run every mixer's gate pipeline and level scan on the gfx950 HIP kernels.
+        """Run every mixer's gate pipeline and level scan on the gfx950 HIP kernels (and, without
+        autograd in bf16, every attention layer on the banded-attention kernel).
 
         Loads the kernel library now (raising ImportError if it is missing) rather than in the
         middle of a forward. The fused path needs GPU tensors; returns self.
         """
         if enabled:
-            from . import fused_gates  # noqa: F401  (fail now, not mid-forward)
+            from . import fused_attention, fused_gates  # noqa: F401  (fail now, not mid-forward)
         for blk in self.blocks:
             if hasattr(blk, "mixer"):
                 blk.mixer.use_fused_gates = bool(enabled)
+            if hasattr(blk, "attn"):
+                # inference only: attention layers take the banded-attention kernel (bf16)
+                blk.attn.use_fused = bool(enabled)
         return self
 
     @torch.no_grad()

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 8
+#define DH_ABI_VERSION 9
 
 enum dh_status {
   DH_OK = 0,
@@ -180,6 +180,29 @@ int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const int64_t* x
                    const int64_t* out_bstride, const int64_t* out_t_stride, const int* N,
                    const void* resid, int64_t resid_bstride, const int64_t* resid_rows, int swiglu,
                    const int64_t* t_dev, int64_t* t_advance, int B, int K, void* stream);
+
+/*
+ * Banded causal attention of a whole sequence (the parallel forward and the decoder prefill of an
+ * attention layer) as ONE launch: RoPE of q and k, scores over s <= t with t - s < window (window
+ * 0: all s <= t), softmax, value average. Replaces the torch attention of WindowAttention.forward
+ * and of the decoders' attention prefill (reference dispatcher_hybrid/modeling_dispatcher.py:
+ * 168-182, dispatcher_hybrid/decoding.py:143-185).
+ *   q, k, v        (B, T, H*hd) projections before RoPE, rows stride_t and batches stride_b
+ *                  elements apart (the same strides for all three), 16-byte aligned rows.
+ *   rope_cos/sin   (>= T, hd/2) tables.
+ *   y              (B, T, H*hd) output, rows y_stride_t / batches y_stride_b apart.
+ *   K_cache, V_cache  nullable (both or neither): (B, H, Tmax, hd) decoder caches, rows [0, T)
+ *                  receive rope(k) and v (bit-identical to the eager prefill's), strides
+ *                  cache_stride_b / cache_stride_h elements.
+ * bf16 only; hd in {32, 64, 128}. Rounding: each RoPE product and sum, the score (before the fp32
+ * scale 1/sqrt(hd)), the probabilities, the output; the softmax is normalised at the end (online
+ * over 64-key blocks), so outputs match the eager path to bf16 rounding.
+ */
+int dh_window_attention_fwd(int dtype, const void* q, const void* k, const void* v, int64_t stride_b,
+                            int64_t stride_t, const void* rope_cos, const void* rope_sin, void* y,
+                            int64_t y_stride_b, int64_t y_stride_t, void* K_cache, void* V_cache,
+                            int64_t cache_stride_b, int64_t cache_stride_h, int Tmax, int B, int T, int H,
+                            int hd, int window, void* stream);
 
 /*
  * One decode step of a windowed RoPE attention layer: rotation of the new query and key at the
