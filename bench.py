@@ -13,6 +13,8 @@ out-projection + residual, RMSNorm + SwiGLU, down-projection + residual). A step
   prefill_*         C2: 292M bf16 forward at B=1, T=1024, fused gates vs eager
   forward_c5_*      C5: 292M bf16 forward at B=8, T=4096, fused gates vs eager (+ peak HBM)
   gate_path_c5_*    one mixer layer at the C5 shape, fused vs eager
+  prefill_kernels_c5  the parallel path's kernels at the C5 shape, HIP-event timed, each against its
+                    roofline (gate pre-activations and banded attention: MFMA; level scan: HBM)
   roofline          dh_decode_gemv, the dominant kernel (57 of the 95 launches of a step, ~55% of
                     its time): algorithmic bytes / HIP-event-timed launch duration
   mixer_step        the decoder's mixer step (dh_decode_gates + dh_decode_scan) per tree layer
@@ -54,6 +56,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--cpu-prompt", type=int, default=1024)
+    ap.add_argument("--leg", default="all", choices=["all", "prefill-kernels"],
+                    help="prefill-kernels: only the C5 kernel timings (for rocprofv3 runs)")
     return ap.parse_args()
 
 
@@ -261,6 +265,67 @@ def mixer_step_time(torch, model, dec, copies=400, reps=5):
     return nbytes, us
 
 
+def prefill_kernels(torch, dev, reps=10):
+    """The parallel path's three gfx950 kernels at the C5 shape (b 8, T 4096, GH 1024, 16 heads of 64,
+    12 levels, doc mask; attention window 1024), each timed with HIP events on its launch stream over
+    `reps` launches, on synthetic bf16 inputs: the activated gate pre-activations (MFMA-bound: FLOPs
+    2 b T L GH 3H), the level scan (HBM: gates + V0 in, V out) and the banded attention (MFMA: 4 b H hd
+    sum_t min(t+1, W) FLOPs for QK^T and PV)."""
+    from dispatcher_hybrid import fused_attention as fa
+    from dispatcher_hybrid import fused_gates as fg
+    b, T, GH, H, hd, L, W = 8, 4096, 1024, 16, 64, 12, 1024
+    d = H * hd
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(11)
+    A = torch.randn(b, T, GH, device=dev, generator=g).to(bf)
+    B = torch.randn(b, T, GH, device=dev, generator=g).to(bf)
+    Ws = [(torch.randn(L, H, GH, device=dev, generator=g) / GH ** 0.5).to(bf) for _ in range(3)]
+    bs = [torch.randn(L, H, device=dev, generator=g) for _ in range(3)]
+    mask = (torch.rand(b, T, L, device=dev, generator=g) > 0.001).to(bf)
+    V0 = torch.randn(b, T, d, device=dev, generator=g).to(bf)
+    V = torch.empty_like(V0)
+    buf = torch.empty((3, b, H, L, T), device=dev, dtype=bf)
+    gates = [buf[i].permute(0, 3, 2, 1) for i in range(3)]
+    q, k, v = (torch.randn(b, T, d, device=dev, generator=g).to(bf) for _ in range(3))
+    ang = torch.outer(torch.arange(T, device=dev, dtype=torch.float32),
+                      torch.pow(10000.0, -torch.arange(0, hd, 2, device=dev, dtype=torch.float32) / hd))
+    cos, sin = ang.cos().to(bf), ang.sin().to(bf)
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    gate_us = timed(lambda: fg._preacts_launch(A, B, *Ws, *bs, mask, gates, gates[0].stride(), 1, L, "bench"))
+    scan_us = timed(lambda: fg._scan_launch(*gates, None, V0, V, H, L, True, "bench"))
+    attn_us = timed(lambda: fa.window_attention(q, k, v, cos, sin, H, W))
+    gate_fl = 2 * b * T * L * GH * 3 * H
+    gate_bytes = 2 * (2 * b * T * GH + 3 * L * H * GH + 3 * b * T * L * H + b * T * L)
+    scan_bytes = 2 * (3 * b * T * L * H + 2 * b * T * d)
+    attn_fl = 4 * b * H * hd * sum(min(t + 1, W) for t in range(T))
+    tf = lambda fl, us: fl / (us * 1e-6) / 1e12
+    gb = lambda by, us: by / (us * 1e-6) / 1e9
+    return {
+        "shape": f"b {b}, T {T}, GH {GH}, {H} heads x {hd}, {L} levels, window {W}, bf16",
+        "gate_preacts": {"us": round(gate_us, 1), "bound": "mfma", "achieved": round(tf(gate_fl, gate_us), 1),
+                         "peak": MFMA_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf(gate_fl, gate_us) / MFMA_BF16_TFLOPS, 4),
+                         "hbm_gbs": round(gb(gate_bytes, gate_us), 1), "flops": gate_fl, "bytes": gate_bytes},
+        "level_scan": {"us": round(scan_us, 1), "bound": "hbm", "achieved": round(gb(scan_bytes, scan_us), 1),
+                       "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gb(scan_bytes, scan_us) / HBM_PEAK_GBS, 4),
+                       "bytes": scan_bytes},
+        "window_attention": {"us": round(attn_us, 1), "bound": "mfma", "achieved": round(tf(attn_fl, attn_us), 1),
+                             "peak": MFMA_BF16_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(tf(attn_fl, attn_us) / MFMA_BF16_TFLOPS, 4), "flops": attn_fl},
+    }
+
+
 def copy_probe(torch, dev, mib=256):
     """One plain device-to-device copy of `mib` MiB (read once, written once). Under rocprofv3
     --pmc its FETCH_SIZE / WRITE_SIZE readings turn those counters into bytes for the other
@@ -314,6 +379,11 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.leg == "prefill-kernels":
+        pk = prefill_kernels(torch, dev)
+        log("C5 prefill kernels: " + ", ".join(f"{k} {v['us']} us" for k, v in pk.items() if isinstance(v, dict)))
+        print(json.dumps({"prefill_kernels_c5": pk}), flush=True)
+        return
     copy_probe(torch, dev)
     model = build_model(torch, dev)
     max_len = model.config.max_len
@@ -405,6 +475,11 @@ def main():
         out["gate_path_c5_eager_ms"] = round(em, 3)
         out["gate_path_c5_speedup"] = round(em / fm, 2)
         log(f"C5 mixer layer: fused {fm:.2f} ms, eager {em:.2f} ms")
+        del x, mask, ids
+        torch.cuda.empty_cache()
+        pk = prefill_kernels(torch, dev)
+        out["prefill_kernels_c5"] = pk
+        log("C5 prefill kernels: " + ", ".join(f"{k} {v['us']} us" for k, v in pk.items() if isinstance(v, dict)))
 
     if not args.no_cpu_baseline:
         log("CPU baseline ...")

@@ -15,7 +15,7 @@ import os
 
 import torch
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 _LIB_NAME = "libdh_mixer.so"
 
 DH_F32, DH_BF16 = 0, 1

@@ -37,15 +37,17 @@ def window_attention(q, k, v, rope_cos, rope_sin, num_heads, window, k_cache=Non
     if rope_cos.shape[0] < T or rope_cos.shape[-1] != hd // 2 or not rope_cos.is_contiguous() or not rope_sin.is_contiguous():
         raise ValueError("window_attention: rope tables must be contiguous (>= T, hd/2)")
     y = torch.empty(B, T, d, device=q.device, dtype=q.dtype)
-    Tmax, cb, ch = 0, 0, 0
     if (k_cache is None) != (v_cache is None):
         raise ValueError("window_attention: give both caches or neither")
-    if k_cache is not None:
+    if k_cache is None:      # the kernel stages rope(k) and v head-major: scratch for the forward
+        k_cache = torch.empty(B, num_heads, T, hd, device=q.device, dtype=q.dtype)
+        v_cache = torch.empty_like(k_cache)
+    else:
         if (k_cache.shape != v_cache.shape or k_cache.dtype != q.dtype or k_cache.shape[0] != B or
                 k_cache.shape[1] != num_heads or k_cache.shape[3] != hd or k_cache.stride(-1) != 1 or
                 k_cache.stride(2) != hd or k_cache.stride() != v_cache.stride()):
             raise ValueError("window_attention: caches must be (B, H, Tmax, hd) with rows of hd elements")
-        Tmax, cb, ch = k_cache.shape[2], k_cache.stride(0), k_cache.stride(1)
+    Tmax, cb, ch = k_cache.shape[2], k_cache.stride(0), k_cache.stride(1)
     p = _hip.ptr
     st = _hip.lib.dh_window_attention_fwd(
         _hip.dtype_code(q.dtype), p(q), p(k), p(v), q.stride(0), q.stride(1), p(rope_cos), p(rope_sin),

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 9
+#define DH_ABI_VERSION 10
 
 enum dh_status {
   DH_OK = 0,
@@ -191,12 +191,13 @@ int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const int64_t* x
  *                  elements apart (the same strides for all three), 16-byte aligned rows.
  *   rope_cos/sin   (>= T, hd/2) tables.
  *   y              (B, T, H*hd) output, rows y_stride_t / batches y_stride_b apart.
- *   K_cache, V_cache  nullable (both or neither): (B, H, Tmax, hd) decoder caches, rows [0, T)
- *                  receive rope(k) and v (bit-identical to the eager prefill's), strides
- *                  cache_stride_b / cache_stride_h elements.
- * bf16 only; hd in {32, 64, 128}. Rounding: each RoPE product and sum, the score (before the fp32
- * scale 1/sqrt(hd)), the probabilities, the output; the softmax is normalised at the end (online
- * over 64-key blocks), so outputs match the eager path to bf16 rounding.
+ *   K_cache, V_cache  (B, H, Tmax, hd) buffers, T <= Tmax: rows [0, T) receive rope(k) and v
+ *                  (bit-identical to the eager prefill's), which the attention then reads -- the
+ *                  decoder caches, or scratch; strides cache_stride_b / cache_stride_h elements.
+ * Two launches (the rope/copy pre-pass, then the attention).
+ * bf16 only; hd in {32, 64, 128}. Rounding: each RoPE product and sum, the probabilities, the
+ * output (scores stay fp32); the softmax is normalised at the end (online over 64-key blocks), so
+ * outputs match the eager path to bf16 rounding.
  */
 int dh_window_attention_fwd(int dtype, const void* q, const void* k, const void* v, int64_t stride_b,
                             int64_t stride_t, const void* rope_cos, const void* rope_sin, void* y,
