@@ -15,7 +15,7 @@ out-projection + residual, RMSNorm + SwiGLU, down-projection + residual). A step
   gate_path_c5_*    one mixer layer at the C5 shape, fused vs eager
   prefill_kernels_c5  the parallel path's kernels at the C5 shape, HIP-event timed, each against its
                     roofline (gate pre-activations and banded attention: MFMA; level scan: HBM)
-  roofline          dh_decode_gemv, the dominant kernel (57 of the 95 launches of a step, ~55% of
+  roofline          dh_decode_gemv, the dominant kernel (57 of the 97 launches of a step, ~55% of
                     its time): algorithmic bytes / HIP-event-timed launch duration
   mixer_step        the decoder's mixer step (dh_decode_gates + dh_decode_scan) per tree layer
   step_roofline     whole decode step: bf16 weight bytes per token x tok/s vs 8 TB/s
@@ -43,7 +43,7 @@ EOT = 50256
 # HBM bytes per dh_decode_gemv launch, averaged over the decode step's 57 launches: rocprofv3 --pmc
 # FETCH_SIZE (x 1.99974, the factor a 256 MiB copy's reading gives) + WRITE_SIZE (x 1.0), from
 # profiles/decode_c3_b1_kernels.md
-TRAFFIC_GEMV_LAUNCH = 9_453_519
+TRAFFIC_GEMV_LAUNCH = 9_453_170
 
 
 def parse():
@@ -380,6 +380,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.leg == "prefill-kernels":
+        copy_probe(torch, dev)                  # scale reference for counter runs
         pk = prefill_kernels(torch, dev)
         log("C5 prefill kernels: " + ", ".join(f"{k} {v['us']} us" for k, v in pk.items() if isinstance(v, dict)))
         print(json.dumps({"prefill_kernels_c5": pk}), flush=True)

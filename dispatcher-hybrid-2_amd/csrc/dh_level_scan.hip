@@ -246,9 +246,9 @@ __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
 // neither the writes nor the shifted reads conflict on LDS banks) and r[t] once, and the
 // destination forms coef = a[t] * r[t - 2^l] once per position, then V = f * V + coef * V_src:
 // two VALU operations per element and level instead of three. 144 KB of LDS at T = 4096.
-template <typename T, int PPT, int MODE>
+template <typename T, int C, int PPT, int MODE>
 __global__ __launch_bounds__(1024) void level_scan_wide_kernel(ScanArgs a) {
-  constexpr int C = 8, NT = 1024, TC = PPT * NT;
+  constexpr int NT = 1024, TC = PPT * NT;
   __shared__ float2 vs[C / 2][TC];
   __shared__ float rs[TC];
   const int nchunks = a.hd / C;
@@ -370,12 +370,13 @@ __global__ __launch_bounds__(1024) void level_scan_wide_kernel(ScanArgs a) {
 
 template <typename T, int PPT>
 void launch_wide(const ScanArgs& a, int mode, hipStream_t s) {
-  const int nchunks = a.hd / 8;
+  constexpr int C = 8;                    // measured: 4 columns (two workgroups per CU) is slower
+  const int nchunks = a.hd / C;
   const int grid = ((a.b * a.H + 7) / 8) * 8 * nchunks;
   auto go = [&](auto kern) { kern<<<dim3(grid), dim3(1024), 0, s>>>(a); };
-  if (mode == kActivated) go(level_scan_wide_kernel<T, PPT, kActivated>);
-  else if (mode == kPreMask) go(level_scan_wide_kernel<T, PPT, kPreMask>);
-  else go(level_scan_wide_kernel<T, PPT, kPreNoMask>);
+  if (mode == kActivated) go(level_scan_wide_kernel<T, C, PPT, kActivated>);
+  else if (mode == kPreMask) go(level_scan_wide_kernel<T, C, PPT, kPreMask>);
+  else go(level_scan_wide_kernel<T, C, PPT, kPreNoMask>);
 }
 
 template <typename T, int C, int PPT>
