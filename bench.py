@@ -88,9 +88,21 @@ def time_decode(torch, model, batch, prompt, warmup, steps, sample):
 
     from dispatcher_hybrid import fused_step
 
+    if not sample:
+        # greedy as fast_generate runs it: the pick (device argmax, torch.argmax's token) is the last
+        # part of the captured step and feeds the next one; one graph replay per token
+        dec.greedy_start(logits)
+        for _ in range(warmup):
+            dec.step_greedy()
+        sync_barrier(torch)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            dec.step_greedy()
+        sync_barrier(torch)
+        dt = time.perf_counter() - t0
+        return batch * steps / dt, 1e3 * dt / steps, dec
+
     def next_tok(lg):
-        if not sample:
-            return fused_step.argmax_tokens(lg)           # device argmax (same token as torch's)
         # temperature 0.8 / top-k 50 sampling on the device, draws keyed by (seed, position, row)
         return fused_step.sample_tokens(lg, 0.8, 50, 5, dec.t_buf)
 

@@ -98,3 +98,39 @@ __device__ __forceinline__ T load_uniform(const T* p) {
 
 __host__ __device__ __forceinline__ int64_t ring_offset(int j) { return ((int64_t)2 << j) - 2; }
 __host__ __device__ __forceinline__ int64_t ring_mask(int j) { return ((int64_t)2 << j) - 1; }
+
+// ----------------------------------------------------------------------------------------------
+// argmax with torch.argmax's order: (value, index) a beats b when its value is larger, NaN above
+// every number, the lower index on ties
+// ----------------------------------------------------------------------------------------------
+struct Cand {
+  float v;
+  int i;
+};
+
+__device__ __forceinline__ bool beats(float va, int ia, float vb, int ib) {
+  const bool na = va != va, nb = vb != vb;
+  if (na || nb) return na && (!nb || ia < ib);
+  return va > vb || (va == vb && ia < ib);
+}
+
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ void dpp_pair(float& v, int& i) {
+  // lanes outside ROWMASK keep their own pair (old = own value), so the comparison is a no-op there
+  const float ov = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWMASK, 0xf, false));
+  const int oi = __builtin_amdgcn_update_dpp(i, i, CTRL, ROWMASK, 0xf, false);
+  if (beats(ov, oi, v, i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+// best (value, index) of a wave, in lane 63
+__device__ __forceinline__ void wave_best(float& best, int& bidx) {
+  dpp_pair<0xb1, 0xf>(best, bidx);      // quad_perm(1,0,3,2)
+  dpp_pair<0x4e, 0xf>(best, bidx);      // quad_perm(2,3,0,1)
+  dpp_pair<0x141, 0xf>(best, bidx);     // row_half_mirror
+  dpp_pair<0x140, 0xf>(best, bidx);     // row_mirror
+  dpp_pair<0x142, 0xa>(best, bidx);     // row_bcast:15 into rows 1, 3
+  dpp_pair<0x143, 0xc>(best, bidx);     // row_bcast:31 into rows 2, 3
+}

@@ -53,6 +53,7 @@ struct GemvArgs {
   Seg seg[kMaxSeg];
   int nseg;
   int B, K, Nrows;
+  Cand* cand;                   // nullable (B = 1): the launch's argmax candidate per workgroup
 };
 
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
@@ -435,6 +436,8 @@ __global__ __launch_bounds__(NT) void decode_gemv_row_kernel(GemvArgs a) {
 #pragma unroll
     for (int q = 0; q < NW; ++q) acc[r][q] = wave_sum(acc[r][q]);
   // ---- epilogue: lane r < R writes output row rbase + r
+  float cv = -INFINITY;                                // argmax candidate of this lane (none: -inf)
+  int ci = 0x7fffffff;
   if (lane < R && rbase + lane < a.Nrows) {
     float v0 = 0.f, v1 = 0.f;
     int s = 0, loc = 0;
@@ -458,6 +461,23 @@ __global__ __launch_bounds__(NT) void decode_gemv_row_kernel(GemvArgs a) {
       }
     }
     Elem<T>::store(out_ptr<T>(a, s, 0, t, loc), out);
+    cv = out;
+    ci = rbase + lane;
+  }
+  if (a.cand) {                                        // uniform: greedy pick fused into the head
+    // every output of the workgroup is one (rounded value, row) candidate; the workgroup's best,
+    // in torch.argmax's order, goes to cand[blockIdx.x]
+    __shared__ Cand wbest[NWV];
+    wave_best(cv, ci);
+    if (lane == 63) wbest[wave] = Cand{cv, ci};
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      Cand c = wbest[0];
+#pragma unroll
+      for (int w2 = 1; w2 < NWV; ++w2)
+        if (beats(wbest[w2].v, wbest[w2].i, c.v, c.i)) c = wbest[w2];
+      a.cand[blockIdx.x] = c;
+    }
   }
   advance_position(a);
 }
@@ -678,14 +698,32 @@ void pick_cg(const GemvArgs& a, int C, int R, hipStream_t s) {
 
 bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
 
+// Rows per wave. Single row (measured on MI355X, weights streamed from HBM): about 4 KB of weights
+// per wave while the launch keeps >= ~1.5k waves -- two rows of K = 1024 bf16 for the 3072-row
+// projection, one row for 1024-row outputs, for SwiGLU (whose wave already reads a gate and an up
+// row) and for K = 2816; four rows for the vocabulary head (> 12k waves). Batched calls stage the
+// rows once per workgroup and reuse each weight chunk across all of them, so more rows per wave
+// pay off there.
+int rows_per_wave(int B, int Nrows, int K, int esz, bool swiglu) {
+  if (B == 1) return Nrows >= 16384 ? 4 : (!swiglu && K * esz <= 2048 && Nrows >= 3072 ? 2 : 1);
+  return Nrows >= 2048 ? 4 : 2;
+}
+
 }  // namespace
+
+extern "C" int64_t dh_decode_gemv_candidates(int dtype, int N, int K) {
+  if ((dtype != DH_F32 && dtype != DH_BF16) || N < 1 || K < 1) return 0;
+  const int R = rows_per_wave(1, N, K, dtype == DH_BF16 ? 2 : 4, false);
+  const int rows_per_block = (kRowThreads / 64) * R;
+  return (N + rows_per_block - 1) / rows_per_block;
+}
 
 extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const int64_t* x_rows,
                               const void* norm_w, float eps, int nseg, const void* const* W,
                               void* const* out, const int64_t* out_bstride, const int64_t* out_t_stride,
                               const int* N, const void* resid, int64_t resid_bstride,
                               const int64_t* resid_rows, int swiglu, const int64_t* t_dev, int64_t* t_advance,
-                              int B, int K, void* stream) {
+                              void* argmax_cand, int B, int K, void* stream) {
   const char* who = "dh_decode_gemv";
   DH_REQUIRE(dtype == DH_F32 || dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d", who, dtype);
   const int vec = dtype == DH_BF16 ? 8 : 4;             // elements per 16-byte chunk
@@ -699,7 +737,10 @@ extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const
              who);
   DH_REQUIRE(aligned(x, 16) && (x_bstride * (dtype == DH_BF16 ? 2 : 4)) % 16 == 0 && (!norm_w || aligned(norm_w, 16)),
              DH_ERR_INVALID_ARG, "%s: x rows and the norm weight need 16-byte alignment", who);
+  DH_REQUIRE(!argmax_cand || (B == 1 && nseg == 1 && !swiglu && !resid), DH_ERR_INVALID_ARG,
+             "%s: argmax candidates need B = 1 and one plain output segment", who);
   GemvArgs a{};
+  a.cand = (Cand*)argmax_cand;
   a.x = x;
   a.x_bstride = x_bstride;
   a.x_rows = x_rows;
@@ -730,18 +771,8 @@ extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const
   a.Nrows = total;
   const int C = (K / vec + 63) / 64;
   DH_REQUIRE(C <= 12, DH_ERR_UNSUPPORTED_SHAPE, "%s: K=%d exceeds %d elements per row", who, K, 12 * 64 * vec);
-  // Rows per wave. Single row (measured on MI355X, weights streamed from HBM): about 4 KB of
-  // weights per wave while the launch keeps >= ~1.5k waves -- two rows of K = 1024 bf16 for the
-  // 3072-row projection, one row for 1024-row outputs, for SwiGLU (whose wave already reads a gate
-  // and an up row) and for K = 2816; four rows for the vocabulary head (> 12k waves). Batched calls
-  // stage the rows once per workgroup and reuse each weight chunk across all of them, so more rows
-  // per wave pay off there.
   const int esz = dtype == DH_BF16 ? 2 : 4;
-  int R;
-  if (B == 1)
-    R = a.Nrows >= 16384 ? 4 : (!swiglu && K * esz <= 2048 && a.Nrows >= 3072 ? 2 : 1);
-  else
-    R = a.Nrows >= 2048 ? 4 : 2;
+  const int R = rows_per_wave(B, a.Nrows, K, esz, swiglu != 0);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DH_BF16) {
     if (swiglu) pick_cg<bf16_t, true>(a, C, R, s); else pick_cg<bf16_t, false>(a, C, R, s);

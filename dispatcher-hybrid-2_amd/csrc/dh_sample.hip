@@ -13,42 +13,8 @@
 
 namespace {
 
-
-// a beats b: larger value, NaN above all numbers, lower index on ties
-__device__ __forceinline__ bool beats(float va, int ia, float vb, int ib) {
-  const bool na = va != va, nb = vb != vb;
-  if (na || nb) return na && (!nb || ia < ib);
-  return va > vb || (va == vb && ia < ib);
-}
-
-template <int CTRL, int ROWMASK>
-__device__ __forceinline__ void dpp_pair(float& v, int& i) {
-  // lanes outside ROWMASK keep their own pair (old = own value), so the comparison is a no-op there
-  const float ov = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWMASK, 0xf, false));
-  const int oi = __builtin_amdgcn_update_dpp(i, i, CTRL, ROWMASK, 0xf, false);
-  if (beats(ov, oi, v, i)) {
-    v = ov;
-    i = oi;
-  }
-}
-
 constexpr int kSlice = 2048;              // elements per first-pass workgroup
 constexpr int kT1 = 256;                  // first-pass threads: kSlice / kT1 = 8 elements each
-
-struct Cand {
-  float v;
-  int i;
-};
-
-// best (value, index) of a wave, in lane 63
-__device__ __forceinline__ void wave_best(float& best, int& bidx) {
-  dpp_pair<0xb1, 0xf>(best, bidx);      // quad_perm(1,0,3,2)
-  dpp_pair<0x4e, 0xf>(best, bidx);      // quad_perm(2,3,0,1)
-  dpp_pair<0x141, 0xf>(best, bidx);     // row_half_mirror
-  dpp_pair<0x140, 0xf>(best, bidx);     // row_mirror
-  dpp_pair<0x142, 0xa>(best, bidx);     // row_bcast:15 into rows 1, 3
-  dpp_pair<0x143, 0xc>(best, bidx);     // row_bcast:31 into rows 2, 3
-}
 
 template <typename T>
 __global__ __launch_bounds__(kT1) void argmax_slices(const T* logits, int64_t row_stride, int V, Cand* cand) {
@@ -96,6 +62,47 @@ __global__ __launch_bounds__(64) void argmax_final(const Cand* cand, int nslice,
   }
   wave_best(best, bidx);
   if (lane == 63) out[b] = bidx;
+}
+
+// The greedy pick after a vocabulary head that wrote one candidate per workgroup (dh_decode_gemv
+// with argmax_cand): one workgroup of 1024 threads per row, every thread's candidates requested
+// before any comparison (a loop of dependent loads would serialise them), wave reductions, one
+// LDS step. Optionally the token is also stored at hist[b * hist_stride + *t_dev] (the position
+// the decoder just advanced to), when that index is below hist_len.
+constexpr int kRT = 1024;
+constexpr int kRPer = 8;                   // candidates per thread: up to 8192 per row
+
+__global__ __launch_bounds__(kRT) void argmax_reduce_kernel(const Cand* cand, int ncand, int64_t* out,
+                                                            const int64_t* t_dev, int64_t* hist,
+                                                            int64_t hist_stride, int64_t hist_len) {
+  __shared__ Cand wb[kRT / 64];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const Cand* cb = cand + (int64_t)b * ncand;
+  Cand c[kRPer];
+#pragma unroll
+  for (int k = 0; k < kRPer; ++k) c[k] = cb[min(tid + k * kRT, ncand - 1)];
+  float best = -INFINITY;
+  int bidx = 0x7fffffff;
+#pragma unroll
+  for (int k = 0; k < kRPer; ++k)
+    if (tid + k * kRT < ncand && beats(c[k].v, c[k].i, best, bidx)) {
+      best = c[k].v;
+      bidx = c[k].i;
+    }
+  wave_best(best, bidx);
+  if (lane == 63) wb[wave] = Cand{best, bidx};
+  __syncthreads();
+  if (tid == 0) {
+    Cand r = wb[0];
+#pragma unroll
+    for (int w = 1; w < kRT / 64; ++w)
+      if (beats(wb[w].v, wb[w].i, r.v, r.i)) r = wb[w];
+    out[b] = r.i;
+    if (hist) {
+      const int64_t t = load_uniform(t_dev);
+      if (t >= 0 && t < hist_len) hist[(int64_t)b * hist_stride + t] = r.i;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -378,5 +385,18 @@ extern "C" int dh_argmax(int dtype, const void* logits, int64_t row_stride, int 
   else
     argmax_slices<float><<<g1, kT1, 0, s>>>((const float*)logits, row_stride, V, cand);
   argmax_final<<<B, 64, 0, s>>>(cand, nslice, out);
+  return dh_check_launch(who);
+}
+
+extern "C" int dh_argmax_reduce(const void* cand, int B, int ncand, int64_t* out, const int64_t* t_dev,
+                                int64_t* hist, int64_t hist_stride, int64_t hist_len, void* stream) {
+  const char* who = "dh_argmax_reduce";
+  DH_REQUIRE(cand && out, DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
+  DH_REQUIRE(B >= 1 && ncand >= 1 && ncand <= kRT * kRPer, DH_ERR_UNSUPPORTED_SHAPE,
+             "%s: B=%d ncand=%d (1..%d candidates per row)", who, B, ncand, kRT * kRPer);
+  DH_REQUIRE(!hist || (t_dev && hist_len >= 1 && hist_stride >= hist_len), DH_ERR_INVALID_ARG,
+             "%s: a history needs t_dev and hist_stride >= hist_len >= 1", who);
+  argmax_reduce_kernel<<<dim3(B), dim3(kRT), 0, (hipStream_t)stream>>>((const Cand*)cand, ncand, out, t_dev,
+                                                                         hist, hist_stride, hist_len);
   return dh_check_launch(who);
 }

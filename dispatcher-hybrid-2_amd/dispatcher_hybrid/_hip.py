@@ -15,7 +15,7 @@ import os
 
 import torch
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 _LIB_NAME = "libdh_mixer.so"
 
 DH_F32, DH_BF16 = 0, 1
@@ -62,7 +62,9 @@ def _load():
         "dh_decode_mixer_step": ([i32] + [vp] * 13 + [i32] * 7 + [vp], i32),
         "dh_step_gates": ([i32] + [vp] * 12 + [i32] * 5 + [vp], i32),
         "dh_decode_gemv": ([i32, vp, i64, vp, vp, ctypes.c_float, i32, vp, vp, vp, vp, vp,
-                            vp, i64, vp, i32, vp, vp, i32, i32, vp], i32),
+                            vp, i64, vp, i32, vp, vp, vp, i32, i32, vp], i32),
+        "dh_decode_gemv_candidates": ([i32, i32, i32], i64),
+        "dh_argmax_reduce": ([vp, i32, i32, vp, vp, vp, i64, i64, vp], i32),
         "dh_step_scan": ([i32] + [vp] * 7 + [i32] * 6 + [vp], i32),
         "dh_decode_attention": ([i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, i64,
                                  i32, i32, i32, i32, i32, vp], i32),

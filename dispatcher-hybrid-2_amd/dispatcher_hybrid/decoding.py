@@ -291,18 +291,20 @@ class _FusedPrefillDecoder(IncrementalDecoder):
 
 
 class _GraphedBase:
-    def _capture(self, step_fn):
+    def _capture(self, step_fn, attr="graph"):
         g = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
+        tok = self.token_buf.clone()
         with torch.cuda.stream(side):
             for _ in range(3):                      # warm-ups: allocator pools, library handles
                 step_fn()
                 self.t_buf.fill_(self.t)            # undo the warm-up's position advance
+                self.token_buf.copy_(tok)           # and a fused greedy pick's token
         torch.cuda.current_stream().wait_stream(side)
         with torch.cuda.graph(g):
             step_fn()
-        self.graph = g
+        setattr(self, attr, g)
 
     @torch.no_grad()
     def step(self, tokens):
@@ -460,6 +462,14 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         self.stage = torch.zeros(self._fused_step.stage_floats(Bb, mix0.num_heads, mix0.levels,
                                                                mix0.head_dim), device=dev)
         # small batches split each head's attention window over several workgroups
+        # greedy decoding on the device: the step's vocabulary head also writes argmax candidates
+        # (batch 1) and a second graph ends with the pick, which becomes the next step's input
+        self._greedy_graph = None
+        self._greedy_capture = False
+        self.tok_hist = torch.zeros(Bb, self.max_len + 1, dtype=torch.long, device=dev)
+        self.cand = None
+        if Bb == 1:
+            self.cand = self._fused_step.candidate_buffer(dt, self.logits_out.shape[1], cfg.d_model, 1, dev)
         att0 = next((b.attn for b in self.m.blocks if isinstance(b, AttentionBlock)), None)
         self.attn_ws = None
         if att0 is not None and Bb * att0.num_heads <= 64:
@@ -529,7 +539,41 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
             else:
                 self._tree_step_f(blk, cache, i == 0)
         V = self.logits_out.shape[1]
+        fs = self._fused_step
+        cand = self.cand if self._greedy_capture else None
         # the last launch also advances the device position (no separate add kernel)
-        self._fused_step.decode_gemv(self.x_buf, [(self.m.lm_head.weight, self.logits_out, V, 0)],
-                                     self.t_buf, norm_weight=self.m.norm_out.weight,
-                                     eps=self._eps(self.m.norm_out, self.dtype), t_advance=self.t_buf)
+        fs.decode_gemv(self.x_buf, [(self.m.lm_head.weight, self.logits_out, V, 0)], self.t_buf,
+                       norm_weight=self.m.norm_out.weight, eps=self._eps(self.m.norm_out, self.dtype),
+                       t_advance=self.t_buf, argmax_cand=cand)
+        if self._greedy_capture:
+            # greedy pick into the next step's token input and the token history (at the new position)
+            if cand is not None:
+                fs.argmax_reduce(cand, self.token_buf, self.t_buf, self.tok_hist)
+            else:
+                fs.argmax_tokens(self.logits_out, out=self.token_buf)
+                self.tok_hist.index_copy_(1, self.t_buf, self.token_buf.unsqueeze(1))
+
+    @torch.no_grad()
+    def greedy_start(self, logits):
+        """Start device-side greedy decoding after prefill: the argmax of `logits` (the prefill's
+        last-position logits, (B, V) or (V,)) becomes the token fed to the next step and the first
+        entry of tok_hist (at the current position)."""
+        lg = logits.view(-1, logits.shape[-1])
+        self._fused_step.argmax_tokens(lg, out=self.token_buf)
+        self.tok_hist[:, self.t] = self.token_buf
+
+    @torch.no_grad()
+    def step_greedy(self):
+        """One decode step fed by the token in token_buf, ending with the greedy pick: the next token
+        goes to token_buf and to tok_hist[:, t + 1] on the device -- one graph replay, no host work
+        per token (what fast_generate's greedy branch runs; same tokens as argmax of step())."""
+        if self.t >= self.max_len:
+            raise ValueError(f"context exhausted at max_len {self.max_len}")
+        if self._greedy_graph is None:
+            self._greedy_capture = True
+            try:
+                self._capture(self._step_all, attr="_greedy_graph")
+            finally:
+                self._greedy_capture = False
+        self._greedy_graph.replay()
+        self.t += 1

@@ -81,7 +81,7 @@ def decode_mixer_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring,
 
 
 def decode_gemv(x, segments, t_buf, norm_weight=None, eps=None, resid=None, swiglu=False,
-                x_rows=None, resid_rows=None, t_advance=None):
+                x_rows=None, resid_rows=None, t_advance=None, argmax_cand=None):
     """Fused matrix-vector products of the decode step (``dh_decode_gemv``).
 
     x: (B, K) activations (or the embedding table with ``x_rows`` = token ids: row b is
@@ -92,7 +92,9 @@ def decode_gemv(x, segments, t_buf, norm_weight=None, eps=None, resid=None, swig
     ``resid_rows`` when given); swiglu: segments are (gate, up) and silu(gate) * up goes to the
     gate segment's destination. t_advance: an int64 device tensor the launch adds one to (the
     decode step's position advance, folded into its last launch; outputs may then not use
-    t_stride). Everything in one dtype (fp32 or bf16) on one GPU.
+    t_stride). argmax_cand: a buffer of ``gemv_candidates(dtype, N, K)`` 8-byte records (batch 1,
+    one plain segment) that receives each workgroup's best (value, row) for ``argmax_reduce``.
+    Everything in one dtype (fp32 or bf16) on one GPU.
     """
     _hip.require_gpu(x, "decode_gemv")
     dt = x.dtype
@@ -113,8 +115,42 @@ def decode_gemv(x, segments, t_buf, norm_weight=None, eps=None, resid=None, swig
     st = _hip.lib.dh_decode_gemv(
         _hip.dtype_code(dt), p(x), x.stride(0), p(x_rows), p(norm_weight), float(eps or 0.0), n,
         Ws, outs, obs, ots, Ns, p(resid), resid.stride(0) if resid is not None else 0, p(resid_rows),
-        int(bool(swiglu)), p(t_buf), p(t_advance), B, K, _hip.stream_handle(x.device))
+        int(bool(swiglu)), p(t_buf), p(t_advance), p(argmax_cand), B, K, _hip.stream_handle(x.device))
     _hip.check(st, "dh_decode_gemv")
+
+
+def gemv_candidates(dtype, N, K):
+    """Argmax candidate records a batch-1 decode_gemv with N rows of K elements writes."""
+    return int(_hip.lib.dh_decode_gemv_candidates(_hip.dtype_code(dtype), int(N), int(K)))
+
+
+def candidate_buffer(dtype, N, K, B, device):
+    """A buffer for B rows of candidate records (8 bytes each), as int64 elements."""
+    n = gemv_candidates(dtype, N, K)
+    if n < 1:
+        raise ValueError("candidate_buffer: unsupported shape")
+    return torch.empty(B, n, dtype=torch.int64, device=device)
+
+
+def argmax_reduce(cand, out, t_buf=None, hist=None):
+    """Greedy tokens from decode_gemv's argmax candidates (``dh_argmax_reduce``): out[b] = the row
+    of the best candidate of cand[b] in torch.argmax's order. hist (B, L) int64: the token is also
+    stored at hist[b, t_buf[0]] when that index is inside the buffer."""
+    B, ncand = cand.shape
+    if cand.dtype != torch.int64 or not cand.is_contiguous():
+        raise ValueError("argmax_reduce: candidates are a contiguous (B, ncand) int64 buffer")
+    if out.dtype != torch.long or out.numel() != B or not out.is_contiguous():
+        raise ValueError("argmax_reduce: out must be a contiguous int64 tensor of B elements")
+    hs, hl = 0, 0
+    if hist is not None:
+        if hist.dtype != torch.long or hist.dim() != 2 or hist.shape[0] != B or hist.stride(1) != 1 or t_buf is None:
+            raise ValueError("argmax_reduce: hist must be (B, L) int64 with unit inner stride, with t_buf")
+        hs, hl = hist.stride(0), hist.shape[1]
+    p = _hip.ptr
+    st = _hip.lib.dh_argmax_reduce(p(cand), B, ncand, p(out), p(t_buf), p(hist), hs, hl,
+                                   _hip.stream_handle(cand.device))
+    _hip.check(st, "dh_argmax_reduce")
+    return out
 
 
 def stage_floats(B, H, L, hd):

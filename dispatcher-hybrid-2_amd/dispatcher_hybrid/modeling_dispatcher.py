@@ -454,6 +454,17 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
 
         Bb = ids.shape[0]
         logits = dec.prefill(ids)[:, -1]                     # ids is 2-D: (B, T, V) -> (B, V)
+        if isinstance(dec, FusedGraphedHybridDecoder) and not do_sample and eos_token_id is None:
+            # greedy without eos: every pick stays on the device (fused into the graphed step); the
+            # loop below appends min(max_new_tokens, max_len - t + 1) tokens, the same count here
+            n = min(max_new_tokens, dec.max_len - dec.t + 1)
+            if n <= 0:
+                return ids
+            t0 = dec.t
+            dec.greedy_start(logits)
+            for _ in range(n - 1):
+                dec.step_greedy()
+            return torch.cat([ids, dec.tok_hist[:, t0:t0 + n]], dim=1)
         finished = torch.zeros(Bb, dtype=torch.bool, device=ids.device)
         out = [ids]
         # Through the fused decoder the next token is picked on the device. Greedy: the argmax

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 10
+#define DH_ABI_VERSION 11
 
 enum dh_status {
   DH_OK = 0,
@@ -170,7 +170,10 @@ int dh_decode_mixer_step(int dtype, const void* A, const void* B_hist, const voi
  *   t = *t_dev (device position; e.g. the B_hist row of the source projection), read only when
  *   some out_t_stride is non-zero. t_advance (nullable): the launch adds one to *t_advance (the
  *   decode step's position advance folded into its last launch); not allowed together with a
- *   non-zero out_t_stride.
+ *   non-zero out_t_stride. argmax_cand (nullable; B = 1, one plain segment): each workgroup also
+ *   writes the best (rounded output value, row) of its rows in torch.argmax's order (NaN above all,
+ *   lowest row on ties) -- dh_decode_gemv_candidates(dtype, N, K) records -- for dh_argmax_reduce:
+ *   the greedy pick fused into the vocabulary head (reference modeling_dispatcher.py:426-441).
  * All activations and weights in dtype; fp32 accumulation. The array arguments W, out, out_bstride,
  * out_t_stride and N are host arrays of nseg entries. K must be a multiple of 8 (bf16) or 4 (fp32):
  * rows are read in 16-byte chunks.
@@ -179,7 +182,15 @@ int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const int64_t* x
                    const void* norm_w, float eps, int nseg, const void* const* W, void* const* out,
                    const int64_t* out_bstride, const int64_t* out_t_stride, const int* N,
                    const void* resid, int64_t resid_bstride, const int64_t* resid_rows, int swiglu,
-                   const int64_t* t_dev, int64_t* t_advance, int B, int K, void* stream);
+                   const int64_t* t_dev, int64_t* t_advance, void* argmax_cand, int B, int K,
+                   void* stream);
+
+/*
+ * Number of argmax candidate records (8 bytes each: float value, int index) a batch-1
+ * dh_decode_gemv launch with N output rows of K elements writes when given argmax_cand (one per
+ * workgroup); 0 for unsupported arguments.
+ */
+int64_t dh_decode_gemv_candidates(int dtype, int N, int K);
 
 /*
  * Banded causal attention of a whole sequence (the parallel forward and the decoder prefill of an
@@ -283,6 +294,16 @@ int dh_decode_scan_out(int dtype, const void* V0, const float* stage, const int6
 int64_t dh_argmax_workspace_bytes(int B, int V);
 int dh_argmax(int dtype, const void* logits, int64_t row_stride, int B, int V, int64_t* out, void* workspace,
               int64_t workspace_bytes, void* stream);
+
+/*
+ * The greedy token of each of B rows from the per-workgroup candidates of a dh_decode_gemv launch
+ * (argmax_cand, ncand records per row, e.g. dh_decode_gemv_candidates): out[b] = the index of the
+ * best candidate in torch.argmax's order. hist (nullable): the token is also stored at
+ * hist[b * hist_stride + *t_dev] when 0 <= *t_dev < hist_len (the decoder's generated-token
+ * history, indexed by the position the step advanced to). ncand <= 8192.
+ */
+int dh_argmax_reduce(const void* cand, int B, int ncand, int64_t* out, const int64_t* t_dev, int64_t* hist,
+                     int64_t hist_stride, int64_t hist_len, void* stream);
 
 /*
  * Temperature / top-k sampling of the next token, on the device. Replaces the do_sample branch of

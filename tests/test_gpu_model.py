@@ -193,6 +193,31 @@ def test_fast_generate_fused_equals_eager_greedy():
     assert torch.equal(auto, eager)
 
 
+@pytest.mark.parametrize("B", [1, 2])
+def test_step_greedy_equals_argmax_of_step(B):
+    """The device greedy loop (pick fused into the captured step; batch 1 through the vocabulary
+    head's candidates, batch 2 through dh_argmax) yields the tokens argmax(step(tok)) yields, and
+    tok_hist holds them at their positions."""
+    from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder
+    cfgd, sd = tiny("tiny_b")
+    m = product_model(cfgd, sd, device=DEV)
+    prompt = torch.randint(0, 250, (B, 9), device=DEV, generator=torch.Generator(device=DEV).manual_seed(B))
+    ref_dec, dec = FusedGraphedHybridDecoder(m), FusedGraphedHybridDecoder(m)
+    lg = ref_dec.prefill(prompt)[:, -1]
+    ref = []
+    for _ in range(20):
+        tok = lg.argmax(-1)
+        ref.append(tok)
+        lg = ref_dec.step(tok)
+    t0 = 9
+    dec.greedy_start(dec.prefill(prompt)[:, -1])
+    for _ in range(19):
+        dec.step_greedy()
+    got = dec.tok_hist[:, t0:t0 + 20]
+    assert torch.equal(got, torch.stack(ref, 1))
+    assert torch.equal(dec.token_buf, ref[-1])
+
+
 def test_fast_generate_fused_sampling_support_and_reproducibility():
     """do_sample through the fused decoder draws on the device (dh_sample_topk): every generated
     token lies in the top-k set of the logits at its position (teacher-forced fp32 oracle forward

@@ -46,6 +46,64 @@ def test_argmax_ties_nan_and_strided_rows(dtype):
     assert torch.equal(got, x.argmax(-1))
 
 
+def _cand_records(pairs):
+    """(value, index) pairs as the 8-byte candidate records of dh_decode_gemv (float, int32)."""
+    import struct
+    raw = b"".join(struct.pack("<fi", v, i) for v, i in pairs)
+    return torch.frombuffer(bytearray(raw), dtype=torch.int64).to(DEV).view(1, -1)
+
+
+def test_argmax_reduce_order_and_history():
+    """The candidate reduce of the fused greedy pick: torch.argmax's order (larger value, NaN above
+    all, lowest index on ties) over up to 8192 records, and the optional history write at t_buf."""
+    from dispatcher_hybrid import fused_step
+    out = torch.empty(1, dtype=torch.long, device=DEV)
+    cases = [([(1.0, 5), (3.0, 9), (3.0, 2), (-1.0, 0)], 2),                 # tie: lowest index
+             ([(float("-inf"), 7), (float("nan"), 40), (5.0, 1), (float("nan"), 12)], 12),   # first NaN
+             ([(float(k % 97), k) for k in range(8192)], 96)]               # 8192 records, first 96
+    for pairs, want in cases:
+        fused_step.argmax_reduce(_cand_records(pairs), out)
+        torch.cuda.synchronize()
+        assert int(out) == want
+    hist = torch.full((1, 10), -1, dtype=torch.long, device=DEV)
+    t_buf = torch.tensor([5], device=DEV)
+    fused_step.argmax_reduce(_cand_records([(2.0, 31), (1.0, 4)]), out, t_buf, hist)
+    t_buf.fill_(12)                                                       # past the history: no write
+    fused_step.argmax_reduce(_cand_records([(2.0, 8)]), out, t_buf, hist)
+    torch.cuda.synchronize()
+    assert hist[0, 5].item() == 31 and int(out) == 8
+    assert int((hist != -1).sum()) == 1
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_lm_head_candidates_give_torch_argmax(dtype):
+    """dh_decode_gemv's per-workgroup candidates (the release vocabulary head shape) reduced by
+    dh_argmax_reduce equal torch.argmax of the logits the same launch wrote: random rows, two tied
+    maximal rows (the lower wins), and a NaN row (NaN wins)."""
+    from dispatcher_hybrid import fused_step
+    V, K = 50257, 1024
+    g = torch.Generator(device=DEV).manual_seed(9)
+    W = (torch.randn(V, K, device=DEV, generator=g) / K ** 0.5).to(dtype)
+    x = torch.randn(1, K, device=DEV, generator=g).to(dtype)
+    w = torch.ones(K, device=DEV, dtype=dtype)
+    t_buf = torch.zeros(1, dtype=torch.long, device=DEV)
+    for variant in ("random", "tie", "nan"):
+        if variant == "tie":
+            W[40000] = W[123] = x[0] * 3                                    # equal maximal rows
+        if variant == "nan":
+            W[31000, 5] = float("nan")
+        logits = torch.empty(1, V, device=DEV, dtype=dtype)
+        cand = fused_step.candidate_buffer(dtype, V, K, 1, DEV)
+        fused_step.decode_gemv(x, [(W, logits, V, 0)], t_buf, norm_weight=w, argmax_cand=cand)
+        out = fused_step.argmax_reduce(cand, torch.empty(1, dtype=torch.long, device=DEV))
+        torch.cuda.synchronize()
+        assert int(out) == int(logits.argmax(-1)), variant
+        if variant == "tie":
+            assert int(out) == 123
+        if variant == "nan":
+            assert int(out) == 31000
+
+
 def test_argmax_rejects_bad_shapes():
     from dispatcher_hybrid import fused_step
     with pytest.raises(ValueError):
