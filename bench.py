@@ -56,8 +56,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--cpu-prompt", type=int, default=1024)
-    ap.add_argument("--leg", default="all", choices=["all", "prefill-kernels"],
-                    help="prefill-kernels: only the C5 kernel timings (for rocprofv3 runs)")
+    ap.add_argument("--leg", default="all", choices=["all", "prefill-kernels", "decode-b16"],
+                    help="prefill-kernels: only the C5 kernel timings; decode-b16: only the batch-16 "
+                         "sampling decode (for rocprofv3 runs)")
     return ap.parse_args()
 
 
@@ -400,6 +401,13 @@ def main():
     copy_probe(torch, dev)
     model = build_model(torch, dev)
     max_len = model.config.max_len
+    if args.leg == "decode-b16":
+        steps16 = min(args.steps, 128)
+        p16 = min(args.prompt, max_len - args.warmup - steps16)
+        tok16, ms16, _ = time_decode(torch, model, 16, p16, args.warmup, steps16, sample=True)
+        log(f"C4 decode B=16: {tok16:.1f} tok/s ({ms16:.3f} ms/step)")
+        print(json.dumps({"decode_b16_tok_s": round(tok16, 1), "decode_b16_ms_per_step": round(ms16, 4)}), flush=True)
+        return
     prompt = min(args.prompt, max_len - args.warmup - args.steps)
     if prompt < 1:
         raise SystemExit("--steps + --warmup exceed the 4096-token context")

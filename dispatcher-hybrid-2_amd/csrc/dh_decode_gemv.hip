@@ -644,6 +644,215 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_staged_kernel(GemvArgs a
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Batched decode GEMV on the matrix cores (bf16, 2 <= B <= 16). out[b, n] = W[n] . h[b] for a batch
+// of up to 16 rows is a skinny GEMM whose batch dimension is exactly the 16 rows of
+// v_mfma_f32_16x16x32_bf16: A = the (normalised) activation rows staged in LDS (rows padded to
+// K*2 + 16 bytes: conflict-free 16-byte reads; rows past B are zero), B = 16 weight rows straight
+// from memory (lane (row n, k-group g) holds 16 bytes of W[n]), and the C fragment already holds
+// one output row per lane column and four batch rows per lane -- no cross-lane reduction, where the
+// batched CUDA-style kernel above reduces every (row, batch row) dot product across a wave. A
+// workgroup owns one 16-row output tile (two for SwiGLU: gate and up) and splits K over KSPLIT
+// waves (4..16, so a launch keeps ~1000+ waves streaming weights); their partial tiles are summed
+// through LDS by wave 0, which applies the same epilogues and rounding points as the kernels above.
+// Requests: the activation rows first (small, from L2), then every weight fragment of the wave,
+// then the waits.
+typedef __attribute__((__vector_size__(8 * sizeof(short)))) short mf_bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float mf_f32x4;
+
+template <int KSPLIT, int TPW, int KSW, bool SW>
+__global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(GemvArgs a, int steps_per_wave) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int NT = 64 * KSPLIT * TPW;               // TPW 16-row tiles per workgroup share the staging
+  constexpr int NW = SW ? 2 : 1;
+  constexpr int XC = 8;                                // staged 16-byte chunks per thread (host: 2K <= XC*NT)
+  const int lane = threadIdx.x & 63, wwave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tile = wwave / KSPLIT, wave = wwave % KSPLIT;   // this wave's tile and K slice
+  const int r = lane & 15, g = lane >> 4;
+  const int K = a.K, B = a.B;
+  const int kc = K / 8;                                // 16-byte chunks per row
+  const int rowb = K * 2 + 16;                         // padded LDS row (bytes)
+  unsigned char* hs = smem;                            // [16][rowb] staged rows
+  float* red = reinterpret_cast<float*>(smem + 16 * rowb);   // [TPW][KSPLIT][NW][64][4] partial tiles
+  const int n0 = min((blockIdx.x * TPW + tile) * 16, ((a.Nrows - 1) / 16) * 16);   // past the end: last tile
+  const bool tile_live = (blockIdx.x * TPW + tile) * 16 < a.Nrows;
+  const RowSeg seg0 = SW ? RowSeg{0, n0} : row_segment(a, n0);
+  // a partial last tile (one segment only) reads its last real row in place of the missing ones
+  const bool row_ok = n0 + r < a.Nrows;
+  const int wrow = seg0.local + (row_ok ? r : a.Nrows - 1 - n0);
+  const bf16_t* w0 = (const bf16_t*)pick_seg(seg0.s, a.seg[0].W, a.seg[1].W, a.seg[2].W) + (int64_t)wrow * K;
+  const bf16_t* w1 = SW ? (const bf16_t*)a.seg[1].W + (int64_t)wrow * K : w0;
+
+  // ---- requests: activation chunks (chunk i = row i / kc, column i % kc), then the weights
+  // (predicated: only chunks of real rows, only the wave's own k-steps -- clamped duplicates would
+  // multiply the launch's requests)
+  uint4 xs[XC];
+#pragma unroll
+  for (int j = 0; j < XC; ++j) {
+    const int i = threadIdx.x + j * NT;
+    xs[j] = make_uint4(0u, 0u, 0u, 0u);
+    if (i < B * kc) {
+      const int b = i / kc;
+      const int64_t xrow = a.x_rows ? load_uniform(a.x_rows + b) : (int64_t)b;
+      xs[j] = ld16((const bf16_t*)a.x + xrow * a.x_bstride + (int64_t)(i % kc) * 8);
+    }
+  }
+  const int nsteps = K / 32;
+  const int s0 = wave * steps_per_wave;
+  const int my_steps = min(steps_per_wave, nsteps - s0);
+  uint4 wf[NW][KSW];
+#pragma unroll
+  for (int j = 0; j < KSW; ++j) {
+    if (j < my_steps) {
+      wf[0][j] = ld16(w0 + (s0 + j) * 32 + 8 * g);
+      if (SW) wf[NW - 1][j] = ld16(w1 + (s0 + j) * 32 + 8 * g);
+    }
+  }
+  // the residual operands of this lane's outputs (row n0 + r, batch rows 4g + i), requested now so
+  // the epilogue does not wait a memory round trip
+  uint32_t rres[4] = {0u, 0u, 0u, 0u};
+  if (!SW && a.resid && wave == 0) {                  // uniform
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = min(4 * g + i, B - 1);
+      const int64_t rrow = a.resid_rows ? a.resid_rows[b] : (int64_t)b;
+      rres[i] = Raw<bf16_t>::load((const bf16_t*)a.resid + rrow * a.resid_bstride + seg0.local + (row_ok ? r : 0));
+    }
+  }
+  const int64_t t = a.uses_t ? load_uniform(a.t_dev) : 0;
+  DH_ISSUE_FENCE();
+
+  // ---- stage the rows (zeros past B), then normalise each once (wave w: rows w, w + KSPLIT, ...)
+#pragma unroll
+  for (int j = 0; j < XC; ++j) {
+    const int i = threadIdx.x + j * NT;
+    if (i < 16 * kc) {
+      const int b = i / kc;
+      *reinterpret_cast<uint4*>(hs + b * rowb + (i % kc) * 16) = b < B ? xs[j] : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  __syncthreads();
+  if (a.g != nullptr) {                                // uniform
+    for (int b = wwave; b < B; b += KSPLIT * TPW) {
+      float ss = 0.f;
+      for (int c = lane; c < kc; c += 64) {
+        float xf[8];
+        Vec<bf16_t>::unpack(*reinterpret_cast<const uint4*>(hs + b * rowb + c * 16), xf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += xf[e] * xf[e];
+      }
+      const float rs = rsqrtf(wave_sum(ss) / (float)K + a.eps);
+      for (int c = lane; c < kc; c += 64) {
+        float xf[8], gw[8];
+        Vec<bf16_t>::unpack(*reinterpret_cast<const uint4*>(hs + b * rowb + c * 16), xf);
+        Vec<bf16_t>::unpack(ld16((const bf16_t*)a.g + c * 8), gw);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[e] = Elem<bf16_t>::round(xf[e] * rs * gw[e]);
+        *reinterpret_cast<uint4*>(hs + b * rowb + c * 16) = Vec<bf16_t>::pack(xf);
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- this wave's k-steps on the matrix cores
+  mf_f32x4 acc[NW];
+#pragma unroll
+  for (int q = 0; q < NW; ++q) acc[q] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < KSW; ++j) {
+    if (j < my_steps) {                                // uniform
+      mf_bf16x8 av, bv;
+      const uint4 xa = *reinterpret_cast<const uint4*>(hs + r * rowb + ((s0 + j) * 32 + 8 * g) * 2);
+      __builtin_memcpy(&av, &xa, 16);
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        __builtin_memcpy(&bv, &wf[q][j], 16);
+        acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc[q], 0, 0, 0);
+      }
+    }
+  }
+  // ---- partial tiles through LDS; wave 0 sums them and writes (row n0 + r, batch rows 4g + i)
+#pragma unroll
+  for (int q = 0; q < NW; ++q)
+    *reinterpret_cast<mf_f32x4*>(red + (((tile * KSPLIT + wave) * NW + q) * 64 + lane) * 4) = acc[q];
+  __syncthreads();
+  if (wave == 0 && tile_live) {
+    float v[NW][4];
+#pragma unroll
+    for (int q = 0; q < NW; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[q][i] = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < KSPLIT; ++w2)
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        const mf_f32x4 p = *reinterpret_cast<const mf_f32x4*>(red + (((tile * KSPLIT + w2) * NW + q) * 64 + lane) * 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[q][i] += p[i];
+      }
+    const int loc = seg0.local + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = 4 * g + i;
+      if (b >= B || !row_ok) continue;
+      float out;
+      if (SW) {
+        out = Elem<bf16_t>::round(Elem<bf16_t>::round(silu(Elem<bf16_t>::round(v[0][i]))) *
+                                  Elem<bf16_t>::round(v[NW - 1][i]));
+      } else {
+        out = Elem<bf16_t>::round(v[0][i]);
+        if (a.resid) out = Elem<bf16_t>::round(out + Raw<bf16_t>::f(rres[i]));
+      }
+      Elem<bf16_t>::store(out_ptr<bf16_t>(a, seg0.s, b, t, loc), out);
+    }
+  }
+  advance_position(a);
+}
+
+template <int KSPLIT, int TPW, int KSW, bool SW>
+void launch_mfma_k(const GemvArgs& a, int steps_per_wave, hipStream_t s) {
+  const size_t lds = (size_t)16 * (a.K * 2 + 16) + (size_t)TPW * KSPLIT * (SW ? 2 : 1) * 64 * 16;
+  auto kern = &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW>;
+  if (lds > 64 * 1024)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lds);
+  const int tiles = (a.Nrows + 15) / 16;
+  kern<<<dim3((tiles + TPW - 1) / TPW), dim3(64 * KSPLIT * TPW), lds, s>>>(a, steps_per_wave);
+}
+
+// K split: enough waves to stream the weights (~1024+ per launch), at least 4 per workgroup (they
+// share the staged rows) and enough for the staging (2K <= 8 * 64 * KSPLIT)
+// (SwiGLU: at most 8 waves -- two weight tiles per wave do not fit 16 waves' registers)
+bool mfma_gemv_fits(const GemvArgs& a, bool swiglu) {
+  if (a.B < 2 || a.B > 16 || a.K % 32 != 0 || a.K > (swiglu ? 2048 : 4096)) return false;
+  if (a.nseg == 1 && !swiglu) return true;            // a partial last tile is handled
+  for (int s = 0; s < a.nseg; ++s)
+    if (a.seg[s].N % 16 != 0) return false;
+  return true;
+}
+
+template <bool SW>
+void launch_mfma(const GemvArgs& a, hipStream_t s) {
+  const int tiles = (a.Nrows + 15) / 16, nsteps = a.K / 32;
+  constexpr int kmax = SW ? 8 : 16;
+  int ks = 4;
+  while (ks < kmax && (tiles * ks < 1024 || a.K > 256 * ks)) ks *= 2;
+  const int spw = (nsteps + ks - 1) / ks;             // <= 8: K <= 256 * ks
+  const bool small = spw <= 4;
+  if constexpr (!SW) {
+    // many tiles (the vocabulary head): four tiles per workgroup share one staging of the rows
+    if (ks == 4 && tiles >= 4 * 512) {
+      if (small) launch_mfma_k<4, 4, 4, SW>(a, spw, s); else launch_mfma_k<4, 4, 8, SW>(a, spw, s);
+      return;
+    }
+  }
+  if (ks == 4) { if (small) launch_mfma_k<4, 1, 4, SW>(a, spw, s); else launch_mfma_k<4, 1, 8, SW>(a, spw, s); }
+  else if (ks == 8) { if (small) launch_mfma_k<8, 1, 4, SW>(a, spw, s); else launch_mfma_k<8, 1, 8, SW>(a, spw, s); }
+  else if constexpr (!SW) {
+    if (small) launch_mfma_k<16, 1, 4, SW>(a, spw, s); else launch_mfma_k<16, 1, 8, SW>(a, spw, s);
+  }
+}
+
 constexpr int kStageBytes = 96 * 1024;                 // LDS for staged batch rows
 #ifndef DH_GEMV_ROW_THREADS
 #define DH_GEMV_ROW_THREADS 256
@@ -774,6 +983,10 @@ extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const
   const int esz = dtype == DH_BF16 ? 2 : 4;
   const int R = rows_per_wave(B, a.Nrows, K, esz, swiglu != 0);
   hipStream_t s = (hipStream_t)stream;
+  if (dtype == DH_BF16 && !argmax_cand && mfma_gemv_fits(a, swiglu != 0)) {
+    if (swiglu) launch_mfma<true>(a, s); else launch_mfma<false>(a, s);
+    return dh_check_launch(who);
+  }
   if (dtype == DH_BF16) {
     if (swiglu) pick_cg<bf16_t, true>(a, C, R, s); else pick_cg<bf16_t, false>(a, C, R, s);
   } else {

@@ -154,9 +154,10 @@ def test_down_projection_release_shape(B, dtype):
     assert rel_err(x, ref) < (1e-5 if dtype == torch.float32 else 1e-2)
 
 
-@pytest.mark.parametrize("B", [1, 2])
+@pytest.mark.parametrize("B", [1, 2, 16])
 def test_lm_head_shape(B):
-    """A vocabulary-sized output (N = 50257, not a multiple of the row tiling)."""
+    """A vocabulary-sized output (N = 50257, not a multiple of the row tiling; batch 2 and 16 take
+    the matrix-core kernel with a partial last 16-row tile)."""
     from dispatcher_hybrid import fused_step
     g = torch.Generator(device=DEV).manual_seed(5)
     V, K = 50257, 1024
