@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kRT) void argmax_reduce_kernel(const Cand* cand, in
 // [64t, 64t + 64), kept as order-preserving 32-bit keys; slots past V hold key 0, below every number).
 // kth, exactly: tau = the top_k-th largest of the 1024 per-thread maxima is a lower bound (at least
 // top_k elements are >= tau), so kth is the top_k-th largest of the elements >= tau; those are
-// compacted into LDS (usually a few hundred) and bitonic-sorted as order-preserving 32-bit keys.
+// compacted into LDS (usually a few hundred) and radix-selected (four 8-bit histogram passes).
 // When they exceed the LDS buffer (or top_k > 1024), a binary search over the key space with
 // block-wide counts finds kth instead. Then weights exp(l_i - max) on the kept elements, a block
 // prefix scan of the per-thread sums, and one uniform draw u in [0, 1) per row from Philox4x32-10
@@ -188,22 +188,61 @@ __device__ __forceinline__ V block_scan(V v, V* red, V& total) {
   return base + incl - v;
 }
 
-// descending bitonic sort of buf[0, n), n a power of two; callers synchronise before
-__device__ __forceinline__ void bitonic_desc(uint32_t* buf, int n) {
-  for (int size = 2; size <= n; size <<= 1)
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < (n >> 1); i += kST) {
-        const int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1));
-        const int hi = lo + stride;
-        const uint32_t a = buf[lo], b = buf[hi];
-        const bool desc = (lo & size) == 0;
-        if (desc ? (a < b) : (a > b)) {
-          buf[lo] = b;
-          buf[hi] = a;
+// The k-th largest (duplicates counted) of the non-zero keys vals[0, n) in LDS, by radix select:
+// four 8-bit passes from the top; each pass histograms the keys that share the digits found so far
+// (LDS atomics), and one wave finds, from the top bin down, the bin where the running count reaches
+// k. Returns 0 when fewer than k keys are non-zero. Callers synchronise before; every thread gets
+// the result. hist: 256 entries; state: 4 (a pair per pass parity, so that thread 0 can reset the
+// next pass's pair while other threads still read this one's).
+__device__ __forceinline__ uint32_t radix_kth(const uint32_t* vals, int n, int k, uint32_t* hist, uint32_t* state) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  uint32_t prefix = 0;
+  uint32_t kk = (uint32_t)k;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    if (tid < 256) hist[tid] = 0u;
+    uint32_t* st = state + 2 * (pass & 1);
+    if (tid == 0) {
+      st[0] = 0xffffffffu;                           // not found
+      st[1] = 0u;
+    }
+    __syncthreads();
+    for (int i = tid; i < n; i += kST) {
+      const uint32_t v = vals[i];
+      if (v != 0u && ((uint64_t)v >> (shift + 8)) == prefix) atomicAdd(&hist[(v >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid < 64) {                                  // lane i: bins 255 - 4i .. 252 - 4i, descending
+      uint32_t c[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) c[q] = hist[255 - 4 * lane - q];
+      const uint32_t sum = c[0] + c[1] + c[2] + c[3];
+      uint32_t incl = sum;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t u = (uint32_t)__shfl_up((int)incl, o);
+        if (lane >= o) incl += u;
+      }
+      const uint32_t excl = incl - sum;
+      if (excl < kk && kk <= incl) {
+        uint32_t acc = excl;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (acc < kk && kk <= acc + c[q]) {
+            st[0] = (uint32_t)(255 - 4 * lane - q);
+            st[1] = kk - acc;
+          }
+          acc += c[q];
         }
       }
-      __syncthreads();
     }
+    __syncthreads();
+    const uint32_t d = st[0];
+    if (d == 0xffffffffu) return 0u;                 // uniform: fewer than k keys
+    kk = st[1];
+    prefix = (prefix << 8) | d;
+  }
+  return prefix;
 }
 
 template <typename T>
@@ -213,6 +252,7 @@ __global__ __launch_bounds__(kST) void sample_topk_kernel(const T* logits, int64
   __shared__ uint32_t buf[kCap + 1];                   // + a slot for unselected writes
   __shared__ float fred[kST / 64];
   __shared__ uint32_t ured[kST / 64];
+  __shared__ uint32_t hist[256], rstate[4];
   __shared__ int chosen, fallback;
   const int b = blockIdx.x, tid = threadIdx.x;
   const T* row = logits + (int64_t)b * row_stride;
@@ -266,13 +306,13 @@ __global__ __launch_bounds__(kST) void sample_topk_kernel(const T* logits, int64
     if (top_k <= kST) {
       buf[tid] = kmax;
       __syncthreads();
-      bitonic_desc(buf, kST);
-      const uint32_t tau = buf[top_k - 1];
+      // tau: the top_k-th largest per-thread maximum (0 when fewer threads hold elements)
+      const uint32_t tau = radix_kth(buf, kST, top_k, hist, rstate);
       uint32_t c = 0;
 #pragma unroll
       for (int j = 0; j < kSPT; ++j) c += (xk[j] >= tau && xk[j] != 0u) ? 1u : 0u;
       uint32_t C;
-      uint32_t r = block_scan(c, ured, C);             // (its barriers also end the reads of buf)
+      uint32_t r = block_scan(c, ured, C);
       if (C <= (uint32_t)kCap) {
 #pragma unroll
         for (int j = 0; j < kSPT; ++j) {              // branch-free: unselected keys go to buf[kCap]
@@ -280,13 +320,9 @@ __global__ __launch_bounds__(kST) void sample_topk_kernel(const T* logits, int64
           buf[take ? r : kCap] = xk[j];
           r += take ? 1u : 0u;
         }
-        int n = 64;
-        while (n < (int)C) n <<= 1;
-        for (int i = (int)C + tid; i < n; i += kST) buf[i] = 0u;
         __syncthreads();
-        bitonic_desc(buf, n);
-        kkey = buf[top_k - 1];
-        found = true;
+        kkey = radix_kth(buf, (int)C, top_k, hist, rstate);
+        found = kkey != 0u;
       }
     }
     if (!found) {                                      // uniform: the largest v with count(key >= v) >= top_k
