@@ -41,9 +41,9 @@ MFMA_BF16_TFLOPS = 2500.0              # MI355X dense bf16
 REF_DECODE_TOK_S = 525.1               # reference FusedGraphedHybridDecoder @3900 ctx (A6000, README.md:76-81)
 EOT = 50256
 # HBM bytes per dh_decode_gemv launch, averaged over the decode step's 57 launches: rocprofv3 --pmc
-# FETCH_SIZE (x 1.99974, the factor a 256 MiB copy's reading gives) + WRITE_SIZE (x 1.0), from
+# FETCH_SIZE (x 1.99975, the factor a 256 MiB copy's reading gives) + WRITE_SIZE (x 1.0), from
 # profiles/decode_c3_b1_kernels.md
-TRAFFIC_GEMV_LAUNCH = 9_453_170
+TRAFFIC_GEMV_LAUNCH = 9_465_653
 
 
 def parse():

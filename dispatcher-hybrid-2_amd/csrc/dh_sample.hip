@@ -65,22 +65,27 @@ __global__ __launch_bounds__(64) void argmax_final(const Cand* cand, int nslice,
 }
 
 // The greedy pick after a vocabulary head that wrote one candidate per workgroup (dh_decode_gemv
-// with argmax_cand): one workgroup of 1024 threads per row, every thread's candidates requested
+// with argmax_cand): one workgroup of 256 threads per row, every thread's candidates requested
 // before any comparison (a loop of dependent loads would serialise them), wave reductions, one
 // LDS step. Optionally the token is also stored at hist[b * hist_stride + *t_dev] (the position
 // the decoder just advanced to), when that index is below hist_len.
-constexpr int kRT = 1024;
-constexpr int kRPer = 8;                   // candidates per thread: up to 8192 per row
+constexpr int kRT = 256;
+constexpr int kRPer = 32;                  // candidates per thread: up to 8192 per row
 
 __global__ __launch_bounds__(kRT) void argmax_reduce_kernel(const Cand* cand, int ncand, int64_t* out,
                                                             const int64_t* t_dev, int64_t* hist,
                                                             int64_t hist_stride, int64_t hist_len) {
   __shared__ Cand wb[kRT / 64];
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the history position first: a scalar load that then lands while the candidates are in flight
+  const int64_t t = hist ? load_uniform(t_dev) : -1;
   const Cand* cb = cand + (int64_t)b * ncand;
   Cand c[kRPer];
 #pragma unroll
-  for (int k = 0; k < kRPer; ++k) c[k] = cb[min(tid + k * kRT, ncand - 1)];
+  for (int k = 0; k < kRPer; ++k) {                   // only the row's candidates are requested
+    c[k] = Cand{-INFINITY, 0x7fffffff};
+    if (tid + k * kRT < ncand) c[k] = cb[tid + k * kRT];
+  }
   float best = -INFINITY;
   int bidx = 0x7fffffff;
 #pragma unroll
@@ -98,10 +103,7 @@ __global__ __launch_bounds__(kRT) void argmax_reduce_kernel(const Cand* cand, in
     for (int w = 1; w < kRT / 64; ++w)
       if (beats(wb[w].v, wb[w].i, r.v, r.i)) r = wb[w];
     out[b] = r.i;
-    if (hist) {
-      const int64_t t = load_uniform(t_dev);
-      if (t >= 0 && t < hist_len) hist[(int64_t)b * hist_stride + t] = r.i;
-    }
+    if (hist && t >= 0 && t < hist_len) hist[(int64_t)b * hist_stride + t] = r.i;
   }
 }
 
