@@ -325,7 +325,6 @@ __global__ __launch_bounds__(kSThreads) void decode_attention_split_kernel(AttnA
   const int j0 = min(sg * P, n), j1 = min(n, j0 + P); // this segment's indices [j0, j1)
   const bool has_t = j0 <= n - 1 && n - 1 < j1;
   const int jc1 = min(j1, n - 1);                     // cached indices [j0, jc1)
-  const int cmax = max(n - 2, 0);                     // clamp: a written cache row (results discarded)
   const int64_t head_off = ((int64_t)b * a.H + h) * a.Tmax * HD;
   T* Kh = (T*)a.K + head_off;
   T* Vh = (T*)a.V + head_off;
@@ -347,18 +346,23 @@ __global__ __launch_bounds__(kSThreads) void decode_attention_split_kernel(AttnA
     rop[7] = raw_load((const T*)a.v + base + 1);
   }
   DH_ISSUE_FENCE();
+  // only this segment's cached rows are requested (a segment is often shorter than one sweep)
   uint4 krow[KCH];
   {
-    const int i = min(j0 + tid, cmax);
+    const int i = j0 + tid;
 #pragma unroll
-    for (int c = 0; c < KCH; ++c) krow[c] = reinterpret_cast<const uint4*>(Kh + (int64_t)(lo + i) * HD)[c];
+    for (int c = 0; c < KCH; ++c) {
+      krow[c] = make_uint4(0u, 0u, 0u, 0u);
+      if (i < jc1) krow[c] = reinterpret_cast<const uint4*>(Kh + (int64_t)(lo + i) * HD)[c];
+    }
   }
   const int slot = lane / KCH, dg = lane % KCH;
   uint4 vrow[VCH];
 #pragma unroll
   for (int u = 0; u < VCH; ++u) {
-    const int i = min(j0 + (u * NW + wave) * RPI + slot, cmax);
-    vrow[u] = reinterpret_cast<const uint4*>(Vh + (int64_t)(lo + i) * HD)[dg];
+    const int i = j0 + (u * NW + wave) * RPI + slot;
+    vrow[u] = make_uint4(0u, 0u, 0u, 0u);
+    if (i < jc1) vrow[u] = reinterpret_cast<const uint4*>(Vh + (int64_t)(lo + i) * HD)[dg];
   }
   DH_ISSUE_FENCE();
   if (roper) {
@@ -410,9 +414,9 @@ __global__ __launch_bounds__(kSThreads) void decode_attention_split_kernel(AttnA
   float mx = -INFINITY;
   for (int i0 = j0; i0 < jc1; i0 += kSThreads) {
     const int i = i0 + tid;
-    if (i0 > j0) {                                     // sweeps past the first (long segments)
+    if (i0 > j0 && i < jc1) {                          // sweeps past the first (long segments)
 #pragma unroll
-      for (int c = 0; c < KCH; ++c) krow[c] = reinterpret_cast<const uint4*>(Kh + (int64_t)(lo + min(i, cmax)) * HD)[c];
+      for (int c = 0; c < KCH; ++c) krow[c] = reinterpret_cast<const uint4*>(Kh + (int64_t)(lo + i) * HD)[c];
     }
     const float s0 = score(krow);
     if (i < jc1) {
@@ -453,7 +457,7 @@ __global__ __launch_bounds__(kSThreads) void decode_attention_split_kernel(AttnA
 #pragma unroll
   for (int e = 0; e < VE; ++e) acc[e] = 0.f;
   auto accumulate = [&](const uint4& w, int i) {
-    if (i >= jc1) return;                              // a clamped row: never folded in
+    if (i >= jc1) return;                              // a row outside the segment: never folded in
     const float p = sc[i - j0];
     const uint32_t wsd[4] = {w.x, w.y, w.z, w.w};
     if constexpr (sizeof(T) == 2) {
@@ -471,8 +475,10 @@ __global__ __launch_bounds__(kSThreads) void decode_attention_split_kernel(AttnA
   for (int u = 0; u < VCH; ++u) accumulate(vrow[u], j0 + (u * NW + wave) * RPI + slot);
   for (int i0 = j0 + VCH * NW * RPI; i0 < jc1; i0 += VCH * NW * RPI) {   // segments past the prefetch
 #pragma unroll
-    for (int u = 0; u < VCH; ++u)
-      vrow[u] = reinterpret_cast<const uint4*>(Vh + (int64_t)(lo + min(i0 + (u * NW + wave) * RPI + slot, cmax)) * HD)[dg];
+    for (int u = 0; u < VCH; ++u) {
+      const int i = i0 + (u * NW + wave) * RPI + slot;
+      if (i < jc1) vrow[u] = reinterpret_cast<const uint4*>(Vh + (int64_t)(lo + i) * HD)[dg];
+    }
 #pragma unroll
     for (int u = 0; u < VCH; ++u) accumulate(vrow[u], i0 + (u * NW + wave) * RPI + slot);
   }
