@@ -39,6 +39,7 @@ W_BYTES = 2 * N_PARAMS                 # bf16 weight bytes streamed per decode s
 HBM_PEAK_GBS = 8000.0                  # MI355X HBM3E
 MFMA_BF16_TFLOPS = 2500.0              # MI355X dense bf16
 REF_DECODE_TOK_S = 525.1               # reference FusedGraphedHybridDecoder @3900 ctx (A6000, README.md:76-81)
+REF_DECODE_BY_CTX = {256: 534.8, 1024: 534.1, 2048: 534.1, 3900: 525.1}   # same table, by context
 EOT = 50256
 # HBM bytes per dh_decode_gemv launch, averaged over the decode step's 57 launches: rocprofv3 --pmc
 # FETCH_SIZE (x 1.99975, the factor a 256 MiB copy's reading gives) + WRITE_SIZE (x 1.0), from
@@ -474,6 +475,16 @@ def main():
         out["prefill_speedup_vs_eager"] = round(f_tok / e_tok, 3)
         out["prefill_mfma_frac"] = round(flops / (f_ms * 1e-3) / 1e12 / MFMA_BF16_TFLOPS, 4)
         log(f"C2 prefill: fused {f_tok:.0f} tok/s, eager {e_tok:.0f} tok/s")
+
+        # batch-1 greedy decode at the reference README's contexts (flat in context: the tree reads
+        # O(log t) state and attention a fixed window); 3900 runs the 196 steps that fit max_len
+        ctx = {}
+        for p_ctx, ref in REF_DECODE_BY_CTX.items():
+            n_ctx = min(128, 4096 - p_ctx - 16) if p_ctx != 3900 else 196 - 16
+            tk, _, _ = time_decode(torch, model, 1, p_ctx, 16, n_ctx, sample=False)
+            ctx[str(p_ctx)] = {"tok_s": round(tk, 1), "steps": n_ctx, "vs_reference": round(tk / ref, 3)}
+        out["decode_b1_by_context"] = ctx
+        log("C3 decode by context: " + ", ".join(f"{k}: {v['tok_s']} tok/s" for k, v in ctx.items()))
 
         g = torch.Generator(device=dev).manual_seed(6)
         ids = torch.randint(0, 50257, (8, 4096), device=dev, generator=g)
