@@ -45,6 +45,12 @@ EOT = 50256
 # FETCH_SIZE (x 1.99975, the factor a 256 MiB copy's reading gives) + WRITE_SIZE (x 1.0), from
 # profiles/decode_c3_b1_kernels.md
 TRAFFIC_GEMV_LAUNCH = 9_465_653
+# HBM bytes per decode_persistent_kernel launch (one batch-1 step), same counters and factors, from
+# profiles/decode_c3_b1_persistent.md
+TRAFFIC_PERSISTENT_LAUNCH = 611_679_125
+# algorithmic bytes of one batch-1 step at context >= 1024: weights 584,316,928 + tree state
+# 1,224,704 + windowed keys and values 8,396,800
+STEP_BYTES = 584_316_928 + 1_224_704 + 8_396_800
 
 
 def parse():
@@ -97,11 +103,18 @@ def time_decode(torch, model, batch, prompt, warmup, steps, sample):
         for _ in range(warmup):
             dec.step_greedy()
         sync_barrier(torch)
+        # HIP events on the stream the steps are launched on (torch's current stream): with the
+        # one-launch step this is the kernel's average duration plus the small gap between launches
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
+        e0.record()
         for _ in range(steps):
             dec.step_greedy()
+        e1.record()
         sync_barrier(torch)
         dt = time.perf_counter() - t0
+        dec.check_persistent()                             # raises if a one-launch step timed out
+        dec.event_us_per_step = e0.elapsed_time(e1) * 1e3 / steps
         return batch * steps / dt, 1e3 * dt / steps, dec
 
     def next_tok(lg):
@@ -424,7 +437,9 @@ def main():
         "config": {"workload": "C3: 292M bf16 batch-1 greedy decode via FusedGraphedHybridDecoder, "
                                f"prompt {prompt} then {args.warmup}+{args.steps} steps "
                                f"(context {prompt}-{prompt + args.warmup + args.steps})",
-                   "batch": 1, "prompt_len": prompt, "max_len": max_len},
+                   "batch": 1, "prompt_len": prompt, "max_len": max_len,
+                   "step": "one launch per token (dh_decode_persistent_step)" if dec1._pers
+                           else "graph of launches (dh_decode_gemv, dh_decode_gates, ...)"},
         "vs_baseline_ref": "reference FusedGraphedHybridDecoder 525.1 tok/s @3900 ctx on A6000 (README.md:76-81)",
     }
     step_gbs = W_BYTES * tok_s / 1e9
@@ -437,14 +452,26 @@ def main():
                          "us": round(mus, 3), "bytes": mb,
                          "achieved_gbs": round(mb / (mus * 1e-6) / 1e9, 1)}
     log(f"mixer step (gates + scan): {mus:.2f} us per layer")
+    if dec1._pers:
+        # the dominant (only) kernel of the step: algorithmic bytes = every weight once, the tree
+        # state rows and the windowed keys and values of one token (full-byte definition)
+        us = dec1.event_us_per_step
+        ach = STEP_BYTES / (us * 1e-6) / 1e9
+        out["roofline"] = {"kernel": "decode_persistent_kernel: one batch-1 decode step per launch "
+                                     "(dh_decode_persistent_step)",
+                           "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_PERSISTENT_LAUNCH,
+                           "bytes_per_launch": STEP_BYTES, "avg_launch_us": round(us, 3)}
+        log(f"one-launch step: {us:.1f} us/launch, {ach:.0f} GB/s")
     nbytes, avg_us, nl = gemv_chain_roofline(torch, model)
     achieved = nbytes / nl / (avg_us * 1e-6) / 1e9
-    out["roofline"] = {"kernel": "dh_decode_gemv: the 57 launches of one batch-1 decode step "
-                                 "(decode_gemv_row_kernel instantiations)",
-                       "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                       "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_GEMV_LAUNCH,
-                       "bytes_per_launch": round(nbytes / nl), "bytes_per_step": nbytes,
-                       "avg_launch_us": round(avg_us, 3), "launches_per_step": nl}
+    out["gemv_chain" if dec1._pers else "roofline"] = {
+        "kernel": "dh_decode_gemv: the 57 launches of one batch-1 decode step (decode_gemv_row_kernel "
+                  "instantiations; the graph-of-launches step)",
+        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_GEMV_LAUNCH,
+        "bytes_per_launch": round(nbytes / nl), "bytes_per_step": nbytes,
+        "avg_launch_us": round(avg_us, 3), "launches_per_step": nl}
     log(f"decode GEMV chain: {nl} launches, {avg_us:.2f} us/launch, {achieved:.0f} GB/s")
     del dec1
     torch.cuda.empty_cache()

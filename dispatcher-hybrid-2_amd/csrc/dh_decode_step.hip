@@ -734,7 +734,8 @@ __global__ __launch_bounds__(kSOThreads) void decode_scan_out_kernel(ScanOutArgs
     const bool on = l < L;                               // uniform
 #pragma unroll
     for (int q = 0; q < kSOEpt; ++q) {
-      const float nv = cf[l].x * v[q] + cf[l].y * vs[l][q];
+      // one explicit fused multiply-add (the one-launch step evaluates the same form)
+      const float nv = __builtin_fmaf(cf[l].y, vs[l][q], cf[l].x * v[q]);
       v[q] = on ? nv : v[q];
       hist[l][q] = v[q];
     }

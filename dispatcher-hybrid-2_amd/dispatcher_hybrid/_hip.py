@@ -15,7 +15,7 @@ import os
 
 import torch
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 _LIB_NAME = "libdh_mixer.so"
 
 DH_F32, DH_BF16 = 0, 1
@@ -80,6 +80,10 @@ def _load():
         "dh_argmax_workspace_bytes": ([i32, i32], i64),
         "dh_decode_gates": ([i32] + [vp] * 12 + [i32] * 7 + [vp], i32),
         "dh_decode_scan": ([i32] + [vp] * 5 + [i32] * 6 + [vp], i32),
+        "dh_decode_persistent_scratch_bytes": ([i32] * 6, i64),
+        "dh_decode_persistent_step": ([vp, vp, i32, vp, vp, ctypes.c_float] + [i32] * 8
+                                      + [vp, vp, vp, i64, vp, vp, i64, vp], i32),
+        "dh_decode_persistent_status": ([vp, vp, vp], i32),
     }
     for name, (argtypes, restype) in sigs.items():
         fn = getattr(lib, name)

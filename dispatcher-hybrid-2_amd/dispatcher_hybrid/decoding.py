@@ -440,9 +440,13 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
 
     _prefill_cls = _FusedPrefillDecoder
 
-    def __init__(self, model, max_len=None, dtype=None):
+    def __init__(self, model, max_len=None, dtype=None, persistent=True):
         from . import fused_step                          # loads libdh_mixer.so
         self._fused_step = fused_step
+        # batch-1 bf16 greedy steps as one cooperative launch each (dh_decode_persistent_step)
+        # where the model fits it; False keeps the graph of launches
+        self.use_persistent = persistent
+        self._pers = None
         super().__init__(model, max_len, dtype)
 
     def _prepare(self):
@@ -474,6 +478,84 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         self.attn_ws = None
         if att0 is not None and Bb * att0.num_heads <= 64:
             self.attn_ws = self._fused_step.attention_workspace(Bb, att0.num_heads, att0.head_dim, dev)
+
+    def _persistent_setup(self):
+        """Layer table and scratch of the one-launch step (a dict), or False when this decoder cannot use it
+        (batch > 1, fp32, or dimensions outside the kernel's)."""
+        fs, m = self._fused_step, self.m
+        cfg = m.config
+        if self.inner.batch != 1 or self.dtype != torch.bfloat16:
+            return False
+        dev = next(m.parameters()).device
+        eps = {self._eps(n, self.dtype) for n in [b.norm1 for b in m.blocks] + [b.norm2 for b in m.blocks]
+               + [m.norm_out]}
+        if len(eps) != 1:
+            return False
+        rows, kinds = [], []
+        dims = None
+        for blk, cache in zip(m.blocks, self.inner.caches):
+            f = blk.ffn
+            w = [0] * fs.LAYER_WORDS
+            w[1] = blk.norm1.weight
+            w[15], w[16], w[17], w[18] = blk.norm2.weight, f.linear_gate.weight, f.linear_up.weight, f.linear_down.weight
+            if isinstance(blk, AttentionBlock):
+                at = blk.attn
+                span = min(at.window, self.max_len) if at.window > 0 else self.max_len
+                if at.head_dim != 64 or span > fs.MAX_WINDOW:
+                    return False
+                kinds.append(1)
+                w[0] = 1
+                w[2], w[3], w[4], w[5] = at.linear_q.weight, at.linear_k.weight, at.linear_v.weight, at.linear_out.weight
+                w[6], w[7], w[8], w[9] = cache.k, cache.v, cache.rope_cos, cache.rope_sin
+                w[10] = int(at.window)
+            else:
+                mx = blk.mixer
+                kinds.append(0)
+                w[2], w[3], w[4] = mx.linear_in.weight, mx.gate_hidden.weight, mx.gate_hidden_src.weight
+                w[5], w[6], w[7] = mx.gate_out, mx.forget_out, mx.reset_out
+                w[8], w[9], w[10] = mx.gate_out_bias, mx.forget_out_bias, mx.reset_out_bias
+                w[11], w[12], w[13], w[14] = mx.linear_out.weight, cache.B_hist, cache.rg_hist, cache.V_ring
+                dims = (cfg.d_model, mx.gate_hidden.out_features, mx.num_heads, mx.head_dim, mx.levels)
+            for i, v in enumerate(w):
+                if isinstance(v, torch.Tensor):
+                    if v.dtype != self.dtype or not v.is_contiguous():
+                        return False
+                    w[i] = v.data_ptr()
+            rows.append(w)
+        if dims is None:
+            return False
+        d, GH, H, hd, L = dims
+        ff, V = cfg.dim_feedforward, self.logits_out.shape[1]
+        grid = torch.cuda.get_device_properties(dev).multi_processor_count
+        if not fs.persistent_fits(d, GH, H, hd, L, ff, grid):
+            return False
+        emb = m.lm_head.weight
+        if emb.data_ptr() != m.embedding.weight.data_ptr() or not emb.is_contiguous() or emb.dtype != self.dtype:
+            return False                                   # the kernel reads one tied table
+        nbytes = fs.persistent_scratch_bytes(d, GH, H, L, ff, grid)
+        scratch = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        table = torch.tensor(rows, dtype=torch.int64, device=dev)
+        return dict(table=table, kinds=kinds, emb=emb, norm_out=m.norm_out.weight, eps=eps.pop(),
+                    dims=(d, GH, H, hd, L, ff, V, self.max_len), scratch=scratch)
+
+    def _persistent_step(self):
+        p = self._pers
+        self._fused_step.persistent_step(p["table"], p["kinds"], p["emb"], p["norm_out"], p["eps"], p["dims"],
+                                         self.t_buf, self.token_buf, self.tok_hist, self.logits_out, p["scratch"])
+
+    def persistent_status(self):
+        """(timed out, first failing phase + 1) of this decoder's one-launch steps (synchronises);
+        (0, 0) when none ran or all completed."""
+        if not self._pers:
+            return 0, 0
+        return self._fused_step.persistent_status(self._pers["scratch"])
+
+    def check_persistent(self):
+        """Raise if a one-launch step of this decoder timed out waiting for another workgroup."""
+        flag, phase = self.persistent_status()
+        if flag:
+            raise RuntimeError(f"dh_decode_persistent_step: a wait timed out in phase {phase - 1}; "
+                               "the decode state of this decoder is invalid")
 
     @staticmethod
     def _eps(norm, dtype):
@@ -569,6 +651,12 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         per token (what fast_generate's greedy branch runs; same tokens as argmax of step())."""
         if self.t >= self.max_len:
             raise ValueError(f"context exhausted at max_len {self.max_len}")
+        if self.use_persistent and self._pers is None:
+            self._pers = self._persistent_setup()
+        if self.use_persistent and self._pers:
+            self._persistent_step()
+            self.t += 1
+            return
         if self._greedy_graph is None:
             self._greedy_capture = True
             try:

@@ -378,3 +378,54 @@ def sample_tokens(logits, temperature=1.0, top_k=None, seed=0, offset=None, out=
                                  _hip.ptr(offset), _hip.ptr(out), _hip.stream_handle(logits.device))
     _hip.check(st, "dh_sample_topk")
     return out
+
+
+# ---------------------------------------------------------------------------------------------
+# One-launch batch-1 step (dh_decode_persistent_step)
+# ---------------------------------------------------------------------------------------------
+LAYER_WORDS = 24          # DH_PERSISTENT_LAYER_WORDS
+MAX_WINDOW = 4096         # DH_PERSISTENT_MAX_WINDOW
+
+
+def persistent_fits(d, GH, H, hd, L, ff, grid):
+    """Whether dh_decode_persistent_step takes these dimensions on `grid` compute units (the
+    checks the entry point makes: every output row of a phase has a wave, 16 attention segments
+    per head fit two per workgroup)."""
+    return (d in (256, 512, 768, 1024) and H * hd == d and 64 <= GH <= 1024 and GH % 64 == 0
+            and 64 <= ff <= 3072 and ff % 32 == 0 and 1 <= L <= 12 and H * L <= 768
+            and grid * 4 >= d and grid * 12 >= d + 2 * GH and grid * 12 >= ff and grid * 2 >= H * 16
+            and grid * 4 >= H * L
+            and grid <= 256)
+
+
+def persistent_scratch_bytes(d, GH, H, L, ff, grid):
+    """Scratch bytes of dh_decode_persistent_step for these dimensions and `grid` compute units."""
+    return int(_hip.lib.dh_decode_persistent_scratch_bytes(int(d), int(GH), int(H), int(L), int(ff), int(grid)))
+
+
+def persistent_step(table, kinds, emb, norm_out, eps, dims, t_buf, token_buf, tok_hist, logits, scratch):
+    """One batch-1 bf16 greedy decode step of the whole model as one cooperative launch.
+
+    table: (n_layers, LAYER_WORDS) int64 device tensor of weight / cache addresses (field order of
+    include/dh_mixer.h); kinds: host list of layer kinds (0 tree, 1 attention); dims: (d, GH, H, hd,
+    L, ff, V, Tmax). Reads the token in token_buf at position t_buf[0]; writes the greedy pick to
+    token_buf and tok_hist[0, t + 1], the logits (1, V) and advances t_buf. scratch: zero-filled once
+    (persistent_scratch_bytes), then kept with the decoder."""
+    n = len(kinds)
+    karr = (ctypes.c_int * n)(*[int(k) for k in kinds])
+    d, GH, H, hd, L, ff, V, Tmax = (int(v) for v in dims)
+    p = _hip.ptr
+    hist_len = tok_hist.shape[-1] if tok_hist is not None else 0
+    st = _hip.lib.dh_decode_persistent_step(
+        p(table), karr, n, p(emb), p(norm_out), float(eps), d, GH, H, hd, L, ff, V, Tmax, p(t_buf), p(token_buf),
+        p(tok_hist), hist_len, p(logits), p(scratch), scratch.numel() * scratch.element_size(),
+        _hip.stream_handle(emb.device))
+    _hip.check(st, "dh_decode_persistent_step")
+
+
+def persistent_status(scratch):
+    """(timed out, first failing phase + 1) of the steps run on `scratch` so far (synchronises)."""
+    out = (ctypes.c_uint32 * 2)()
+    _hip.check(_hip.lib.dh_decode_persistent_status(_hip.ptr(scratch), out, _hip.stream_handle(scratch.device)),
+               "dh_decode_persistent_status")
+    return int(out[0]), int(out[1])

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 11
+#define DH_ABI_VERSION 12
 
 enum dh_status {
   DH_OK = 0,
@@ -334,6 +334,44 @@ int dh_step_gates(int dtype, const void* A, const void* B_hist, const void* Wi, 
 int dh_step_scan(int dtype, const void* V0, const float* IG, const float* FG, const void* rg_hist,
                  void* V_ring, const int64_t* t_dev, void* Y, int B, int Tmax, int S, int H, int hd,
                  int L, void* stream);
+
+/*
+ * One batch-1 bf16 greedy decode step of the whole model as ONE launch (one workgroup
+ * per compute unit, resident for the step): the chain FusedGraphedHybridDecoder.step_greedy
+ * replays as a graph of dependent launches (reference dispatcher_hybrid/decoding.py:437-488 and
+ * modeling_dispatcher.py:426-441: tree steps, attention steps, final norm, vocabulary head,
+ * argmax), with the same arithmetic, so the logits and the picked token equal the graphed step's.
+ * Workgroups hand vectors to each other through tagged words in `scratch` (no fences, no
+ * counters); every wait is bounded, and a step that times out sets the status words
+ * (dh_decode_persistent_status) and writes no token.
+ *   layer_table (device): n_layers records of DH_PERSISTENT_LAYER_WORDS int64 words, by field:
+ *     [0] kind (0 tree layer, 1 attention layer), [1] RMSNorm1 weight,
+ *     tree: [2] linear_in [3] gate_hidden [4] gate_hidden_src [5..7] gate_out, forget_out,
+ *           reset_out (L, H, GH) [8..10] their biases (L, H) [11] linear_out [12] B_hist (Tmax, GH)
+ *           [13] rg_hist (Tmax, L, H) [14] V_ring (2^(L+1)-2, d),
+ *     attention: [2..5] linear_q, _k, _v, _out [6, 7] K, V caches (H, Tmax, 64) [8, 9] RoPE cos,
+ *           sin (Tmax, 32) [10] window (0: none; its span <= DH_PERSISTENT_MAX_WINDOW),
+ *     both: [15] RMSNorm2 weight [16..18] linear_gate, linear_up, linear_down.
+ *   kinds (host): the n_layers kinds again, for the phase count.
+ *   emb (V, d): embedding and (tied) vocabulary head; norm_out (d). *t_dev: position (advanced by
+ *   one); *token: this step's token in, the greedy pick out, also stored at tok_hist[t + 1] when
+ *   below hist_len (tok_hist nullable); logits (V) bf16 out.
+ *   scratch: dh_decode_persistent_scratch_bytes(d, GH, H, L, ff, CUs) bytes, 256-byte aligned,
+ *   zero-filled once before the first step and then kept (it holds the launch counter); steps on
+ *   one scratch must not overlap. d = H*hd in {256, 512, 768, 1024}, GH <= 1024, ff <= 3072,
+ *   L <= 12, head width 64 with attention layers. No counterpart in the reference (its step is a
+ *   graph of launches).
+ */
+#define DH_PERSISTENT_LAYER_WORDS 24
+#define DH_PERSISTENT_MAX_WINDOW 4096
+int64_t dh_decode_persistent_scratch_bytes(int d, int GH, int H, int L, int ff, int grid);
+int dh_decode_persistent_step(const int64_t* layer_table, const int* kinds, int n_layers, const void* emb,
+                              const void* norm_out, float eps, int d, int GH, int H, int hd, int L, int ff, int V,
+                              int Tmax, int64_t* t_dev, int64_t* token, int64_t* tok_hist, int64_t hist_len,
+                              void* logits, void* scratch, int64_t scratch_bytes, void* stream);
+/* status words of the last persistent steps on `scratch`: out2[0] non-zero after a timeout,
+ * out2[1] the first failing phase + 1 (synchronises the stream) */
+int dh_decode_persistent_status(const void* scratch, uint32_t* out2, void* stream);
 
 #ifdef __cplusplus
 }

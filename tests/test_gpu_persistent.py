@@ -1,0 +1,94 @@
+"""dh_decode_persistent_step (one cooperative launch per batch-1 bf16 greedy step) against the
+graph of launches it replaces (FusedGraphedHybridDecoder.step_greedy with persistent=False,
+reference dispatcher_hybrid/decoding.py:437-488): the same arithmetic, so the logits after every
+step, the picked tokens and every decode-state buffer must be equal bit for bit."""
+
+import pytest
+import torch
+
+from helpers import product_model, tiny
+from weights import make_state_dict
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+# head width 64, two attention layers (window 128 < the decoded context), 9 levels
+MID = dict(vocab_size=2048, d_model=512, num_heads=8, dim_feedforward=1024, num_layers=4, max_len=512,
+           attn_layers=(2, 4), attn_window=128, doc_reset=True, eot_token=2047)
+
+
+def _pair(m, prompt):
+    from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder
+    dp, dg = FusedGraphedHybridDecoder(m), FusedGraphedHybridDecoder(m, persistent=False)
+    for dec in (dp, dg):
+        dec.greedy_start(dec.prefill(prompt)[:, -1])
+    return dp, dg
+
+
+def _state(dec):
+    out = []
+    for c in dec.inner.caches:
+        out += [c.B_hist, c.rg_hist, c.V_ring] if hasattr(c, "V_ring") else [c.k, c.v]
+    return out
+
+
+def _run_and_compare(dp, dg, steps):
+    for i in range(steps):
+        dp.step_greedy()
+        dg.step_greedy()
+        assert torch.equal(dp.logits_out, dg.logits_out), f"logits differ at step {i}"
+        assert torch.equal(dp.token_buf, dg.token_buf), f"token differs at step {i}"
+    assert dp._pers, "the one-launch step must have been used"
+    assert dp.persistent_status() == (0, 0)
+    assert torch.equal(dp.t_buf, dg.t_buf) and dp.t == dg.t
+    assert torch.equal(dp.tok_hist, dg.tok_hist)
+    for j, (a, b) in enumerate(zip(_state(dp), _state(dg))):
+        assert torch.equal(a, b), f"decode state buffer {j} differs"
+
+
+def test_persistent_mid_model_bit_exact_and_rerun():
+    """A 4-layer bf16 model (two attention layers, window 128): 160 steps from a 20-token prompt
+    (the window slides), then the same decoder prefilled again with another prompt decodes the
+    same positions once more (words left by the first run carry stale tags)."""
+    sd = make_state_dict(MID, 7)
+    m = product_model(MID, sd, device=DEV, dtype=torch.bfloat16)
+    g = torch.Generator(device=DEV).manual_seed(3)
+    prompt = torch.randint(0, 2047, (1, 20), device=DEV, generator=g)
+    print("persistent: mid model, 160 steps", flush=True)
+    dp, dg = _pair(m, prompt)
+    _run_and_compare(dp, dg, 160)
+    print("persistent: mid model, rerun over the same positions", flush=True)
+    prompt2 = torch.randint(0, 2047, (1, 20), device=DEV, generator=g)
+    for dec in (dp, dg):
+        dec.greedy_start(dec.prefill(prompt2)[:, -1])
+    _run_and_compare(dp, dg, 40)
+
+
+def test_persistent_release_model_bit_exact():
+    """The released 292M architecture (random init), a 1100-token prompt (attention window 1024
+    full and sliding), 24 steps."""
+    from dispatcher_hybrid import DispatcherConfig, DispatcherHybridForCausalLM
+    torch.manual_seed(0)
+    with torch.device(DEV):
+        m = DispatcherHybridForCausalLM(DispatcherConfig())
+    m = m.to(torch.bfloat16).eval()
+    prompt = torch.randint(0, 50256, (1, 1100), device=DEV, generator=torch.Generator(device=DEV).manual_seed(5))
+    print("persistent: release model, 24 steps", flush=True)
+    dp, dg = _pair(m, prompt)
+    _run_and_compare(dp, dg, 24)
+
+
+def test_persistent_not_used_where_unsupported():
+    """fp32 models, batch > 1 and widths outside the kernel keep the graph of launches."""
+    from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder
+    cfgd, sd = tiny("tiny_a")
+    m = product_model(cfgd, sd, device=DEV, dtype=torch.bfloat16)     # d = 128: not supported
+    dec = FusedGraphedHybridDecoder(m)
+    dec.greedy_start(dec.prefill(torch.randint(0, 250, (1, 8), device=DEV))[:, -1])
+    dec.step_greedy()
+    assert dec._pers is False
+    mf = product_model(MID, make_state_dict(MID, 7), device=DEV)     # fp32
+    dec = FusedGraphedHybridDecoder(mf)
+    dec.greedy_start(dec.prefill(torch.randint(0, 2047, (1, 8), device=DEV))[:, -1])
+    dec.step_greedy()
+    assert dec._pers is False
