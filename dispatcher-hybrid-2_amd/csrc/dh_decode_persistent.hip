@@ -86,7 +86,31 @@ __device__ __forceinline__ uint4 pack8(const float (&o)[8]) {
 __device__ __forceinline__ float rnd(float v) { return Elem<bf16_t>::round(v); }
 __device__ __forceinline__ float bfv(uint32_t raw16) { return __uint_as_float(raw16 << 16); }
 __device__ __forceinline__ float silu(float x) { return x * dh_sigmoid(x); }
-__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+// Global-memory access through the addresses in the layer table: those are generic pointers to the
+// compiler (read from memory), which would make every access a flat one, counted against the LDS
+// counter too, so each LDS wait would also wait for the weight fetches in flight. Rebuilding the
+// pointer from its integer value in the global address space keeps them global loads and stores
+// (a cast of the generic pointer itself is dropped).
+typedef unsigned int gu32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int gu32x2 __attribute__((ext_vector_type(2)));
+#define DH_GLOBAL(T, p) ((const __attribute__((address_space(1))) T*)(uintptr_t)(p))
+#define DH_GLOBAL_W(T, p) ((__attribute__((address_space(1))) T*)(uintptr_t)(p))
+__device__ __forceinline__ uint4 ld16(const void* p) {
+  const gu32x4 v = *DH_GLOBAL(gu32x4, p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld8(const void* p) {
+  const gu32x2 v = *DH_GLOBAL(gu32x2, p);
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ bf16_t ld2(const bf16_t* p) { return *DH_GLOBAL(bf16_t, p); }
+__device__ __forceinline__ void st2(bf16_t* p, bf16_t v) { *DH_GLOBAL_W(bf16_t, p) = v; }
+__device__ __forceinline__ void st8(void* p, uint2 v) {
+  gu32x2 w;
+  w.x = v.x;
+  w.y = v.y;
+  *DH_GLOBAL_W(gu32x2, p) = w;
+}
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_move<0xb1, 0xf>(v));
   v = fmaxf(v, dpp_move<0x4e, 0xf>(v));
@@ -310,7 +334,7 @@ __device__ __forceinline__ bool stage_input(const PArgs& a, Smem& S, bool first,
 // in the previous x phase and keeps it in a register (xres); the first layer's comes from the
 // embedding row.
 __device__ __forceinline__ float residual(bool first, const bf16_t* erow, int n, float xres) {
-  return first ? bf16_to_f32(erow[n]) : xres;
+  return first ? bf16_to_f32(ld2(erow + n)) : xres;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -381,7 +405,7 @@ __device__ __forceinline__ bool run_in3(const PArgs& a, Smem& S, const PreFirst&
     const float out = rnd(v0);
     if (n < n0) put16(out0 + n, out, tg.t16(ph));
     else if (n < n0 + n1) put16(out1 + (n - n0), out, tg.t16(ph));
-    else if (plain2) plain2[n - n0 - n1] = f32_to_bf16(out);
+    else if (plain2) st2(plain2 + (n - n0 - n1), f32_to_bf16(out));
     else put16(out2 + (n - n0 - n1), out, tg.t16(ph));
   }
   return true;
@@ -484,15 +508,15 @@ __device__ __forceinline__ void fetch_gates(PreGates& f, const PArgs& a, const i
     f.w[2][c] = ld16((const bf16_t*)(intptr_t)Lt[F_WR] + wrow + k);
   }
   const int64_t gi = (int64_t)l * H + h;
-  f.bi = ((const bf16_t*)(intptr_t)Lt[F_BI])[gi];
-  f.bf = ((const bf16_t*)(intptr_t)Lt[F_BF])[gi];
-  f.br = ((const bf16_t*)(intptr_t)Lt[F_BR])[gi];
+  f.bi = ld2((const bf16_t*)(intptr_t)Lt[F_BI] + gi);
+  f.bf = ld2((const bf16_t*)(intptr_t)Lt[F_BF] + gi);
+  f.br = ld2((const bf16_t*)(intptr_t)Lt[F_BR] + gi);
   const int64_t src = t - ((int64_t)1 << l);
   const int64_t sc = src >= 0 ? src : 0;
 #pragma unroll
   for (int c = 0; c < C; ++c)
     f.bv[c] = ld16((const bf16_t*)(intptr_t)Lt[F_BHIST] + sc * GH + (int64_t)min(lane + 64 * c, nchunk - 1) * 8);
-  f.rsrc = ((const bf16_t*)(intptr_t)Lt[F_RGHIST])[(sc * L + l) * H + h];
+  f.rsrc = ld2((const bf16_t*)(intptr_t)Lt[F_RGHIST] + (sc * L + l) * H + h);
 }
 
 __device__ __forceinline__ void run_gates(const PArgs& a, const PreGates& f, const int64_t* Lt, int64_t t,
@@ -558,7 +582,7 @@ __device__ __forceinline__ void run_gates(const PArgs& a, const PreGates& f, con
     const int64_t rec = (int64_t)h * L + l;
     put32(a.coefw + rec * 2, fg, tg.t32(ph));
     put32(a.coefw + rec * 2 + 1, ig * rs, tg.t32(ph));
-    ((bf16_t*)(intptr_t)Lt[F_RGHIST])[(t * L + l) * H + h] = f32_to_bf16(dh_sigmoid(s2 + bfv(f.br)));
+    st2((bf16_t*)(intptr_t)Lt[F_RGHIST] + (t * L + l) * H + h, f32_to_bf16(dh_sigmoid(s2 + bfv(f.br))));
   }
 }
 
@@ -579,7 +603,7 @@ __device__ __forceinline__ void fetch_scan(PreScan& f, const PArgs& a, const int
     const int lc = min(l, L - 1);
     const int64_t src = t - ((int64_t)1 << lc);
     const int64_t scl = src >= 0 ? src : 0;
-    f.vs[l] = *reinterpret_cast<const uint2*>(ring + (ring_offset(lc) + (scl & ring_mask(lc))) * d + e0);
+    f.vs[l] = ld8(ring + (ring_offset(lc) + (scl & ring_mask(lc))) * d + e0);
   }
 }
 
@@ -657,8 +681,8 @@ __device__ __forceinline__ bool run_scan_out(const PArgs& a, Smem& S, const PreS
   if (blockIdx.x == 0 && tid * 4 < d) {
     bf16_t* rw = (bf16_t*)ring + e0;
     auto st4 = [](bf16_t* p, const float (&x)[4]) {
-      *reinterpret_cast<uint2*>(p) = make_uint2((uint32_t)f32_to_bf16(x[0]) | ((uint32_t)f32_to_bf16(x[1]) << 16),
-                                                (uint32_t)f32_to_bf16(x[2]) | ((uint32_t)f32_to_bf16(x[3]) << 16));
+      st8(p, make_uint2((uint32_t)f32_to_bf16(x[0]) | ((uint32_t)f32_to_bf16(x[1]) << 16),
+                        (uint32_t)f32_to_bf16(x[2]) | ((uint32_t)f32_to_bf16(x[3]) << 16)));
     };
     st4(rw + (t & 1) * d, v0f);
 #pragma unroll
@@ -726,20 +750,20 @@ __device__ __forceinline__ void fetch_attn(PreAttn& f, const PArgs& a, const int
   constexpr int VE = 8, KCH = kHD / VE, RPI = 64 / KCH, NW = kUT / 64, VCH = 8;
   const AttnGeo g = attn_geo(a, Lt, t);
   const int pt = min(g.ut, kHD / 2 - 1);
-  f.rc = ((const bf16_t*)(intptr_t)Lt[F_COS])[t * (kHD / 2) + pt];
-  f.rsn = ((const bf16_t*)(intptr_t)Lt[F_SIN])[t * (kHD / 2) + pt];
+  f.rc = ld2((const bf16_t*)(intptr_t)Lt[F_COS] + t * (kHD / 2) + pt);
+  f.rsn = ld2((const bf16_t*)(intptr_t)Lt[F_SIN] + t * (kHD / 2) + pt);
   const int i = g.j0 + g.ut;
 #pragma unroll
   for (int c = 0; c < KCH; ++c) {
     f.krow[c] = make_uint4(0u, 0u, 0u, 0u);
-    if (i < g.jc1 && g.P <= kMaxSeg) f.krow[c] = reinterpret_cast<const uint4*>(g.Kh + (int64_t)(g.lo + i) * kHD)[c];
+    if (i < g.jc1 && g.P <= kMaxSeg) f.krow[c] = ld16(g.Kh + (int64_t)(g.lo + i) * kHD + c * 8);
   }
   const int slot = g.lane / KCH, dg = g.lane % KCH;
 #pragma unroll
   for (int q = 0; q < VCH; ++q) {
     const int iv = g.j0 + (q * NW + g.wave) * RPI + slot;
     f.vrow[q] = make_uint4(0u, 0u, 0u, 0u);
-    if (iv < g.jc1 && g.P <= kMaxSeg) f.vrow[q] = reinterpret_cast<const uint4*>(g.Vh + (int64_t)(g.lo + iv) * kHD)[dg];
+    if (iv < g.jc1 && g.P <= kMaxSeg) f.vrow[q] = ld16(g.Vh + (int64_t)(g.lo + iv) * kHD + dg * 8);
   }
 }
 
@@ -810,10 +834,10 @@ __device__ __forceinline__ bool run_attn_split(const PArgs& a, Smem& S, const Pr
     S.ks[un][2 * ut] = kr0; S.ks[un][2 * ut + 1] = kr1;
     S.vsh[un][2 * ut] = v0; S.vsh[un][2 * ut + 1] = v1;
     if (has_t) {
-      Kh[t * kHD + 2 * ut] = f32_to_bf16(kr0);
-      Kh[t * kHD + 2 * ut + 1] = f32_to_bf16(kr1);
-      Vh[t * kHD + 2 * ut] = f32_to_bf16(v0);
-      Vh[t * kHD + 2 * ut + 1] = f32_to_bf16(v1);
+      st2(Kh + t * kHD + 2 * ut, f32_to_bf16(kr0));
+      st2(Kh + t * kHD + 2 * ut + 1, f32_to_bf16(kr1));
+      st2(Vh + t * kHD + 2 * ut, f32_to_bf16(v0));
+      st2(Vh + t * kHD + 2 * ut + 1, f32_to_bf16(v1));
     }
   }
   __syncthreads();
@@ -838,7 +862,7 @@ __device__ __forceinline__ bool run_attn_split(const PArgs& a, Smem& S, const Pr
     const int i = i0 + ut;
     if (i0 > j0 && i < jc1) {
 #pragma unroll
-      for (int c = 0; c < KCH; ++c) krow[c] = reinterpret_cast<const uint4*>(Kh + (int64_t)(lo + i) * kHD)[c];
+      for (int c = 0; c < KCH; ++c) krow[c] = ld16(Kh + (int64_t)(lo + i) * kHD + c * 8);
     }
     const float s0 = score(krow);
     if (i < jc1) {
@@ -894,7 +918,7 @@ __device__ __forceinline__ bool run_attn_split(const PArgs& a, Smem& S, const Pr
 #pragma unroll
     for (int q = 0; q < VCH; ++q) {
       const int i = i0 + (q * NW + wave) * RPI + slot;
-      if (i < jc1) vrow[q] = reinterpret_cast<const uint4*>(Vh + (int64_t)(lo + i) * kHD)[dg];
+      if (i < jc1) vrow[q] = ld16(Vh + (int64_t)(lo + i) * kHD + dg * 8);
     }
 #pragma unroll
     for (int q = 0; q < VCH; ++q) accumulate(vrow[q], i0 + (q * NW + wave) * RPI + slot);
