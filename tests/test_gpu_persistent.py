@@ -92,3 +92,34 @@ def test_persistent_not_used_where_unsupported():
     dec.greedy_start(dec.prefill(torch.randint(0, 2047, (1, 8), device=DEV))[:, -1])
     dec.step_greedy()
     assert dec._pers is False
+
+
+def test_persistent_every_position_from_one_token_to_max_len():
+    """A 1-token prompt decoded to the end of the context (t = 1 .. max_len - 1): every level's first
+    source, the attention window filling and sliding (window 64 of 256), the last position; then
+    the decoder refuses a step past max_len as the graph path does."""
+    cfg = dict(MID, max_len=256, attn_window=64)
+    m = product_model(cfg, make_state_dict(cfg, 11), device=DEV, dtype=torch.bfloat16)
+    prompt = torch.randint(0, 2047, (1, 1), device=DEV, generator=torch.Generator(device=DEV).manual_seed(9))
+    print("persistent: positions 1..255", flush=True)
+    dp, dg = _pair(m, prompt)
+    _run_and_compare(dp, dg, 255)
+    assert dp.t == 256
+    with pytest.raises(ValueError, match="context exhausted"):
+        dp.step_greedy()
+
+
+def test_fast_generate_greedy_uses_one_launch_step():
+    """fast_generate's greedy branch (no eos) through the fused decoder gives the same tokens with
+    the one-launch step as with the graph of launches."""
+    from dispatcher_hybrid import decoding
+    m = product_model(MID, make_state_dict(MID, 7), device=DEV, dtype=torch.bfloat16)
+    prompt = torch.randint(0, 2047, (1, 30), device=DEV, generator=torch.Generator(device=DEV).manual_seed(4))
+    out = m.fast_generate(prompt, max_new_tokens=40, decoder="fused")
+    orig = decoding.FusedGraphedHybridDecoder.__init__.__defaults__
+    decoding.FusedGraphedHybridDecoder.__init__.__defaults__ = (None, None, False)   # persistent=False
+    try:
+        ref = m.fast_generate(prompt, max_new_tokens=40, decoder="fused")
+    finally:
+        decoding.FusedGraphedHybridDecoder.__init__.__defaults__ = orig
+    assert torch.equal(out, ref)
