@@ -660,6 +660,16 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_staged_kernel(GemvArgs a
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short mf_bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float mf_f32x4;
 
+// one staged 16-byte chunk c of a row scaled in place by the row's rsqrt and the norm weight
+__device__ __forceinline__ void norm_chunk(unsigned char* row, int c, float rs, uint4 graw) {
+  float xf[8], gw[8];
+  Vec<bf16_t>::unpack(*reinterpret_cast<const uint4*>(row + c * 16), xf);
+  Vec<bf16_t>::unpack(graw, gw);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) xf[e] = Elem<bf16_t>::round(xf[e] * rs * gw[e]);
+  *reinterpret_cast<uint4*>(row + c * 16) = Vec<bf16_t>::pack(xf);
+}
+
 template <int KSPLIT, int TPW, int KSW, bool SW>
 __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(GemvArgs a, int steps_per_wave) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -696,6 +706,16 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
       const int64_t xrow = a.x_rows ? load_uniform(a.x_rows + b) : (int64_t)b;
       xs[j] = ld16((const bf16_t*)a.x + xrow * a.x_bstride + (int64_t)(i % kc) * 8);
     }
+  }
+  // the norm weight chunks this lane applies (chunk lane + 64 i), ahead of the weights: the
+  // normalisation below then waits for them alone, not for the whole weight burst
+  constexpr int GC = 4;                                // K <= 64 * GC * 8 (larger K loads in the loop)
+  const bool g_early = a.g != nullptr && kc <= 64 * GC;
+  uint4 gv[GC];
+#pragma unroll
+  for (int i = 0; i < GC; ++i) {
+    gv[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (g_early && lane + 64 * i < kc) gv[i] = ld16((const bf16_t*)a.g + (lane + 64 * i) * 8);
   }
   const int nsteps = K / 32;
   const int s0 = wave * steps_per_wave;
@@ -742,13 +762,13 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
         for (int e = 0; e < 8; ++e) ss += xf[e] * xf[e];
       }
       const float rs = rsqrtf(wave_sum(ss) / (float)K + a.eps);
-      for (int c = lane; c < kc; c += 64) {
-        float xf[8], gw[8];
-        Vec<bf16_t>::unpack(*reinterpret_cast<const uint4*>(hs + b * rowb + c * 16), xf);
-        Vec<bf16_t>::unpack(ld16((const bf16_t*)a.g + c * 8), gw);
+      unsigned char* row = hs + b * rowb;
+      if (g_early) {                                   // uniform
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xf[e] = Elem<bf16_t>::round(xf[e] * rs * gw[e]);
-        *reinterpret_cast<uint4*>(hs + b * rowb + c * 16) = Vec<bf16_t>::pack(xf);
+        for (int i = 0; i < GC; ++i)
+          if (lane + 64 * i < kc) norm_chunk(row, lane + 64 * i, rs, gv[i]);
+      } else {
+        for (int c = lane; c < kc; c += 64) norm_chunk(row, c, rs, ld16((const bf16_t*)a.g + c * 8));
       }
     }
     __syncthreads();

@@ -24,7 +24,7 @@ def _norm(x, g, dt):
 
 
 # (B, K): K = 176 and 352 are the tiny test models' widths (not multiples of 64 elements)
-CASES = [(1, 1024), (3, 512), (16, 1024), (70, 256), (2, 176), (5, 352)]
+CASES = [(1, 1024), (3, 512), (16, 1024), (70, 256), (2, 176), (5, 352), (8, 3072)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
