@@ -286,6 +286,8 @@ DECODE_CASES = [
     (3, 70, 128, 128, 4, 16, 7),
     (16, 20, 64, 64, 2, 32, 6),
     (2, 24, 4096, 1024, 16, 64, 12),    # release shapes (first positions)
+    (8, 30, 128, 256, 4, 32, 8),        # batched gate readouts (four rows per wave)
+    (5, 24, 64, 128, 8, 16, 7),         # the same with a partial last group of rows
 ]
 
 
