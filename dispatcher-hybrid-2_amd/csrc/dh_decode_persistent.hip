@@ -678,6 +678,21 @@ __device__ __forceinline__ bool run_scan_out(const PArgs& a, Smem& S, const PreS
       hist[l][q] = v[q];
     }
   }
+  if (tid * 4 < d) {
+    *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(S.sx) + e0) =
+        make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                   (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
+  }
+  __syncthreads();
+  if (n < d) {
+    const float rv = residual(first, erow, n, xres);
+    float acc[1][1];
+    dot_rows<1, 1, CG>(S, nchunk, f.w.w, acc);
+    xres = rnd(rnd(acc[0][0]) + rv);
+    if (lane == 0) put16(a.xw + n, xres, tg.t16(ph));
+  }
+  // the ring slots of t are read by later launches only: workgroup 0 writes them after its x rows
+  // are out, so they do not queue ahead of the hand-off
   if (blockIdx.x == 0 && tid * 4 < d) {
     bf16_t* rw = (bf16_t*)ring + e0;
     auto st4 = [](bf16_t* p, const float (&x)[4]) {
@@ -690,18 +705,6 @@ __device__ __forceinline__ bool run_scan_out(const PArgs& a, Smem& S, const PreS
       if (l + 1 < L) st4(rw + (ring_offset(l + 1) + (t & ring_mask(l + 1))) * d, hist[l]);
     if (Yout) st4((bf16_t*)Yout + e0, v);
   }
-  if (tid * 4 < d) {
-    *reinterpret_cast<uint2*>(reinterpret_cast<bf16_t*>(S.sx) + e0) =
-        make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
-                   (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
-  }
-  __syncthreads();
-  if (n >= d) return true;
-  const float rv = residual(first, erow, n, xres);
-  float acc[1][1];
-  dot_rows<1, 1, CG>(S, nchunk, f.w.w, acc);
-  xres = rnd(rnd(acc[0][0]) + rv);
-  if (lane == 0) put16(a.xw + n, xres, tg.t16(ph));
   return true;
 }
 
