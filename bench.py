@@ -113,7 +113,8 @@ def time_decode(torch, model, batch, prompt, warmup, steps, sample):
         e1.record()
         sync_barrier(torch)
         dt = time.perf_counter() - t0
-        dec.check_persistent()                             # raises if a one-launch step timed out
+        if dec.check_persistent():                         # a one-launch step timed out: redone, not timed
+            raise RuntimeError("a one-launch decode step timed out inside the timed loop")
         dec.event_us_per_step = e0.elapsed_time(e1) * 1e3 / steps
         return batch * steps / dt, 1e3 * dt / steps, dec
 

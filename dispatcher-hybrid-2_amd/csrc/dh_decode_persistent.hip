@@ -1104,7 +1104,11 @@ __device__ __forceinline__ void phase_argmax(const PArgs& a, Smem& S, int64_t t,
     if (a.tok_hist && t + 1 < a.hist_len) a.tok_hist[t + 1] = r.i;
     *a.t_dev = t + 1;
   }
-  if (tid == 0) *a.epoch = *a.epoch + 1;             // every launch, also a failed one
+  // The epoch advances at the end of every launch whose pick phase runs, also one that saw an
+  // abort here; a workgroup 0 that left an earlier phase on an abort does not advance it, and the
+  // host advances it when it clears the status (the status is sticky until then, so every launch
+  // in between stops at its first wait).
+  if (tid == 0) *a.epoch = *a.epoch + 1;
 }
 
 // the first phase of layer Lt: the tree in-projection [W_in; W_gh; W_ghs] or attention's [W_q; W_k; W_v]

@@ -17,6 +17,7 @@ Attention layers keep a (B, H, Tmax, hd) K/V cache with RoPE applied at the abso
 """
 
 import math
+import warnings
 
 import torch
 import torch.nn.functional as F
@@ -447,10 +448,16 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         # where the model fits it; False keeps the graph of launches
         self.use_persistent = persistent
         self._pers = None
+        # one-launch steps between status checks (each check synchronises); 0: only check_persistent()
+        self.persistent_check_every = 64
+        self._pers_unchecked = 0
         super().__init__(model, max_len, dtype)
 
     def _prepare(self):
         super()._prepare()
+        # the one-launch step's layer table holds raw addresses of this prefill's caches: a new
+        # prefill (possibly another batch, reallocating them) derives it again
+        self._pers = None
         dev = next(self.m.parameters()).device
         cfg = self.m.config
         Bb, dt = self.inner.batch, self.dtype
@@ -551,11 +558,33 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         return self._fused_step.persistent_status(self._pers["scratch"])
 
     def check_persistent(self):
-        """Raise if a one-launch step of this decoder timed out waiting for another workgroup."""
+        """Verify the one-launch steps issued since the last check (synchronises). Returns the number
+        of steps redone.
+
+        A one-launch step assumes every workgroup of its launch is resident at once; should one not
+        be (other work on the device), a bounded wait times out, the launch ends without advancing
+        t_buf or writing a token, and every later launch on the same scratch stops at its first wait.
+        Everything a step writes is a function of its token, its position and the state before it,
+        so the steps from the device position on are redone through the graph of launches, which
+        this decoder then keeps using. The status is cleared and the tag epoch advanced, so no word
+        of the aborted launches can match a later tag."""
+        self._pers_unchecked = 0
         flag, phase = self.persistent_status()
-        if flag:
-            raise RuntimeError(f"dh_decode_persistent_step: a wait timed out in phase {phase - 1}; "
-                               "the decode state of this decoder is invalid")
+        if not flag:
+            return 0
+        scratch = self._pers["scratch"]
+        t_dev = int(self.t_buf.item())
+        scratch[8:16].zero_()                              # status words
+        scratch[0:8].view(torch.int64).add_(1)             # tag epoch
+        warnings.warn(f"dh_decode_persistent_step: a wait timed out in phase {phase % 1000 - 1} at position "
+                      f"{t_dev}; redoing {self.t - t_dev} step(s) through the graph of launches, which this "
+                      f"decoder uses from now on", RuntimeWarning)
+        self.use_persistent = False
+        self._pers = False
+        redo, self.t = self.t - t_dev, t_dev
+        for _ in range(redo):
+            self.step_greedy()
+        return redo
 
     @staticmethod
     def _eps(norm, dtype):
@@ -656,6 +685,9 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         if self.use_persistent and self._pers:
             self._persistent_step()
             self.t += 1
+            self._pers_unchecked += 1
+            if self.persistent_check_every and self._pers_unchecked >= self.persistent_check_every:
+                self.check_persistent()
             return
         if self._greedy_graph is None:
             self._greedy_capture = True

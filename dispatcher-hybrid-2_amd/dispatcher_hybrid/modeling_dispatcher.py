@@ -464,7 +464,7 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
             dec.greedy_start(logits)
             for _ in range(n - 1):
                 dec.step_greedy()
-            dec.check_persistent()                         # a one-launch step that timed out raises
+            dec.check_persistent()                         # a one-launch step that timed out is redone
             return torch.cat([ids, dec.tok_hist[:, t0:t0 + n]], dim=1)
         finished = torch.zeros(Bb, dtype=torch.bool, device=ids.device)
         out = [ids]

@@ -123,3 +123,61 @@ def test_fast_generate_greedy_uses_one_launch_step():
     finally:
         decoding.FusedGraphedHybridDecoder.__init__.__defaults__ = orig
     assert torch.equal(out, ref)
+
+
+def test_persistent_reprefill_at_other_batch_sizes():
+    """Prefilling the same decoder again at another batch size reallocates its caches: the one-launch
+    step's layer table (raw cache addresses) is derived again, so batch 2 runs the graph of launches
+    and batch 1 again the one-launch step, each equal to a decoder that never used it."""
+    from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder
+    m = product_model(MID, make_state_dict(MID, 7), device=DEV, dtype=torch.bfloat16)
+    g = torch.Generator(device=DEV).manual_seed(12)
+    p1 = torch.randint(0, 2047, (1, 20), device=DEV, generator=g)
+    p2 = torch.randint(0, 2047, (2, 24), device=DEV, generator=g)
+    dp, dg = FusedGraphedHybridDecoder(m), FusedGraphedHybridDecoder(m, persistent=False)
+    print("persistent: batch 1 -> 2 -> 1", flush=True)
+    for prompt, steps, one_launch in ((p1, 6, True), (p2, 6, False), (p1, 8, True)):
+        for dec in (dp, dg):
+            dec.greedy_start(dec.prefill(prompt)[:, -1])
+        for i in range(steps):
+            dp.step_greedy()
+            dg.step_greedy()
+            assert torch.equal(dp.logits_out, dg.logits_out), f"logits differ at step {i}, batch {prompt.shape[0]}"
+            assert torch.equal(dp.token_buf, dg.token_buf)
+        assert bool(dp._pers) == one_launch
+        for j, (a, b) in enumerate(zip(_state(dp), _state(dg))):
+            assert torch.equal(a, b), f"decode state buffer {j} differs (batch {prompt.shape[0]})"
+
+
+def test_persistent_status_set_redoes_steps_on_graph_path():
+    """Recovery after a one-launch step reports a timed-out wait, forced from the host: the status
+    word of the decoder's scratch is set before three steps, so none of them advances the device
+    position or writes a token (every workgroup still exits normally). check_persistent() then
+    redoes the three steps from the device position through the graph of launches, which the decoder
+    keeps using; tokens, logits and every state buffer equal those of a decoder that ran the graph of
+    launches throughout."""
+    m = product_model(MID, make_state_dict(MID, 7), device=DEV, dtype=torch.bfloat16)
+    prompt = torch.randint(0, 2047, (1, 30), device=DEV, generator=torch.Generator(device=DEV).manual_seed(8))
+    dp, dg = _pair(m, prompt)
+    dp.persistent_check_every = 0
+    _run_and_compare(dp, dg, 5)
+    t0 = dp.t
+    status = dp._pers["scratch"][8:16].view(torch.int32)
+    status.copy_(torch.tensor([1, 2001], dtype=torch.int32))   # abort flag; phase 0, "time"
+    print("persistent: three steps with the status word set", flush=True)
+    for _ in range(3):
+        dp.step_greedy()
+    assert dp.t == t0 + 3 and int(dp.t_buf.item()) == t0, "an aborted step advanced the device position"
+    with pytest.warns(RuntimeWarning, match="timed out"):
+        assert dp.check_persistent() == 3
+    assert dp._pers is False and not dp.use_persistent and dp.t == t0 + 3
+    for _ in range(3):
+        dg.step_greedy()
+    assert torch.equal(dp.logits_out, dg.logits_out) and torch.equal(dp.token_buf, dg.token_buf)
+    for i in range(6):
+        dp.step_greedy()
+        dg.step_greedy()
+        assert torch.equal(dp.logits_out, dg.logits_out), f"logits differ at step {i} after recovery"
+    assert torch.equal(dp.t_buf, dg.t_buf) and dp.t == dg.t and torch.equal(dp.tok_hist, dg.tok_hist)
+    for j, (a, b) in enumerate(zip(_state(dp), _state(dg))):
+        assert torch.equal(a, b), f"decode state buffer {j} differs"
