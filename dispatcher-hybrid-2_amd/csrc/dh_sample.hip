@@ -9,6 +9,8 @@
 // comparing any, keeps its best (value, index), and DPP wave reductions plus one LDS step give the
 // slice's candidate. The second launch reduces each row's candidates with the same ordering. A
 // row of a 50k vocabulary thus streams through ~25 compute units instead of one.
+#include <mutex>
+
 #include "dh_common.h"
 
 namespace {
@@ -416,6 +418,66 @@ extern "C" int dh_argmax(int dtype, const void* logits, int64_t row_stride, int 
   DH_REQUIRE((uintptr_t)workspace % 8 == 0, DH_ERR_INVALID_ARG, "%s: workspace needs 8-byte alignment", who);
   const int nslice = (V + kSlice - 1) / kSlice;
   Cand* cand = (Cand*)workspace;
+  hipStream_t s = (hipStream_t)stream;
+  dim3 g1(nslice, B);
+  if (dtype == DH_BF16)
+    argmax_slices<bf16_t><<<g1, kT1, 0, s>>>((const bf16_t*)logits, row_stride, V, cand);
+  else
+    argmax_slices<float><<<g1, kT1, 0, s>>>((const float*)logits, row_stride, V, cand);
+  argmax_final<<<B, 64, 0, s>>>(cand, nslice, out);
+  return dh_check_launch(who);
+}
+
+// ---------------------------------------------------------------------------------------------
+// dh_argmax_noalloc: dh_argmax's two launches with the per-slice candidates in a fixed array of
+// device memory that lives with the loaded code object (one copy per GPU, held until the process
+// ends), for callers that cannot allocate. Nothing in it needs clearing: the final pass reads only
+// the B * nslice candidates the first pass of the same call wrote. Calls that overlap on one GPU
+// (two streams, two host threads) share the array and race.
+// ---------------------------------------------------------------------------------------------
+#define DH_ARGMAX_NOALLOC_CANDS 8192     /* B * ceil(V / 2048) candidates at most: 64 KiB */
+static __device__ __align__(256) Cand scratch[DH_ARGMAX_NOALLOC_CANDS];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+Cand* g_scratch_ptr[kMaxDevices] = {};
+
+// The array's address on device `dev` (current): in host code `scratch` names a host-side stand-in,
+// so kernels get the address hipGetSymbolAddress reports, looked up once per device.
+int noalloc_scratch(int dev, Cand** out, const char* who) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return dh_fail(DH_ERR_LAUNCH_FAILED, "%s: hipGetSymbolAddress of the candidate scratch failed: %s", who,
+                     hipGetErrorString(e));
+    g_scratch_ptr[dev] = (Cand*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DH_OK;
+}
+}  // namespace
+
+extern "C" int dh_argmax_noalloc(int dtype, const void* logits, int64_t row_stride, int B, int V, int64_t* out,
+                                 void* stream) {
+  const char* who = "dh_argmax_noalloc";
+  DH_REQUIRE(dtype == DH_F32 || dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d", who, dtype);
+  DH_REQUIRE(B >= 1 && B <= 65535 && V >= 1 && row_stride >= V, DH_ERR_INVALID_ARG, "%s: B=%d V=%d row_stride=%lld",
+             who, B, V, (long long)row_stride);
+  DH_REQUIRE(logits && out, DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
+  const int nslice = (V + kSlice - 1) / kSlice;
+  DH_REQUIRE((int64_t)B * nslice <= DH_ARGMAX_NOALLOC_CANDS, DH_ERR_UNSUPPORTED_SHAPE,
+             "%s: B=%d rows of V=%d need %lld candidates, beyond the fixed scratch of %d (B * ceil(V / %d)); "
+             "use dh_argmax with a workspace",
+             who, B, V, (long long)B * nslice, DH_ARGMAX_NOALLOC_CANDS, kSlice);
+  int dev = 0;
+  DH_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices, DH_ERR_LAUNCH_FAILED,
+             "%s: no usable current device", who);
+  Cand* cand = nullptr;
+  const int st = noalloc_scratch(dev, &cand, who);
+  if (st != DH_OK) return st;
   hipStream_t s = (hipStream_t)stream;
   dim3 g1(nslice, B);
   if (dtype == DH_BF16)

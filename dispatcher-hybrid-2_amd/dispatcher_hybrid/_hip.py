@@ -15,7 +15,7 @@ import os
 
 import torch
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 _LIB_NAME = "libdh_mixer.so"
 
 DH_F32, DH_BF16 = 0, 1
@@ -69,6 +69,7 @@ def _load():
         "dh_decode_attention": ([i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, i64,
                                  i32, i32, i32, i32, i32, vp], i32),
         "dh_argmax": ([i32, vp, i64, i32, i32, vp, vp, i64, vp], i32),
+        "dh_argmax_noalloc": ([i32, vp, i64, i32, i32, vp, vp], i32),
         "dh_decode_attention_workspace_bytes": ([i32, i32, i32], i64),
         "dh_decode_attention_split": ([i32, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, i64, i32, i32, i32, i32, i32,
                                        vp, i64, vp], i32),

@@ -351,6 +351,23 @@ def argmax_tokens(logits, out=None):
 _ARGMAX_WS = {}           # per-device candidate buffer of argmax_tokens, grown on demand
 
 
+def argmax_tokens_noalloc(logits, out):
+    """argmax_tokens without any allocation (``dh_argmax_noalloc``), for code that cannot allocate
+    device memory, such as a step under HIP graph capture: the candidates live in the library's
+    fixed per-GPU scratch (B * ceil(V / 2048) <= 8192). `out`: caller-provided contiguous int64 of B
+    elements. Calls that overlap on one GPU (other streams or threads) race on that scratch."""
+    _hip.require_gpu(logits, "argmax_tokens_noalloc")
+    if logits.dim() != 2 or logits.stride(-1) != 1:
+        raise ValueError("argmax_tokens_noalloc: logits must be (B, V) with a unit inner stride")
+    B, V = logits.shape
+    if out.dtype != torch.long or out.numel() != B or not out.is_contiguous() or out.device != logits.device:
+        raise ValueError("argmax_tokens_noalloc: out must be a contiguous int64 tensor of B elements on the logits' device")
+    st = _hip.lib.dh_argmax_noalloc(_hip.dtype_code(logits.dtype), _hip.ptr(logits), logits.stride(0), B, V,
+                                    _hip.ptr(out), _hip.stream_handle(logits.device))
+    _hip.check(st, "dh_argmax_noalloc")
+    return out
+
+
 def sample_tokens(logits, temperature=1.0, top_k=None, seed=0, offset=None, out=None):
     """Temperature / top-k sampling on the device (``dh_sample_topk``), the do_sample branch of
     fast_generate (reference modeling_dispatcher.py:426-441): logits.float() / temperature, every

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 12
+#define DH_ABI_VERSION 13
 
 enum dh_status {
   DH_OK = 0,
@@ -294,6 +294,19 @@ int dh_decode_scan_out(int dtype, const void* V0, const float* stage, const int6
 int64_t dh_argmax_workspace_bytes(int B, int V);
 int dh_argmax(int dtype, const void* logits, int64_t row_stride, int B, int V, int64_t* out, void* workspace,
               int64_t workspace_bytes, void* stream);
+
+/*
+ * dh_argmax without a workspace argument and without any allocation: the same two launches and
+ * result as dh_argmax, the per-slice candidates held in a fixed array of device memory that the
+ * library's code object carries (64 KiB per GPU, kept until the process ends). No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). Limit: B * ceil(V / 2048) <= 8192 candidates (e.g.
+ * B <= 327 rows of a 50257-token vocabulary); larger inputs return DH_ERR_UNSUPPORTED_SHAPE.
+ * Every call on one GPU shares the array: calls that overlap on one GPU (other streams, other host
+ * threads) race; calls ordered on one stream do not. The first call on a device looks the array's
+ * address up (hipGetSymbolAddress) with that device current.
+ */
+int dh_argmax_noalloc(int dtype, const void* logits, int64_t row_stride, int B, int V, int64_t* out, void* stream);
 
 /*
  * The greedy token of each of B rows from the per-workgroup candidates of a dh_decode_gemv launch
