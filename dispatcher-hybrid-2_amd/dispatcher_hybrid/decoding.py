@@ -1,19 +1,33 @@
 """Incremental decoders: per-token cost O(log t) in the tree layers, flat in context.
 
-Same classes, constructor arguments and public behaviour as the reference
-(reference dispatcher_hybrid/decoding.py:50-488):
+The reference's classes, constructor arguments and public behaviour (reference
+dispatcher_hybrid/decoding.py:50-488):
 
-    IncrementalDecoder          exact, eager torch ops
-    GraphedHybridDecoder        the whole step captured once as a HIP graph and replayed per token
-    FusedGraphedHybridDecoder   graphed, with each tree layer's gate readouts + level recurrence as
-                                ONE gfx950 kernel (dispatcher_hybrid.fused_step.decode_mixer_step)
+    IncrementalDecoder          one position per step on eager torch ops
+    GraphedHybridDecoder        the same step captured once as a HIP graph, replayed per token
+    FusedGraphedHybridDecoder   graphed, the step on gfx950 kernels (fused_step): per tree layer the
+                                gate readouts, the level recurrence over the rings and the GEMV chain;
+                                at batch 1 in bf16, greedy steps as one launch each
 
-All rows of a batch advance in lockstep (one shared position t). Tree-layer state per layer:
+Design. A decoder keeps one state object per layer (_TreeLayerCache, _AttnCache), and builds both
+halves of decoding from the model's own modules:
+  * prefill runs the model's parallel forward over the prompt (the mixer's eager path with the wrap
+    mask, or the fused kernels), and each layer hands the state a decoder keeps -- W1s rows,
+    transmit gates, the state entering every level, rotated keys and values -- to its state object
+    through a recorder;
+  * a step is one position through every layer, every cache addressed through a DEVICE position
+    tensor (index_select / index_copy_). The eager decoder writes the position before each step;
+    the graphed decoder captures the very same step once and advances the position on the device,
+    so eager and graphed run identical arithmetic and return identical logits.
+
+All rows of a batch advance in lockstep (one shared position t). Tree-layer state (the reference's
+tensors and slot arithmetic, so the state is interchangeable with its decoders):
     B_hist  (B, Tmax, gh)     W1s.h1 of every position (the level-l source row is t - 2^l)
     rg_hist (B, Tmax, L, H)   transmit gates, stored at their source position
     V_ring  (B, S, d)         ring j (offset 2^(j+1)-2, 2^(j+1) slots) holds the state entering
                               level j for the last 2^(j+1) positions; S = 2^(L+1) - 2
-Attention layers keep a (B, H, Tmax, hd) K/V cache with RoPE applied at the absolute position.
+Attention layers keep rotated keys and values head-major, (B, H, Tmax, hd) in `keys` / `values`;
+`k` / `v` are views of them in the reference's (B, Tmax, H, hd) indexing.
 """
 
 import math
@@ -22,12 +36,11 @@ import warnings
 import torch
 import torch.nn.functional as F
 
-from .modeling_dispatcher import (AttentionBlock, active_levels, causal_window_attention,
-                                  level_gate_matmul, rope_rotate)
+from .modeling_dispatcher import AttentionBlock, active_levels, level_gate_matmul, rope_rotate
 
 
 class _TreeLayerCache:
-    """Decode state of one tree layer (layout: reference decoding.py:50-76)."""
+    """Decode state of one tree layer and the per-token step that advances it."""
 
     def __init__(self, mixer, batch, max_len, device, dtype):
         gh = mixer.gate_hidden.out_features
@@ -40,26 +53,136 @@ class _TreeLayerCache:
         self.V_ring = torch.zeros(batch, self.S, H * self.hd, device=device, dtype=dtype)
         self.offsets = torch.tensor([(2 << j) - 2 for j in range(L)], device=device)
         self.masks = torch.tensor([(2 << j) - 1 for j in range(L)], device=device)
+        self.lags = torch.tensor([1 << j for j in range(L)], device=device)
+        # position-major index of (source position, level) in rg_hist viewed as (B, Tmax * L, H)
+        self.level_ids = torch.arange(L, device=device)
+        self.readout_t = None
 
     def slot(self, j, p):
         """Ring slot of position p (int or tensor) at level j."""
         return ((2 << j) - 2) + (p & ((2 << j) - 1))
 
     def write_slab(self, j, slab):
-        """Store the level-j states of a (B, T, d) prefill slab. Only the last 2^(j+1) positions
-        can still be read, and consecutive positions occupy distinct slots."""
+        """Keep the level-j states of a (B, T, d) prompt slab: the last 2^(j+1) positions, which
+        occupy distinct slots of ring j."""
         T = slab.shape[1]
         p0 = max(0, T - (2 << j))
-        pos = torch.arange(p0, T, device=slab.device)
-        self.V_ring[:, self.slot(j, pos)] = slab[:, p0:]
+        self.V_ring[:, self.slot(j, torch.arange(p0, T, device=slab.device))] = slab[:, p0:]
+
+    def bind(self, mixer):
+        """Per-prefill derived data: the gate readouts transposed once, (L, gh, H) contiguous, so a
+        captured step does not copy them on every replay."""
+        self.readout_t = [W.transpose(1, 2).contiguous() for W, _ in mixer._gate_params()]
+
+    def advance(self, mx, h, pos):
+        """One position through the mixer at device position pos ((1,) int64): records B_hist[pos],
+        rg_hist[pos] and the ring slots of pos at every level; returns linear_out of the level-L
+        state (reference decoding.py:187-222, fused_step.py:26-88)."""
+        Bb = h.shape[0]
+        L, H, hd = self.L, self.H, self.hd
+        V0, A, B_t = mx.project(h)
+        self.B_hist.index_copy_(1, pos, B_t.unsqueeze(1))
+        src = pos - self.lags                                        # level-l source position
+        live = (src >= 0).to(h.dtype).view(1, L, 1)
+        src = src.clamp(min=0)
+        hid = F.relu(A.unsqueeze(1) + self.B_hist.index_select(1, src) * live) ** 2      # (B, L, gh)
+        pre = [level_gate_matmul(hid.unsqueeze(1), W, W_t)[:, 0] + b
+               for (W, b), W_t in zip(mx._gate_params(), self.readout_t)]               # (B, L, H)
+        admit, forget, transmit = mx.activate(*pre, live)
+        self.rg_hist.index_copy_(1, pos, transmit.unsqueeze(1))
+        T_max = self.rg_hist.shape[1]
+        r_src = self.rg_hist.view(Bb, T_max * L, H).index_select(1, src * L + self.level_ids)
+        V_src = self.V_ring.index_select(1, self.offsets + (src & self.masks)).view(Bb, L, H, hd)
+        msg = r_src.unsqueeze(-1) * V_src
+        V = V0.view(Bb, H, hd)
+        entering = []
+        for l in range(L):
+            entering.append(V)
+            V = mx.level_update(V, forget[:, l].unsqueeze(-1), admit[:, l].unsqueeze(-1), msg[:, l])
+        self.V_ring.index_copy_(1, self.offsets + (pos & self.masks),
+                                torch.stack(entering, 1).view(Bb, L, H * hd))
+        return mx.linear_out(V.reshape(Bb, H * hd))
+
+    def recorder(self, mx, T):
+        return _PromptRecorder(self, mx, T)
+
+
+class _PromptRecorder:
+    """Takes, from the mixer's parallel forward over a T-token prompt, what the decoder keeps:
+    B_hist rows, transmit gates of every level and the ring slabs (reference decoding.py:143-185).
+    Levels at or beyond n_lv = active_levels(L, T) have no source inside the prompt: their state
+    passes through unchanged, and their transmit gates are those of a masked source, sigmoid of the
+    readout of relu(A)^2."""
+
+    def __init__(self, cache, mx, T):
+        self.c, self.mx, self.T = cache, mx, T
+        self.n_lv = active_levels(cache.L, T)
+
+    def sources(self, A, B_src):
+        c, T = self.c, self.T
+        c.B_hist[:, :T] = B_src
+        if self.n_lv < c.L:
+            hid0 = F.relu(A) ** 2
+            W, b = self.mx.reset_out[self.n_lv:], self.mx.reset_out_bias[self.n_lv:]
+            pre = F.linear(hid0, W.reshape(-1, W.shape[-1])).unflatten(-1, W.shape[:2]) + b
+            c.rg_hist[:, :T, self.n_lv:] = torch.sigmoid(pre)
+
+    def transmit(self, r):                                           # (B*H, T, n_lv)
+        c, T = self.c, self.T
+        c.rg_hist[:, :T, :self.n_lv] = r.view(-1, c.H, T, self.n_lv).permute(0, 2, 3, 1)
+
+    def entering(self, l, V):                                        # (B*H, T, hd)
+        c, T = self.c, self.T
+        slab = V.view(-1, c.H, T, c.hd).transpose(1, 2).reshape(-1, T, c.H * c.hd)
+        if l < c.L:
+            c.write_slab(l, slab)
+        if l == self.n_lv:                         # levels n_lv .. L-1 pass the state through
+            for j in range(l + 1, c.L):
+                c.write_slab(j, slab)
 
 
 class _AttnCache:
+    """Rotated keys and values of one attention layer, head-major (B, H, Tmax, hd) in keys/values,
+    and the per-token step that reads the window through a validity mask over the whole cache (a
+    shape that stays fixed under graph capture; reference decoding.py:411-435)."""
+
     def __init__(self, attn, batch, max_len, device, dtype):
-        self.k = torch.zeros(batch, attn.num_heads, max_len, attn.head_dim, device=device, dtype=dtype)
-        self.v = torch.zeros_like(self.k)
+        self.keys = torch.zeros(batch, attn.num_heads, max_len, attn.head_dim, device=device, dtype=dtype)
+        self.values = torch.zeros_like(self.keys)
         # materialised RoPE tables: graph capture needs stable device tensors to index
         self.rope_cos, self.rope_sin = attn.rope_tables(max_len, device, dtype)
+        self.steps = torch.arange(max_len, device=device)
+
+    @property
+    def k(self):
+        """Keys in the reference's (B, Tmax, H, hd) indexing (a view)."""
+        return self.keys.transpose(1, 2)
+
+    @property
+    def v(self):
+        return self.values.transpose(1, 2)
+
+    def recorder(self, at, T):
+        return self
+
+    def keys_values(self, k, v):                                     # prompt: (B, H, T, hd)
+        T = k.shape[2]
+        self.keys[:, :, :T] = k
+        self.values[:, :, :T] = v
+
+    def advance(self, at, h, pos):
+        Bb, H, hd = h.shape[0], at.num_heads, at.head_dim
+        cos, sin = self.rope_cos.index_select(0, pos), self.rope_sin.index_select(0, pos)
+        q = rope_rotate(at.linear_q(h).view(Bb, H, hd), cos, sin)
+        self.keys.index_copy_(2, pos, rope_rotate(at.linear_k(h).view(Bb, H, hd), cos, sin).unsqueeze(2))
+        self.values.index_copy_(2, pos, at.linear_v(h).view(Bb, H, hd).unsqueeze(2))
+        seen = self.steps <= pos
+        if at.window > 0:
+            seen &= self.steps > pos - at.window
+        scores = torch.matmul(self.keys, q.unsqueeze(-1)).squeeze(-1) / math.sqrt(hd)     # (B, H, Tmax)
+        p = torch.softmax(scores.masked_fill(~seen, float("-inf")).float(), dim=-1).to(h.dtype)
+        y = torch.matmul(p.unsqueeze(2), self.values).squeeze(2)
+        return at.linear_out(y.reshape(Bb, H * hd))
 
 
 def _check_single_document(model, idx):
@@ -94,137 +217,56 @@ class IncrementalDecoder:
         self.caches = None
         self.batch = None
         self.t = 0
+        self.pos = torch.zeros(1, dtype=torch.long, device=self.device)
 
     def _alloc(self, batch):
-        if self.caches is not None and self.batch == batch:
-            return
-        self.batch = batch
-        self.caches = [
-            _AttnCache(blk.attn, batch, self.max_len, self.device, self.dtype)
-            if isinstance(blk, AttentionBlock) else
-            _TreeLayerCache(blk.mixer, batch, self.max_len, self.device, self.dtype)
-            for blk in self.m.blocks]
+        if self.caches is None or self.batch != batch:
+            self.batch = batch
+            self.caches = [
+                _AttnCache(blk.attn, batch, self.max_len, self.device, self.dtype)
+                if isinstance(blk, AttentionBlock) else
+                _TreeLayerCache(blk.mixer, batch, self.max_len, self.device, self.dtype)
+                for blk in self.m.blocks]
+        for blk, cache in zip(self.m.blocks, self.caches):
+            if not isinstance(blk, AttentionBlock):
+                cache.bind(blk.mixer)
 
-    # ---------- tree layer ----------
-    def _tree_prefill(self, blk, cache, x):
-        """Parallel mixer over the prompt that also fills B_hist, rg_hist and the rings
-        (reference decoding.py:143-185)."""
-        mx = blk.mixer
-        Bb, T = x.shape[0], x.shape[1]
-        L, H, hd = cache.L, cache.H, cache.hd
-        h1 = blk.norm1(x)
-        A = mx.gate_hidden(h1)
-        Bs = mx.gate_hidden_src(h1)
-        cache.B_hist[:, :T] = Bs
-        n_lv = active_levels(L, T)
-        V = mx.linear_in(h1).view(Bb, T, H, hd)
-        cache.write_slab(0, V.reshape(Bb, T, H * hd))
-        t = torch.arange(T, device=x.device)
-        wrap = torch.stack([(t >= (1 << l)) for l in range(n_lv)], dim=1).to(x.dtype).unsqueeze(-1)
-        lagged = torch.stack([torch.roll(Bs, shifts=1 << l, dims=1) for l in range(n_lv)], dim=2)
-        hidden = torch.relu(A.unsqueeze(2) + lagged * wrap) ** 2
-        pre_i, pre_f, pre_r = (level_gate_matmul(hidden, W[:n_lv]) + b[:n_lv]
-                               for W, b in mx._gate_params())
-        ig = torch.sigmoid(pre_i) * wrap
-        fg = torch.sigmoid(pre_f) * wrap + (1.0 - wrap)
-        rg = torch.sigmoid(pre_r)
-        cache.rg_hist[:, :T, :n_lv] = rg
-        if n_lv < L:
-            # levels beyond the prompt's horizon send no message yet, but later tokens read the
-            # transmit gates of these positions at those levels
-            hid0 = torch.relu(A) ** 2
-            for l in range(n_lv, L):
-                cache.rg_hist[:, :T, l] = torch.sigmoid(F.linear(hid0, mx.reset_out[l]) + mx.reset_out_bias[l])
-        for l in range(n_lv):
-            msg = torch.roll(rg[:, :, l].unsqueeze(-1) * V, shifts=1 << l, dims=1)
-            V = fg[:, :, l].unsqueeze(-1) * V + ig[:, :, l].unsqueeze(-1) * msg
-            if l + 1 < L:
-                cache.write_slab(l + 1, V.reshape(Bb, T, H * hd))
-        for j in range(n_lv + 1, L):                  # beyond the horizon the state passes through
-            cache.write_slab(j, V.reshape(Bb, T, H * hd))
-        x = x + mx.linear_out(V.reshape(Bb, T, H * hd))
+    def _prefill_layer(self, blk, cache, x, mask):
+        """One layer of the parallel forward over the prompt, its state recorded into `cache`."""
+        h = blk.norm1(x)
+        T = x.shape[1]
+        if isinstance(blk, AttentionBlock):
+            y = blk.attn._forward_eager(h, record=cache.recorder(blk.attn, T))
+        else:
+            mx = blk.mixer
+            y = mx._forward_eager(h, mask, active_levels(mx.levels, T), record=cache.recorder(mx, T))
+        x = x + y
         return x + blk.ffn(blk.norm2(x))
 
-    def _tree_step(self, blk, cache, x, t):
-        """One position through a tree layer (reference decoding.py:187-222)."""
-        mx = blk.mixer
-        Bb = x.shape[0]
-        L, H, hd = cache.L, cache.H, cache.hd
-        h1 = blk.norm1(x)
-        A = mx.gate_hidden(h1)
-        cache.B_hist[:, t] = mx.gate_hidden_src(h1)
-        V = mx.linear_in(h1).view(Bb, H, hd)
-        cache.V_ring[:, cache.slot(0, t)] = V.reshape(Bb, -1)
-        lev = torch.arange(L, device=x.device)
-        src = t - torch.pow(2, lev)
-        ok = src >= 0
-        src_c = src.clamp(min=0)
-        okf = ok.view(1, L, 1)
-        hid = torch.relu(A.unsqueeze(1) + cache.B_hist[:, src_c] * okf) ** 2        # (B, L, gh)
-        gates = [level_gate_matmul(hid.unsqueeze(1), W)[:, 0] + b for W, b in mx._gate_params()]
-        i_ = torch.sigmoid(gates[0]) * okf
-        f_ = torch.sigmoid(gates[1])
-        f_ = f_ * okf + (~okf).to(f_.dtype)                                         # masked: f = 1
-        r_ = torch.sigmoid(gates[2])
-        cache.rg_hist[:, t] = r_
-        rg_src = cache.rg_hist[:, src_c, lev]                                       # (B, L, H)
-        V_src = cache.V_ring[:, cache.offsets + (src_c & cache.masks)].view(Bb, L, H, hd)
-        msg = rg_src.unsqueeze(-1) * V_src
-        for l in range(L):
-            V = f_[:, l].unsqueeze(-1) * V + i_[:, l].unsqueeze(-1) * msg[:, l]
-            if l + 1 < L:
-                cache.V_ring[:, cache.slot(l + 1, t)] = V.reshape(Bb, -1)
-        x = x + mx.linear_out(V.reshape(Bb, -1))
-        return x + blk.ffn(blk.norm2(x))
+    def _advance(self, tokens, pos):
+        """Logits (B, vocab) of `tokens` at device position pos, every layer's state advanced."""
+        x = self.m.embedding(tokens).to(self.dtype)
+        for blk, cache in zip(self.m.blocks, self.caches):
+            layer = blk.attn if isinstance(blk, AttentionBlock) else blk.mixer
+            x = x + cache.advance(layer, blk.norm1(x), pos)
+            x = x + blk.ffn(blk.norm2(x))
+        return self.m.lm_head(self.m.norm_out(x))
 
-    # ---------- attention layer ----------
-    def _attn_prefill(self, blk, cache, x):
-        at = blk.attn
-        Bb, T = x.shape[0], x.shape[1]
-        h1 = blk.norm1(x)
-        shape = (Bb, T, at.num_heads, at.head_dim)
-        q = at.apply_rope(at.linear_q(h1).view(shape).transpose(1, 2), T)
-        k = at.apply_rope(at.linear_k(h1).view(shape).transpose(1, 2), T)
-        v = at.linear_v(h1).view(shape).transpose(1, 2)
-        cache.k[:, :, :T] = k
-        cache.v[:, :, :T] = v
-        window = at.window if 0 < at.window < T else 0
-        y = causal_window_attention(q, k, v, window)
-        x = x + at.linear_out(y.transpose(1, 2).reshape(Bb, T, at.embed_dim))
-        return x + blk.ffn(blk.norm2(x))
-
-    def _attn_step(self, blk, cache, x, t):
-        at = blk.attn
-        Bb = x.shape[0]
-        h1 = blk.norm1(x)
-        cos, sin = cache.rope_cos[t], cache.rope_sin[t]
-        q = rope_rotate(at.linear_q(h1).view(Bb, at.num_heads, at.head_dim), cos, sin)
-        cache.k[:, :, t] = rope_rotate(at.linear_k(h1).view(Bb, at.num_heads, at.head_dim), cos, sin)
-        cache.v[:, :, t] = at.linear_v(h1).view(Bb, at.num_heads, at.head_dim)
-        lo = max(0, t + 1 - at.window) if at.window > 0 else 0
-        k = cache.k[:, :, lo:t + 1]
-        v = cache.v[:, :, lo:t + 1]
-        scores = torch.matmul(k, q.unsqueeze(-1)).squeeze(-1) / math.sqrt(at.head_dim)
-        att = torch.softmax(scores, dim=-1)                      # model-dtype softmax, as eager
-        y = torch.matmul(att.unsqueeze(2), v).squeeze(2).reshape(Bb, -1)
-        x = x + at.linear_out(y)
-        return x + blk.ffn(blk.norm2(x))
-
-    # ---------- public ----------
     @torch.no_grad()
     def prefill(self, idx):
         """idx: (T,) or (B, T) token ids. Returns (T, vocab) or (B, T, vocab) logits."""
         self._squeeze = idx.dim() == 1
         ids = idx.view(1, -1) if self._squeeze else idx
         _check_single_document(self.m, ids)
-        if ids.shape[1] > self.max_len:
-            raise ValueError(f"prompt of {ids.shape[1]} exceeds max_len {self.max_len}")
+        T = ids.shape[1]
+        if T > self.max_len:
+            raise ValueError(f"prompt of {T} exceeds max_len {self.max_len}")
         self._alloc(ids.shape[0])
+        mask = self.m.level_mask(T, ids.device, self.dtype)           # the wrap mask only
         x = self.m.embedding(ids).to(self.dtype)
         for blk, cache in zip(self.m.blocks, self.caches):
-            x = (self._attn_prefill(blk, cache, x) if isinstance(blk, AttentionBlock)
-                 else self._tree_prefill(blk, cache, x))
-        self.t = ids.shape[1]
+            x = self._prefill_layer(blk, cache, x, mask)
+        self.t = T
         out = self.m.lm_head(self.m.norm_out(x))
         return out[0] if self._squeeze else out
 
@@ -233,100 +275,57 @@ class IncrementalDecoder:
         """tokens: scalar, (1,) or (B,). Returns (vocab,) or (B, vocab) logits."""
         if self.t >= self.max_len:
             raise ValueError(f"context exhausted at max_len {self.max_len}")
-        t = self.t
         toks = tokens.view(-1)
         if toks.shape[0] != self.batch and not (self.batch == 1 and toks.shape[0] == 1):
             raise ValueError(f"got {toks.shape[0]} tokens for batch {self.batch}")
-        x = self.m.embedding(toks).to(self.dtype)
-        for blk, cache in zip(self.m.blocks, self.caches):
-            x = (self._attn_step(blk, cache, x, t) if isinstance(blk, AttentionBlock)
-                 else self._tree_step(blk, cache, x, t))
-        self.t = t + 1
-        out = self.m.lm_head(self.m.norm_out(x))
+        self.pos.fill_(self.t)
+        out = self._advance(toks, self.pos)
+        self.t += 1
         return out[0] if self._squeeze else out
-
-
-# ==============================================================================================
-# Graph-replayed decoders. The per-token work is small and launch-bound, so the whole step is
-# captured once (after an eager prefill) and replayed per token. The position lives on the device
-# (t_buf) so one graph serves every position; attention reads the full padded cache under a
-# validity mask so its shapes are capture-stable.
-# ==============================================================================================
 
 
 class _FusedPrefillDecoder(IncrementalDecoder):
     """The fused decoder's prefill: each tree layer runs the parallel gfx950 kernels -- activated
     gates of all L levels in one launch, the level scan over the active levels in a second, which
-    also stores the ring slabs -- instead of the eager roll/level loop, and fills the same state
-    (B_hist, rg_hist for every level, V_ring; reference decoding.py:143-185). Attention layers (bf16,
-    head width 32/64/128) run the banded-attention kernel, which also writes rope(k) and v into the
-    caches; the steps stay those of IncrementalDecoder."""
+    also stores the ring slabs -- and fills the same state (B_hist, rg_hist for every level,
+    V_ring; reference decoding.py:143-185). Attention layers (bf16, head width 32/64/128) run the
+    banded-attention kernel, which also writes the rotated keys and the values into the caches."""
 
-    def _attn_prefill(self, blk, cache, x):
+    def _prefill_layer(self, blk, cache, x, mask):
         from . import fused_attention as fa
-        at = blk.attn
-        if not (fa.supported(x.dtype, at.head_dim) and cache.k.dtype == x.dtype):
-            return super()._attn_prefill(blk, cache, x)
-        T = x.shape[1]
-        h1 = blk.norm1(x)
-        window = at.window if 0 < at.window < T else 0
-        cos, sin = at.rope_tables(T, x.device, x.dtype)
-        y = fa.window_attention(at.linear_q(h1), at.linear_k(h1), at.linear_v(h1), cos, sin, at.num_heads,
-                                window, k_cache=cache.k, v_cache=cache.v)
-        x = x + at.linear_out(y)
-        return x + blk.ffn(blk.norm2(x))
-
-    def _tree_prefill(self, blk, cache, x):
         from .fused_gates import input_projections, prefill_gate_scan
-        mx = blk.mixer
         T = x.shape[1]
-        dt = cache.V_ring.dtype
-        h1 = blk.norm1(x)
-        V0, A, Bs = input_projections(h1, mx)
-        cache.B_hist[:, :T] = Bs
-        (Wi, bi), (Wf, bf), (Wr, br) = mx._gate_params()
-        V = prefill_gate_scan(A.to(dt), Bs.to(dt), Wi, Wf, Wr, bi, bf, br, V0.to(dt), cache.H,
-                              cache.rg_hist, cache.V_ring)
-        x = x + mx.linear_out(V.to(x.dtype))
+        h = blk.norm1(x)
+        if isinstance(blk, AttentionBlock):
+            at = blk.attn
+            if not (fa.supported(x.dtype, at.head_dim) and cache.keys.dtype == x.dtype):
+                return super()._prefill_layer(blk, cache, x, mask)
+            cos, sin = at.rope_tables(T, x.device, x.dtype)
+            y = fa.window_attention(at.linear_q(h), at.linear_k(h), at.linear_v(h), cos, sin, at.num_heads,
+                                    at.band(T), k_cache=cache.keys, v_cache=cache.values)
+            y = at.linear_out(y)
+        else:
+            mx = blk.mixer
+            dt = cache.V_ring.dtype
+            V0, A, Bs = input_projections(h, mx)
+            cache.B_hist[:, :T] = Bs
+            (Wi, bi), (Wf, bf), (Wr, br) = mx._gate_params()
+            V = prefill_gate_scan(A.to(dt), Bs.to(dt), Wi, Wf, Wr, bi, bf, br, V0.to(dt), cache.H,
+                                  cache.rg_hist, cache.V_ring)
+            y = mx.linear_out(V.to(x.dtype))
+        x = x + y
         return x + blk.ffn(blk.norm2(x))
 
 
-class _GraphedBase:
-    def _capture(self, step_fn, attr="graph"):
-        g = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        tok = self.token_buf.clone()
-        with torch.cuda.stream(side):
-            for _ in range(3):                      # warm-ups: allocator pools, library handles
-                step_fn()
-                self.t_buf.fill_(self.t)            # undo the warm-up's position advance
-                self.token_buf.copy_(tok)           # and a fused greedy pick's token
-        torch.cuda.current_stream().wait_stream(side)
-        with torch.cuda.graph(g):
-            step_fn()
-        setattr(self, attr, g)
-
-    @torch.no_grad()
-    def step(self, tokens):
-        if self.t >= self.max_len:
-            raise ValueError(f"context exhausted at max_len {self.max_len}")
-        self.token_buf.copy_(tokens.view(-1))
-        self.graph.replay()
-        self.t += 1
-        # the graph overwrites logits_out on the next replay: hand out a copy
-        out = self.logits_out.clone()
-        return out[0] if self._squeeze else out
-
-
-class GraphedHybridDecoder(_GraphedBase):
-    """Eager prefill, then one HIP-graph replay per generated token."""
+class GraphedHybridDecoder:
+    """The eager decoder's step recorded once into a HIP graph after the prefill and replayed per
+    token; the position lives on the device (t_buf) and the replay advances it."""
 
     _prefill_cls = IncrementalDecoder
 
     def __init__(self, model, max_len=None, dtype=None):
         if not torch.cuda.is_available():
-            raise RuntimeError("GraphedHybridDecoder requires a GPU")
+            raise RuntimeError(f"{type(self).__name__} requires a GPU")
         self.inner = self._prefill_cls(model, max_len, dtype=dtype)
         self.m = model
         self.max_len = self.inner.max_len
@@ -338,86 +337,51 @@ class GraphedHybridDecoder(_GraphedBase):
         out = self.inner.prefill(idx)
         self._squeeze = self.inner._squeeze
         self.t = self.inner.t
-        dev = next(self.m.parameters()).device
+        dev = self.inner.device
         Bb = self.inner.batch
         self.token_buf = torch.zeros(Bb, dtype=torch.long, device=dev)
         self.t_buf = torch.full((1,), self.t, dtype=torch.long, device=dev)
         self.logits_out = torch.zeros(Bb, self.m.lm_head.out_features, device=dev, dtype=self.dtype)
-        self.arangeT = torch.arange(self.max_len, device=dev)
         self._prepare()
-        self._capture(self._step_all)
+        self.graph = self._capture(self._step_all)
         return out
 
     def _prepare(self):
-        # level-major transposed gate weights (L, gh, H) for the batched readout bmm
-        self._gate_wt = {}
-        for i, blk in enumerate(self.m.blocks):
-            if hasattr(blk, "mixer"):
-                self._gate_wt[i] = [W.transpose(1, 2).contiguous() for W, _ in blk.mixer._gate_params()]
-
-    def _tree_step_g(self, i, blk, cache, x):
-        mx = blk.mixer
-        Bb = x.shape[0]
-        L, H, hd = cache.L, cache.H, cache.hd
-        dev = x.device
-        h1 = blk.norm1(x)
-        A = mx.gate_hidden(h1)
-        cache.B_hist.index_copy_(1, self.t_buf, mx.gate_hidden_src(h1).unsqueeze(1))
-        V = mx.linear_in(h1).view(Bb, H, hd)
-        lev = torch.arange(L, device=dev)
-        src = self.t_buf - torch.pow(2, lev)
-        ok = src >= 0
-        src_c = src.clamp(min=0)
-        okf = ok.view(1, L, 1)
-        hid = torch.relu(A.unsqueeze(1) + cache.B_hist.index_select(1, src_c) * okf) ** 2  # (B, L, gh)
-        hid_l = hid.transpose(0, 1).contiguous()                                          # (L, B, gh)
-        (_, bi), (_, bf), (_, br) = mx._gate_params()
-        wi, wf, wr = self._gate_wt[i]
-        i_ = torch.sigmoid(torch.bmm(hid_l, wi).transpose(0, 1) + bi) * okf
-        f_ = torch.sigmoid(torch.bmm(hid_l, wf).transpose(0, 1) + bf)
-        f_ = f_ * okf + (~okf).to(f_.dtype)
-        r_ = torch.sigmoid(torch.bmm(hid_l, wr).transpose(0, 1) + br)
-        cache.rg_hist.index_copy_(1, self.t_buf, r_.unsqueeze(1))
-        rg_src = cache.rg_hist.index_select(1, src_c)[:, lev, lev]
-        V_src = cache.V_ring.index_select(1, cache.offsets + (src_c & cache.masks)).view(Bb, L, H, hd)
-        msg = rg_src.unsqueeze(-1) * V_src
-        levs = [V.reshape(Bb, -1)]
-        for l in range(L):                          # unrolled at capture time
-            V = f_[:, l].unsqueeze(-1) * V + i_[:, l].unsqueeze(-1) * msg[:, l]
-            if l + 1 < L:
-                levs.append(V.reshape(Bb, -1))
-        slots_w = cache.offsets + (self.t_buf & cache.masks)
-        cache.V_ring.index_copy_(1, slots_w, torch.stack(levs, dim=1))
-        x = x + mx.linear_out(V.reshape(Bb, -1))
-        return x + blk.ffn(blk.norm2(x))
-
-    def _attn_step_g(self, blk, cache, x):
-        at = blk.attn
-        Bb = x.shape[0]
-        h1 = blk.norm1(x)
-        cos = cache.rope_cos.index_select(0, self.t_buf)[0]
-        sin = cache.rope_sin.index_select(0, self.t_buf)[0]
-        q = rope_rotate(at.linear_q(h1).view(Bb, at.num_heads, at.head_dim), cos, sin)
-        k_new = rope_rotate(at.linear_k(h1).view(Bb, at.num_heads, at.head_dim), cos, sin)
-        cache.k.index_copy_(2, self.t_buf, k_new.unsqueeze(2))
-        cache.v.index_copy_(2, self.t_buf, at.linear_v(h1).view(Bb, at.num_heads, at.head_dim).unsqueeze(2))
-        valid = self.arangeT <= self.t_buf
-        if at.window > 0:
-            valid = valid & (self.arangeT > self.t_buf - at.window)
-        scores = torch.matmul(cache.k, q.unsqueeze(-1)).squeeze(-1) / math.sqrt(at.head_dim)  # (B, H, Tmax)
-        scores = scores.masked_fill(~valid.view(1, 1, -1), float("-inf"))
-        att = torch.softmax(scores.float(), dim=-1).to(x.dtype)
-        y = torch.matmul(att.unsqueeze(2), cache.v).squeeze(2).reshape(Bb, -1)
-        x = x + at.linear_out(y)
-        return x + blk.ffn(blk.norm2(x))
+        """Buffers of the captured step (subclasses); runs after each prefill, before capture."""
 
     def _step_all(self):
-        x = self.m.embedding(self.token_buf).to(self.dtype)
-        for i, (blk, cache) in enumerate(zip(self.m.blocks, self.inner.caches)):
-            x = (self._attn_step_g(blk, cache, x) if isinstance(blk, AttentionBlock)
-                 else self._tree_step_g(i, blk, cache, x))
-        self.logits_out.copy_(self.m.lm_head(self.m.norm_out(x)))
+        """The captured step: logits of token_buf at t_buf, then t_buf + 1."""
+        self.logits_out.copy_(self.inner._advance(self.token_buf, self.t_buf))
         self.t_buf.add_(1)
+
+    def _capture(self, fn):
+        """Record fn() into a new HIP graph and return it. fn first runs twice on a side stream so
+        allocator pools and library workspaces exist before capture; each warm-up's device position
+        advance and any token it wrote are undone afterwards."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        token0 = self.token_buf.clone()
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                fn()
+                self.t_buf.fill_(self.t)
+                self.token_buf.copy_(token0)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        return graph
+
+    @torch.no_grad()
+    def step(self, tokens):
+        if self.t >= self.max_len:
+            raise ValueError(f"context exhausted at max_len {self.max_len}")
+        self.token_buf.copy_(tokens.view(-1))
+        self.graph.replay()
+        self.t += 1
+        # the next replay overwrites logits_out: return a copy
+        out = self.logits_out.clone()
+        return out[0] if self._squeeze else out
 
 
 class FusedGraphedHybridDecoder(GraphedHybridDecoder):
@@ -513,7 +477,7 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
                 kinds.append(1)
                 w[0] = 1
                 w[2], w[3], w[4], w[5] = at.linear_q.weight, at.linear_k.weight, at.linear_v.weight, at.linear_out.weight
-                w[6], w[7], w[8], w[9] = cache.k, cache.v, cache.rope_cos, cache.rope_sin
+                w[6], w[7], w[8], w[9] = cache.keys, cache.values, cache.rope_cos, cache.rope_sin
                 w[10] = int(at.window)
             else:
                 mx = blk.mixer
@@ -638,7 +602,7 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
                               (at.linear_v.weight, self.v_buf, d, 0)], self.t_buf,
                        norm_weight=blk.norm1.weight, eps=self._eps(blk.norm1, self.dtype), x_rows=rows)
         fs.decode_attention(self.q_buf, self.k_buf, self.v_buf, cache.rope_cos, cache.rope_sin,
-                            cache.k, cache.v, self.t_buf, self.y_buf, at.window, workspace=self.attn_ws)
+                            cache.keys, cache.values, self.t_buf, self.y_buf, at.window, workspace=self.attn_ws)
         fs.decode_gemv(self.y_buf, [(at.linear_out.weight, self.x_buf, d, 0)], self.t_buf,
                        resid=x_in, resid_rows=rows)
         self._ffn_g(blk)
@@ -692,7 +656,7 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         if self._greedy_graph is None:
             self._greedy_capture = True
             try:
-                self._capture(self._step_all, attr="_greedy_graph")
+                self._greedy_graph = self._capture(self._step_all)
             finally:
                 self._greedy_capture = False
         self._greedy_graph.replay()

@@ -37,14 +37,15 @@ def active_levels(levels, length):
     return min(levels, max(int(length), 1).bit_length())
 
 
-def level_gate_matmul(hidden, W):
+def level_gate_matmul(hidden, W, W_t=None):
     """pre[b,t,l,h] = sum_g hidden[b,t,l,g] * W[l,h,g] for hidden (b,t,n,g), W (n,h,g).
 
     Batched over levels with both bmm operands contiguous (a transposed right operand to a bf16
-    bmm is avoided on purpose)."""
+    bmm is avoided on purpose). W_t: W already transposed to a contiguous (n, g, h), for callers
+    that apply the same readout many times."""
     b, t, n, g = hidden.shape
     lhs = hidden.permute(2, 0, 1, 3).reshape(n, b * t, g)
-    rhs = W.transpose(1, 2).contiguous()
+    rhs = W.transpose(1, 2).contiguous() if W_t is None else W_t
     return torch.bmm(lhs, rhs).view(n, b, t, -1).permute(1, 2, 0, 3)
 
 
@@ -77,6 +78,26 @@ class DispatcherMixer(nn.Module):
         return ((self.gate_out, self.gate_out_bias), (self.forget_out, self.forget_out_bias),
                 (self.reset_out, self.reset_out_bias))
 
+    def project(self, h):
+        """The three input projections of a normalised input h (..., d): V0 = W_in.h (the state
+        entering level 0), A = W1x.h (destination half of the gate hidden), B = W1s.h (source half,
+        read again 2^l positions later)."""
+        return self.linear_in(h), self.gate_hidden(h), self.gate_hidden_src(h)
+
+    @staticmethod
+    def activate(pre_i, pre_f, pre_r, m):
+        """Gate heads from pre-activations under the edge mask m (1: level live, 0: no source):
+        admit = sigmoid(pre_i) m, forget = sigmoid(pre_f) m + 1 - m (a dead level keeps its state),
+        transmit = sigmoid(pre_r), unmasked: it is read at the source, where a dead destination
+        already has admit = 0 (reference modeling_dispatcher.py:111-114)."""
+        return (torch.sigmoid(pre_i) * m, torch.sigmoid(pre_f) * m + (1.0 - m), torch.sigmoid(pre_r))
+
+    @staticmethod
+    def level_update(V, forget, admit, msg):
+        """One level of the recurrence: V <- forget V + admit msg, msg = transmit(src) V(src)
+        (reference modeling_dispatcher.py:116-121)."""
+        return forget * V + admit * msg
+
     def forward(self, x, mask):
         """x (B, T, d); mask (T, L) level mask or (B, T, L) level x doc-reset mask."""
         n_lv = active_levels(self.levels, x.shape[1])
@@ -96,36 +117,41 @@ class DispatcherMixer(nn.Module):
             m_heads = lm
         return m_src, m_heads
 
-    def _scan_eager(self, V, pre_i, pre_f, pre_r, m_heads, Bb, T, n_lv):
-        """Sigmoid heads, masks and the level loop on (B*H, T, hd) V (reference :86-88, :111-121)."""
+    def _scan_eager(self, V, pre_i, pre_f, pre_r, m_heads, Bb, T, n_lv, record=None):
+        """Sigmoid heads, masks and the level loop on (B*H, T, hd) V (reference :86-88, :111-121).
+        record (optional): told the transmit gates (B*H, T, n_lv) and the state entering every level
+        (record.transmit, record.entering) -- what an incremental decoder keeps of a prompt."""
         H = self.num_heads
 
         def per_head(pre):
-            return torch.sigmoid(pre).permute(0, 3, 1, 2).reshape(Bb * H, T, n_lv).to(V.dtype)
+            return pre.permute(0, 3, 1, 2).reshape(Bb * H, T, n_lv)
 
-        admit = per_head(pre_i) * m_heads
-        forget = per_head(pre_f) * m_heads + (1.0 - m_heads)   # a masked level keeps its state
-        transmit = per_head(pre_r)
+        admit, forget, transmit = (g.to(V.dtype) for g in self.activate(
+            per_head(pre_i), per_head(pre_f), per_head(pre_r), m_heads))
+        if record is not None:
+            record.transmit(transmit)
+            record.entering(0, V)
         for l, shift in enumerate(self.shifts[:n_lv]):
-            if shift > T:
-                break
             msg = torch.roll(transmit[..., l:l + 1] * V, shifts=shift, dims=1)
-            V = forget[..., l:l + 1] * V + admit[..., l:l + 1] * msg
+            V = self.level_update(V, forget[..., l:l + 1], admit[..., l:l + 1], msg)
+            if record is not None:
+                record.entering(l + 1, V)
         return V
 
-    def _forward_eager(self, x, mask, n_lv):
+    def _forward_eager(self, x, mask, n_lv, record=None):
         Bb, T = x.shape[0], x.shape[1]
         H, hd = self.num_heads, self.head_dim
+        V0, A, Bs = self.project(x)
+        if record is not None:
+            record.sources(A, Bs)
         # heads go to the batch axis through a transpose (a plain reshape would tile the sequence)
-        V = self.linear_in(x).view(Bb, T, H, hd).transpose(1, 2).reshape(Bb * H, T, hd)
-        A = self.gate_hidden(x)
-        Bs = self.gate_hidden_src(x)
+        V = V0.view(Bb, T, H, hd).transpose(1, 2).reshape(Bb * H, T, hd)
         m_src, m_heads = self._masks(mask, Bb, T, n_lv)
         lagged = torch.stack([torch.roll(Bs, shifts=s, dims=1) for s in self.shifts[:n_lv]], dim=2)
         hidden = F.relu(A.unsqueeze(2) + lagged * m_src) ** 2            # (B, T, n, gh)
         pre_i, pre_f, pre_r = (level_gate_matmul(hidden, W[:n_lv]) + b[:n_lv]
                                for W, b in self._gate_params())
-        V = self._scan_eager(V, pre_i, pre_f, pre_r, m_heads, Bb, T, n_lv)
+        V = self._scan_eager(V, pre_i, pre_f, pre_r, m_heads, Bb, T, n_lv, record)
         V = V.view(Bb, H, T, hd).transpose(1, 2).reshape(Bb, T, self.embed_dim)
         return self.linear_out(V)
 
@@ -224,21 +250,32 @@ class WindowAttention(nn.Module):
         return rope_rotate(x, cos, sin)
 
     def forward(self, x):
-        Bb, T = x.shape[0], x.shape[1]
-        window = self.window if 0 < self.window < T else 0
+        T = x.shape[1]
         if self.use_fused and not torch.is_grad_enabled() and x.is_cuda:
             from . import fused_attention as fa
             if fa.supported(x.dtype, self.head_dim):
                 # RoPE, banded scores, softmax and the value average in one launch, (B, T, d) in/out
                 cos, sin = self.rope_tables(T, x.device, x.dtype)
                 y = fa.window_attention(self.linear_q(x), self.linear_k(x), self.linear_v(x), cos, sin,
-                                        self.num_heads, window)
+                                        self.num_heads, self.band(T))
                 return self.linear_out(y)
+        return self._forward_eager(x)
+
+    def band(self, T):
+        """The window a length-T sequence sees; 0 when it covers the whole sequence."""
+        return self.window if 0 < self.window < T else 0
+
+    def _forward_eager(self, x, record=None):
+        """record (optional): told the rotated keys and the values, (B, H, T, hd) -- what an
+        incremental decoder keeps of a prompt."""
+        Bb, T = x.shape[0], x.shape[1]
         shape = (Bb, T, self.num_heads, self.head_dim)
         q = self.apply_rope(self.linear_q(x).view(shape).transpose(1, 2), T)
         k = self.apply_rope(self.linear_k(x).view(shape).transpose(1, 2), T)
         v = self.linear_v(x).view(shape).transpose(1, 2)
-        y = causal_window_attention(q, k, v, window)
+        if record is not None:
+            record.keys_values(k, v)
+        y = causal_window_attention(q, k, v, self.band(T))
         return self.linear_out(y.transpose(1, 2).reshape(Bb, T, self.embed_dim))
 
 
