@@ -19,7 +19,11 @@ out-projection + residual, RMSNorm + SwiGLU, down-projection + residual). A step
                     its time): algorithmic bytes / HIP-event-timed launch duration
   mixer_step        the decoder's mixer step (dh_decode_gates + dh_decode_scan) per tree layer
   step_roofline     whole decode step: bf16 weight bytes per token x tok/s vs 8 TB/s
-  cpu_baseline      the oracle's eager torch decoder (reference algorithm) on the host CPU, fp32
+  parity_bf16       the north star's bf16 quantities (logit max-abs, greedy-argmax agreement) of the
+                    C2 fused-gates forward and the C3 one-launch step against the eager bf16 and fp32 paths
+  c1_mixer_gpu_*    C1: one fp32 mixer layer (d 512, 8 levels, T 256) through the fused path
+  cpu_baseline      the oracle's eager torch path (reference algorithm) on the host CPU, fp32: C3 decode
+                    (value), C2 prefill and the C1 mixer layer
 All inputs are synthetic (uniform token ids) and the weights are a random init of the released
 architecture. Rank 0 prints one JSON line.
 """
@@ -173,16 +177,22 @@ def time_forward(torch, model, ids, fused, reps=3):
 
 
 def time_mixer(torch, mixer, x, mask, fused, reps=5):
+    """Milliseconds per mixer layer, and the layer's peak device memory above what was allocated
+    before it (its activations and temporaries, bytes)."""
     mixer.use_fused_gates = fused
     with torch.no_grad():
         mixer(x, mask)
         torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
         t0 = time.perf_counter()
         for _ in range(reps):
             mixer(x, mask)
         torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / reps * 1e3
+        peak = torch.cuda.max_memory_allocated() - base
     mixer.use_fused_gates = False
-    return (time.perf_counter() - t0) / reps * 1e3
+    return dt, peak
 
 
 def _graph_time(torch, launch, n, reps):
@@ -365,11 +375,30 @@ def copy_probe(torch, dev, mib=256):
     del a, b
 
 
+def _cpu_threads():
+    """Threads for the CPU legs: the process's affinity set, capped at the OMP_NUM_THREADS share the
+    host grants one GPU's job (16 on the GPU boxes here)."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS")
+    return min(n, int(cap)) if cap and cap.isdigit() and int(cap) > 0 else n
+
+
+def _cpu_model_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
 def cpu_baseline(torch, model, prompt, steps):
-    """The oracle's eager decoder (the reference's eager torch path) in fp32 on the host cores."""
+    """The oracle's eager torch path (the reference's eager algorithm) in fp32 on the host cores:
+    C3 decode (the reported baseline), plus the C1 mixer layer and the C2 prefill rows."""
     sys.path.insert(0, ROOT)
     from oracle import torch_eager
-    n = min(16, len(os.sched_getaffinity(0)))
+    n = _cpu_threads()
     torch.set_num_threads(n)
     sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
     if "lm_head.weight" not in sd:
@@ -384,18 +413,138 @@ def cpu_baseline(torch, model, prompt, steps):
     for _ in range(steps):
         logits = dec.step(logits.argmax(-1))
     dt = time.perf_counter() - t0
-    model_name = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model_name = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    del dec
+    # C2: the 292M forward over 1024 tokens (one warm-up, one timed run)
+    ids2 = torch.randint(0, 50257, (1, 1024), generator=torch.Generator().manual_seed(2))
+    with torch.no_grad():
+        torch_eager.forward(sd, spec, ids2)
+        t0 = time.perf_counter()
+        torch_eager.forward(sd, spec, ids2)
+        c2 = time.perf_counter() - t0
+    del sd
+    c1 = c1_cpu(torch, torch_eager)
     return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": n, "kind": "port",
             "sample": f"fp32 eager decode (oracle/torch_eager.EagerDecoder, reference algorithm), "
                       f"batch 1, {steps} timed steps after a {prompt}-token prefill (per-token cost "
-                      f"is flat in context past the tree's O(log t) reads); host CPU: {model_name}"}
+                      f"is flat in context past the tree's O(log t) reads); {n} threads of host CPU: "
+                      f"{_cpu_model_name()}",
+            "c2_prefill_tok_s": round(1024 / c2, 1),
+            "c2_sample": "fp32 eager forward of the 292M model over 1024 tokens (oracle/torch_eager.forward), "
+                         "one timed run after a warm-up",
+            "c1_mixer_ms": round(c1, 3),
+            "c1_sample": "one mixer layer, d 512, 8 heads, 8 levels, T 256, fp32, x ~ N(0,1), weights "
+                         "N(0, 0.02), biases 0 (oracle/torch_eager.mixer): median of 7 runs"}
+
+
+def _c1_layer(torch):
+    """The C1 single mixer layer (d 512, 8 heads of 64, 8 levels, T 256): state dict, input, mask."""
+    g = torch.Generator().manual_seed(1)
+    d, H, L, T = 512, 8, 8, 256
+    w = lambda *shape: torch.randn(*shape, generator=g) * 0.02
+    sd = {"m.linear_in.weight": w(d, d), "m.gate_hidden.weight": w(d, d), "m.gate_hidden_src.weight": w(d, d),
+          "m.linear_out.weight": w(d, d), "m.gate_out": w(L, H, d), "m.forget_out": w(L, H, d),
+          "m.reset_out": w(L, H, d), "m.gate_out_bias": torch.zeros(L, H),
+          "m.forget_out_bias": torch.zeros(L, H), "m.reset_out_bias": torch.zeros(L, H)}
+    x = torch.randn(1, T, d, generator=torch.Generator().manual_seed(0))
+    t = torch.arange(T).unsqueeze(1)
+    lag = torch.tensor([1 << l for l in range(L)])
+    mask = ((t >= lag) & (lag < T)).float()
+    return sd, x, mask
+
+
+def c1_cpu(torch, torch_eager):
+    from dispatcher_hybrid import DispatcherConfig
+    sd, x, mask = _c1_layer(torch)
+    spec = torch_eager.Spec(DispatcherConfig(d_model=512, num_heads=8, max_len=256, num_layers=1, attn_layers=(),
+                                             vocab_size=512, dim_feedforward=1024))
+    with torch.no_grad():
+        torch_eager.mixer(sd, "m.", x, mask, spec)
+        ts = []
+        for _ in range(7):
+            t0 = time.perf_counter()
+            torch_eager.mixer(sd, "m.", x, mask, spec)
+            ts.append(time.perf_counter() - t0)
+    return sorted(ts)[3] * 1e3
+
+
+def c1_gpu(torch, dev, reps=20):
+    """The C1 layer (fp32) through the fused mixer on the GPU: milliseconds per layer."""
+    from dispatcher_hybrid import DispatcherConfig
+    from dispatcher_hybrid.modeling_dispatcher import DispatcherMixer
+    sd, x, mask = _c1_layer(torch)
+    mx = DispatcherMixer(DispatcherConfig(d_model=512, num_heads=8, max_len=256, num_layers=1, attn_layers=(),
+                                          vocab_size=512, dim_feedforward=1024))
+    mx.load_state_dict({k[2:]: v for k, v in sd.items()})
+    mx = mx.to(dev).eval()
+    mx.use_fused_gates = True
+    x, mask = x.to(dev), mask.to(dev)
+    with torch.no_grad():
+        for _ in range(3):
+            mx(x, mask)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            mx(x, mask)
+        torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / reps * 1e3
+
+
+def _agreement(torch, fused16, eager16, truth32):
+    """The north-star bf16 quantities of fused bf16 logits (n, V): max-abs and raw greedy-argmax
+    agreement against the eager bf16 path, the same against the fp32 eager path for both bf16 paths,
+    and argmax agreement where the fp32 path's top-2 margin exceeds 0.1 (decisive positions)."""
+    top2 = torch.topk(truth32, 2, dim=-1).values
+    decisive = (top2[..., 0] - top2[..., 1]) > 0.1
+    agree32 = fused16.argmax(-1) == truth32.argmax(-1)
+    return {"max_abs_vs_eager_bf16": round((fused16 - eager16).abs().max().item(), 4),
+            "argmax_vs_eager_bf16": round((fused16.argmax(-1) == eager16.argmax(-1)).double().mean().item(), 4),
+            "max_abs_vs_eager_fp32": round((fused16 - truth32).abs().max().item(), 4),
+            "eager_bf16_max_abs_vs_eager_fp32": round((eager16 - truth32).abs().max().item(), 4),
+            "argmax_vs_eager_fp32": round(agree32.double().mean().item(), 4),
+            "argmax_vs_eager_fp32_decisive": round(agree32[decisive].double().mean().item(), 4)
+            if bool(decisive.any()) else None,
+            "decisive_positions": int(decisive.sum()), "positions": int(decisive.numel())}
+
+
+def parity_bf16(torch, model, prompt, steps=16):
+    """bf16 parity figures of the measured paths on the bench's own inputs: C2 (fused-gates forward,
+    T = 1024) and C3 (the one-launch greedy step at the bench's context, teacher-forcing the eager
+    decoders with its tokens)."""
+    import copy
+
+    from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder, IncrementalDecoder
+    dev = next(model.parameters()).device
+    m32 = copy.deepcopy(model).float()
+    g = torch.Generator(device=dev).manual_seed(2)
+    ids = torch.randint(0, 50257, (1, 1024), device=dev, generator=g)
+    with torch.no_grad():
+        e16 = model(ids).logits[0].float()
+        f16 = model.enable_fused_gates()(ids).logits[0].float()
+        model.enable_fused_gates(False)
+        e32 = m32(ids).logits[0].float()
+    out = {"c2": _agreement(torch, f16, e16, e32)}
+    del e16, f16, e32
+    ids = torch.randint(0, EOT, (1, prompt), device=dev, generator=torch.Generator(device=dev).manual_seed(3))
+    dec = FusedGraphedHybridDecoder(model)
+    dec.greedy_start(dec.prefill(ids)[:, -1])
+    got = []
+    for _ in range(steps):
+        dec.step_greedy()
+        got.append(dec.logits_out[0].float().clone())
+    toks = dec.tok_hist[:, prompt:prompt + steps]
+    used = bool(dec._pers)
+    del dec
+
+    def forced(m):
+        d_ = IncrementalDecoder(m)
+        d_.prefill(ids)
+        return torch.stack([d_.step(toks[:, j])[0].float() for j in range(steps)])
+
+    out["c3"] = _agreement(torch, torch.stack(got), forced(model), forced(m32))
+    out["c3"]["path"] = "one-launch step" if used else "graph of launches"
+    del m32
+    torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -529,22 +678,29 @@ def main():
         mixer = next(b.mixer for b in model.blocks if hasattr(b, "mixer"))
         x = torch.randn(8, 4096, 1024, device=dev, dtype=torch.bfloat16, generator=g)
         mask = model._tree_mask(ids, 4096)
-        fm = time_mixer(torch, mixer, x, mask, True)
-        em = time_mixer(torch, mixer, x, mask, False)
+        fm, fpk = time_mixer(torch, mixer, x, mask, True)
+        em, epk = time_mixer(torch, mixer, x, mask, False)
         out["gate_path_c5_fused_ms"] = round(fm, 3)
         out["gate_path_c5_eager_ms"] = round(em, 3)
         out["gate_path_c5_speedup"] = round(em / fm, 2)
-        log(f"C5 mixer layer: fused {fm:.2f} ms, eager {em:.2f} ms")
+        out["gate_path_c5_fused_peak_gb"] = round(fpk / 1e9, 3)
+        out["gate_path_c5_eager_peak_gb"] = round(epk / 1e9, 3)
+        log(f"C5 mixer layer: fused {fm:.2f} ms ({fpk / 1e9:.2f} GB), eager {em:.2f} ms ({epk / 1e9:.2f} GB)")
         del x, mask, ids
         torch.cuda.empty_cache()
         pk = prefill_kernels(torch, dev)
         out["prefill_kernels_c5"] = pk
         log("C5 prefill kernels: " + ", ".join(f"{k} {v['us']} us" for k, v in pk.items() if isinstance(v, dict)))
+        out["c1_mixer_gpu_fp32_ms"] = round(c1_gpu(torch, dev), 4)
+        out["parity_bf16"] = parity_bf16(torch, model, prompt)
+        log(f"bf16 parity: {json.dumps(out['parity_bf16'])}")
 
     if not args.no_cpu_baseline:
         log("CPU baseline ...")
         out["cpu_baseline"] = cpu_baseline(torch, model, args.cpu_prompt, args.cpu_steps)
-        log(f"CPU baseline: {out['cpu_baseline']['value']} tok/s on {out['cpu_baseline']['cores']} threads")
+        cb = out["cpu_baseline"]
+        log(f"CPU baseline: C3 {cb['value']} tok/s, C2 {cb['c2_prefill_tok_s']} tok/s, C1 {cb['c1_mixer_ms']} ms "
+            f"on {cb['cores']} threads")
     print(json.dumps(out), flush=True)
 
 
