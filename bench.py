@@ -67,9 +67,10 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--cpu-prompt", type=int, default=1024)
-    ap.add_argument("--leg", default="all", choices=["all", "prefill-kernels", "decode-b16"],
+    ap.add_argument("--leg", default="all", choices=["all", "prefill-kernels", "decode-b16", "decode-trace"],
                     help="prefill-kernels: only the C5 kernel timings; decode-b16: only the batch-16 "
-                         "sampling decode (for rocprofv3 runs)")
+                         "sampling decode (for rocprofv3 runs); decode-trace: per-phase timestamps of "
+                         "the one-launch batch-1 step (wait vs work table)")
     return ap.parse_args()
 
 
@@ -375,6 +376,70 @@ def copy_probe(torch, dev, mib=256):
     del a, b
 
 
+def decode_trace(torch, model, prompt, warmup, steps):
+    """Per-phase timing of the one-launch batch-1 step (dh_decode_persistent_trace) over `steps`
+    greedy steps after `warmup` untraced ones. Per phase of a step: the critical-path increment (the
+    latest workgroup's end minus the previous phase's), the median workgroup's wait (start to the
+    end of its wait for other workgroups' words) and work (wait end to phase end), and the spread
+    of the wait ends over workgroups; averaged by phase kind over layers and steps (microseconds)."""
+    import numpy as np
+
+    from dispatcher_hybrid import fused_step
+    from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder
+    dev = next(model.parameters()).device
+    ids = torch.randint(0, EOT, (1, prompt), device=dev, generator=torch.Generator(device=dev).manual_seed(3))
+    dec = FusedGraphedHybridDecoder(model)
+    dec.greedy_start(dec.prefill(ids)[:, -1])
+    for _ in range(warmup):
+        dec.step_greedy()
+    if not dec._pers:
+        raise SystemExit("decode-trace: the one-launch step is not used for this model")
+    kinds = dec._pers["kinds"]
+    nph = fused_step.persistent_phases(kinds)
+    grid = torch.cuda.get_device_properties(dev).multi_processor_count
+    tr = torch.zeros(steps, grid, nph, 3, dtype=torch.int64, device=dev)
+    torch.cuda.synchronize()
+    for i in range(steps):
+        dec._persistent_step(trace=tr[i])
+        dec.t += 1
+    torch.cuda.synchronize()
+    if dec.check_persistent():
+        raise SystemExit("decode-trace: a traced step timed out")
+    a = tr.cpu().numpy().astype(np.float64) / 100.0                 # 100 MHz counter -> us
+    names = []
+    for k in kinds:
+        names += ["in-projection", "gate readouts", "recurrence + out-projection"] if k == 0 else \
+                 ["attention q/k/v", "attention segments", "attention combine", "attention out-projection"]
+        names += ["feed-forward up", "feed-forward down"]
+    names += ["vocabulary head", "greedy pick"]
+    start, ready, end = a[..., 0], a[..., 1], a[..., 2]
+    end_max = end.max(axis=1)                                       # (steps, nph)
+    t0 = np.where(start[:, :, 0] > 0, start[:, :, 0], np.inf).min(axis=1)
+    inc = np.diff(np.concatenate([t0[:, None], end_max], axis=1), axis=1)
+    rows = {}
+    for p_, nm in enumerate(names):
+        live = ready[:, :, p_] > 0
+        w = np.where(live, ready[:, :, p_] - start[:, :, p_], np.nan)
+        k_ = np.where(live, end[:, :, p_] - ready[:, :, p_], np.nan)
+        sp = np.where(live, ready[:, :, p_], np.nan)
+        spread = np.nanmax(sp, axis=1) - np.nanmin(sp, axis=1)
+        r = rows.setdefault(nm, {"n": 0, "span": 0.0, "wait": 0.0, "work": 0.0, "spread": 0.0})
+        r["n"] += 1
+        r["span"] += float(inc[:, p_].mean())
+        r["wait"] += float(np.nanmean(np.nanmedian(w, axis=1)))
+        r["work"] += float(np.nanmean(np.nanmedian(k_, axis=1)))
+        r["spread"] += float(np.nanmean(spread))
+    table = []
+    for nm, r in rows.items():
+        table.append({"phase": nm, "per_step": r["n"], "span_us": round(r["span"] / r["n"], 3),
+                      "wait_us": round(r["wait"] / r["n"], 3), "work_us": round(r["work"] / r["n"], 3),
+                      "ready_spread_us": round(r["spread"] / r["n"], 3),
+                      "span_total_us": round(r["span"], 2)})
+    total = float((end_max[:, -1] - t0).mean())
+    return {"step_us": round(total, 2), "phases": nph, "workgroups": grid, "steps": steps,
+            "context": f"{prompt + warmup}-{prompt + warmup + steps}", "table": table}
+
+
 def _cpu_threads():
     """Threads for the CPU legs: the process's affinity set, capped at the OMP_NUM_THREADS share the
     host grants one GPU's job (16 on the GPU boxes here)."""
@@ -565,6 +630,14 @@ def main():
     copy_probe(torch, dev)
     model = build_model(torch, dev)
     max_len = model.config.max_len
+    if args.leg == "decode-trace":
+        res = decode_trace(torch, model, min(args.prompt, max_len - args.warmup - args.steps), args.warmup, args.steps)
+        for r in res["table"]:
+            log(f"{r['phase']:28s} x{r['per_step']:2d}  span {r['span_us']:6.2f}  wait {r['wait_us']:6.2f}  "
+                f"work {r['work_us']:6.2f}  spread {r['ready_spread_us']:6.2f}  total {r['span_total_us']:7.1f}")
+        log(f"step {res['step_us']} us over {res['phases']} phases")
+        print(json.dumps({"decode_trace": res}), flush=True)
+        return
     if args.leg == "decode-b16":
         steps16 = min(args.steps, 128)
         p16 = min(args.prompt, max_len - args.warmup - steps16)

@@ -50,6 +50,16 @@ enum : int {
   F_NORM2 = 15, F_WGATE = 16, F_WUP = 17, F_WDOWN = 18,
 };
 
+// A layer's row of the layer table, read from the workgroup's LDS copy: LDS reads wait on the LDS
+// counter only, so a table field read after a phase's wait never waits for the weight requests in
+// flight (a table read through global memory would: vector-memory loads retire in order).
+typedef const __attribute__((address_space(3))) int64_t lds_i64;
+struct LayerRef {
+  lds_i64* p;
+  __device__ __forceinline__ int64_t operator[](int f) const { return p[f]; }
+  __device__ __forceinline__ LayerRef next() const { return LayerRef{p + DH_PERSISTENT_LAYER_WORDS}; }
+};
+
 struct PArgs {
   const int64_t* table;      // device, n_layers * kLW words
   int n_layers;
@@ -64,6 +74,7 @@ struct PArgs {
   uint32_t* status;          // [0] abort flag, [1] first failing phase + 1
   uint32_t *xw, *v0w, *aw, *hw, *qw, *kw, *vw, *yw;   // tagged bf16 vectors
   uint64_t *coefw, *partw, *candw;                     // tagged fp32 records
+  uint64_t* trace;           // nullable: per-phase timestamps (dh_decode_persistent_trace)
   float eps;
   int d, GH, H, hd, L, ff, V, Tmax, nph;
 };
@@ -148,6 +159,15 @@ __device__ __forceinline__ uint4 get16x4(const uint32_t* base, int nwords, int w
 __device__ __forceinline__ bool tag_ok(uint32_t w, uint32_t tag) { return (w & 0xffffu) == tag; }
 __device__ __forceinline__ uint64_t now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
 
+// Optional timing record of a traced step: per workgroup and phase, the 100 MHz real-time counter
+// when the phase starts (k = 0), when its wait for other workgroups' words ended (k = 1; a phase
+// without a wait in this workgroup leaves 0) and when it ends (k = 2). Thread 0 stamps.
+#define DH_MARK(a, ph, k)                                                                             \
+  do {                                                                                                \
+    if ((a).trace && threadIdx.x == 0)                                                                \
+      (a).trace[((int64_t)blockIdx.x * (a).nph + (ph)) * 3 + (k)] = now_ticks();                      \
+  } while (0)
+
 __device__ __forceinline__ bool aborted(const PArgs& a) { return get16(a.status) != 0u; }
 // the first failure records its phase + 1, and in decimal digits above it the wait's end condition
 // (thousands: 1 another wait failed, 2 time, 3 rounds) and its rounds (ten-thousands, capped)
@@ -218,6 +238,7 @@ __device__ __forceinline__ bool wg_poll16(const PArgs& a, Smem& S, const uint32_
       return false;
     }
   }
+  DH_MARK(a, ph, 1);
 #pragma unroll
   for (int j = 0; j < 3; ++j) {
     const int q = tid + j * kPT;
@@ -258,17 +279,13 @@ __device__ __forceinline__ void norm_staged(Smem& S, int K, float eps) {
   __syncthreads();
 }
 
-// stage a plain bf16 row (an embedding row) and, if given, a norm weight
-__device__ __forceinline__ void stage_plain(Smem& S, const bf16_t* x, const bf16_t* g, int K) {
-  const int nchunk = K / 8;
-  for (int i = threadIdx.x; i < nchunk; i += kPT) S.sx[i] = ld16(x + (int64_t)i * 8);
-  if (g)
-    for (int i = threadIdx.x; i < nchunk; i += kPT) S.sg[i] = ld16(g + (int64_t)i * 8);
-  __syncthreads();
+// A row of K <= 4 * kPT bf16 elements held four per thread (requested with a phase's weights) into
+// the staged row or the norm-weight region of LDS.
+__device__ __forceinline__ void stage_regs(uint4* dst, uint2 v, int K) {
+  if ((int)threadIdx.x * 4 < K) reinterpret_cast<uint2*>(dst)[threadIdx.x] = v;
 }
-__device__ __forceinline__ void stage_norm_weight(Smem& S, const bf16_t* g, int K) {
-  const int nchunk = K / 8;
-  for (int i = threadIdx.x; i < nchunk; i += kPT) S.sg[i] = ld16(g + (int64_t)i * 8);
+__device__ __forceinline__ uint2 fetch_row4(const bf16_t* src, int K) {
+  return ld8(src + (int64_t)min((int)threadIdx.x * 4, K - 4));
 }
 
 // the dot products of R rows (CG chunks per lane) with the staged row
@@ -315,27 +332,26 @@ __device__ __forceinline__ void load_rows(uint4 (&w)[R][NW][CG], const bf16_t* c
   }
 }
 
-// ---- the layer input: tagged x (or the embedding row for the first layer), normalised
-__device__ __forceinline__ bool stage_input(const PArgs& a, Smem& S, bool first, const bf16_t* erow, const bf16_t* g, uint32_t xtag,
-                            int ph) {
+// ---- the layer input: tagged x (or the embedding row, x0, for the first layer), normalised with
+// the norm weight g (both requested with the phase's weights)
+__device__ __forceinline__ bool stage_input(const PArgs& a, Smem& S, bool first, uint2 x0, uint2 g, uint32_t xtag, int ph) {
+  stage_regs(S.sg, g, a.d);
   if (first) {
-    stage_plain(S, erow, g, a.d);
+    stage_regs(S.sx, x0, a.d);
+    DH_MARK(a, ph, 1);
   } else {
-    stage_norm_weight(S, g, a.d);
     if (!wg_poll16(a, S, a.xw, a.d, xtag, reinterpret_cast<bf16_t*>(S.sx), ph)) return false;
-    __syncthreads();
   }
+  __syncthreads();
   norm_staged(S, a.d, a.eps);
   return true;
 }
 
 // The residual of output row n. The x phases (tree out-projection, attention out-projection, down
 // projection) give row n to global wave n, so the wave that adds the residual of row n produced it
-// in the previous x phase and keeps it in a register (xres); the first layer's comes from the
-// embedding row.
-__device__ __forceinline__ float residual(bool first, const bf16_t* erow, int n, float xres) {
-  return first ? bf16_to_f32(ld2(erow + n)) : xres;
-}
+// in the previous x phase and keeps it in a register (xres); before the first x phase xres holds
+// the embedding row's element n, loaded when the step starts.
+__device__ __forceinline__ float residual(bool, const bf16_t*, int, float xres) { return xres; }
 
 // ---------------------------------------------------------------------------------------------
 // GEMV phases
@@ -358,7 +374,10 @@ __device__ __forceinline__ void fetch_rows(Rows<R, NW, CG>& f, const bf16_t* con
 // first phase of a layer (in-projection / q,k,v: 3 rows per wave, K = d) or the vocabulary head's
 // first group (4 rows per wave): one register shape for both, so the fetch for "the next layer's
 // first phase" has one type
-typedef Rows<4, 1, 2> PreFirst;
+struct PreFirst : Rows<4, 1, 2> {
+  uint2 g;                         // the RMSNorm weight (norm1, or norm_out for the head), 4 per thread
+  uint2 x0;                        // the first layer: the token's embedding row, 4 per thread
+};
 
 // RMSNorm + [W_a; W_b; W_c] rows of global wave gw: base row gw * 3 of N = n0 + n1 + n2
 __device__ __forceinline__ void fetch_in3(PreFirst& f, const PArgs& a, int n0, int n1, int n2, const bf16_t* W0,
@@ -379,8 +398,8 @@ __device__ __forceinline__ void fetch_in3(PreFirst& f, const PArgs& a, int n0, i
 
 // Segments 0 and 1 go to tagged vectors; segment 2 to `plain2` (the B_hist row of t) or a third
 // tagged vector. The launch has at least N / 3 waves.
-__device__ __forceinline__ bool run_in3(const PArgs& a, Smem& S, const PreFirst& f, const bf16_t* norm_w, bool first,
-                                        const bf16_t* erow, uint32_t xtag, int ph, Tags tg, uint32_t* out0,
+__device__ __forceinline__ bool run_in3(const PArgs& a, Smem& S, const PreFirst& f, bool first,
+                                        uint32_t xtag, int ph, Tags tg, uint32_t* out0,
                                         uint32_t* out1, uint32_t* out2, bf16_t* plain2, int n0, int n1, int n2) {
   constexpr int R = 3, CG = 2;                        // K = d <= 1024
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -388,7 +407,7 @@ __device__ __forceinline__ bool run_in3(const PArgs& a, Smem& S, const PreFirst&
   const int nchunk = a.d / 8;
   const int base = (blockIdx.x * kPW + wave) * R;
   if (blockIdx.x * kPW * R >= N) return true;         // uniform: no rows in this workgroup
-  if (!stage_input(a, S, first, erow, norm_w, xtag, ph)) return false;
+  if (!stage_input(a, S, first, f.x0, f.g, xtag, ph)) return false;
   if (base >= N) return true;                          // uniform per wave
   uint4 w[R][1][CG];
 #pragma unroll
@@ -412,13 +431,16 @@ __device__ __forceinline__ bool run_in3(const PArgs& a, Smem& S, const PreFirst&
 }
 
 // RMSNorm2 + SwiGLU(W_gate, W_up) -> tagged h (ff words), R = 3 rows per wave
-typedef Rows<3, 2, 2> PreUp;
-__device__ __forceinline__ void fetch_ffn_up(PreUp& f, const PArgs& a, const int64_t* Lt) {
+struct PreUp : Rows<3, 2, 2> {
+  uint2 g;                         // norm2, 4 per thread
+};
+__device__ __forceinline__ void fetch_ffn_up(PreUp& f, const PArgs& a, LayerRef Lt) {
   constexpr int R = 3;
   const int N = a.ff;
   const int base = (blockIdx.x * kPW + (threadIdx.x >> 6)) * R;
   const bf16_t* Wg = (const bf16_t*)(intptr_t)Lt[F_WGATE];
   const bf16_t* Wu = (const bf16_t*)(intptr_t)Lt[F_WUP];
+  f.g = fetch_row4((const bf16_t*)(intptr_t)Lt[F_NORM2], a.d);
   const bf16_t* rows[R][2];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -428,14 +450,14 @@ __device__ __forceinline__ void fetch_ffn_up(PreUp& f, const PArgs& a, const int
   }
   fetch_rows<3, 2, 2>(f, rows, a.d / 8);
 }
-__device__ __forceinline__ bool run_ffn_up(const PArgs& a, Smem& S, const PreUp& f, const int64_t* Lt, uint32_t xtag,
+__device__ __forceinline__ bool run_ffn_up(const PArgs& a, Smem& S, const PreUp& f, LayerRef Lt, uint32_t xtag,
                                            int ph, Tags tg) {
   constexpr int R = 3, CG = 2;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int N = a.ff, nchunk = a.d / 8;
   const int base = (blockIdx.x * kPW + wave) * R;
   if (blockIdx.x * kPW * R >= N) return true;
-  stage_norm_weight(S, (const bf16_t*)(intptr_t)Lt[F_NORM2], a.d);
+  stage_regs(S.sg, f.g, a.d);
   if (!wg_poll16(a, S, a.xw, a.d, xtag, reinterpret_cast<bf16_t*>(S.sx), ph)) return false;
   __syncthreads();
   norm_staged(S, a.d, a.eps);
@@ -491,7 +513,7 @@ struct PreGates {                 // raw words: converting them here would wait 
   uint32_t bi, bf, br, rsrc;
 };
 // the wave's (level, head) unit: u = global wave (H * L units over >= H * L waves)
-__device__ __forceinline__ void fetch_gates(PreGates& f, const PArgs& a, const int64_t* Lt, int64_t t) {
+__device__ __forceinline__ void fetch_gates(PreGates& f, const PArgs& a, LayerRef Lt, int64_t t) {
   constexpr int C = 2;                                // GH <= 1024
   const int lane = threadIdx.x & 63;
   const int u = blockIdx.x * kPW + (threadIdx.x >> 6);
@@ -519,7 +541,7 @@ __device__ __forceinline__ void fetch_gates(PreGates& f, const PArgs& a, const i
   f.rsrc = ld2((const bf16_t*)(intptr_t)Lt[F_RGHIST] + (sc * L + l) * H + h);
 }
 
-__device__ __forceinline__ void run_gates(const PArgs& a, const PreGates& f, const int64_t* Lt, int64_t t,
+__device__ __forceinline__ void run_gates(const PArgs& a, const PreGates& f, LayerRef Lt, int64_t t,
                                           uint32_t atag, int ph, Tags tg) {
   constexpr int C = 2;
   const int lane = threadIdx.x & 63;
@@ -552,6 +574,7 @@ __device__ __forceinline__ void run_gates(const PArgs& a, const PreGates& f, con
       return;
     }
   }
+  DH_MARK(a, ph, 1);
   float s0 = 0.f, s1 = 0.f, s2 = 0.f;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
@@ -593,7 +616,7 @@ struct PreScan {
   Rows<1, 1, 2> w;                 // this wave's out-projection row
   uint2 vs[kLMax];                 // raw ring sources of this thread's four elements, per level
 };
-__device__ __forceinline__ void fetch_scan(PreScan& f, const PArgs& a, const int64_t* Lt, int64_t t) {
+__device__ __forceinline__ void fetch_scan(PreScan& f, const PArgs& a, LayerRef Lt, int64_t t) {
   const int d = a.d, L = a.L;
   const int e0 = min((int)threadIdx.x * 4, d - 4);
   const bf16_t* ring = (const bf16_t*)(intptr_t)Lt[F_VRING];
@@ -607,7 +630,7 @@ __device__ __forceinline__ void fetch_scan(PreScan& f, const PArgs& a, const int
   }
 }
 
-__device__ __forceinline__ bool run_scan_out(const PArgs& a, Smem& S, const PreScan& f, const int64_t* Lt, int64_t t,
+__device__ __forceinline__ bool run_scan_out(const PArgs& a, Smem& S, const PreScan& f, LayerRef Lt, int64_t t,
                                              bool first, const bf16_t* erow, float& xres, int v0ph, int gph, int ph,
                                              Tags tg, void* Yout) {
   constexpr int CG = 2;                               // d <= 1024
@@ -656,6 +679,7 @@ __device__ __forceinline__ bool run_scan_out(const PArgs& a, Smem& S, const PreS
         return false;
       }
     }
+    DH_MARK(a, ph, 1);
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
       const int i = tid + j * kPT;
@@ -718,7 +742,7 @@ struct AttnGeo {
   bool live, has_t;
   bf16_t *Kh, *Vh;
 };
-__device__ __forceinline__ AttnGeo attn_geo(const PArgs& a, const int64_t* Lt, int64_t t) {
+__device__ __forceinline__ AttnGeo attn_geo(const PArgs& a, LayerRef Lt, int64_t t) {
   AttnGeo g;
   const int tid = threadIdx.x;
   g.un = tid / kUT;
@@ -749,7 +773,7 @@ struct PreAttn {
   uint4 vrow[8];                   // its first value rows (lane -> (row slot, chunk))
   uint32_t rc, rsn;                // raw rotation operands of t
 };
-__device__ __forceinline__ void fetch_attn(PreAttn& f, const PArgs& a, const int64_t* Lt, int64_t t) {
+__device__ __forceinline__ void fetch_attn(PreAttn& f, const PArgs& a, LayerRef Lt, int64_t t) {
   constexpr int VE = 8, KCH = kHD / VE, RPI = 64 / KCH, NW = kUT / 64, VCH = 8;
   const AttnGeo g = attn_geo(a, Lt, t);
   const int pt = min(g.ut, kHD / 2 - 1);
@@ -770,7 +794,7 @@ __device__ __forceinline__ void fetch_attn(PreAttn& f, const PArgs& a, const int
   }
 }
 
-__device__ __forceinline__ bool run_attn_split(const PArgs& a, Smem& S, const PreAttn& f, const int64_t* Lt, int64_t t,
+__device__ __forceinline__ bool run_attn_split(const PArgs& a, Smem& S, const PreAttn& f, LayerRef Lt, int64_t t,
                                                int qph, int ph, Tags tg) {
   constexpr int VE = 8, KCH = kHD / VE, RPI = 64 / KCH, NW = kUT / 64, VCH = 8;
   const int tid = threadIdx.x;
@@ -819,6 +843,7 @@ __device__ __forceinline__ bool run_attn_split(const PArgs& a, Smem& S, const Pr
         return false;
       }
     }
+    DH_MARK(a, ph, 1);
     q0 = bfv(wq0 >> 16); q1 = bfv(wq1 >> 16);
     k0 = bfv(wk0 >> 16); k1 = bfv(wk1 >> 16);
     v0 = bfv(wv0 >> 16); v1 = bfv(wv1 >> 16);
@@ -986,6 +1011,7 @@ __device__ __forceinline__ void phase_attn_combine(const PArgs& a, int sph, int 
       }
     }
   }
+  DH_MARK(a, ph, 1);
   float M = -INFINITY;
 #pragma unroll
   for (int s = 0; s < kSplitS; ++s) M = fmaxf(M, m[s]);
@@ -1011,6 +1037,7 @@ __device__ __forceinline__ void fetch_head_rows(uint4 (&w)[4][1][2], const PArgs
 }
 __device__ __forceinline__ void fetch_lm_head(PreFirst& f, const PArgs& a) {
   fetch_head_rows(f.w, a, (blockIdx.x * kPW + (threadIdx.x >> 6)) * 4);
+  f.g = fetch_row4(a.norm_out, a.d);
 }
 
 __device__ __forceinline__ bool run_lm_head(const PArgs& a, Smem& S, const PreFirst& f, uint32_t xtag, int ph, Tags tg) {
@@ -1026,7 +1053,7 @@ __device__ __forceinline__ bool run_lm_head(const PArgs& a, Smem& S, const PreFi
 #pragma unroll
     for (int c = 0; c < CG; ++c) w[r][0][c] = f.w[r][0][c];
   auto fetch = [&](int base) { fetch_head_rows(w, a, base); };
-  stage_norm_weight(S, a.norm_out, K);
+  stage_regs(S.sg, f.g, K);
   if (!wg_poll16(a, S, a.xw, K, xtag, reinterpret_cast<bf16_t*>(S.sx), ph)) return false;
   __syncthreads();
   norm_staged(S, K, a.eps);
@@ -1092,6 +1119,7 @@ __device__ __forceinline__ void phase_argmax(const PArgs& a, Smem& S, int64_t t,
       bidx = ix;
     }
   }
+  DH_MARK(a, ph, 1);
   wave_best(best, bidx);
   if (lane == 63) S.wbest[wave] = Cand{best, bidx};
   __syncthreads();
@@ -1112,7 +1140,9 @@ __device__ __forceinline__ void phase_argmax(const PArgs& a, Smem& S, int64_t t,
 }
 
 // the first phase of layer Lt: the tree in-projection [W_in; W_gh; W_ghs] or attention's [W_q; W_k; W_v]
-__device__ __forceinline__ void fetch_first(PreFirst& f, const PArgs& a, const int64_t* Lt) {
+__device__ __forceinline__ void fetch_first(PreFirst& f, const PArgs& a, LayerRef Lt, const bf16_t* erow) {
+  f.g = fetch_row4((const bf16_t*)(intptr_t)Lt[F_NORM1], a.d);
+  if (erow) f.x0 = fetch_row4(erow, a.d);
   if (Lt[F_KIND] == 0)
     fetch_in3(f, a, a.d, a.GH, a.GH, (const bf16_t*)(intptr_t)Lt[F_WIN], (const bf16_t*)(intptr_t)Lt[F_WGH],
               (const bf16_t*)(intptr_t)Lt[F_WGS]);
@@ -1133,13 +1163,20 @@ __global__ __launch_bounds__(kPT) void decode_persistent_kernel(PArgs a) {
   if (t < 0 || t >= a.Tmax) return;                   // uniform: nothing to do (the graphed step writes nothing either)
   const Tags tg{(uint64_t)ep * (uint64_t)a.nph};
   const bf16_t* erow = a.emb + (int64_t)tok * a.d;
+  // the layer table, copied once into LDS (fields are then read without touching the vector-memory
+  // counter the weight requests occupy)
+  __shared__ int64_t s_tab[kMaxLayers * kLW];
+  for (int i = threadIdx.x; i < a.n_layers * kLW; i += kPT) s_tab[i] = a.table[i];
+  const int xrow = min((int)(blockIdx.x * kPW + (threadIdx.x >> 6)), a.d - 1);
+  float xres = bf16_to_f32(ld2(erow + xrow));          // x[n] this wave last wrote (its x-phase row n)
+  __syncthreads();
+  const LayerRef tab0{(lds_i64*)s_tab};
   int ph = 0;
   int xph = -1;                                        // phase that last wrote x (-1: the embedding row)
-  float xres = 0.f;                                    // x[n] this wave last wrote (its x-phase row n)
   PreFirst pf;                                         // the next layer's first phase (then the head's)
-  fetch_first(pf, a, a.table);
+  fetch_first(pf, a, tab0, erow);
   for (int li = 0; li < a.n_layers; ++li) {
-    const int64_t* Lt = a.table + (int64_t)li * kLW;
+    const LayerRef Lt{tab0.p + (int64_t)li * kLW};
     const bool first = xph < 0;
     const uint32_t xtag = first ? 0u : tg.t16(xph);
     PreUp pu;
@@ -1147,49 +1184,71 @@ __global__ __launch_bounds__(kPT) void decode_persistent_kernel(PArgs a) {
       PreGates pg;
       fetch_gates(pg, a, Lt, t);
       const int p_in = ph++;                           // V0, A (tagged), B_hist[t] (plain)
-      if (!run_in3(a, S, pf, (const bf16_t*)(intptr_t)Lt[F_NORM1], first, erow, xtag, p_in, tg, a.v0w, a.aw, nullptr,
+      DH_MARK(a, p_in, 0);
+      if (!run_in3(a, S, pf, first, xtag, p_in, tg, a.v0w, a.aw, nullptr,
                    (bf16_t*)(intptr_t)Lt[F_BHIST] + t * a.GH, a.d, a.GH, a.GH))
         return;
+      DH_MARK(a, p_in, 2);
       PreScan ps;
       fetch_scan(ps, a, Lt, t);
       const int p_g = ph++;
+      DH_MARK(a, p_g, 0);
       run_gates(a, pg, Lt, t, p_in, p_g, tg);
+      DH_MARK(a, p_g, 2);
       fetch_ffn_up(pu, a, Lt);
       const int p_s = ph++;
+      DH_MARK(a, p_s, 0);
       if (!run_scan_out(a, S, ps, Lt, t, first, erow, xres, p_in, p_g, p_s, tg, nullptr)) return;
+      DH_MARK(a, p_s, 2);
       xph = p_s;
     } else {
       PreAttn pa;
       fetch_attn(pa, a, Lt, t);
       const int p_q = ph++;
-      if (!run_in3(a, S, pf, (const bf16_t*)(intptr_t)Lt[F_NORM1], first, erow, xtag, p_q, tg, a.qw, a.kw, a.vw,
+      DH_MARK(a, p_q, 0);
+      if (!run_in3(a, S, pf, first, xtag, p_q, tg, a.qw, a.kw, a.vw,
                    nullptr, a.d, a.d, a.d))
         return;
+      DH_MARK(a, p_q, 2);
       const int p_a = ph++;
+      DH_MARK(a, p_a, 0);
       if (!run_attn_split(a, S, pa, Lt, t, p_q, p_a, tg)) return;
+      DH_MARK(a, p_a, 2);
       Rows<1, 1, 2> po;
       fetch_row<2>(po, (const bf16_t*)(intptr_t)Lt[F_WO], a.d, a.d);
       const int p_c = ph++;
+      DH_MARK(a, p_c, 0);
       phase_attn_combine(a, p_a, p_c, tg);
+      DH_MARK(a, p_c, 2);
       fetch_ffn_up(pu, a, Lt);
       const int p_o = ph++;
+      DH_MARK(a, p_o, 0);
       if (!run_rows_resid<2>(a, S, po, a.d, a.yw, tg.t16(p_c), first, erow, xres, p_o, tg)) return;
+      DH_MARK(a, p_o, 2);
       xph = p_o;
     }
     Rows<1, 1, 6> pd;
     fetch_row<6>(pd, (const bf16_t*)(intptr_t)Lt[F_WDOWN], a.ff, a.d);
     const int p_u = ph++;
+    DH_MARK(a, p_u, 0);
     if (!run_ffn_up(a, S, pu, Lt, tg.t16(xph), p_u, tg)) return;
-    if (li + 1 < a.n_layers) fetch_first(pf, a, Lt + kLW);
+    DH_MARK(a, p_u, 2);
+    if (li + 1 < a.n_layers) fetch_first(pf, a, Lt.next(), nullptr);
     else fetch_lm_head(pf, a);
     const int p_d = ph++;
+    DH_MARK(a, p_d, 0);
     if (!run_rows_resid<6>(a, S, pd, a.ff, a.hw, tg.t16(p_u), false, erow, xres, p_d, tg)) return;
+    DH_MARK(a, p_d, 2);
     xph = p_d;
   }
   const int p_n = ph++;
+  DH_MARK(a, p_n, 0);
   if (!run_lm_head(a, S, pf, tg.t16(xph), p_n, tg)) return;
+  DH_MARK(a, p_n, 2);
   const int p_m = ph++;
+  DH_MARK(a, p_m, 0);
   phase_argmax(a, S, t, p_n, p_m, tg);
+  DH_MARK(a, p_m, 2);
 }
 
 // phases of a step: 5 per tree layer, 6 per attention layer, 2 for the head and the pick
@@ -1208,12 +1267,11 @@ extern "C" int64_t dh_decode_persistent_scratch_bytes(int d, int GH, int H, int 
   return 256 + (w16 * 4 + 255) / 256 * 256 + w32 * 8 + 256;
 }
 
-extern "C" int dh_decode_persistent_step(const int64_t* layer_table, const int* kinds, int n_layers, const void* emb,
-                                         const void* norm_out, float eps, int d, int GH, int H, int hd, int L, int ff,
-                                         int V, int Tmax, int64_t* t_dev, int64_t* token, int64_t* tok_hist,
-                                         int64_t hist_len, void* logits, void* scratch, int64_t scratch_bytes,
-                                         void* stream) {
-  const char* who = "dh_decode_persistent_step";
+namespace {
+int launch_persistent(const char* who, const int64_t* layer_table, const int* kinds, int n_layers, const void* emb,
+                      const void* norm_out, float eps, int d, int GH, int H, int hd, int L, int ff, int V, int Tmax,
+                      int64_t* t_dev, int64_t* token, int64_t* tok_hist, int64_t hist_len, void* logits,
+                      void* scratch, int64_t scratch_bytes, uint64_t* trace, int64_t trace_words, void* stream) {
   DH_REQUIRE(layer_table && kinds && emb && norm_out && t_dev && token && logits && scratch, DH_ERR_INVALID_ARG,
              "%s: null pointer argument", who);
   DH_REQUIRE(n_layers >= 1 && n_layers <= kMaxLayers, DH_ERR_UNSUPPORTED_SHAPE, "%s: %d layers (1..%d)", who,
@@ -1252,6 +1310,10 @@ extern "C" int dh_decode_persistent_step(const int64_t* layer_table, const int* 
   a.eps = eps;
   a.d = d; a.GH = GH; a.H = H; a.hd = hd; a.L = L; a.ff = ff; a.V = V; a.Tmax = Tmax;
   a.nph = count_phases(kinds, n_layers);
+  DH_REQUIRE(!trace || trace_words >= (int64_t)grid * a.nph * 3, DH_ERR_INVALID_ARG,
+             "%s: trace of %lld words, needs %lld (CUs x phases x 3)", who, (long long)trace_words,
+             (long long)grid * a.nph * 3);
+  a.trace = trace;
   char* p = (char*)scratch;
   a.epoch = (int64_t*)p;
   a.status = (uint32_t*)(p + 8);
@@ -1285,6 +1347,30 @@ extern "C" int dh_decode_persistent_step(const int64_t* layer_table, const int* 
   decode_persistent_kernel<<<dim3(grid), dim3(kPT), 0, (hipStream_t)stream>>>(a);
   return dh_check_launch(who);
 }
+}  // namespace
+
+extern "C" int dh_decode_persistent_step(const int64_t* layer_table, const int* kinds, int n_layers, const void* emb,
+                                         const void* norm_out, float eps, int d, int GH, int H, int hd, int L, int ff,
+                                         int V, int Tmax, int64_t* t_dev, int64_t* token, int64_t* tok_hist,
+                                         int64_t hist_len, void* logits, void* scratch, int64_t scratch_bytes,
+                                         void* stream) {
+  return launch_persistent("dh_decode_persistent_step", layer_table, kinds, n_layers, emb, norm_out, eps, d, GH, H, hd,
+                           L, ff, V, Tmax, t_dev, token, tok_hist, hist_len, logits, scratch, scratch_bytes, nullptr, 0,
+                           stream);
+}
+
+extern "C" int dh_decode_persistent_trace(const int64_t* layer_table, const int* kinds, int n_layers, const void* emb,
+                                          const void* norm_out, float eps, int d, int GH, int H, int hd, int L, int ff,
+                                          int V, int Tmax, int64_t* t_dev, int64_t* token, int64_t* tok_hist,
+                                          int64_t hist_len, void* logits, void* scratch, int64_t scratch_bytes,
+                                          uint64_t* trace, int64_t trace_words, void* stream) {
+  DH_REQUIRE(trace, DH_ERR_INVALID_ARG, "dh_decode_persistent_trace: null trace");
+  return launch_persistent("dh_decode_persistent_trace", layer_table, kinds, n_layers, emb, norm_out, eps, d, GH, H,
+                           hd, L, ff, V, Tmax, t_dev, token, tok_hist, hist_len, logits, scratch, scratch_bytes, trace,
+                           trace_words, stream);
+}
+
+extern "C" int dh_decode_persistent_phases(const int* kinds, int n_layers) { return count_phases(kinds, n_layers); }
 
 extern "C" int dh_decode_persistent_status(const void* scratch, uint32_t* out2, void* stream) {
   DH_REQUIRE(scratch && out2, DH_ERR_INVALID_ARG, "dh_decode_persistent_status: null pointer argument");

@@ -85,6 +85,9 @@ def _load():
         "dh_decode_persistent_step": ([vp, vp, i32, vp, vp, ctypes.c_float] + [i32] * 8
                                       + [vp, vp, vp, i64, vp, vp, i64, vp], i32),
         "dh_decode_persistent_status": ([vp, vp, vp], i32),
+        "dh_decode_persistent_trace": ([vp, vp, i32, vp, vp, ctypes.c_float] + [i32] * 8
+                                       + [vp, vp, vp, i64, vp, vp, i64, vp, i64, vp], i32),
+        "dh_decode_persistent_phases": ([vp, i32], i32),
     }
     for name, (argtypes, restype) in sigs.items():
         fn = getattr(lib, name)

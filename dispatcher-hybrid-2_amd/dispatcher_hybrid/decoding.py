@@ -509,10 +509,11 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         return dict(table=table, kinds=kinds, emb=emb, norm_out=m.norm_out.weight, eps=eps.pop(),
                     dims=(d, GH, H, hd, L, ff, V, self.max_len), scratch=scratch)
 
-    def _persistent_step(self):
+    def _persistent_step(self, trace=None):
         p = self._pers
         self._fused_step.persistent_step(p["table"], p["kinds"], p["emb"], p["norm_out"], p["eps"], p["dims"],
-                                         self.t_buf, self.token_buf, self.tok_hist, self.logits_out, p["scratch"])
+                                         self.t_buf, self.token_buf, self.tok_hist, self.logits_out, p["scratch"],
+                                         trace=trace)
 
     def persistent_status(self):
         """(timed out, first failing phase + 1) of this decoder's one-launch steps (synchronises);

@@ -420,24 +420,37 @@ def persistent_scratch_bytes(d, GH, H, L, ff, grid):
     return int(_hip.lib.dh_decode_persistent_scratch_bytes(int(d), int(GH), int(H), int(L), int(ff), int(grid)))
 
 
-def persistent_step(table, kinds, emb, norm_out, eps, dims, t_buf, token_buf, tok_hist, logits, scratch):
+def persistent_phases(kinds):
+    """Phases of one one-launch step for these layer kinds."""
+    n = len(kinds)
+    return int(_hip.lib.dh_decode_persistent_phases((ctypes.c_int * n)(*[int(k) for k in kinds]), n))
+
+
+def persistent_step(table, kinds, emb, norm_out, eps, dims, t_buf, token_buf, tok_hist, logits, scratch, trace=None):
     """One batch-1 bf16 greedy decode step of the whole model as one cooperative launch.
 
     table: (n_layers, LAYER_WORDS) int64 device tensor of weight / cache addresses (field order of
     include/dh_mixer.h); kinds: host list of layer kinds (0 tree, 1 attention); dims: (d, GH, H, hd,
     L, ff, V, Tmax). Reads the token in token_buf at position t_buf[0]; writes the greedy pick to
     token_buf and tok_hist[0, t + 1], the logits (1, V) and advances t_buf. scratch: zero-filled once
-    (persistent_scratch_bytes), then kept with the decoder."""
+    (persistent_scratch_bytes), then kept with the decoder. trace (optional): a zeroed uint64-sized
+    (CUs, phases, 3) int64 tensor that receives each workgroup's real-time counter at every phase's
+    start, wait end and end (dh_decode_persistent_trace)."""
     n = len(kinds)
     karr = (ctypes.c_int * n)(*[int(k) for k in kinds])
     d, GH, H, hd, L, ff, V, Tmax = (int(v) for v in dims)
     p = _hip.ptr
     hist_len = tok_hist.shape[-1] if tok_hist is not None else 0
-    st = _hip.lib.dh_decode_persistent_step(
-        p(table), karr, n, p(emb), p(norm_out), float(eps), d, GH, H, hd, L, ff, V, Tmax, p(t_buf), p(token_buf),
-        p(tok_hist), hist_len, p(logits), p(scratch), scratch.numel() * scratch.element_size(),
-        _hip.stream_handle(emb.device))
-    _hip.check(st, "dh_decode_persistent_step")
+    args = (p(table), karr, n, p(emb), p(norm_out), float(eps), d, GH, H, hd, L, ff, V, Tmax, p(t_buf), p(token_buf),
+            p(tok_hist), hist_len, p(logits), p(scratch), scratch.numel() * scratch.element_size())
+    if trace is None:
+        st = _hip.lib.dh_decode_persistent_step(*args, _hip.stream_handle(emb.device))
+        _hip.check(st, "dh_decode_persistent_step")
+    else:
+        if trace.dtype != torch.int64 or not trace.is_contiguous():
+            raise ValueError("persistent_step: trace must be a contiguous int64 tensor")
+        st = _hip.lib.dh_decode_persistent_trace(*args, p(trace), trace.numel(), _hip.stream_handle(emb.device))
+        _hip.check(st, "dh_decode_persistent_trace")
 
 
 def persistent_status(scratch):

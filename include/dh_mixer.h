@@ -382,6 +382,21 @@ int dh_decode_persistent_step(const int64_t* layer_table, const int* kinds, int 
                               const void* norm_out, float eps, int d, int GH, int H, int hd, int L, int ff, int V,
                               int Tmax, int64_t* t_dev, int64_t* token, int64_t* tok_hist, int64_t hist_len,
                               void* logits, void* scratch, int64_t scratch_bytes, void* stream);
+/*
+ * dh_decode_persistent_step with a timing record, for profiling the step's phases: trace
+ * (caller-zeroed device memory, >= CUs x phases x 3 uint64 words) receives, per workgroup and
+ * phase, the 100 MHz real-time counter at the phase's start, at the end of its wait for other
+ * workgroups' words (0 where the workgroup has none) and at its end. Same arguments and results
+ * otherwise; no counterpart in the reference.
+ */
+int dh_decode_persistent_trace(const int64_t* layer_table, const int* kinds, int n_layers, const void* emb,
+                               const void* norm_out, float eps, int d, int GH, int H, int hd, int L, int ff, int V,
+                               int Tmax, int64_t* t_dev, int64_t* token, int64_t* tok_hist, int64_t hist_len,
+                               void* logits, void* scratch, int64_t scratch_bytes, uint64_t* trace,
+                               int64_t trace_words, void* stream);
+/* phases of one step for these layer kinds (0 tree, 1 attention): 5 per tree layer, 6 per
+ * attention layer, 2 for the vocabulary head and the pick */
+int dh_decode_persistent_phases(const int* kinds, int n_layers);
 /* status words of the last persistent steps on `scratch`: out2[0] non-zero after a timeout,
  * out2[1] the first failing phase + 1 (synchronises the stream) */
 int dh_decode_persistent_status(const void* scratch, uint32_t* out2, void* stream);
