@@ -705,8 +705,11 @@ void launch_fwd_lds(const FwdArgs& a, hipStream_t s) {
 }
 
 // Tile per workgroup (measured on MI355X at the released widths): two levels x 64 positions once
-// the launch has >= 1024 workgroups (b = 8, T = 4096: 154 us, against 169 for 2 x 128 and 172
-// for 1 x 64), else one level x 64 positions, the most workgroups for short prefills.
+// the launch has >= 1024 workgroups (b = 8, T = 4096: 135 us, against 143 / 155 / 224 for three /
+// four / six levels -- fewer waves per SIMD -- and 169 for 2 x 128), else one level x 64 positions,
+// the most workgroups for short prefills. Handing each XCD whole batch rows (a tile's level groups
+// and its lagged B rows then share one L2) measured the same, 136 us, and so did rounding the hidden
+// tile once instead of at the eager path's two points (the launch is not bound by that VALU work).
 void dispatch_fwd_lds(const FwdArgs& a, hipStream_t s) {
   const int64_t wgs21 = (int64_t)((a.T + 63) / 64) * ((a.n_lv + 1) / 2) * a.b;
   if (wgs21 >= 1024) launch_fwd_lds<2, 1>(a, s);
