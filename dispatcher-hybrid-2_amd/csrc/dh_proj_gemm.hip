@@ -4,14 +4,19 @@
 // B = gate_hidden_src(x) -- three GEMMs over the same rows, done here as one launch over the
 // concatenated N = N_0 + N_1 + N_2 columns). fp32 accumulation; bf16 outputs rounded once.
 //
-// Work decomposition: a workgroup (4 wave64s) computes a 128 x 128 output tile; each wave a 64 x 64
-// quadrant as 4 x 4 MFMA tiles of 16 x 16 (v_mfma_f32_16x16x32_bf16; fp32 models use
-// v_mfma_f32_16x16x4f32). K advances in tiles of 128 bytes per row (64 bf16 / 32 fp32): both operand
-// tiles (128 rows each) are staged in LDS with a 16-byte row pad (conflict-free 16-byte fragment
-// reads), double-buffered, the next tile's global loads in flight in registers while the current one
-// is multiplied; one barrier per K tile. The weight tile is the MFMA's A operand and the activation
-// tile its B operand, so the accumulator of a lane holds four consecutive output columns of one
-// output row: the epilogue writes 8 (bf16) or 16 (fp32) contiguous bytes per lane and tile.
+// Work decomposition: a workgroup (4 wave64s, a 2 x 2 grid) computes a square output tile of
+// 32 * WT rows and columns; each wave a quadrant of WT x WT MFMA tiles of 16 x 16
+// (v_mfma_f32_16x16x32_bf16; fp32 models use v_mfma_f32_16x16x4f32). Two tile sizes:
+//   WT = 4: 128 x 128 tiles, for launches with too few 256 x 256 tiles to fill the 256 CUs;
+//   WT = 8: 256 x 256 tiles (bf16), for many rows: each wave's 128 x 128 quadrant reads 512 LDS bytes
+//           per k for 32 KFLOP, half the LDS traffic per MFMA of the 128 x 128 tile, whose 64 x 64
+//           quadrants need the LDS at its full read rate to keep the MFMA pipe busy.
+// K advances in tiles of 128 bytes per row (64 bf16 / 32 fp32): both operand tiles are staged in LDS
+// with a 16-byte row pad (conflict-free 16-byte fragment reads), double-buffered, the next tile's
+// global loads in flight in registers while the current one is multiplied; one barrier per K tile.
+// The weight tile is the MFMA's A operand and the activation tile its B operand, so the accumulator
+// of a lane holds four consecutive output columns of one output row: the epilogue writes 8 (bf16) or
+// 16 (fp32) contiguous bytes per lane and MFMA tile.
 // Block order is XCD-aware: with round-robin dispatch over the 8 XCDs, block id % 8 picks the XCD,
 // and every column tile of a row tile goes to the same XCD, so the row tile's activations are
 // fetched once into that XCD's L2.
@@ -187,7 +192,169 @@ __global__ __launch_bounds__(kThreads) void proj_gemm_kernel(GemmArgs a) {
   }
 }
 
+// LDS byte address of a __shared__ pointer (the M0 operand of global_load_lds)
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {          // s_waitcnt vmcnt(N), other counters untouched
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Output of a bf16 tile with 16-byte stores: MFMA tiles j and j + 1 (16 columns each) of a lane's
+// row are exchanged between lane rows g and g ^ 1 (v_permlane16_swap), after which lane (r, g) holds
+// 8 consecutive columns: 16 j' + 16 (g & 1) + 8 (g >> 1) .. + 7 of the 32-column pair j' = 2p.
+// Non-temporal: the output is not read again by the launch, so it need not displace the operand
+// tiles from L2. Needs column pairs in one segment (segment widths multiples of 8) and 16-byte
+// aligned output rows.
+template <int TM, int TN, int WGM>
+__device__ __forceinline__ void store_tile_x4(const GemmArgs& a, const f32x4 (&acc)[TN][TM], int m0, int n0, int wm,
+                                              int wn, int r, int g) {
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  static_assert(TN % 2 == 0, "column tiles in pairs");
+#pragma unroll
+  for (int p = 0; p < TN / 2; ++p) {
+    const int n = n0 + wn * 16 * TN + p * 32 + (g & 1) * 16 + (g >> 1) * 8;
+    int loc;
+    const int s = seg_of(a, min(n, a.Ntot - 1), loc);
+    bf16_t* o = (bf16_t*)pick(s, a.out[0], a.out[1], a.out[2]);
+    const int64_t ld = pick(s, a.ldo[0], a.ldo[1], a.ldo[2]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * 16 * TM + i * 16 + r;
+      const f32x4& X = acc[2 * p][i];
+      const f32x4& Y = acc[2 * p + 1][i];
+      const uint32_t x0 = (uint32_t)f32_to_bf16(X[0]) | ((uint32_t)f32_to_bf16(X[1]) << 16);
+      const uint32_t x1 = (uint32_t)f32_to_bf16(X[2]) | ((uint32_t)f32_to_bf16(X[3]) << 16);
+      const uint32_t y0 = (uint32_t)f32_to_bf16(Y[0]) | ((uint32_t)f32_to_bf16(Y[1]) << 16);
+      const uint32_t y1 = (uint32_t)f32_to_bf16(Y[2]) | ((uint32_t)f32_to_bf16(Y[3]) << 16);
+      // rows 2q + 1 of the first operand trade places with rows 2q of the second
+      const auto s0 = __builtin_amdgcn_permlane16_swap(x0, y0, false, false);
+      const auto s1 = __builtin_amdgcn_permlane16_swap(x1, y1, false, false);
+      const u32x4v v = {s0[0], s1[0], s0[1], s1[1]};
+      if (m < a.M && n < a.Ntot) __builtin_nontemporal_store(v, reinterpret_cast<u32x4v*>(o + (int64_t)m * ld + loc));
+    }
+  }
+}
+
+// Fragment ping-pong variant (bf16, 2 LDS stages): the MFMA operands of a K tile's two 32-k steps
+// live in two register sets, so the LDS reads of one step are in flight while the MFMAs of the other
+// run, across the K-tile boundary too: the barrier sits between the two steps' MFMAs. Row swizzle
+// swz2(R) = (R & 7) ^ ((R >> 3) & 1), which for the fragment rows base + 16 j + r (base a multiple of
+// 16) depends on r alone: a lane's fragment addresses are one register per step plus immediate
+// offsets. Conflict-free like swz: 8 distinct slots per 8 consecutive rows, and rows r, r + 8 apart.
+// The loads take a scalar base (operand + K offset; a weight segment is uniform over a wave's 8-row
+// group when every segment width is a multiple of 8) and 32-bit lane offsets.
+__device__ __forceinline__ int swz2(int R) { return (R & 7) ^ ((R >> 3) & 1); }
+
+__device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base)
+               : "memory", "m0");
+}
+
+template <int TM, int TN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) void proj_gemm_pp_kernel(GemmArgs a) {
+  typedef bf16_t T;
+  typedef Frag<T> F;
+  constexpr int NW = WGM * WGN;
+  constexpr int BM = 16 * TM * WGM, BN = 16 * TN * WGN;
+  constexpr int GX = BM / 8 / NW, GW = BN / 8 / NW;    // 8-row load groups per wave and operand
+  static_assert(GX * 8 * NW == BM && GW * 8 * NW == BN, "tile rows must split into 8-row groups per wave");
+  static_assert(F::KSTEPS == 2, "two 32-k steps per 128-byte K tile");
+  __shared__ __align__(1024) unsigned char sw[2][BN * kRowBytes];   // weight tiles
+  __shared__ __align__(1024) unsigned char sx[2][BM * kRowBytes];   // activation tiles
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int wm = wave % WGM, wn = wave / WGM;
+  const int nk = a.K / 64;
+  const int nvirt = ((a.mtiles + 7) / 8) * 8 * a.ntiles;
+
+  // fragment byte offsets within a stage: row R = quadrant base + 16 j + r, chunk 4 ks + g
+  const int fw = (wn * 16 * TN + r) * kRowBytes, fx = (wm * 16 * TM + r) * kRowBytes;
+  const int sr = swz2(r);
+  const int c0 = (g ^ sr) << 4, c1 = ((4 + g) ^ sr) << 4;
+  auto read = [&](uint4 (&wf)[TN], uint4 (&xf)[TM], int st, int cofs) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) wf[j] = *reinterpret_cast<const uint4*>(&sw[st][fw + j * 16 * kRowBytes + cofs]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) xf[i] = *reinterpret_cast<const uint4*>(&sx[st][fx + i * 16 * kRowBytes + cofs]);
+  };
+  f32x4 acc[TN][TM];
+  auto mma_all = [&](const uint4 (&wf)[TN], const uint4 (&xf)[TM]) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) F::mma(acc[j][i], wf[j], xf[i]);
+  };
+
+  // load group q of this wave: rows 8G .. 8G+7, G = NW q + wave; lane -> row 8G + lane / 8 whose
+  // slot lane % 8 takes chunk (lane % 8) ^ swz2(row); byte offsets from the operand base
+  uint32_t xo[GX], wo[GW];
+  int wsg[GW];
+  auto issue = [&](int kt, int st) {
+    const int kb = kt * kRowBytes;
+#pragma unroll
+    for (int q = 0; q < GW; ++q)
+      dma16s((const char*)pick(wsg[q], a.W[0], a.W[1], a.W[2]) + kb, wo[q], lds_addr(&sw[st][(NW * q + wave) * 1024]));
+#pragma unroll
+    for (int q = 0; q < GX; ++q) dma16s((const char*)a.X + kb, xo[q], lds_addr(&sx[st][(NW * q + wave) * 1024]));
+  };
+  uint4 aw[TN], ax[TM], bw[TN], bx[TM];                // step-0 and step-1 operand sets
+  int pm0 = -1, pn0 = 0;                               // the tile whose output acc holds
+  for (int id = blockIdx.x; id < nvirt; id += gridDim.x) {
+    const int xcd = id & 7, slot = id >> 3;
+    const int mt = (slot / a.ntiles) * 8 + xcd, nt = slot % a.ntiles;
+    if (mt >= a.mtiles) continue;                      // uniform
+    const int m0 = mt * BM, n0 = nt * BN;
+#pragma unroll
+    for (int q = 0; q < GX; ++q) {
+      const int R = 8 * (NW * q + wave) + (lane >> 3);
+      const int m = min(m0 + R, a.M - 1);
+      xo[q] = ((uint32_t)m * (uint32_t)a.ldx + (uint32_t)(((lane & 7) ^ swz2(R)) * 8)) * 2u;
+    }
+#pragma unroll
+    for (int q = 0; q < GW; ++q) {
+      const int R = 8 * (NW * q + wave) + (lane >> 3);
+      int loc;
+      const int n = min(n0 + R, a.Ntot - 1);
+      wsg[q] = __builtin_amdgcn_readfirstlane(seg_of(a, n, loc));
+      wo[q] = ((uint32_t)loc * (uint32_t)a.K + (uint32_t)(((lane & 7) ^ swz2(R)) * 8)) * 2u;
+    }
+    __syncthreads();                                   // the previous tile's LDS reads are done
+    issue(0, 0);
+    if (pm0 >= 0) store_tile_x4<TM, TN, WGM>(a, acc, pm0, pn0, wm, wn, r, g);   // under K tile 0's loads
+    pm0 = m0;
+    pn0 = n0;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    wait_vm<0>();                                      // K tile 0 (and the stores) done
+    __syncthreads();
+    issue(min(1, nk - 1), 1);
+    read(aw, ax, 0, c0);
+    for (int kt = 0; kt < nk; ++kt) {
+      const int st = kt & 1;
+      read(bw, bx, st, c1);                            // step 1 of tile kt ...
+      mma_all(aw, ax);                                 // ... in flight under step 0's MFMAs
+      wait_vm<0>();                                    // tile kt + 1 has landed (this wave's part)
+      __syncthreads();                                 // everyone's; every read of stage st is done
+      issue(min(kt + 2, nk - 1), st);                  // (repeats of the last tile are harmless)
+      if (kt + 1 < nk) read(aw, ax, st ^ 1, c0);       // step 0 of tile kt + 1 ...
+      mma_all(bw, bx);                                 // ... under step 1's MFMAs
+    }
+    wait_vm<0>();                                      // repeated tail loads land before LDS is reused
+  }
+  if (pm0 >= 0) store_tile_x4<TM, TN, WGM>(a, acc, pm0, pn0, wm, wn, r, g);
+}
+
 bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
+
+constexpr int64_t kWideMinTiles = 256;    // 256 x 256 tiles: one per CU at least
+constexpr int64_t kWideGrid = 256;        // persistent workgroups: one per CU (128 KB of LDS each)
 
 }  // namespace
 
@@ -222,14 +389,31 @@ extern "C" int dh_proj_gemm(int dtype, const void* X, int64_t ldx, int M, int K,
     total += N[s];
   }
   a.Ntot = total;
+  hipStream_t s = (hipStream_t)stream;
+  // bf16 launches with at least one 256 x 256 output tile per CU take the persistent 8-wave kernel
+  // (32-bit operand offsets, segment widths multiples of 8, 16-byte aligned output rows); the rest
+  // the 128 x 128 register-staged kernel, which keeps all 256 CUs busy on fewer rows.
+  bool wide = dtype == DH_BF16 && (int64_t)M * ldx * esz < (1ll << 31);
+  for (int i = 0; i < nseg; ++i)
+    wide = wide && N[i] % 8 == 0 && (int64_t)N[i] * K * esz < (1ll << 31) && ldo[i] % 8 == 0 && aligned(out[i], 16);
+  const int64_t tiles256 = (int64_t)((M + 255) / 256) * ((total + 255) / 256);
+  if (wide && tiles256 >= kWideMinTiles) {
+    a.mtiles = (M + 255) / 256;
+    a.ntiles = (total + 255) / 256;
+    const int64_t nvirt = (int64_t)((a.mtiles + 7) / 8) * 8 * a.ntiles;
+    DH_REQUIRE(nvirt < (1ll << 31), DH_ERR_UNSUPPORTED_SHAPE, "%s: M=%d too large", who, M);
+    const unsigned grid = (unsigned)(nvirt < kWideGrid ? nvirt : kWideGrid);
+    proj_gemm_pp_kernel<8, 4, 2, 4><<<dim3(grid), dim3(512), 0, s>>>(a);
+    return dh_check_launch(who);
+  }
   a.mtiles = (M + kBM - 1) / kBM;
   a.ntiles = (total + kBN - 1) / kBN;
   const int64_t grid = (int64_t)((a.mtiles + 7) / 8) * 8 * a.ntiles;
   DH_REQUIRE(grid < (1ll << 31), DH_ERR_UNSUPPORTED_SHAPE, "%s: M=%d too large", who, M);
-  hipStream_t s = (hipStream_t)stream;
   if (dtype == DH_BF16)
     proj_gemm_kernel<bf16_t><<<dim3((unsigned)grid), dim3(kThreads), 0, s>>>(a);
   else
     proj_gemm_kernel<float><<<dim3((unsigned)grid), dim3(kThreads), 0, s>>>(a);
   return dh_check_launch(who);
 }
+

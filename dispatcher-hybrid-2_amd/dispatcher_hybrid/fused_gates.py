@@ -329,18 +329,14 @@ def fused_projections(x, weights):
     return outs
 
 
-# dh_proj_gemm beats three library GEMMs up to this many rows on MI355X (K = 1024, N = 3 x 1024,
-# bf16: 20 us vs 58 us at 1024 rows); past it hipBLASLt's larger tiles win (172 vs 299 us at 32768)
-PROJ_GEMM_MAX_ROWS = 4096
-
-
 def input_projections(x, mixer):
     """V0 = linear_in(x), A = gate_hidden(x), B = gate_hidden_src(x) (reference
-    modeling_dispatcher.py:63-74): one dh_proj_gemm launch for up to PROJ_GEMM_MAX_ROWS rows of a
-    bias-free mixer, else the three nn.Linear calls. Inference only."""
+    modeling_dispatcher.py:63-74): one dh_proj_gemm launch for a bias-free mixer whose widths the
+    kernel takes (K a multiple of 64 for bf16 / 32 for fp32, widths multiples of 4) -- every row
+    count, the 4096 x 8 rows of a C5 layer included; the three nn.Linear calls only for other
+    layers. Inference only."""
     lins = (mixer.linear_in, mixer.gate_hidden, mixer.gate_hidden_src)
-    rows = x.numel() // x.shape[-1]
-    if (x.is_cuda and rows <= PROJ_GEMM_MAX_ROWS and all(l.bias is None for l in lins)
+    if (x.is_cuda and all(l.bias is None for l in lins)
             and all(l.weight.dtype == x.dtype for l in lins)
             and x.shape[-1] % (64 if x.dtype == torch.bfloat16 else 32) == 0
             and all(l.weight.shape[0] % 4 == 0 for l in lins)):

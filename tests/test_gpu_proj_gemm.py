@@ -18,6 +18,10 @@ CASES = [
     (1000, 256, [64, 192, 128]),          # segments that straddle the 128-column tiles
     (4096, 1024, [1024, 1024, 1024]),     # the released mixer (d = gh = 1024)
     (257, 1024, [1024]),
+    # bf16 launches with >= 256 output tiles of 256 x 256 take the persistent 8-wave kernel:
+    (6000, 1024, [1000, 1024, 1048]),     # ragged rows, segments straddling its 256-column tiles
+    (9000, 512, [3000]),                  # one segment, width not a multiple of 256
+    (32768, 1024, [1024, 1024, 1024]),    # the C5 layer: b = 8, T = 4096 rows
 ]
 
 
