@@ -99,8 +99,6 @@ def time_decode(torch, model, batch, prompt, warmup, steps, sample):
     logits = dec.prefill(ids)[:, -1]
     torch.manual_seed(5)
 
-    from dispatcher_hybrid import fused_step
-
     if not sample:
         # greedy as fast_generate runs it: the pick (device argmax, torch.argmax's token) is the last
         # part of the captured step and feeds the next one; one graph replay per token
@@ -123,16 +121,16 @@ def time_decode(torch, model, batch, prompt, warmup, steps, sample):
         dec.event_us_per_step = e0.elapsed_time(e1) * 1e3 / steps
         return batch * steps / dt, 1e3 * dt / steps, dec
 
-    def next_tok(lg):
-        # temperature 0.8 / top-k 50 sampling on the device, draws keyed by (seed, position, row)
-        return fused_step.sample_tokens(lg, 0.8, 50, 5, dec.t_buf)
-
+    # temperature 0.8 / top-k 50 sampling on the device (draws keyed by seed, position and row) as
+    # the last launch of the captured step: one graph replay per token, the sampled token feeding
+    # the next replay on the device (fast_generate's sampling branch)
+    dec.sample_start(logits, 0.8, 50, 5)
     for _ in range(warmup):
-        logits = dec.step(next_tok(logits))
+        dec.step_sample()
     sync_barrier(torch)
     t0 = time.perf_counter()
     for _ in range(steps):
-        logits = dec.step(next_tok(logits))
+        dec.step_sample()
     sync_barrier(torch)
     dt = time.perf_counter() - t0
     return batch * steps / dt, 1e3 * dt / steps, dec

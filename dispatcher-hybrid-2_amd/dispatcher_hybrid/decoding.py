@@ -441,6 +441,11 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         # (batch 1) and a second graph ends with the pick, which becomes the next step's input
         self._greedy_graph = None
         self._greedy_capture = False
+        # sampled decoding on the device: a third graph ends with the top-k sampler (its settings
+        # are part of the recorded launch, so a change of settings records it again)
+        self._sample_graph = None
+        self._sample_cfg = None
+        self._sample_capture = None
         self.tok_hist = torch.zeros(Bb, self.max_len + 1, dtype=torch.long, device=dev)
         self.cand = None
         if Bb == 1:
@@ -628,6 +633,11 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
             else:
                 fs.argmax_tokens(self.logits_out, out=self.token_buf)
                 self.tok_hist.index_copy_(1, self.t_buf, self.token_buf.unsqueeze(1))
+        elif self._sample_capture is not None:
+            # sampled pick (draws keyed by the new position) into token_buf and the token history
+            temperature, top_k, seed = self._sample_capture
+            fs.sample_tokens(self.logits_out, temperature, top_k, seed, self.t_buf, out=self.token_buf)
+            self.tok_hist.index_copy_(1, self.t_buf, self.token_buf.unsqueeze(1))
 
     @torch.no_grad()
     def greedy_start(self, logits):
@@ -637,6 +647,39 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         lg = logits.view(-1, logits.shape[-1])
         self._fused_step.argmax_tokens(lg, out=self.token_buf)
         self.tok_hist[:, self.t] = self.token_buf
+
+    @torch.no_grad()
+    def sample_start(self, logits, temperature=1.0, top_k=None, seed=0):
+        """Start device-side sampled decoding after prefill: temperature / top-k sampling
+        (fused_step.sample_tokens: Philox draws keyed by `seed`, the device position and the row) of
+        `logits` (the prefill's last-position logits) becomes the token fed to the next step and the
+        first entry of tok_hist; step_sample() then keeps the same settings. The tokens equal those
+        of step() followed by sample_tokens(logits, temperature, top_k, seed, t_buf)."""
+        cfg = (float(temperature), top_k, int(seed))
+        if cfg != self._sample_cfg:
+            self._sample_graph = None
+            self._sample_cfg = cfg
+        lg = logits.view(-1, logits.shape[-1])
+        self._fused_step.sample_tokens(lg, cfg[0], top_k, cfg[2], self.t_buf, out=self.token_buf)
+        self.tok_hist[:, self.t] = self.token_buf
+
+    @torch.no_grad()
+    def step_sample(self):
+        """One decode step fed by the token in token_buf, ending with the sampler of sample_start():
+        the next token goes to token_buf and tok_hist[:, t + 1] on the device -- one graph replay per
+        token, no host work (the sampling branch of fast_generate)."""
+        if self._sample_cfg is None:
+            raise RuntimeError("step_sample: call sample_start() first")
+        if self.t >= self.max_len:
+            raise ValueError(f"context exhausted at max_len {self.max_len}")
+        if self._sample_graph is None:
+            self._sample_capture = self._sample_cfg
+            try:
+                self._sample_graph = self._capture(self._step_all)
+            finally:
+                self._sample_capture = None
+        self._sample_graph.replay()
+        self.t += 1
 
     @torch.no_grad()
     def step_greedy(self):

@@ -491,17 +491,25 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
 
         Bb = ids.shape[0]
         logits = dec.prefill(ids)[:, -1]                     # ids is 2-D: (B, T, V) -> (B, V)
-        if isinstance(dec, FusedGraphedHybridDecoder) and not do_sample and eos_token_id is None:
-            # greedy without eos: every pick stays on the device (fused into the graphed step); the
-            # loop below appends min(max_new_tokens, max_len - t + 1) tokens, the same count here
+        if isinstance(dec, FusedGraphedHybridDecoder) and eos_token_id is None:
+            # without eos every pick stays on the device (the last launches of the graphed step); the
+            # loop below appends min(max_new_tokens, max_len - t + 1) tokens, the same count here.
+            # Sampling: draws keyed by a seed from torch's generator and the device position, the
+            # same tokens as the loop's sample_tokens picks
             n = min(max_new_tokens, dec.max_len - dec.t + 1)
             if n <= 0:
                 return ids
             t0 = dec.t
-            dec.greedy_start(logits)
-            for _ in range(n - 1):
-                dec.step_greedy()
-            dec.check_persistent()                         # a one-launch step that timed out is redone
+            if do_sample:
+                seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+                dec.sample_start(logits, max(temperature, 1e-6), top_k, seed)
+                for _ in range(n - 1):
+                    dec.step_sample()
+            else:
+                dec.greedy_start(logits)
+                for _ in range(n - 1):
+                    dec.step_greedy()
+                dec.check_persistent()                     # a one-launch step that timed out is redone
             return torch.cat([ids, dec.tok_hist[:, t0:t0 + n]], dim=1)
         finished = torch.zeros(Bb, dtype=torch.bool, device=ids.device)
         out = [ids]

@@ -269,3 +269,49 @@ def test_sample_rejects_bad_arguments():
         fused_step.sample_tokens(x, 0.0, 5)
     with pytest.raises(ValueError, match="65536"):
         fused_step.sample_tokens(torch.zeros(1, 70000, device=DEV), 1.0, 5)
+
+
+@pytest.mark.parametrize("batch", [1, 16])
+def test_step_sample_matches_step_then_sample(batch):
+    """FusedGraphedHybridDecoder.step_sample (the sampler recorded as the last launch of the graphed
+    step, the sampled token feeding the next replay on the device) against step() followed by
+    sample_tokens(logits, T, k, seed, t_buf) per token, the loop fast_generate ran before: the same
+    logits after every step and the same tokens; fast_generate's sampling branch returns them."""
+    from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder
+    from dispatcher_hybrid import fused_step
+    from helpers import product_model
+    from weights import make_state_dict
+    cfg = dict(vocab_size=2048, d_model=512, num_heads=8, dim_feedforward=1024, num_layers=4, max_len=256,
+               attn_layers=(2, 4), attn_window=64, doc_reset=True, eot_token=2047)
+    m = product_model(cfg, make_state_dict(cfg, 7), device=DEV, dtype=torch.bfloat16)
+    g = torch.Generator(device=DEV).manual_seed(21)
+    prompt = torch.randint(0, 2047, (1, 24), device=DEV, generator=g).expand(batch, -1).contiguous()
+    print(f"step_sample: batch {batch}", flush=True)
+    da, db = FusedGraphedHybridDecoder(m), FusedGraphedHybridDecoder(m)
+    la, lb = da.prefill(prompt)[:, -1], db.prefill(prompt)[:, -1]
+    t0 = da.t
+    da.sample_start(la, 0.8, 50, 77)
+    tok = fused_step.sample_tokens(lb, 0.8, 50, 77, db.t_buf)
+    toks = [tok.clone()]
+    for i in range(30):
+        da.step_sample()
+        lb = db.step(tok)
+        assert torch.equal(da.logits_out, lb), f"logits differ at step {i}"
+        tok = fused_step.sample_tokens(lb, 0.8, 50, 77, db.t_buf)
+        toks.append(tok.clone())
+    assert torch.equal(da.tok_hist[:, t0:t0 + 31], torch.stack(toks, 1))
+    assert torch.equal(da.token_buf, tok) and da.t == db.t
+    # fast_generate's sampling branch (no eos): the seed comes from torch's generator
+    torch.manual_seed(3)
+    out = m.fast_generate(prompt, max_new_tokens=12, do_sample=True, temperature=0.8, top_k=50, decoder="fused")
+    torch.manual_seed(3)
+    seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+    dc = FusedGraphedHybridDecoder(m)
+    lc = dc.prefill(prompt)[:, -1]
+    ref = []
+    for i in range(12):
+        tk = fused_step.sample_tokens(lc, 0.8, 50, seed, dc.t_buf)
+        ref.append(tk.clone())
+        if i < 11:
+            lc = dc.step(tk)
+    assert torch.equal(out[:, 24:], torch.stack(ref, 1))
