@@ -67,6 +67,53 @@ def test_fused_autograd_matches_eager():
         assert rel_err(pf.grad, pe.grad) < 1e-3, n
 
 
+def _gate_eager(A, Bs, params, n_lv, m3):
+    """The reference's gate pre-activations (modeling_dispatcher.py:100-109) in the inputs' dtype."""
+    from dispatcher_hybrid.modeling_dispatcher import level_gate_matmul
+    lagged = torch.stack([torch.roll(Bs, shifts=1 << l, dims=1) for l in range(n_lv)], dim=2)
+    hidden = torch.relu(A.unsqueeze(2) + lagged * m3.unsqueeze(-1).to(A.dtype)) ** 2
+    return [level_gate_matmul(hidden, W[:n_lv]) + b[:n_lv] for W, b in params]
+
+
+def test_fused_gate_backward_bf16_release_widths():
+    """bf16 gradients of dispatcher::gate_preacts_fwd (its bwd op, reference fused_gates.py:225-257)
+    at the released widths (GH 1024, 16 heads, 12 levels; b 2, T 512, a doc-reset style mask) for
+    dA, dB and the three readout weights and biases: each within 1.25x the eager bf16 autograd's
+    relative error against float32 autograd of the same formula (or 2e-3)."""
+    torch.manual_seed(11)
+    b, T, GH, H, L = 2, 512, 1024, 16, 12
+    A = (torch.randn(b, T, GH, device=DEV) * 0.5).bfloat16()
+    Bs = (torch.randn(b, T, GH, device=DEV) * 0.5).bfloat16()
+    params = [((torch.randn(L, H, GH, device=DEV) / 32).bfloat16(), (torch.randn(L, H, device=DEV) * 0.1).bfloat16())
+              for _ in range(3)]
+    t = torch.arange(T, device=DEV)
+    m3 = (t[None, :, None] >= (1 << torch.arange(L, device=DEV))[None, None, :]).float().expand(b, T, L).clone()
+    m3[0, 200:, 3:] = 0                                   # a document boundary in row 0
+    m3[1, 37, :] = 0
+    G = [torch.randn(b, T, L, H, device=DEV) for _ in range(3)]
+
+    def grads(fn, dtype, dev=DEV):
+        leaf = lambda x: x.detach().to(dev, dtype).clone().requires_grad_()
+        leaves = [leaf(A), leaf(Bs)]
+        ps = [(leaf(W), leaf(bb)) for W, bb in params]
+        outs = fn(leaves[0], leaves[1], ps, m3.to(dev))
+        loss = sum((o.float() * g.to(dev)).sum() for o, g in zip(outs, G))
+        loss.backward()
+        return [x.to(DEV) for x in [leaves[0].grad, leaves[1].grad] + [x.grad for W, bb in ps for x in (W, bb)]]
+
+    fused = grads(lambda a, bs, ps, mk: torch.ops.dispatcher.gate_preacts_fwd(
+        a, bs, ps[0][0], ps[1][0], ps[2][0], ps[0][1], ps[1][1], ps[2][1], L, mk), torch.bfloat16)
+    # eager bf16 autograd on the CPU: its bmm backward takes transposed bf16 operands, kept off the GPU
+    eager = grads(lambda a, bs, ps, mk: _gate_eager(a, bs, ps, L, mk), torch.bfloat16, "cpu")
+    truth = grads(lambda a, bs, ps, mk: _gate_eager(a, bs, ps, L, mk), torch.float32)
+    names = ["dA", "dB", "dWi", "dbi", "dWf", "dbf", "dWr", "dbr"]
+    for n, f, e, tr in zip(names, fused, eager, truth):
+        assert f.dtype == torch.bfloat16 and f.shape == tr.shape, n
+        ef, ee = rel_err(f.float(), tr), rel_err(e.float(), tr)
+        print(f"gate bwd bf16 {n}: fused rel {ef:.2e}  eager bf16 rel {ee:.2e}", flush=True)
+        assert ef <= max(1.25 * ee, 2e-3), n
+
+
 def _compare_decoder(dec_cls, m, vocab, device, prompt=40, steps=12, tol=1e-4):
     """reference tests/test_decoding.py:33-44 on seeded weights."""
     torch.manual_seed(0)
