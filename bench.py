@@ -67,10 +67,12 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--cpu-prompt", type=int, default=1024)
-    ap.add_argument("--leg", default="all", choices=["all", "prefill-kernels", "decode-b16", "decode-trace"],
-                    help="prefill-kernels: only the C5 kernel timings; decode-b16: only the batch-16 "
-                         "sampling decode (for rocprofv3 runs); decode-trace: per-phase timestamps of "
-                         "the one-launch batch-1 step (wait vs work table)")
+    ap.add_argument("--leg", default="all",
+                    choices=["all", "prefill-kernels", "prefill-c2", "decode-b16", "decode-trace"],
+                    help="prefill-kernels: only the C5 kernel timings; prefill-c2: only the C2 fused "
+                         "forward (for rocprofv3 runs); decode-b16: only the batch-16 sampling decode "
+                         "(for rocprofv3 runs); decode-trace: per-phase timestamps of the one-launch "
+                         "batch-1 step (wait vs work table)")
     return ap.parse_args()
 
 
@@ -303,11 +305,12 @@ def mixer_step_time(torch, model, dec, copies=400, reps=5):
 
 
 def prefill_kernels(torch, dev, reps=10):
-    """The parallel path's three gfx950 kernels at the C5 shape (b 8, T 4096, GH 1024, 16 heads of 64,
+    """The parallel path's gfx950 kernels at the C5 shape (b 8, T 4096, GH 1024, 16 heads of 64,
     12 levels, doc mask; attention window 1024), each timed with HIP events on its launch stream over
     `reps` launches, on synthetic bf16 inputs: the activated gate pre-activations (MFMA-bound: FLOPs
     2 b T L GH 3H), the level scan (HBM: gates + V0 in, V out) and the banded attention (MFMA: 4 b H hd
-    sum_t min(t+1, W) FLOPs for QK^T and PV)."""
+    sum_t min(t+1, W) FLOPs for QK^T and PV), and the three input projections as one dh_proj_gemm
+    launch (MFMA: 2 b T d (d + 2 GH) FLOPs) beside the three library GEMMs it replaces."""
     from dispatcher_hybrid import fused_attention as fa
     from dispatcher_hybrid import fused_gates as fg
     b, T, GH, H, hd, L, W = 8, 4096, 1024, 16, 64, 12, 1024
@@ -339,6 +342,10 @@ def prefill_kernels(torch, dev, reps=10):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e3 / reps
 
+    xin = torch.randn(b, T, d, device=dev, generator=g).to(bf)
+    Wp = [(torch.randn(n, d, device=dev, generator=g) / d ** 0.5).to(bf) for n in (d, GH, GH)]
+    proj_us = timed(lambda: fg.fused_projections(xin, Wp))
+    lib_us = timed(lambda: [torch.nn.functional.linear(xin, w) for w in Wp])
     gate_us = timed(lambda: fg._preacts_launch(A, B, *Ws, *bs, mask, gates, gates[0].stride(), 1, L, "bench"))
     scan_us = timed(lambda: fg._scan_launch(*gates, None, V0, V, H, L, True, "bench"))
     attn_us = timed(lambda: fa.window_attention(q, k, v, cos, sin, H, W))
@@ -348,8 +355,13 @@ def prefill_kernels(torch, dev, reps=10):
     attn_fl = 4 * b * H * hd * sum(min(t + 1, W) for t in range(T))
     tf = lambda fl, us: fl / (us * 1e-6) / 1e12
     gb = lambda by, us: by / (us * 1e-6) / 1e9
+    proj_fl = 2 * b * T * d * (d + 2 * GH)
     return {
         "shape": f"b {b}, T {T}, GH {GH}, {H} heads x {hd}, {L} levels, window {W}, bf16",
+        "input_projections": {"us": round(proj_us, 1), "bound": "mfma", "achieved": round(tf(proj_fl, proj_us), 1),
+                              "peak": MFMA_BF16_TFLOPS, "unit": "TFLOP/s",
+                              "frac": round(tf(proj_fl, proj_us) / MFMA_BF16_TFLOPS, 4), "flops": proj_fl,
+                              "three_library_gemms_us": round(lib_us, 1)},
         "gate_preacts": {"us": round(gate_us, 1), "bound": "mfma", "achieved": round(tf(gate_fl, gate_us), 1),
                          "peak": MFMA_BF16_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf(gate_fl, gate_us) / MFMA_BF16_TFLOPS, 4),
@@ -635,6 +647,13 @@ def main():
                 f"work {r['work_us']:6.2f}  spread {r['ready_spread_us']:6.2f}  total {r['span_total_us']:7.1f}")
         log(f"step {res['step_us']} us over {res['phases']} phases")
         print(json.dumps({"decode_trace": res}), flush=True)
+        return
+    if args.leg == "prefill-c2":
+        g = torch.Generator(device=dev).manual_seed(2)
+        ids = torch.randint(0, 50257, (1, 1024), device=dev, generator=g)
+        f_tok, f_ms, _ = time_forward(torch, model, ids, True, reps=5)
+        log(f"C2 prefill (fused gates): {f_tok:.0f} tok/s, {f_ms:.3f} ms per forward")
+        print(json.dumps({"prefill_tok_s": round(f_tok, 1), "prefill_ms": round(f_ms, 3)}), flush=True)
         return
     if args.leg == "decode-b16":
         steps16 = min(args.steps, 128)
