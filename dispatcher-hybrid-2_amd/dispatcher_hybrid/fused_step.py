@@ -2,10 +2,12 @@
 
 Drop-in for the reference module of the same name (reference dispatcher_hybrid/fused_step.py),
 whose two Triton kernels run the gate readouts over (row, level) and the level recurrence over
-(row, head). Here the whole step is ONE kernel per layer (``dh_decode_mixer_step``): one
-workgroup per (head, block of rows) reads its head's 3*L gate weight rows once, reduces them
-against every row's hidden vectors for all L levels, and runs the head's L-level recurrence over
-the ring buffers; no workgroup waits on another and no scratch memory is needed.
+(row, head). FusedGraphedHybridDecoder runs them as ``decode_gates_scan`` (``dh_decode_gates``, one
+wave per (level, head), then ``dh_decode_scan``) or, at batch 1, ``decode_gates_scan_out`` (the
+recurrence inside the out-projection launch), and batch-1 bf16 greedy steps as ONE launch per
+token (``persistent_step``). ``decode_mixer_step`` (``dh_decode_mixer_step``: the layer's whole
+step in one launch, one workgroup per (head, block of rows)) is the test reference the other forms
+are checked against; no decoder runs it.
 
 Ring layout (unchanged, reference dispatcher_hybrid/decoding.py:28-37, fused_step.py:13-16):
 level j's state is read only at lag 2^j, so ring j keeps 2^(j+1) slots at offset 2^(j+1)-2 and
