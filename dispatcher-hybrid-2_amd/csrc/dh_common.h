@@ -30,6 +30,20 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t x) { return __uint_as_float(
 // subnormals, overflow to infinity), a NaN for every NaN.
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
 
+// The dot product of two 16-byte chunks of 8 bf16 values on the dot-product unit: four
+// v_dot2c_f32_bf16 steps, element pairs (0,1), (2,3), (4,5), (6,7) in that order, from 0. Every
+// decode kernel whose result another path must equal bit for bit (the one-launch step and the
+// graph of launches) forms its bf16 chunk products with this one function.
+typedef __bf16 dh_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot8_bf16(const uint4& a, const uint4& b) {
+  float s = 0.f;
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(dh_bf16x2, a.x), __builtin_bit_cast(dh_bf16x2, b.x), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(dh_bf16x2, a.y), __builtin_bit_cast(dh_bf16x2, b.y), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(dh_bf16x2, a.z), __builtin_bit_cast(dh_bf16x2, b.z), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(dh_bf16x2, a.w), __builtin_bit_cast(dh_bf16x2, b.w), s, false);
+  return s;
+}
+
 template <typename T> struct Elem;
 template <> struct Elem<float> {
   __device__ __forceinline__ static float load(const float* p) { return *p; }

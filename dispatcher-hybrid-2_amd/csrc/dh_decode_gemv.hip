@@ -418,16 +418,20 @@ __global__ __launch_bounds__(NT) void decode_gemv_row_kernel(GemvArgs a) {
   for (int c = 0; c < CG; ++c) {
     const bool live = lane + 64 * c < nchunk;
     float hv[V];
-    Vec<T>::unpack(xc[c], hv);
+    if constexpr (sizeof(T) != 2) Vec<T>::unpack(xc[c], hv);
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int q = 0; q < NW; ++q) {
-        float wv[V];
-        Vec<T>::unpack(w[r][q][c], wv);
         float sdot = 0.f;
+        if constexpr (sizeof(T) == 2) {
+          sdot = dot8_bf16(w[r][q][c], xc[c]);         // as the one-launch step's dot_rows
+        } else {
+          float wv[V];
+          Vec<T>::unpack(w[r][q][c], wv);
 #pragma unroll
-        for (int e = 0; e < V; ++e) sdot += wv[e] * hv[e];
+          for (int e = 0; e < V; ++e) sdot += wv[e] * hv[e];
+        }
         acc[r][q] += live ? sdot : 0.f;
       }
   }

@@ -299,17 +299,12 @@ __device__ __forceinline__ void dot_rows(const Smem& S, int nchunk, const uint4 
 #pragma unroll
   for (int c = 0; c < CG; ++c) {
     const bool live = lane + 64 * c < nchunk;
-    float hv[8];
-    unpack8(S.sx[min(lane + 64 * c, nchunk - 1)], hv);
+    const uint4 hx = S.sx[min(lane + 64 * c, nchunk - 1)];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int q = 0; q < NW; ++q) {
-        float wv[8];
-        unpack8(w[r][q][c], wv);
-        float sdot = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sdot += wv[e] * hv[e];
+        const float sdot = dot8_bf16(w[r][q][c], hx);
         acc[r][q] += live ? sdot : 0.f;
       }
   }

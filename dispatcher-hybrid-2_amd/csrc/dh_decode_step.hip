@@ -762,14 +762,18 @@ __global__ __launch_bounds__(kSOThreads) void decode_scan_out_kernel(ScanOutArgs
   for (int c = 0; c < CG; ++c) {
     const int ch = lane + 64 * c;
     float yv[V];
-    Chunk<T>::unpack(sy[min(ch, nchunk - 1)], yv);
+    if constexpr (sizeof(T) != 2) Chunk<T>::unpack(sy[min(ch, nchunk - 1)], yv);
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
-      float wv[V];
-      Chunk<T>::unpack(w[r][c], wv);
       float part = 0.f;
+      if constexpr (sizeof(T) == 2) {
+        part = dot8_bf16(w[r][c], sy[min(ch, nchunk - 1)]);   // as the one-launch step's dot_rows
+      } else {
+        float wv[V];
+        Chunk<T>::unpack(w[r][c], wv);
 #pragma unroll
-      for (int e = 0; e < V; ++e) part += wv[e] * yv[e];
+        for (int e = 0; e < V; ++e) part += wv[e] * yv[e];
+      }
       acc[r] += ch < nchunk ? part : 0.f;
     }
   }
