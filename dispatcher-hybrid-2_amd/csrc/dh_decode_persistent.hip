@@ -1042,20 +1042,25 @@ __device__ __forceinline__ bool run_lm_head(const PArgs& a, Smem& S, const PreFi
   const int gw = blockIdx.x * kPW + wave, nw = gridDim.x * kPW;
   float cv = -INFINITY;
   int ci = 0x7fffffff;
-  uint4 w[R][1][CG];
+  // two row groups in flight: wa holds rows base (requested a phase ahead for the first group), wb
+  // the next group of the stride, each refilled two groups ahead as soon as its dot products are done
+  uint4 wa[R][1][CG], wb[R][1][CG];
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int c = 0; c < CG; ++c) w[r][0][c] = f.w[r][0][c];
-  auto fetch = [&](int base) { fetch_head_rows(w, a, base); };
+    for (int c = 0; c < CG; ++c) wa[r][0][c] = f.w[r][0][c];
+  const int stride = nw * R;
   stage_regs(S.sg, f.g, K);
   if (!wg_poll16(a, S, a.xw, K, xtag, reinterpret_cast<bf16_t*>(S.sx), ph)) return false;
+  // requested after the poll: loads complete in issue order, so an earlier request would hold up
+  // the poll's rounds
+  if (gw * R + stride < N) fetch_head_rows(wb, a, gw * R + stride);
   __syncthreads();
   norm_staged(S, K, a.eps);
-  for (int base = gw * R; base < N; base += nw * R) {
+  auto group = [&](uint4 (&w)[R][1][CG], int base) {
     float acc[R][1];
     dot_rows<R, 1, CG>(S, nchunk, w, acc);
-    if (base + nw * R < N) fetch(base + nw * R);      // the next rows fly during the epilogue
+    if (base + 2 * stride < N) fetch_head_rows(w, a, base + 2 * stride);
     if (lane < R && base + lane < N) {
       float v0 = 0.f;
 #pragma unroll
@@ -1067,6 +1072,10 @@ __device__ __forceinline__ bool run_lm_head(const PArgs& a, Smem& S, const PreFi
         ci = base + lane;
       }
     }
+  };
+  for (int base = gw * R; base < N; base += 2 * stride) {
+    group(wa, base);
+    if (base + stride < N) group(wb, base + stride);
   }
   wave_best(cv, ci);
   if (lane == 63) S.wbest[wave] = Cand{cv, ci};
