@@ -279,6 +279,70 @@ __device__ __forceinline__ void norm_staged(Smem& S, int K, float eps) {
   __syncthreads();
 }
 
+// The same wait for a row of n tagged words (n % 8 == 0, n <= 8 * kPT) with the words of chunk i
+// polled by thread i (two 16-byte loads) and returned in its registers (xc, bf16); threads past the
+// row only take part in the rounds' barriers.
+__device__ __forceinline__ bool wg_poll16_chunk(const PArgs& a, Smem& S, const uint32_t* src, int n, uint32_t tag,
+                                                uint4& xc, int ph) {
+  const int tid = threadIdx.x;
+  const bool mine = tid * 8 < n;
+  uint4 w0 = make_uint4(0u, 0u, 0u, 0u), w1 = w0;
+  Waiter wt;
+  while (true) {
+    bool ok = true;
+    if (mine) {
+      w0 = get16x4(src, n, tid * 8);
+      w1 = get16x4(src, n, tid * 8 + 4);
+    }
+    const uint32_t stw = tid == 0 ? get16(a.status) : 0u;
+    if (mine)
+      ok = tag_ok(w0.x, tag) && tag_ok(w0.y, tag) && tag_ok(w0.z, tag) && tag_ok(w0.w, tag) && tag_ok(w1.x, tag) &&
+           tag_ok(w1.y, tag) && tag_ok(w1.z, tag) && tag_ok(w1.w, tag);
+    if (tid == 0) S.stop = wt.expired(stw) ? 1 : 0;
+    if (__syncthreads_and(ok ? 1 : 0)) break;
+    if (S.stop) {
+      if (tid == 0) raise_abort(a, ph, wt.why, wt.polls);
+      return false;
+    }
+  }
+  DH_MARK(a, ph, 1);
+  xc = make_uint4((w0.x >> 16) | (w0.y & 0xffff0000u), (w0.z >> 16) | (w0.w & 0xffff0000u),
+                  (w1.x >> 16) | (w1.y & 0xffff0000u), (w1.z >> 16) | (w1.w & 0xffff0000u));
+  return true;
+}
+
+// norm_staged for a row whose chunk i thread i holds in registers (K <= 8 * kPT): the same sums
+// (chunk i's squares in order, DPP wave sums, the kPW wave sums in order) and rounding; the
+// normalised chunks go to the staged row. One barrier fewer, and no round trip of the raw row
+// through LDS.
+__device__ __forceinline__ void norm_chunk_regs(Smem& S, int K, float eps, const uint4& xc) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nchunk = K / 8;
+  const bool mine = tid < nchunk;
+  float xf[8];
+  unpack8(xc, xf);
+  float ss = 0.f;
+  if (mine) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += xf[e] * xf[e];
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) S.red[wave] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w2 = 0; w2 < kPW; ++w2) tot += S.red[w2];
+  const float rs = rsqrtf(tot / (float)K + eps);
+  if (mine) {
+    float gw[8];
+    unpack8(S.sg[tid], gw);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xf[e] = rnd(xf[e] * rs * gw[e]);
+    S.sx[tid] = pack8(xf);
+  }
+  __syncthreads();
+}
+
 // A row of K <= 4 * kPT bf16 elements held four per thread (requested with a phase's weights) into
 // the staged row or the norm-weight region of LDS.
 __device__ __forceinline__ void stage_regs(uint4* dst, uint2 v, int K) {
@@ -334,11 +398,13 @@ __device__ __forceinline__ bool stage_input(const PArgs& a, Smem& S, bool first,
   if (first) {
     stage_regs(S.sx, x0, a.d);
     DH_MARK(a, ph, 1);
+    __syncthreads();
+    norm_staged(S, a.d, a.eps);
   } else {
-    if (!wg_poll16(a, S, a.xw, a.d, xtag, reinterpret_cast<bf16_t*>(S.sx), ph)) return false;
+    uint4 xc;
+    if (!wg_poll16_chunk(a, S, a.xw, a.d, xtag, xc, ph)) return false;
+    norm_chunk_regs(S, a.d, a.eps, xc);
   }
-  __syncthreads();
-  norm_staged(S, a.d, a.eps);
   return true;
 }
 
@@ -453,9 +519,9 @@ __device__ __forceinline__ bool run_ffn_up(const PArgs& a, Smem& S, const PreUp&
   const int base = (blockIdx.x * kPW + wave) * R;
   if (blockIdx.x * kPW * R >= N) return true;
   stage_regs(S.sg, f.g, a.d);
-  if (!wg_poll16(a, S, a.xw, a.d, xtag, reinterpret_cast<bf16_t*>(S.sx), ph)) return false;
-  __syncthreads();
-  norm_staged(S, a.d, a.eps);
+  uint4 xc;
+  if (!wg_poll16_chunk(a, S, a.xw, a.d, xtag, xc, ph)) return false;
+  norm_chunk_regs(S, a.d, a.eps, xc);
   if (base >= N) return true;
   float acc[R][2];
   dot_rows<R, 2, CG>(S, nchunk, f.w, acc);
@@ -1051,12 +1117,12 @@ __device__ __forceinline__ bool run_lm_head(const PArgs& a, Smem& S, const PreFi
     for (int c = 0; c < CG; ++c) wa[r][0][c] = f.w[r][0][c];
   const int stride = nw * R;
   stage_regs(S.sg, f.g, K);
-  if (!wg_poll16(a, S, a.xw, K, xtag, reinterpret_cast<bf16_t*>(S.sx), ph)) return false;
+  uint4 xc;
+  if (!wg_poll16_chunk(a, S, a.xw, K, xtag, xc, ph)) return false;
   // requested after the poll: loads complete in issue order, so an earlier request would hold up
   // the poll's rounds
   if (gw * R + stride < N) fetch_head_rows(wb, a, gw * R + stride);
-  __syncthreads();
-  norm_staged(S, K, a.eps);
+  norm_chunk_regs(S, K, a.eps, xc);
   auto group = [&](uint4 (&w)[R][1][CG], int base) {
     float acc[R][1];
     dot_rows<R, 1, CG>(S, nchunk, w, acc);
