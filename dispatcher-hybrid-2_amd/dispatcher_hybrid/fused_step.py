@@ -2,12 +2,12 @@
 
 Drop-in for the reference module of the same name (reference dispatcher_hybrid/fused_step.py),
 whose two Triton kernels run the gate readouts over (row, level) and the level recurrence over
-(row, head). FusedGraphedHybridDecoder runs them as ``decode_gates_scan`` (``dh_decode_gates``, one
-wave per (level, head), then ``dh_decode_scan``) or, at batch 1, ``decode_gates_scan_out`` (the
-recurrence inside the out-projection launch), and batch-1 bf16 greedy steps as ONE launch per
-token (``persistent_step``). ``decode_mixer_step`` (``dh_decode_mixer_step``: the layer's whole
-step in one launch, one workgroup per (head, block of rows)) is the test reference the other forms
-are checked against; no decoder runs it.
+(row, head). FusedGraphedHybridDecoder runs them at batch 1 as ``decode_gates_scan_out``
+(``dh_decode_gates``, one wave per (level, head), then the recurrence inside the out-projection
+launch) and batch-1 bf16 greedy steps as ONE launch per token (``persistent_step``); at batch > 1
+as ``decode_mixer_step`` (``dh_decode_mixer_step``: the layer's whole step in one launch, one
+workgroup per (head, block of rows)), also the baseline the tests check the other forms against.
+``decode_gates_scan`` (``dh_decode_gates`` then ``dh_decode_scan``) is the two-launch form.
 
 Ring layout (unchanged, reference dispatcher_hybrid/decoding.py:28-37, fused_step.py:13-16):
 level j's state is read only at lag 2^j, so ring j keeps 2^(j+1) slots at offset 2^(j+1)-2 and

@@ -137,9 +137,9 @@ int dh_level_scan_fwd(int dtype, const void* pre_i, const void* pre_f, const voi
  * Computes what the Triton kernels `step_gates_kernel` + `step_scan_kernel` (reference
  * dispatcher_hybrid/fused_step.py:26-59 and :62-88) compute as launched by
  * FusedGraphedHybridDecoder._tree_step_g (reference dispatcher_hybrid/decoding.py:477-486).
- * A test reference: the tests check it against the oracle and the decoder's forms
- * (dh_decode_gates + dh_decode_scan / dh_decode_scan_out, the one-launch batch-1 step) against it;
- * no decoder runs it.
+ * FusedGraphedHybridDecoder runs it at batch > 1; the tests check it against the oracle and the
+ * other forms (dh_decode_gates + dh_decode_scan / dh_decode_scan_out, the one-launch batch-1 step)
+ * against it.
  *   A         (B, GH) destination features W1x.h1 of the current token.
  *   B_hist    (B, Tmax, GH); row t (the current token) already written.
  *   Wi,Wf,Wr  (L, H, GH) contiguous; bi,bf,br (L, H) contiguous, dtype `dtype`.
