@@ -241,13 +241,15 @@ __device__ __forceinline__ void store_tile_x4(const GemmArgs& a, const f32x4 (&a
 
 // Fragment ping-pong variant (bf16, 2 LDS stages): the MFMA operands of a K tile's two 32-k steps
 // live in two register sets, so the LDS reads of one step are in flight while the MFMAs of the other
-// run, across the K-tile boundary too: the barrier sits between the two steps' MFMAs. Row swizzle
-// swz2(R) = (R & 7) ^ ((R >> 3) & 1), which for the fragment rows base + 16 j + r (base a multiple of
-// 16) depends on r alone: a lane's fragment addresses are one register per step plus immediate
-// offsets. Conflict-free like swz: 8 distinct slots per 8 consecutive rows, and rows r, r + 8 apart.
-// The loads take a scalar base (operand + K offset; a weight segment is uniform over a wave's 8-row
-// group when every segment width is a multiple of 8) and 32-bit lane offsets.
-__device__ __forceinline__ int swz2(int R) { return (R & 7) ^ ((R >> 3) & 1); }
+// run, across the K-tile boundary too: the barrier sits between the two steps' MFMAs. Row swizzle:
+// slot p of row R holds chunk p ^ (R & 7). Measured with the LDS counters on MI355X, the fragment
+// reads (16 lanes = 16 consecutive rows, one chunk; ds_read_b128) then take 4 LDS cycles per
+// instruction, the conflict-free minimum, where (R & 7) ^ ((R >> 3) & 1) or a 144-byte row pitch
+// take 8. For the fragment rows base + 16 j + r (base a multiple of 16) it depends on r alone, so a
+// lane's fragment addresses are one register per step plus immediate offsets. The loads take a
+// scalar base (operand + K offset; a weight segment is uniform over a wave's 8-row group when every
+// segment width is a multiple of 8) and 32-bit lane offsets.
+__device__ __forceinline__ int swz2(int R) { return R & 7; }
 
 __device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base)
