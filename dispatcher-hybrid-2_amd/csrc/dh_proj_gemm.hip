@@ -342,11 +342,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void proj_gemm_pp_kernel(GemmArgs a
       const int st = kt & 1;
       read(bw, bx, st, c1);                            // step 1 of tile kt ...
       mma_all(aw, ax);                                 // ... in flight under step 0's MFMAs
+      // Scheduling fences: without them the compiler sinks step 0's MFMAs below the barrier (they
+      // touch no memory), which leaves step 1's reads waited on with nothing in flight under them.
+      __builtin_amdgcn_sched_barrier(0);
       wait_vm<0>();                                    // tile kt + 1 has landed (this wave's part)
       __syncthreads();                                 // everyone's; every read of stage st is done
       issue(min(kt + 2, nk - 1), st);                  // (repeats of the last tile are harmless)
       if (kt + 1 < nk) read(aw, ax, st ^ 1, c0);       // step 0 of tile kt + 1 ...
+      __builtin_amdgcn_sched_barrier(0);
       mma_all(bw, bx);                                 // ... under step 1's MFMAs
+      __builtin_amdgcn_sched_barrier(0);
     }
     wait_vm<0>();                                      // repeated tail loads land before LDS is reused
   }
