@@ -48,10 +48,10 @@ EOT = 50256
 # HBM bytes per dh_decode_gemv launch, averaged over the decode step's 57 launches: rocprofv3 --pmc
 # FETCH_SIZE (x 1.99975, the factor a 256 MiB copy's reading gives) + WRITE_SIZE (x 1.0), from
 # profiles/decode_c3_b1_kernels.md
-TRAFFIC_GEMV_LAUNCH = 9_465_653
+TRAFFIC_GEMV_LAUNCH = 9_453_050
 # HBM bytes per decode_persistent_kernel launch (one batch-1 step), same counters and factors, from
 # profiles/decode_c3_b1_persistent.md
-TRAFFIC_PERSISTENT_LAUNCH = 611_723_293
+TRAFFIC_PERSISTENT_LAUNCH = 611_990_965
 # algorithmic bytes of one batch-1 step at context >= 1024: weights 584,316,928 + tree state
 # 1,224,704 + windowed keys and values 8,396,800
 STEP_BYTES = 584_316_928 + 1_224_704 + 8_396_800
@@ -65,6 +65,8 @@ def parse():
     ap.add_argument("--prompt", type=int, default=3840)
     ap.add_argument("--skip-extras", action="store_true", help="decode batch-1 only")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph-step", action="store_true",
+                    help="C3 on the graph of launches instead of the one-launch step (profiling)")
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--cpu-prompt", type=int, default=1024)
     ap.add_argument("--leg", default="all",
@@ -92,12 +94,12 @@ def sync_barrier(torch):
     torch.cuda.synchronize()
 
 
-def time_decode(torch, model, batch, prompt, warmup, steps, sample):
+def time_decode(torch, model, batch, prompt, warmup, steps, sample, persistent=True):
     from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder
     dev = next(model.parameters()).device
     g = torch.Generator(device=dev).manual_seed(3 if batch == 1 else 4)
     ids = torch.randint(0, EOT, (1, prompt), device=dev, generator=g).expand(batch, -1).contiguous()
-    dec = FusedGraphedHybridDecoder(model)
+    dec = FusedGraphedHybridDecoder(model, persistent=persistent)
     logits = dec.prefill(ids)[:, -1]
     torch.manual_seed(5)
 
@@ -666,7 +668,8 @@ def main():
     if prompt < 1:
         raise SystemExit("--steps + --warmup exceed the 4096-token context")
     log(f"C3 decode: B=1 prompt={prompt} warmup={args.warmup} steps={args.steps}")
-    tok_s, ms_step, dec1 = time_decode(torch, model, 1, prompt, args.warmup, args.steps, sample=False)
+    tok_s, ms_step, dec1 = time_decode(torch, model, 1, prompt, args.warmup, args.steps, sample=False,
+                                       persistent=not args.graph_step)
     log(f"C3 decode: {tok_s:.1f} tok/s ({ms_step * 1e3:.1f} us/token)")
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
