@@ -198,11 +198,13 @@ __device__ __forceinline__ V block_scan(V v, V* red, V& total) {
 // k. Returns 0 when fewer than k keys are non-zero. Callers synchronise before; every thread gets
 // the result. hist: 256 entries; state: 4 (a pair per pass parity, so that thread 0 can reset the
 // next pass's pair while other threads still read this one's).
+// NP < 4 passes: keys whose low 32 - 8 NP bits are zero (the result keeps them zero).
+template <int NP = 4>
 __device__ __forceinline__ uint32_t radix_kth(const uint32_t* vals, int n, int k, uint32_t* hist, uint32_t* state) {
   const int tid = threadIdx.x, lane = tid & 63;
   uint32_t prefix = 0;
   uint32_t kk = (uint32_t)k;
-  for (int pass = 0; pass < 4; ++pass) {
+  for (int pass = 0; pass < NP; ++pass) {
     const int shift = 24 - 8 * pass;
     if (tid < 256) hist[tid] = 0u;
     uint32_t* st = state + 2 * (pass & 1);
@@ -246,7 +248,7 @@ __device__ __forceinline__ uint32_t radix_kth(const uint32_t* vals, int n, int k
     kk = st[1];
     prefix = (prefix << 8) | d;
   }
-  return prefix;
+  return prefix << (8 * (4 - NP));
 }
 
 template <typename T>
@@ -377,6 +379,171 @@ __global__ __launch_bounds__(kST) void sample_topk_kernel(const T* logits, int64
   if (tid == 0) out[b] = chosen != 0x7fffffff ? chosen : (fallback >= 0 ? fallback : 0);
 }
 
+// bf16 logits with 0 < top_k <= kST: the same selection, weights and draw on 16-bit order keys of
+// the logits themselves, two per register (the 32-bit keys of the kernel above take 64 registers per
+// thread and spill). Division by a positive temperature is monotone and keeps distinct bf16 values
+// distinct in fp32 (their spacing, 2^-8 relative, is far above fp32 rounding), so the order, the
+// ties and the kept set of x and of l = x / temperature are the same. The candidates (keys >= tau)
+// are compacted into LDS as (key << 16) | index, in index order, so after kth is known each thread
+// walks only its own few entries: l = x / temperature and the weights exp(l - max l) are formed,
+// as above, for the kept elements only, twice (for the sums, then for the draw), in the same order
+// and association as the kernel above, whose output this kernel reproduces bit for bit (measured
+// over 12,300 draws of tie-heavy, signed-zero, -inf and random rows). Rows whose candidates exceed
+// the LDS list fall back to the key-space search and a walk over the registers.
+__device__ __forceinline__ uint32_t key16x2(uint32_t w) {   // order keys of the two bf16 halves
+  const uint32_t sgn = (w >> 15) & 0x00010001u;              // sign bit of each half
+  return w ^ 0x80008000u ^ (sgn * 0x7fffu);                  // negative: ~h, else h | 0x8000
+}
+__device__ __forceinline__ float key16_value(uint32_t k) {  // inverse of one half's key
+  const uint32_t h = (k & 0x8000u) ? (k ^ 0x8000u) : (k ^ 0xffffu);
+  return __uint_as_float(h << 16);
+}
+
+__global__ __launch_bounds__(kST) void sample_topk_bf16_kernel(const bf16_t* logits, int64_t row_stride, int V,
+                                                               float temperature, int top_k, uint64_t seed,
+                                                               const int64_t* offset_dev, int64_t* out) {
+  constexpr int NP = kSPT / 2;                         // registers of packed key pairs
+  __shared__ uint32_t buf[kCap + 1];
+  __shared__ float fred[kST / 64];
+  __shared__ uint32_t ured[kST / 64];
+  __shared__ uint32_t hist[256], rstate[4];
+  __shared__ int chosen, fallback;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const bf16_t* row = logits + (int64_t)b * row_stride;
+  const int i0 = tid * kSPT;                           // this thread's elements: [i0, i0 + kSPT)
+  const int nv = min(max(V - i0, 0), kSPT);
+  const int64_t off = offset_dev ? load_uniform(offset_dev) : 0;
+
+  // ---- keys: pair i holds elements 2i (low half) and 2i + 1 (high half); key 0 past V
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(row), (short)0, (int)(V * 2), 0x00020000);
+  uint32_t kp[NP];
+#pragma unroll
+  for (int c = 0; c < NP / 4; ++c) {
+    const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   rsrc, (uint32_t)(i0 * 2) + c * 16, 0, 0));
+    kp[4 * c] = key16x2(v.x);
+    kp[4 * c + 1] = key16x2(v.y);
+    kp[4 * c + 2] = key16x2(v.z);
+    kp[4 * c + 3] = key16x2(v.w);
+  }
+  uint32_t kmax = 0u;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    kp[i] = 2 * i + 1 < nv ? kp[i] : (2 * i < nv ? (kp[i] & 0xffffu) : 0u);
+    kmax = max(kmax, max(kp[i] & 0xffffu, kp[i] >> 16));
+  }
+  if (tid == 0) {
+    chosen = 0x7fffffff;
+    fallback = -1;
+  }
+  uint32_t bm = kmax;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) bm = max(bm, (uint32_t)__shfl_xor((int)bm, o));
+  if ((tid & 63) == 0) ured[tid >> 6] = bm;
+  __syncthreads();
+  uint32_t mkey = ured[0];
+#pragma unroll
+  for (int w = 1; w < kST / 64; ++w) mkey = max(mkey, ured[w]);
+  const float M = key16_value(mkey) / temperature;
+
+  auto count_ge = [&](uint32_t thr) {                  // this thread's non-zero keys >= thr
+    uint32_t c = 0;
+    if (kmax < thr) return c;                          // most threads, once thr is near the top
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const uint32_t lo = kp[i] & 0xffffu, hi = kp[i] >> 16;
+      c += (lo >= thr && lo != 0u) ? 1u : 0u;
+      c += (hi >= thr && hi != 0u) ? 1u : 0u;
+    }
+    return c;
+  };
+  // ---- kth largest (exact), as a key: tau = the top_k-th largest per-thread maximum bounds it.
+  // The keys >= tau (and -0.0 beside +0.0) are compacted into LDS in index order as (key << 16) |
+  // index; kth is their top_k-th largest, and the kept elements are among them.
+  buf[tid] = kmax << 16;
+  __syncthreads();
+  uint32_t tau = radix_kth<2>(buf, kST, top_k, hist, rstate) >> 16;
+  tau = tau == 0x8000u ? 0x7fffu : tau;
+  const uint32_t cnt = count_ge(tau);
+  uint32_t C;
+  const uint32_t r0 = block_scan(cnt, ured, C);
+  uint32_t kkey = 0u;
+  const bool compact = C <= (uint32_t)kCap;            // uniform
+  if (compact) {
+    if (cnt > 0u) {
+      uint32_t r = r0;
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t k = h ? kp[i] >> 16 : kp[i] & 0xffffu;
+          if (k >= tau && k != 0u) buf[r++] = (k << 16) | (uint32_t)(i0 + 2 * i + h);
+        }
+      }
+    }
+    __syncthreads();
+    kkey = radix_kth<2>(buf, (int)C, top_k, hist, rstate) >> 16;
+  }
+  if (kkey == 0u) {                                    // uniform: the largest v with count(key >= v) >= top_k
+    uint32_t lo = 1u, hi = mkey;
+    while (lo < hi) {
+      const uint32_t mid = lo + ((hi - lo + 1u) >> 1);
+      uint32_t n;
+      (void)block_scan(count_ge(mid), ured, n);
+      if (n >= (uint32_t)top_k) lo = mid; else hi = mid - 1u;
+    }
+    kkey = lo;
+  }
+  // kept: x >= kth as floats (-0.0 ties +0.0: key 0x7fff next to +0.0's 0x8000) and x > -inf
+  // (key 0x007f); empty slots (key 0) are below both
+  const uint32_t thr = max(kkey == 0x8000u ? 0x7fffu : kkey, 0x0080u);
+  const bool listed = compact && thr >= tau;            // uniform: every kept element is in buf
+  auto weight = [&](uint32_t k) { return __expf(key16_value(k) / temperature - M); };
+  // this thread's kept elements in index order, from its compacted entries or its registers
+  auto for_kept = [&](auto&& fn) {
+    if (listed) {
+      for (uint32_t e = r0; e < r0 + cnt; ++e) {
+        const uint32_t v = buf[e];
+        if ((v >> 16) >= thr) fn(v >> 16, (int)(v & 0xffffu));
+      }
+    } else if (kmax >= thr) {
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t k = h ? kp[i] >> 16 : kp[i] & 0xffffu;
+          if (k >= thr) fn(k, i0 + 2 * i + h);
+        }
+      }
+    }
+  };
+  float s = 0.f;
+  for_kept([&](uint32_t k, int) { s += weight(k); });
+  float total;
+  const float excl = block_scan(s, fred, total);
+
+  // ---- the draw: the element whose cumulative interval (index order) holds u * total
+  const uint32_t rnd = philox4x32_10(seed, (uint64_t)off, (uint32_t)b);
+  const float target = (float)(rnd >> 8) * 0x1.0p-24f * total;
+  if (s > 0.f) {
+    int hit = 0x7fffffff, last = -1;
+    float c = excl;
+    for_kept([&](uint32_t k, int j) {
+      const float w = weight(k);
+      if (w > 0.f) {
+        if (hit == 0x7fffffff && target >= c && target < c + w) hit = j;
+        last = j;
+      }
+      c += w;
+    });
+    if (hit != 0x7fffffff) atomicMin(&chosen, hit);
+    atomicMax(&fallback, last);
+  }
+  __syncthreads();
+  if (tid == 0) out[b] = chosen != 0x7fffffff ? chosen : (fallback >= 0 ? fallback : 0);
+}
+
 }  // namespace
 
 extern "C" int dh_sample_topk(int dtype, const void* logits, int64_t row_stride, int B, int V, float temperature,
@@ -392,7 +559,10 @@ extern "C" int dh_sample_topk(int dtype, const void* logits, int64_t row_stride,
              who, (double)temperature);
   DH_REQUIRE(logits && out, DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == DH_BF16)
+  if (dtype == DH_BF16 && top_k > 0 && top_k <= kST && top_k < V)
+    sample_topk_bf16_kernel<<<B, kST, 0, s>>>((const bf16_t*)logits, row_stride, V, temperature, top_k, seed,
+                                               offset_dev, out);
+  else if (dtype == DH_BF16)
     sample_topk_kernel<bf16_t><<<B, kST, 0, s>>>((const bf16_t*)logits, row_stride, V, temperature, top_k, seed,
                                                   offset_dev, out);
   else

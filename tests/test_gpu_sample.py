@@ -188,6 +188,34 @@ def test_sample_full_softmax_and_temperature():
     _chi2_ok(d, p[0], "full softmax")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sample_signed_zero_tie_and_minus_inf(dtype):
+    """The kth value is +0.0 and other logits are -0.0: torch's mask (l < kth) keeps both signs, so
+    every zero is drawable. -inf logits are never drawn, also when top_k reaches into them."""
+    from dispatcher_hybrid import fused_step
+    V, rows = 3000, 8192
+    base = torch.full((V,), -5.0, device=DEV)
+    base[10:20] = 1.0
+    base[100:150:2] = 0.0
+    base[101:151:2] = -0.0
+    logits = base.to(dtype).expand(rows, V).contiguous()
+    k = 11                                              # 10 ones, then the zeros tie at the kth
+    kept, p = _kept_and_probs(logits[:1], 0.7, k)
+    assert int(kept.sum()) == 10 + 50
+    d = fused_step.sample_tokens(logits, 0.7, k, seed=3, offset=None)
+    torch.cuda.synchronize()
+    assert bool(kept[0, d].all()), "a draw outside torch's kept set"
+    zeros = d[(d >= 100) & (d < 150)]
+    assert int((zeros % 2 == 1).sum()) > 0 and int((zeros % 2 == 0).sum()) > 0   # both signs drawn
+    _chi2_ok(d, p[0], f"signed zeros {dtype}")
+    inf = torch.full((4, 200), float("-inf"), device=DEV)
+    inf[:, :3] = torch.tensor([0.5, -1.0, 2.0], device=DEV)
+    inf = inf.to(dtype)
+    d2 = fused_step.sample_tokens(inf, 1.0, 50, seed=1, offset=None)
+    torch.cuda.synchronize()
+    assert int(d2.max()) < 3, "a -inf logit was drawn"
+
+
 @pytest.mark.parametrize("V,k", [(5000, 2000), (50257, 50)])
 def test_sample_wide_top_k_and_all_ties(V, k):
     """top_k > 1024 (the kth found by the exact key-space search) and a row of one repeated value
