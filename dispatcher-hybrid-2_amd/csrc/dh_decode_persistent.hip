@@ -206,6 +206,8 @@ struct Smem {
   float sc[2][kMaxSeg];
   float ared[2][2];
   float part[2][2][kHD];
+  // attention combine: the head's segment records, gathered by the workgroup's waves
+  float cm[kSplitS], cl[kSplitS], co[kSplitS][kHD];
 };
 
 // Workgroup wait for n tagged bf16 words (n % 4 == 0, n <= 4 * kPT * 3); the values land in dst
@@ -795,7 +797,7 @@ __device__ __forceinline__ bool run_scan_out(const PArgs& a, Smem& S, const PreS
 
 // ---------------------------------------------------------------------------------------------
 // Attention layer: split-window segments (16 per head, two per workgroup of 128 threads each),
-// then one wave per head combines the segment records.
+// then one workgroup per head combines the segment records.
 // ---------------------------------------------------------------------------------------------
 // geometry of this thread's attention segment unit (two units of kUT threads per workgroup)
 struct AttnGeo {
@@ -1040,48 +1042,67 @@ __device__ __forceinline__ bool run_attn_split(const PArgs& a, Smem& S, const Pr
   return true;
 }
 
-// one wave per head: y[h*64 + e] = round(sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s) -> tagged y
-__device__ __forceinline__ void phase_attn_combine(const PArgs& a, int sph, int ph, Tags tg) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int gw = blockIdx.x * kPW + wave;
-  if (gw >= a.H) return;
-  const int h = gw, e = lane;
+// one workgroup per head: y[h*64 + e] = round(sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s) -> tagged y.
+// The four waves poll four segments each (eight loads a lane per round instead of 32 for one
+// wave), the records meet in LDS, and wave 0 forms y with the same sums, in the same order, as
+// the combine launch of the graph of launches.
+static_assert(kSplitS == 4 * kPW, "four segments per wave");
+__device__ __forceinline__ void phase_attn_combine(const PArgs& a, Smem& S, int sph, int ph, Tags tg) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if ((int)blockIdx.x >= a.H) return;                  // uniform
+  const int h = blockIdx.x, e = lane;
   const uint64_t* rec = a.partw + (int64_t)h * kSplitS * (2 + kHD);
   const uint32_t* rec32 = reinterpret_cast<const uint32_t*>(rec);
   const int nw32 = kSplitS * (2 + kHD) * 2;
   const uint32_t st = tg.t32(sph);
-  float m[kSplitS], l[kSplitS], o[kSplitS];
+  float m4[4], l4[4], o4[4];
   {
     Waiter wt;
     while (true) {
-      const uint32_t stw = get16(a.status);
+      const uint32_t stw = tid == 0 ? get16(a.status) : 0u;
       bool ok = true;
 #pragma unroll
-      for (int s = 0; s < kSplitS; ++s) {
-        const uint4 ml = get16x4(rec32, nw32, s * (2 + kHD) * 2);          // m, l of segment s
-        const uint64_t ow = get32(rec + s * (2 + kHD) + 2 + e);
+      for (int q = 0; q < 4; ++q) {
+        const int sg = 4 * wave + q;
+        const uint4 ml = get16x4(rec32, nw32, sg * (2 + kHD) * 2);         // m, l of segment sg
+        const uint64_t ow = get32(rec + sg * (2 + kHD) + 2 + e);
         ok = ok && ml.y == st && ml.w == st && (uint32_t)(ow >> 32) == st;
-        m[s] = __uint_as_float(ml.x);
-        l[s] = __uint_as_float(ml.z);
-        o[s] = __uint_as_float((uint32_t)ow);
+        m4[q] = __uint_as_float(ml.x);
+        l4[q] = __uint_as_float(ml.z);
+        o4[q] = __uint_as_float((uint32_t)ow);
       }
-      if (__all(ok)) break;
-      if (wt.expired(__builtin_amdgcn_readfirstlane(stw))) {
-        raise_abort(a, ph, wt.why, wt.polls);
+      if (tid == 0) S.stop = wt.expired(stw) ? 1 : 0;
+      if (__syncthreads_and(ok ? 1 : 0)) break;
+      if (S.stop) {
+        if (tid == 0) raise_abort(a, ph, wt.why, wt.polls);
         return;
       }
     }
   }
   DH_MARK(a, ph, 1);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    S.co[4 * wave + q][e] = o4[q];
+    if (e == 0) {
+      S.cm[4 * wave + q] = m4[q];
+      S.cl[4 * wave + q] = l4[q];
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float m[kSplitS];
   float M = -INFINITY;
 #pragma unroll
-  for (int s = 0; s < kSplitS; ++s) M = fmaxf(M, m[s]);
+  for (int s = 0; s < kSplitS; ++s) {
+    m[s] = S.cm[s];
+    M = fmaxf(M, m[s]);
+  }
   float Lsum = 0.f, y = 0.f;
 #pragma unroll
   for (int s = 0; s < kSplitS; ++s) {
     const float w = m[s] > -INFINITY ? __expf(m[s] - M) : 0.f;
-    Lsum += w * l[s];
-    y += w * o[s];
+    Lsum += w * S.cl[s];
+    y += w * S.co[s][e];
   }
   put16(a.yw + h * kHD + e, y / Lsum, tg.t16(ph));
 }
@@ -1288,7 +1309,7 @@ __global__ __launch_bounds__(kPT) void decode_persistent_kernel(PArgs a) {
       fetch_row<2>(po, (const bf16_t*)(intptr_t)Lt[F_WO], a.d, a.d);
       const int p_c = ph++;
       DH_MARK(a, p_c, 0);
-      phase_attn_combine(a, p_a, p_c, tg);
+      phase_attn_combine(a, S, p_a, p_c, tg);
       DH_MARK(a, p_c, 2);
       fetch_ffn_up(pu, a, Lt);
       const int p_o = ph++;
