@@ -833,6 +833,155 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
   advance_position(a);
 }
 
+// Many 16-row tiles without a residual (the vocabulary head at batch > 1): persistent workgroups,
+// as many as the GPU has CUs, walk the groups of TPW tiles gridDim.x apart. The activation rows are
+// staged and normalised once per workgroup instead of once per group, and each group's weights are
+// requested before the previous group's matrix-core steps, so the weight stream does not stop at a
+// group boundary. Per output element the arithmetic is the kernel above's.
+template <int KSPLIT, int TPW, int KSW>
+__global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_pers_kernel(GemvArgs a, int steps_per_wave,
+                                                                                  int ngroups) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int NT = 64 * KSPLIT * TPW;
+  constexpr int XC = 8;                                // staged 16-byte chunks per thread (host: 2K <= XC*NT)
+  const int lane = threadIdx.x & 63, wwave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tile = wwave / KSPLIT, wave = wwave % KSPLIT;
+  const int r = lane & 15, g = lane >> 4;
+  const int K = a.K, B = a.B;
+  const int kc = K / 8;
+  const int rowb = K * 2 + 16;
+  unsigned char* hs = smem;                            // [16][rowb] staged rows
+  float* red = reinterpret_cast<float*>(smem + 16 * rowb);   // [TPW][KSPLIT][64][4] partial tiles
+
+  uint4 xs[XC];
+#pragma unroll
+  for (int j = 0; j < XC; ++j) {
+    const int i = threadIdx.x + j * NT;
+    xs[j] = make_uint4(0u, 0u, 0u, 0u);
+    if (i < B * kc) {
+      const int b = i / kc;
+      const int64_t xrow = a.x_rows ? load_uniform(a.x_rows + b) : (int64_t)b;
+      xs[j] = ld16((const bf16_t*)a.x + xrow * a.x_bstride + (int64_t)(i % kc) * 8);
+    }
+  }
+  constexpr int GC = 4;
+  const bool g_early = a.g != nullptr && kc <= 64 * GC;
+  uint4 gv[GC];
+#pragma unroll
+  for (int i = 0; i < GC; ++i) {
+    gv[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (g_early && lane + 64 * i < kc) gv[i] = ld16((const bf16_t*)a.g + (lane + 64 * i) * 8);
+  }
+  const int nsteps = K / 32;
+  const int s0 = wave * steps_per_wave;
+  const int my_steps = min(steps_per_wave, nsteps - s0);
+  // a group's tile geometry for this wave: first row, real rows, the weight row this lane reads
+  struct Geo { int n0, loc, s; bool live, row_ok; const bf16_t* w; };
+  auto geo = [&](int grp) {
+    Geo q;
+    const int tl = grp * TPW + tile;
+    q.n0 = min(tl * 16, ((a.Nrows - 1) / 16) * 16);
+    q.live = tl * 16 < a.Nrows;
+    const RowSeg sg = row_segment(a, q.n0);
+    q.s = sg.s;
+    q.row_ok = q.n0 + r < a.Nrows;
+    q.loc = sg.local + r;
+    const int wrow = sg.local + (q.row_ok ? r : a.Nrows - 1 - q.n0);
+    q.w = (const bf16_t*)pick_seg(sg.s, a.seg[0].W, a.seg[1].W, a.seg[2].W) + (int64_t)wrow * K;
+    return q;
+  };
+  auto load_w = [&](uint4 (&wf)[KSW], const Geo& q) {
+#pragma unroll
+    for (int j = 0; j < KSW; ++j)
+      if (j < my_steps) wf[j] = ld16(q.w + (s0 + j) * 32 + 8 * g);
+  };
+  uint4 wa[KSW], wb[KSW];
+  Geo ga = geo(blockIdx.x);
+  load_w(wa, ga);
+  const int64_t t = a.uses_t ? load_uniform(a.t_dev) : 0;
+  DH_ISSUE_FENCE();
+
+  // ---- stage the rows (zeros past B), then normalise each once (wave w: rows w, w + KSPLIT * TPW, ...)
+#pragma unroll
+  for (int j = 0; j < XC; ++j) {
+    const int i = threadIdx.x + j * NT;
+    if (i < 16 * kc) {
+      const int b = i / kc;
+      *reinterpret_cast<uint4*>(hs + b * rowb + (i % kc) * 16) = b < B ? xs[j] : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  __syncthreads();
+  if (a.g != nullptr) {                                // uniform
+    for (int b = wwave; b < B; b += KSPLIT * TPW) {
+      float ss = 0.f;
+      for (int c = lane; c < kc; c += 64) {
+        float xf[8];
+        Vec<bf16_t>::unpack(*reinterpret_cast<const uint4*>(hs + b * rowb + c * 16), xf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += xf[e] * xf[e];
+      }
+      const float rs = rsqrtf(wave_sum(ss) / (float)K + a.eps);
+      unsigned char* row = hs + b * rowb;
+      if (g_early) {                                   // uniform
+#pragma unroll
+        for (int i = 0; i < GC; ++i)
+          if (lane + 64 * i < kc) norm_chunk(row, lane + 64 * i, rs, gv[i]);
+      } else {
+        for (int c = lane; c < kc; c += 64) norm_chunk(row, c, rs, ld16((const bf16_t*)a.g + c * 8));
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- one group: the next group's weights requested first, then this group's k-steps, partial
+  // tiles through LDS, wave 0 of each tile sums them and writes (row n0 + r, batch rows 4g + i)
+  auto group = [&](int grp, const Geo& q, const uint4 (&wf)[KSW], uint4 (&wn)[KSW], Geo& qn) {
+    const int nxt = grp + (int)gridDim.x;
+    if (nxt < ngroups) {                               // uniform
+      qn = geo(nxt);
+      load_w(wn, qn);
+    }
+    mf_f32x4 acc = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KSW; ++j) {
+      if (j < my_steps) {                              // uniform
+        mf_bf16x8 av, bv;
+        const uint4 xa = *reinterpret_cast<const uint4*>(hs + r * rowb + ((s0 + j) * 32 + 8 * g) * 2);
+        __builtin_memcpy(&av, &xa, 16);
+        __builtin_memcpy(&bv, &wf[j], 16);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
+      }
+    }
+    *reinterpret_cast<mf_f32x4*>(red + ((tile * KSPLIT + wave) * 64 + lane) * 4) = acc;
+    __syncthreads();
+    if (wave == 0 && q.live) {
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w2 = 0; w2 < KSPLIT; ++w2) {
+        const mf_f32x4 p = *reinterpret_cast<const mf_f32x4*>(red + ((tile * KSPLIT + w2) * 64 + lane) * 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] += p[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int b = 4 * g + i;
+        if (b >= B || !q.row_ok) continue;
+        Elem<bf16_t>::store(out_ptr<bf16_t>(a, q.s, b, t, q.loc), Elem<bf16_t>::round(v[i]));
+      }
+    }
+    __syncthreads();                                   // red is rewritten by the next group
+  };
+  Geo gb = ga;
+  for (int grp = blockIdx.x; grp < ngroups;) {
+    group(grp, ga, wa, wb, gb);
+    grp += gridDim.x;
+    if (grp >= ngroups) break;
+    group(grp, gb, wb, wa, ga);
+    grp += gridDim.x;
+  }
+  advance_position(a);
+}
+
 template <int KSPLIT, int TPW, int KSW, bool SW>
 void launch_mfma_k(const GemvArgs& a, int steps_per_wave, hipStream_t s) {
   const size_t lds = (size_t)16 * (a.K * 2 + 16) + (size_t)TPW * KSPLIT * (SW ? 2 : 1) * 64 * 16;
@@ -864,8 +1013,24 @@ void launch_mfma(const GemvArgs& a, hipStream_t s) {
   const int spw = (nsteps + ks - 1) / ks;             // <= 8: K <= 256 * ks
   const bool small = spw <= 4;
   if constexpr (!SW) {
-    // many tiles (the vocabulary head): four tiles per workgroup share one staging of the rows
+    // many tiles (the vocabulary head): four tiles per workgroup share one staging of the rows; with
+    // no residual, persistent workgroups walk the tile groups
     if (ks == 4 && tiles >= 4 * 512) {
+      if (a.resid == nullptr) {
+        const int ngroups = (tiles + 3) / 4;
+        int dev = 0, ncu = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+          ncu = 256;
+        const int grid = ngroups < ncu ? ngroups : ncu;
+        const size_t lds = (size_t)16 * (a.K * 2 + 16) + (size_t)4 * 4 * 64 * 16;
+        auto go = [&](auto kern) {
+          if (lds > 64 * 1024)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+          kern<<<dim3(grid), dim3(1024), lds, s>>>(a, spw, ngroups);
+        };
+        if (small) go(&decode_gemv_mfma_pers_kernel<4, 4, 4>); else go(&decode_gemv_mfma_pers_kernel<4, 4, 8>);
+        return;
+      }
       if (small) launch_mfma_k<4, 4, 4, SW>(a, spw, s); else launch_mfma_k<4, 4, 8, SW>(a, spw, s);
       return;
     }
