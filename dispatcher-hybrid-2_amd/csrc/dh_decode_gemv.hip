@@ -102,6 +102,19 @@ template <> struct Raw<float> {
   __device__ __forceinline__ static float f(uint32_t r) { return __uint_as_float(r); }
 };
 
+// Raw buffer access: a descriptor (base, byte range) in scalar registers and a per-lane byte offset;
+// a read past the range returns zeros without a memory request. dword3 = 0x00020000 is the
+// gfx9-family raw-buffer format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bld16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+__device__ __forceinline__ uint32_t bld2(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0);
+}
+
 // Segment of concatenated output row n, from uniform selects over the argument fields (indexing
 // the argument array with a runtime value makes the compiler read it with vector loads, and wait
 // for them, before the weight requests).
@@ -674,7 +687,7 @@ __device__ __forceinline__ void norm_chunk(unsigned char* row, int c, float rs, 
   *reinterpret_cast<uint4*>(row + c * 16) = Vec<bf16_t>::pack(xf);
 }
 
-template <int KSPLIT, int TPW, int KSW, bool SW>
+template <int KSPLIT, int TPW, int KSW, bool SW, bool GA>
 __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(GemvArgs a, int steps_per_wave) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NT = 64 * KSPLIT * TPW;               // TPW 16-row tiles per workgroup share the staging
@@ -694,53 +707,95 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
   // a partial last tile (one segment only) reads its last real row in place of the missing ones
   const bool row_ok = n0 + r < a.Nrows;
   const int wrow = seg0.local + (row_ok ? r : a.Nrows - 1 - n0);
-  const bf16_t* w0 = (const bf16_t*)pick_seg(seg0.s, a.seg[0].W, a.seg[1].W, a.seg[2].W) + (int64_t)wrow * K;
-  const bf16_t* w1 = SW ? (const bf16_t*)a.seg[1].W + (int64_t)wrow * K : w0;
+  // this tile's weight rows (segment rows seg0.local .. +15; a lane reads row wrow)
+  const bf16_t* wt0 = (const bf16_t*)pick_seg(seg0.s, a.seg[0].W, a.seg[1].W, a.seg[2].W) + (int64_t)seg0.local * K;
+  const bf16_t* wt1 = SW ? (const bf16_t*)a.seg[1].W + (int64_t)seg0.local * K : wt0;
 
-  // ---- requests: activation chunks (chunk i = row i / kc, column i % kc), then the weights
-  // (predicated: only chunks of real rows, only the wave's own k-steps -- clamped duplicates would
-  // multiply the launch's requests)
-  uint4 xs[XC];
-#pragma unroll
-  for (int j = 0; j < XC; ++j) {
-    const int i = threadIdx.x + j * NT;
-    xs[j] = make_uint4(0u, 0u, 0u, 0u);
-    if (i < B * kc) {
-      const int b = i / kc;
-      const int64_t xrow = a.x_rows ? load_uniform(a.x_rows + b) : (int64_t)b;
-      xs[j] = ld16((const bf16_t*)a.x + xrow * a.x_bstride + (int64_t)(i % kc) * 8);
-    }
-  }
-  // the norm weight chunks this lane applies (chunk lane + 64 i), ahead of the weights: the
-  // normalisation below then waits for them alone, not for the whole weight burst
+  // ---- requests: activation chunks (chunk i = row i / kc, column i % kc), the norm weight, this
+  // wave's weight fragments, the residual operands -- in that order, then the waits. Rows in place
+  // (GA false) take raw buffer loads: an offset past the resource reads zeros and makes no memory
+  // request, so every load is issued unconditionally and the compiler can wait for the activation
+  // rows alone before staging them, for the norm weight alone before the normalisation. (A load
+  // that a lane predicate or branch may skip after them makes it wait for every load, the weight
+  // burst included, before the staging: ~1-2 us of exposed weight latency per launch.)
+  constexpr uint32_t kOOB = 0x80000000u;               // past every resource below (each < 2 GB)
   constexpr int GC = 4;                                // K <= 64 * GC * 8 (larger K loads in the loop)
   const bool g_early = a.g != nullptr && kc <= 64 * GC;
-  uint4 gv[GC];
-#pragma unroll
-  for (int i = 0; i < GC; ++i) {
-    gv[i] = make_uint4(0u, 0u, 0u, 0u);
-    if (g_early && lane + 64 * i < kc) gv[i] = ld16((const bf16_t*)a.g + (lane + 64 * i) * 8);
-  }
   const int nsteps = K / 32;
   const int s0 = wave * steps_per_wave;
   const int my_steps = min(steps_per_wave, nsteps - s0);
-  uint4 wf[NW][KSW];
-#pragma unroll
-  for (int j = 0; j < KSW; ++j) {
-    if (j < my_steps) {
-      wf[0][j] = ld16(w0 + (s0 + j) * 32 + 8 * g);
-      if (SW) wf[NW - 1][j] = ld16(w1 + (s0 + j) * 32 + 8 * g);
-    }
-  }
-  // the residual operands of this lane's outputs (row n0 + r, batch rows 4g + i), requested now so
-  // the epilogue does not wait a memory round trip
+  const int wr = wrow - seg0.local;                    // 0..15
+  uint4 xs[XC], gv[GC], wf[NW][KSW];
   uint32_t rres[4] = {0u, 0u, 0u, 0u};
-  if (!SW && a.resid && wave == 0) {                  // uniform
+  if constexpr (!GA) {
+    // (whole slots past the rows are skipped by a uniform branch: the loads issued after every
+    // activation slot do not depend on it, so the waits stay exact)
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, (uint32_t)(((int64_t)(B - 1) * a.x_bstride + K) * 2));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int b = min(4 * g + i, B - 1);
-      const int64_t rrow = a.resid_rows ? a.resid_rows[b] : (int64_t)b;
-      rres[i] = Raw<bf16_t>::load((const bf16_t*)a.resid + rrow * a.resid_bstride + seg0.local + (row_ok ? r : 0));
+    for (int j = 0; j < XC; ++j) {
+      xs[j] = make_uint4(0u, 0u, 0u, 0u);
+      if (j * NT < B * kc) {                           // uniform
+        const int i = threadIdx.x + j * NT;
+        const uint32_t off = i < B * kc ? (uint32_t)(((int64_t)(i / kc) * a.x_bstride + (i % kc) * 8) * 2) : kOOB;
+        xs[j] = bld16(rx, off);
+      }
+    }
+    const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.g, g_early ? (uint32_t)(K * 2) : 0u);
+#pragma unroll
+    for (int i = 0; i < GC; ++i) gv[i] = bld16(rg, (uint32_t)(lane + 64 * i) * 16u);   // past K: zeros
+    const uint32_t wbytes = (uint32_t)(16 * K * 2);
+    const __amdgpu_buffer_rsrc_t rw0 = buf_rsrc(wt0, wbytes);
+    const __amdgpu_buffer_rsrc_t rw1 = buf_rsrc(wt1, wbytes);
+#pragma unroll
+    for (int j = 0; j < KSW; ++j) {
+      const uint32_t off = j < my_steps ? (uint32_t)((wr * K + (s0 + j) * 32 + 8 * g) * 2) : kOOB;
+      wf[0][j] = bld16(rw0, off);
+      if (SW) wf[NW - 1][j] = bld16(rw1, off);
+    }
+    if (!SW) {
+      // the residual operands of this lane's outputs (row n0 + r, batch rows 4g + i), requested now so
+      // the epilogue does not wait a memory round trip (wave 0 only: the other waves' resource is
+      // empty; a branch here would make the compiler wait for these loads to merge the values)
+      const uint32_t rbytes = a.resid != nullptr && wave == 0
+                                  ? (uint32_t)(((int64_t)(B - 1) * a.resid_bstride + seg0.local + 16) * 2) : 0u;
+      const __amdgpu_buffer_rsrc_t rr = buf_rsrc(a.resid, rbytes);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int b = min(4 * g + i, B - 1);
+        rres[i] = bld2(rr, (uint32_t)(((int64_t)b * a.resid_bstride + seg0.local + (row_ok ? r : 0)) * 2));
+      }
+    }
+  } else {
+    // gathered rows (the first layer reads embedding rows by token id): predicated global loads
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+      const int i = threadIdx.x + j * NT;
+      xs[j] = make_uint4(0u, 0u, 0u, 0u);
+      if (i < B * kc) {
+        const int b = i / kc;
+        const int64_t xrow = a.x_rows ? load_uniform(a.x_rows + b) : (int64_t)b;
+        xs[j] = ld16((const bf16_t*)a.x + xrow * a.x_bstride + (int64_t)(i % kc) * 8);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < GC; ++i) {
+      gv[i] = make_uint4(0u, 0u, 0u, 0u);
+      if (g_early && lane + 64 * i < kc) gv[i] = ld16((const bf16_t*)a.g + (lane + 64 * i) * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < KSW; ++j) {
+      if (j < my_steps) {
+        wf[0][j] = ld16(wt0 + (int64_t)wr * K + (s0 + j) * 32 + 8 * g);
+        if (SW) wf[NW - 1][j] = ld16(wt1 + (int64_t)wr * K + (s0 + j) * 32 + 8 * g);
+      }
+    }
+    if (!SW && a.resid && wave == 0) {                // uniform
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int b = min(4 * g + i, B - 1);
+        const int64_t rrow = a.resid_rows ? a.resid_rows[b] : (int64_t)b;
+        rres[i] = Raw<bf16_t>::load((const bf16_t*)a.resid + rrow * a.resid_bstride + seg0.local + (row_ok ? r : 0));
+      }
     }
   }
   const int64_t t = a.uses_t ? load_uniform(a.t_dev) : 0;
@@ -854,14 +909,23 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_pers_kerne
   float* red = reinterpret_cast<float*>(smem + 16 * rowb);   // [TPW][KSPLIT][64][4] partial tiles
 
   uint4 xs[XC];
+  if (a.x_rows == nullptr) {                          // uniform (as in the kernel above)
 #pragma unroll
-  for (int j = 0; j < XC; ++j) {
-    const int i = threadIdx.x + j * NT;
-    xs[j] = make_uint4(0u, 0u, 0u, 0u);
-    if (i < B * kc) {
-      const int b = i / kc;
-      const int64_t xrow = a.x_rows ? load_uniform(a.x_rows + b) : (int64_t)b;
-      xs[j] = ld16((const bf16_t*)a.x + xrow * a.x_bstride + (int64_t)(i % kc) * 8);
+    for (int j = 0; j < XC; ++j) {
+      const int i = threadIdx.x + j * NT;
+      xs[j] = make_uint4(0u, 0u, 0u, 0u);
+      if (i < B * kc) xs[j] = ld16((const bf16_t*)a.x + (int64_t)(i / kc) * a.x_bstride + (int64_t)(i % kc) * 8);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < XC; ++j) {
+      const int i = threadIdx.x + j * NT;
+      xs[j] = make_uint4(0u, 0u, 0u, 0u);
+      if (i < B * kc) {
+        const int b = i / kc;
+        const int64_t xrow = load_uniform(a.x_rows + b);
+        xs[j] = ld16((const bf16_t*)a.x + xrow * a.x_bstride + (int64_t)(i % kc) * 8);
+      }
     }
   }
   constexpr int GC = 4;
@@ -985,7 +1049,8 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_pers_kerne
 template <int KSPLIT, int TPW, int KSW, bool SW>
 void launch_mfma_k(const GemvArgs& a, int steps_per_wave, hipStream_t s) {
   const size_t lds = (size_t)16 * (a.K * 2 + 16) + (size_t)TPW * KSPLIT * (SW ? 2 : 1) * 64 * 16;
-  auto kern = &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW>;
+  auto kern = a.x_rows || a.resid_rows ? &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, true>
+                                       : &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, false>;
   if (lds > 64 * 1024)
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)lds);
@@ -998,6 +1063,10 @@ void launch_mfma_k(const GemvArgs& a, int steps_per_wave, hipStream_t s) {
 // (SwiGLU: at most 8 waves -- two weight tiles per wave do not fit 16 waves' registers)
 bool mfma_gemv_fits(const GemvArgs& a, bool swiglu) {
   if (a.B < 2 || a.B > 16 || a.K % 32 != 0 || a.K > (swiglu ? 2048 : 4096)) return false;
+  // rows in place are read through buffer resources of < 2 GB (activations, residual)
+  const int64_t lim = (int64_t)1 << 30;                // elements of 2 bytes
+  if ((int64_t)(a.B - 1) * a.x_bstride + a.K >= lim) return false;
+  if (a.resid && (int64_t)(a.B - 1) * a.resid_bstride + a.Nrows >= lim) return false;
   if (a.nseg == 1 && !swiglu) return true;            // a partial last tile is handled
   for (int s = 0; s < a.nseg; ++s)
     if (a.seg[s].N % 16 != 0) return false;
