@@ -223,11 +223,11 @@ template <> struct Raw<float> {
 // Memory round trips are the cost of this latency-bound kernel, so loads are issued in exactly two
 // waves before any barrier: (1) the position t together with everything that does not depend on
 // it (gate weights, destination features A, V0, biases); (2) everything addressed through t
-// (source rows of B_hist, ring slots, transmit gates). Every load is unconditional, at an address
-// clamped to a valid element, with the predicate applied to the value afterwards: a load under a
-// divergent branch whose value is consumed inside the branch makes the compiler wait for it on the
-// spot, serialising the round trips. Barriers (which wait on outstanding loads) only come once
-// every load is in flight.
+// (source rows of B_hist, ring slots, transmit gates). Loads are unconditional, at addresses
+// clamped to a valid element, with the predicate applied to the value afterwards, or sit under a
+// wave-uniform branch whose values are used only after the last request of that wave: a load
+// under a branch whose value is consumed (or converted) inside the branch makes the compiler wait
+// for it, and for every load before it, on the spot, serialising the round trips.
 // Gate phase: wave l owns level l (L <= 16 waves); its lanes cover K in 16-byte chunks (C per
 // lane), so each (row, gate) dot product ends in one DPP wave reduction and one plain LDS store.
 // RPB = batch rows per workgroup, C = chunks per lane; both compile-time so the operands stay in
@@ -244,8 +244,6 @@ __global__ __launch_bounds__(kFusedThreads) void decode_mixer_step_kernel(StepAr
   const int nchunk = GH / V;                   // host: nchunk <= 64 * C
   const int gl = min(wave, L - 1);             // gate role: wave gl owns level gl (waves < L)
   const bool gate_wave = wave < L;             // wave-uniform
-  const int scan_waves = (nb * hd + 63) / 64;
-  const bool scan_wave = wave < scan_waves;    // wave-uniform
   __shared__ float acc[RPB][LMAX][3];
   __shared__ float gate_i[RPB][LMAX];
   __shared__ float gate_f[RPB][LMAX];
@@ -273,14 +271,14 @@ __global__ __launch_bounds__(kFusedThreads) void decode_mixer_step_kernel(StepAr
   const int64_t brow = b0 + (scan_role ? sr : 0);
   const int ar = tid / L, al = tid % L;        // activation role: (row, level)
   const bool act_role = tid < nb * L;
-  uint32_t v0raw = 0, bir = 0, bfr = 0, brr = 0;
-  if (scan_wave) v0raw = Raw<T>::load((const T*)a.V0 + brow * d + (int64_t)h * hd + se);
-  if (wave < (nb * L + 63) / 64) {
-    const int64_t gi = (int64_t)al * H + h;
-    bir = Raw<T>::load((const T*)a.bi + gi);
-    bfr = Raw<T>::load((const T*)a.bf + gi);
-    brr = Raw<T>::load((const T*)a.br + gi);
-  }
+  // every thread reads these (their addresses are valid for any tid): under a role branch the
+  // compiler converts the value inside the branch and so waits there for it, and for the weights
+  // requested before it, ahead of the position-dependent requests below
+  const uint32_t v0raw = Raw<T>::load((const T*)a.V0 + brow * d + (int64_t)h * hd + se);
+  const int64_t gi = (int64_t)al * H + h;
+  const uint32_t bir = Raw<T>::load((const T*)a.bi + gi);
+  const uint32_t bfr = Raw<T>::load((const T*)a.bf + gi);
+  const uint32_t brr = Raw<T>::load((const T*)a.br + gi);
   if (t < 0 || t >= a.Tmax) return;             // uniform: every thread read the same t
 
   // ---- load wave 2: operands addressed through t
@@ -297,14 +295,34 @@ __global__ __launch_bounds__(kFusedThreads) void decode_mixer_step_kernel(StepAr
     }
   }
   T* ring = (T*)a.V_ring + brow * a.S * d + (int64_t)h * hd + se;
-  uint32_t vraw[LMAX], rraw[LMAX];
-  if (scan_wave) {
+  // the recurrence's sources (ring value and transmit gate of position t - 2^l per level), read
+  // and staged in LDS by the waves without a gate role when there are enough of them: the loader
+  // waits for its loads on the spot, which then holds up no gate readout
+  {
+    const int ld0 = (kFusedThreads / 64 - L) * 64 >= nb * hd ? 64 * L : 0;   // uniform
+    const int u = tid - ld0;
+    if (u >= 0 && u < nb * hd) {
+      const int ur = u / hd, ue = u % hd;
+      const int64_t urow = b0 + ur;
+      const T* uring = (const T*)a.V_ring + urow * a.S * d + (int64_t)h * hd + ue;
+      uint32_t vraw[LMAX], rraw[LMAX];
 #pragma unroll
-    for (int l = 0; l < LMAX; ++l) {            // straight-line: levels past L re-read level L-1
-      const int lc = min(l, L - 1);
-      const int64_t sc = max(t - ((int64_t)1 << lc), (int64_t)0);
-      vraw[l] = Raw<T>::load(ring + (ring_offset(lc) + (sc & ring_mask(lc))) * d);
-      rraw[l] = Raw<T>::load((const T*)a.rg_hist + ((brow * a.Tmax + sc) * L + lc) * H + h);
+      for (int l = 0; l < LMAX; ++l) {          // straight-line: levels past L re-read level L-1
+        const int lc = min(l, L - 1);
+        const int64_t sc = max(t - ((int64_t)1 << lc), (int64_t)0);
+        vraw[l] = Raw<T>::load(uring + (ring_offset(lc) + (sc & ring_mask(lc))) * d);
+        rraw[l] = Raw<T>::load((const T*)a.rg_hist + ((urow * a.Tmax + sc) * L + lc) * H + h);
+      }
+#pragma unroll
+      for (int l = 0; l < LMAX; ++l) {
+        if (l < L) {
+          const bool live = (t - ((int64_t)1 << l)) >= 0;
+          src_v[ur][l][ue] = live ? Raw<T>::f(vraw[l]) : 0.f;
+          // every lane of the row writes the same value (a predicate on this store lets the
+          // compiler sink the load under it: one more round trip)
+          src_r[ur][l] = live ? Raw<T>::f(rraw[l]) : 0.f;
+        }
+      }
     }
   }
 
@@ -344,23 +362,13 @@ __global__ __launch_bounds__(kFusedThreads) void decode_mixer_step_kernel(StepAr
   }
   __syncthreads();                                // acc complete; every load above has landed
 
-  // ---- sigmoid heads, masks, transmit gate of position t; stage the recurrence's sources
+  // ---- sigmoid heads, masks, transmit gate of position t
   if (act_role) {
     const float okf = (t - ((int64_t)1 << al)) >= 0 ? 1.f : 0.f;
     gate_i[ar][al] = dh_sigmoid(acc[ar][al][0] + Raw<T>::f(bir)) * okf;
     gate_f[ar][al] = dh_sigmoid(acc[ar][al][1] + Raw<T>::f(bfr)) * okf + (1.f - okf);
     const float rg = dh_sigmoid(acc[ar][al][2] + Raw<T>::f(brr));
     Elem<T>::store((T*)a.rg_hist + (((int64_t)(b0 + ar) * a.Tmax + t) * L + al) * H + h, rg);
-  }
-  if (scan_role) {
-#pragma unroll
-    for (int l = 0; l < LMAX; ++l) {
-      if (l < L) {
-        const bool live = (t - ((int64_t)1 << l)) >= 0;
-        src_v[sr][l][se] = live ? Raw<T>::f(vraw[l]) : 0.f;
-        if (se == 0) src_r[sr][l] = live ? Raw<T>::f(rraw[l]) : 0.f;
-      }
-    }
   }
   __syncthreads();
 
