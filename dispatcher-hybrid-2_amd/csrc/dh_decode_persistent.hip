@@ -157,6 +157,13 @@ __device__ __forceinline__ uint4 get16x4(const uint32_t* base, int nwords, int w
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)word * 4u, 0, 16));
 }
 __device__ __forceinline__ bool tag_ok(uint32_t w, uint32_t tag) { return (w & 0xffffu) == tag; }
+// The x vector (the residual stream, written by one wave per row, the four rows of a workgroup
+// consecutive) keeps each workgroup's four words in a 64-byte segment of its own: writers from
+// several workgroups sharing a segment made every hand-off of x ~0.2 us slower (probe, 256
+// workgroups). Word n of x sits at xpos(n); a 4-word chunk c at c * kXSeg.
+constexpr int kXSeg = 16;
+__device__ __forceinline__ int xpos(int n) { return (n >> 2) * kXSeg + (n & 3); }
+static_assert(kPW == 4, "xpos: the four x rows of a workgroup share a segment");
 __device__ __forceinline__ uint64_t now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
 
 // Optional timing record of a traced step: per workgroup and phase, the 100 MHz real-time counter
@@ -281,20 +288,21 @@ __device__ __forceinline__ void norm_staged(Smem& S, int K, float eps) {
   __syncthreads();
 }
 
-// The same wait for a row of n tagged words (n % 8 == 0, n <= 8 * kPT) with the words of chunk i
-// polled by thread i (two 16-byte loads) and returned in its registers (xc, bf16); threads past the
-// row only take part in the rounds' barriers.
+// The same wait for the x vector (n tagged words, n % 8 == 0, n <= 8 * kPT, laid out by xpos) with
+// the eight words of thread i (chunks 2i and 2i + 1) polled by thread i (two 16-byte loads) and
+// returned in its registers (xc, bf16); threads past the row only take part in the rounds' barriers.
 __device__ __forceinline__ bool wg_poll16_chunk(const PArgs& a, Smem& S, const uint32_t* src, int n, uint32_t tag,
                                                 uint4& xc, int ph) {
   const int tid = threadIdx.x;
   const bool mine = tid * 8 < n;
+  const int nw = n / 4 * kXSeg;                      // padded extent
   uint4 w0 = make_uint4(0u, 0u, 0u, 0u), w1 = w0;
   Waiter wt;
   while (true) {
     bool ok = true;
     if (mine) {
-      w0 = get16x4(src, n, tid * 8);
-      w1 = get16x4(src, n, tid * 8 + 4);
+      w0 = get16x4(src, nw, (2 * tid) * kXSeg);
+      w1 = get16x4(src, nw, (2 * tid + 1) * kXSeg);
     }
     const uint32_t stw = tid == 0 ? get16(a.status) : 0u;
     if (mine)
@@ -563,7 +571,7 @@ __device__ __forceinline__ bool run_rows_resid(const PArgs& a, Smem& S, const Ro
   float acc[1][1];
   dot_rows<1, 1, CG>(S, nchunk, f.w, acc);
   xres = rnd(rnd(acc[0][0]) + rv);
-  if (lane == 0) put16(a.xw + n, xres, tg.t16(ph));
+  if (lane == 0) put16(a.xw + xpos(n), xres, tg.t16(ph));
   return true;
 }
 
@@ -776,7 +784,7 @@ __device__ __forceinline__ bool run_scan_out(const PArgs& a, Smem& S, const PreS
     float acc[1][1];
     dot_rows<1, 1, CG>(S, nchunk, f.w.w, acc);
     xres = rnd(rnd(acc[0][0]) + rv);
-    if (lane == 0) put16(a.xw + n, xres, tg.t16(ph));
+    if (lane == 0) put16(a.xw + xpos(n), xres, tg.t16(ph));
   }
   // the ring slots of t are read by later launches only: workgroup 0 writes them after its x rows
   // are out, so they do not queue ahead of the hand-off
@@ -1353,7 +1361,7 @@ int count_phases(const int* kinds, int n) {
 
 extern "C" int64_t dh_decode_persistent_scratch_bytes(int d, int GH, int H, int L, int ff, int grid) {
   // tagged bf16 vectors: x, V0, A, h, q, k, v, y; fp32 records: gates, segment records, candidates
-  const int64_t w16 = (int64_t)d * 7 + GH + ff;
+  const int64_t w16 = (int64_t)d * 6 + (int64_t)d / 4 * kXSeg + GH + ff;   // x padded (xpos)
   const int64_t w32 = (int64_t)H * L * 2 + (int64_t)H * kSplitS * (2 + kHD) + (int64_t)2 * grid;
   return 256 + (w16 * 4 + 255) / 256 * 256 + w32 * 8 + 256;
 }
@@ -1409,7 +1417,7 @@ int launch_persistent(const char* who, const int64_t* layer_table, const int* ki
   a.epoch = (int64_t*)p;
   a.status = (uint32_t*)(p + 8);
   uint32_t* w = (uint32_t*)(p + 256);
-  a.xw = w; w += d;
+  a.xw = w; w += d / 4 * kXSeg;
   a.v0w = w; w += d;
   a.aw = w; w += GH;
   a.hw = w; w += ff;
@@ -1417,7 +1425,7 @@ int launch_persistent(const char* who, const int64_t* layer_table, const int* ki
   a.kw = w; w += d;
   a.vw = w; w += d;
   a.yw = w; w += d;
-  uint64_t* r = (uint64_t*)(p + 256 + ((int64_t)(7 * d + GH + ff) * 4 + 255) / 256 * 256);
+  uint64_t* r = (uint64_t*)(p + 256 + ((int64_t)(6 * d + d / 4 * kXSeg + GH + ff) * 4 + 255) / 256 * 256);
   a.coefw = r; r += (int64_t)H * L * 2;
   a.partw = r; r += (int64_t)H * kSplitS * (2 + kHD);
   a.candw = r;
