@@ -72,7 +72,8 @@ struct PArgs {
   bf16_t* logits;            // (V)
   int64_t* epoch;            // launches so far (tags)
   uint32_t* status;          // [0] abort flag, [1] first failing phase + 1
-  uint32_t *xw, *v0w, *aw, *hw, *qw, *kw, *vw, *yw;   // tagged bf16 vectors
+  uint32_t *xw, *i3w, *hw, *yw;   // tagged bf16 vectors: x, in-projection group, h, y
+  int n3w, nhw;                    // padded extents (words) of i3w and hw
   uint64_t *coefw, *partw, *candw;                     // tagged fp32 records
   uint64_t* trace;           // nullable: per-phase timestamps (dh_decode_persistent_trace)
   float eps;
@@ -164,6 +165,13 @@ __device__ __forceinline__ bool tag_ok(uint32_t w, uint32_t tag) { return (w & 0
 constexpr int kXSeg = 16;
 __device__ __forceinline__ int xpos(int n) { return (n >> 2) * kXSeg + (n & 3); }
 static_assert(kPW == 4, "xpos: the four x rows of a workgroup share a segment");
+// Likewise the phases of three rows per wave (the in-projection group V0 | A or q | k | v, and h):
+// the kR3 rows of a workgroup in a 64-byte segment, row n at p3(n). The in-projection group is
+// laid out by its global row (V0 then A; q, k, v), as its workgroups produce it.
+constexpr int kR3 = 3 * kPW;
+static_assert(kR3 <= kXSeg && kR3 % 4 == 0, "p3: a workgroup's rows fill one segment in whole chunks");
+__device__ __forceinline__ int p3(int n) { return (n / kR3) * kXSeg + n % kR3; }
+__host__ __device__ constexpr int p3_extent(int n) { return (n + kR3 - 1) / kR3 * kXSeg; }
 __device__ __forceinline__ uint64_t now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
 
 // Optional timing record of a traced step: per workgroup and phase, the 100 MHz real-time counter
@@ -217,13 +225,14 @@ struct Smem {
   float cm[kSplitS], cl[kSplitS], co[kSplitS][kHD];
 };
 
-// Workgroup wait for n tagged bf16 words (n % 4 == 0, n <= 4 * kPT * 3); the values land in dst
-// (LDS) as bf16. One barrier per round: thread 0 publishes the end condition through LDS before it
+// Workgroup wait for n tagged bf16 words (n % 4 == 0, n <= 4 * kPT * 3; contiguous, or laid out by
+// p3); the values land in dst (LDS) as bf16. One barrier per round: thread 0 publishes the end condition through LDS before it
 // (a later round's write may race a slow thread's read of the earlier value; the condition only
 // ever turns true). Every thread returns the same answer; false: the step was aborted.
-__device__ __forceinline__ bool wg_poll16(const PArgs& a, Smem& S, const uint32_t* src, int n, uint32_t tag, bf16_t* dst,
-                                          int ph) {
+__device__ __forceinline__ bool wg_poll16(const PArgs& a, Smem& S, const uint32_t* src, int n, bool pad3, uint32_t tag,
+                                          bf16_t* dst, int ph) {
   const int tid = threadIdx.x;
+  const int nw = pad3 ? p3_extent(n) : n;            // pad3: laid out by p3
   uint4 w[3];
   Waiter wt;
   while (true) {
@@ -231,7 +240,7 @@ __device__ __forceinline__ bool wg_poll16(const PArgs& a, Smem& S, const uint32_
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
       const int q = tid + j * kPT;
-      if (q * 4 < n) w[j] = get16x4(src, n, q * 4);
+      if (q * 4 < n) w[j] = get16x4(src, nw, pad3 ? p3(q * 4) : q * 4);
     }
     const uint32_t stw = tid == 0 ? get16(a.status) : 0u;
 #pragma unroll
@@ -467,11 +476,10 @@ __device__ __forceinline__ void fetch_in3(PreFirst& f, const PArgs& a, int n0, i
   }
 }
 
-// Segments 0 and 1 go to tagged vectors; segment 2 to `plain2` (the B_hist row of t) or a third
-// tagged vector. The launch has at least N / 3 waves.
+// Segments 0 and 1 go to the tagged in-projection group (global row n at p3(n)); segment 2 to
+// `plain2` (the B_hist row of t) or the group. The launch has at least N / 3 waves.
 __device__ __forceinline__ bool run_in3(const PArgs& a, Smem& S, const PreFirst& f, bool first,
-                                        uint32_t xtag, int ph, Tags tg, uint32_t* out0,
-                                        uint32_t* out1, uint32_t* out2, bf16_t* plain2, int n0, int n1, int n2) {
+                                        uint32_t xtag, int ph, Tags tg, bf16_t* plain2, int n0, int n1, int n2) {
   constexpr int R = 3, CG = 2;                        // K = d <= 1024
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int N = n0 + n1 + n2;
@@ -493,10 +501,8 @@ __device__ __forceinline__ bool run_in3(const PArgs& a, Smem& S, const PreFirst&
     for (int r = 0; r < R; ++r) v0 = r == lane ? acc[r][0] : v0;
     const int n = base + lane;
     const float out = rnd(v0);
-    if (n < n0) put16(out0 + n, out, tg.t16(ph));
-    else if (n < n0 + n1) put16(out1 + (n - n0), out, tg.t16(ph));
-    else if (plain2) st2(plain2 + (n - n0 - n1), f32_to_bf16(out));
-    else put16(out2 + (n - n0 - n1), out, tg.t16(ph));
+    if (n >= n0 + n1 && plain2) st2(plain2 + (n - n0 - n1), f32_to_bf16(out));
+    else put16(a.i3w + p3(n), out, tg.t16(ph));
   }
   return true;
 }
@@ -542,7 +548,7 @@ __device__ __forceinline__ bool run_ffn_up(const PArgs& a, Smem& S, const PreUp&
       v0 = r == lane ? acc[r][0] : v0;
       v1 = r == lane ? acc[r][1] : v1;
     }
-    put16(a.hw + base + lane, rnd(rnd(silu(rnd(v0))) * rnd(v1)), tg.t16(ph));
+    put16(a.hw + p3(base + lane), rnd(rnd(silu(rnd(v0))) * rnd(v1)), tg.t16(ph));
   }
   return true;
 }
@@ -558,13 +564,13 @@ __device__ __forceinline__ void fetch_row(Rows<1, 1, CG>& f, const bf16_t* W, in
 }
 template <int CG>
 __device__ __forceinline__ bool run_rows_resid(const PArgs& a, Smem& S, const Rows<1, 1, CG>& f, int K,
-                                               const uint32_t* in, uint32_t in_tag, bool first, const bf16_t* erow,
-                                               float& xres, int ph, Tags tg) {
+                                               const uint32_t* in, bool in_pad3, uint32_t in_tag, bool first,
+                                               const bf16_t* erow, float& xres, int ph, Tags tg) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int N = a.d, nchunk = K / 8;
   const int n = blockIdx.x * kPW + wave;
   if (blockIdx.x * kPW >= N) return true;
-  if (!wg_poll16(a, S, in, K, in_tag, reinterpret_cast<bf16_t*>(S.sx), ph)) return false;
+  if (!wg_poll16(a, S, in, K, in_pad3, in_tag, reinterpret_cast<bf16_t*>(S.sx), ph)) return false;
   __syncthreads();
   if (n >= N) return true;
   const float rv = residual(first, erow, n, xres);
@@ -633,7 +639,7 @@ __device__ __forceinline__ void run_gates(const PArgs& a, const PreGates& f, Lay
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const int ch = min(lane + 64 * c, nchunk - 1);
-      const uint4 p0 = get16x4(a.aw, GH, ch * 8), p1 = get16x4(a.aw, GH, ch * 8 + 4);
+      const uint4 p0 = get16x4(a.i3w, a.n3w, p3(a.d + ch * 8)), p1 = get16x4(a.i3w, a.n3w, p3(a.d + ch * 8 + 4));
       okw = okw && tag_ok(p0.x, tg16) && tag_ok(p0.y, tg16) && tag_ok(p0.z, tg16) && tag_ok(p0.w, tg16) &&
             tag_ok(p1.x, tg16) && tag_ok(p1.y, tg16) && tag_ok(p1.z, tg16) && tag_ok(p1.w, tg16);
       av[c] = make_uint4((p0.x >> 16) | (p0.y & 0xffff0000u), (p0.z >> 16) | (p0.w & 0xffff0000u),
@@ -673,9 +679,9 @@ __device__ __forceinline__ void run_gates(const PArgs& a, const PreGates& f, Lay
     const float ig = dh_sigmoid(s0 + bfv(f.bi)) * okf;
     const float fg = dh_sigmoid(s1 + bfv(f.bf)) * okf + (1.f - okf);
     const float rs = ok ? bfv(f.rsrc) : 0.f;
-    const int64_t rec = (int64_t)h * L + l;
-    put32(a.coefw + rec * 2, fg, tg.t32(ph));
-    put32(a.coefw + rec * 2 + 1, ig * rs, tg.t32(ph));
+    // records in unit order (u = l * H + h): a workgroup's four units fill one 64-byte segment
+    put32(a.coefw + (int64_t)u * 2, fg, tg.t32(ph));
+    put32(a.coefw + (int64_t)u * 2 + 1, ig * rs, tg.t32(ph));
     st2((bf16_t*)(intptr_t)Lt[F_RGHIST] + (t * L + l) * H + h, f32_to_bf16(dh_sigmoid(s2 + bfv(f.br))));
   }
 }
@@ -741,7 +747,7 @@ __device__ __forceinline__ bool run_scan_out(const PArgs& a, Smem& S, const PreS
           ok = ok && cw[j].y == gt && cw[j].w == gt;
         }
       }
-      vw = get16x4(a.v0w, d, e0);
+      vw = get16x4(a.i3w, a.n3w, p3(e0));
       ok = ok && tag_ok(vw.x, vt) && tag_ok(vw.y, vt) && tag_ok(vw.z, vt) && tag_ok(vw.w, vt);
       if (tid == 0) S.stop = wt.expired(stw) ? 1 : 0;
       if (__syncthreads_and(ok ? 1 : 0)) break;
@@ -753,8 +759,8 @@ __device__ __forceinline__ bool run_scan_out(const PArgs& a, Smem& S, const PreS
     DH_MARK(a, ph, 1);
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
-      const int i = tid + j * kPT;
-      if (i < ncf) S.coef[i] = make_float2(__uint_as_float(cw[j].x), __uint_as_float(cw[j].z));
+      const int i = tid + j * kPT;                     // record i: unit (level i / H, head i % H)
+      if (i < ncf) S.coef[(i % H) * L + i / H] = make_float2(__uint_as_float(cw[j].x), __uint_as_float(cw[j].z));
     }
     v0f[0] = bfv(vw.x >> 16); v0f[1] = bfv(vw.y >> 16); v0f[2] = bfv(vw.z >> 16); v0f[3] = bfv(vw.w >> 16);
   }
@@ -902,9 +908,10 @@ __device__ __forceinline__ bool run_attn_split(const PArgs& a, Smem& S, const Pr
       const uint32_t stw = tid == 0 ? get16(a.status) : 0u;
       bool ok = true;
       if (roper && unit_live) {
-        wq0 = get16(a.qw + base); wq1 = get16(a.qw + base + 1);
-        wk0 = get16(a.kw + base); wk1 = get16(a.kw + base + 1);
-        wv0 = get16(a.vw + base); wv1 = get16(a.vw + base + 1);
+        const int pq = p3(base), pk = p3(a.d + base), pv = p3(2 * a.d + base);   // base even: +1 stays in its chunk
+        wq0 = get16(a.i3w + pq); wq1 = get16(a.i3w + pq + 1);
+        wk0 = get16(a.i3w + pk); wk1 = get16(a.i3w + pk + 1);
+        wv0 = get16(a.i3w + pv); wv1 = get16(a.i3w + pv + 1);
         ok = tag_ok(wq0, tq) && tag_ok(wq1, tq) && tag_ok(wk0, tq) && tag_ok(wk1, tq) && tag_ok(wv0, tq) && tag_ok(wv1, tq);
       }
       if (tid == 0) S.stop = wt.expired(stw) ? 1 : 0;
@@ -1180,8 +1187,8 @@ __device__ __forceinline__ bool run_lm_head(const PArgs& a, Smem& S, const PreFi
 #pragma unroll
     for (int w2 = 1; w2 < kPW; ++w2)
       if (beats(S.wbest[w2].v, S.wbest[w2].i, r.v, r.i)) r = S.wbest[w2];
-    put32(a.candw + 2 * blockIdx.x, r.v, tg.t32(ph));
-    put32(a.candw + 2 * blockIdx.x + 1, __int_as_float(r.i), tg.t32(ph));
+    put32(a.candw + 8 * blockIdx.x, r.v, tg.t32(ph));      // a 64-byte segment per workgroup
+    put32(a.candw + 8 * blockIdx.x + 1, __int_as_float(r.i), tg.t32(ph));
   }
   return true;
 }
@@ -1203,7 +1210,7 @@ __device__ __forceinline__ void phase_argmax(const PArgs& a, Smem& S, int64_t t,
       Waiter wt;
       while (!dead) {
         const uint32_t stw = get16(a.status);
-        const uint4 cw = get16x4(c32, (int)gridDim.x * 4, min(i, (int)gridDim.x - 1) * 4);
+        const uint4 cw = get16x4(c32, (int)gridDim.x * 16, min(i, (int)gridDim.x - 1) * 16);
         v = __uint_as_float(cw.x);
         ix = (int)cw.z;
         if (__all(!want || (cw.y == ct && cw.w == ct))) break;
@@ -1284,8 +1291,7 @@ __global__ __launch_bounds__(kPT) void decode_persistent_kernel(PArgs a) {
       fetch_gates(pg, a, Lt, t);
       const int p_in = ph++;                           // V0, A (tagged), B_hist[t] (plain)
       DH_MARK(a, p_in, 0);
-      if (!run_in3(a, S, pf, first, xtag, p_in, tg, a.v0w, a.aw, nullptr,
-                   (bf16_t*)(intptr_t)Lt[F_BHIST] + t * a.GH, a.d, a.GH, a.GH))
+      if (!run_in3(a, S, pf, first, xtag, p_in, tg, (bf16_t*)(intptr_t)Lt[F_BHIST] + t * a.GH, a.d, a.GH, a.GH))
         return;
       DH_MARK(a, p_in, 2);
       PreScan ps;
@@ -1305,8 +1311,7 @@ __global__ __launch_bounds__(kPT) void decode_persistent_kernel(PArgs a) {
       fetch_attn(pa, a, Lt, t);
       const int p_q = ph++;
       DH_MARK(a, p_q, 0);
-      if (!run_in3(a, S, pf, first, xtag, p_q, tg, a.qw, a.kw, a.vw,
-                   nullptr, a.d, a.d, a.d))
+      if (!run_in3(a, S, pf, first, xtag, p_q, tg, nullptr, a.d, a.d, a.d))
         return;
       DH_MARK(a, p_q, 2);
       const int p_a = ph++;
@@ -1322,7 +1327,7 @@ __global__ __launch_bounds__(kPT) void decode_persistent_kernel(PArgs a) {
       fetch_ffn_up(pu, a, Lt);
       const int p_o = ph++;
       DH_MARK(a, p_o, 0);
-      if (!run_rows_resid<2>(a, S, po, a.d, a.yw, tg.t16(p_c), first, erow, xres, p_o, tg)) return;
+      if (!run_rows_resid<2>(a, S, po, a.d, a.yw, false, tg.t16(p_c), first, erow, xres, p_o, tg)) return;
       DH_MARK(a, p_o, 2);
       xph = p_o;
     }
@@ -1336,7 +1341,7 @@ __global__ __launch_bounds__(kPT) void decode_persistent_kernel(PArgs a) {
     else fetch_lm_head(pf, a);
     const int p_d = ph++;
     DH_MARK(a, p_d, 0);
-    if (!run_rows_resid<6>(a, S, pd, a.ff, a.hw, tg.t16(p_u), false, erow, xres, p_d, tg)) return;
+    if (!run_rows_resid<6>(a, S, pd, a.ff, a.hw, true, tg.t16(p_u), false, erow, xres, p_d, tg)) return;
     DH_MARK(a, p_d, 2);
     xph = p_d;
   }
@@ -1361,8 +1366,9 @@ int count_phases(const int* kinds, int n) {
 
 extern "C" int64_t dh_decode_persistent_scratch_bytes(int d, int GH, int H, int L, int ff, int grid) {
   // tagged bf16 vectors: x, V0, A, h, q, k, v, y; fp32 records: gates, segment records, candidates
-  const int64_t w16 = (int64_t)d * 6 + (int64_t)d / 4 * kXSeg + GH + ff;   // x padded (xpos)
-  const int64_t w32 = (int64_t)H * L * 2 + (int64_t)H * kSplitS * (2 + kHD) + (int64_t)2 * grid;
+  // x (xpos), the in-projection group (p3 over max(d + GH, 3d) rows), h (p3), y
+  const int64_t w16 = (int64_t)d / 4 * kXSeg + p3_extent(d + GH > 3 * d ? d + GH : 3 * d) + p3_extent(ff) + d;
+  const int64_t w32 = (int64_t)H * L * 2 + (int64_t)H * kSplitS * (2 + kHD) + (int64_t)8 * grid;
   return 256 + (w16 * 4 + 255) / 256 * 256 + w32 * 8 + 256;
 }
 
@@ -1417,15 +1423,13 @@ int launch_persistent(const char* who, const int64_t* layer_table, const int* ki
   a.epoch = (int64_t*)p;
   a.status = (uint32_t*)(p + 8);
   uint32_t* w = (uint32_t*)(p + 256);
+  a.n3w = p3_extent(d + GH > 3 * d ? d + GH : 3 * d);
+  a.nhw = p3_extent(ff);
   a.xw = w; w += d / 4 * kXSeg;
-  a.v0w = w; w += d;
-  a.aw = w; w += GH;
-  a.hw = w; w += ff;
-  a.qw = w; w += d;
-  a.kw = w; w += d;
-  a.vw = w; w += d;
+  a.i3w = w; w += a.n3w;
+  a.hw = w; w += a.nhw;
   a.yw = w; w += d;
-  uint64_t* r = (uint64_t*)(p + 256 + ((int64_t)(6 * d + d / 4 * kXSeg + GH + ff) * 4 + 255) / 256 * 256);
+  uint64_t* r = (uint64_t*)(p + 256 + ((int64_t)(w - (uint32_t*)(p + 256)) * 4 + 255) / 256 * 256);
   a.coefw = r; r += (int64_t)H * L * 2;
   a.partw = r; r += (int64_t)H * kSplitS * (2 + kHD);
   a.candw = r;
