@@ -33,6 +33,8 @@ constexpr int kMaxLayers = 64;
 constexpr int kLMax = 12;                // recurrence levels held in registers
 constexpr int kSplitS = 16;              // attention window segments
 constexpr int kHD = 64;                  // attention head width
+constexpr int kRecW = 72;                // 64-bit words per segment record (m, l, kHD outputs): 64-byte multiple
+static_assert(kRecW >= 2 + kHD && kRecW % 8 == 0, "segment records fill whole 64-byte segments");
 constexpr int kUT = 128;                 // threads per attention segment unit (two per workgroup)
 constexpr int kMaxSeg = DH_PERSISTENT_MAX_WINDOW / kSplitS;
 constexpr uint64_t kSpinTicks = 20000000ull;   // 200 ms of the 100 MHz real-time counter
@@ -1042,7 +1044,7 @@ __device__ __forceinline__ bool run_attn_split(const PArgs& a, Smem& S, const Pr
   }
   __syncthreads();
   if (unit_live) {
-    uint64_t* rec = a.partw + ((int64_t)h * kSplitS + sg) * (2 + kHD);
+    uint64_t* rec = a.partw + ((int64_t)h * kSplitS + sg) * kRecW;
     if (ut < kHD) {
       float o = has_t ? sc[nw_ - 1 - j0] * S.vsh[un][ut] : 0.f;
 #pragma unroll
@@ -1066,9 +1068,9 @@ __device__ __forceinline__ void phase_attn_combine(const PArgs& a, Smem& S, int 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if ((int)blockIdx.x >= a.H) return;                  // uniform
   const int h = blockIdx.x, e = lane;
-  const uint64_t* rec = a.partw + (int64_t)h * kSplitS * (2 + kHD);
+  const uint64_t* rec = a.partw + (int64_t)h * kSplitS * kRecW;
   const uint32_t* rec32 = reinterpret_cast<const uint32_t*>(rec);
-  const int nw32 = kSplitS * (2 + kHD) * 2;
+  const int nw32 = kSplitS * kRecW * 2;
   const uint32_t st = tg.t32(sph);
   float m4[4], l4[4], o4[4];
   {
@@ -1079,8 +1081,8 @@ __device__ __forceinline__ void phase_attn_combine(const PArgs& a, Smem& S, int 
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int sg = 4 * wave + q;
-        const uint4 ml = get16x4(rec32, nw32, sg * (2 + kHD) * 2);         // m, l of segment sg
-        const uint64_t ow = get32(rec + sg * (2 + kHD) + 2 + e);
+        const uint4 ml = get16x4(rec32, nw32, sg * kRecW * 2);         // m, l of segment sg
+        const uint64_t ow = get32(rec + sg * kRecW + 2 + e);
         ok = ok && ml.y == st && ml.w == st && (uint32_t)(ow >> 32) == st;
         m4[q] = __uint_as_float(ml.x);
         l4[q] = __uint_as_float(ml.z);
@@ -1368,7 +1370,7 @@ extern "C" int64_t dh_decode_persistent_scratch_bytes(int d, int GH, int H, int 
   // tagged bf16 vectors: x, V0, A, h, q, k, v, y; fp32 records: gates, segment records, candidates
   // x (xpos), the in-projection group (p3 over max(d + GH, 3d) rows), h (p3), y
   const int64_t w16 = (int64_t)d / 4 * kXSeg + p3_extent(d + GH > 3 * d ? d + GH : 3 * d) + p3_extent(ff) + d;
-  const int64_t w32 = (int64_t)H * L * 2 + (int64_t)H * kSplitS * (2 + kHD) + (int64_t)8 * grid;
+  const int64_t w32 = ((int64_t)H * L * 2 + 7) / 8 * 8 + (int64_t)H * kSplitS * kRecW + (int64_t)8 * grid;
   return 256 + (w16 * 4 + 255) / 256 * 256 + w32 * 8 + 256;
 }
 
@@ -1430,8 +1432,8 @@ int launch_persistent(const char* who, const int64_t* layer_table, const int* ki
   a.hw = w; w += a.nhw;
   a.yw = w; w += d;
   uint64_t* r = (uint64_t*)(p + 256 + ((int64_t)(w - (uint32_t*)(p + 256)) * 4 + 255) / 256 * 256);
-  a.coefw = r; r += (int64_t)H * L * 2;
-  a.partw = r; r += (int64_t)H * kSplitS * (2 + kHD);
+  a.coefw = r; r += ((int64_t)H * L * 2 + 7) / 8 * 8;   // regions start on 64-byte boundaries
+  a.partw = r; r += (int64_t)H * kSplitS * kRecW;
   a.candw = r;
   // One workgroup per compute unit, all resident: the kernel's registers (>256 VGPRs over four
   // waves) admit at most one workgroup per CU, so a launch of exactly one per CU on an idle device
