@@ -620,40 +620,51 @@ __device__ __forceinline__ void fetch_gates(PreGates& f, const PArgs& a, LayerRe
   f.rsrc = ld2((const bf16_t*)(intptr_t)Lt[F_RGHIST] + (sc * L + l) * H + h);
 }
 
-__device__ __forceinline__ void run_gates(const PArgs& a, const PreGates& f, LayerRef Lt, int64_t t,
+__device__ __forceinline__ void run_gates(const PArgs& a, Smem& S, const PreGates& f, LayerRef Lt, int64_t t,
                                           uint32_t atag, int ph, Tags tg) {
   constexpr int C = 2;
-  const int lane = threadIdx.x & 63;
-  const int u = blockIdx.x * kPW + (threadIdx.x >> 6);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int u = blockIdx.x * kPW + (tid >> 6);
   const int H = a.H, L = a.L, GH = a.GH;
+  if (blockIdx.x * kPW >= H * L) return;               // uniform: no unit in this workgroup
+  const int nchunk = GH / 8;                           // <= kPT
+  // A polled once per workgroup (thread i: chunk i, 8 tagged words) into LDS, instead of by every
+  // wave: a quarter of the poll traffic, and the workgroup's waves see A in the same round
+  {
+    const bool mine = tid < nchunk;
+    const uint32_t tg16 = tg.t16(atag);
+    uint4 p0 = make_uint4(0u, 0u, 0u, 0u), p1 = p0;
+    Waiter wt;
+    while (true) {
+      bool okw = true;
+      if (mine) {
+        p0 = get16x4(a.i3w, a.n3w, p3(a.d + tid * 8));
+        p1 = get16x4(a.i3w, a.n3w, p3(a.d + tid * 8 + 4));
+      }
+      const uint32_t stw = tid == 0 ? get16(a.status) : 0u;   // with the data: no extra round trip
+      if (mine)
+        okw = tag_ok(p0.x, tg16) && tag_ok(p0.y, tg16) && tag_ok(p0.z, tg16) && tag_ok(p0.w, tg16) &&
+              tag_ok(p1.x, tg16) && tag_ok(p1.y, tg16) && tag_ok(p1.z, tg16) && tag_ok(p1.w, tg16);
+      if (tid == 0) S.stop = wt.expired(stw) ? 1 : 0;
+      if (__syncthreads_and(okw ? 1 : 0)) break;
+      if (S.stop) {
+        if (tid == 0) raise_abort(a, ph, wt.why, wt.polls);
+        return;
+      }
+    }
+    DH_MARK(a, ph, 1);
+    if (mine)
+      S.sx[tid] = make_uint4((p0.x >> 16) | (p0.y & 0xffff0000u), (p0.z >> 16) | (p0.w & 0xffff0000u),
+                             (p1.x >> 16) | (p1.y & 0xffff0000u), (p1.z >> 16) | (p1.w & 0xffff0000u));
+    __syncthreads();
+  }
   if (u >= H * L) return;                              // uniform per wave
   const int h = u % H, l = u / H;
-  const int nchunk = GH / 8;
   const int64_t src = t - ((int64_t)1 << l);
   const bool ok = src >= 0;
-  // A: 8 tagged words per chunk, chunk lane + 64c
   uint4 av[C];
-  Waiter wt;
-  const uint32_t tg16 = tg.t16(atag);
-  while (true) {
-    const uint32_t stw = get16(a.status);               // with the data: no extra round trip
-    bool okw = true;
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-      const int ch = min(lane + 64 * c, nchunk - 1);
-      const uint4 p0 = get16x4(a.i3w, a.n3w, p3(a.d + ch * 8)), p1 = get16x4(a.i3w, a.n3w, p3(a.d + ch * 8 + 4));
-      okw = okw && tag_ok(p0.x, tg16) && tag_ok(p0.y, tg16) && tag_ok(p0.z, tg16) && tag_ok(p0.w, tg16) &&
-            tag_ok(p1.x, tg16) && tag_ok(p1.y, tg16) && tag_ok(p1.z, tg16) && tag_ok(p1.w, tg16);
-      av[c] = make_uint4((p0.x >> 16) | (p0.y & 0xffff0000u), (p0.z >> 16) | (p0.w & 0xffff0000u),
-                         (p1.x >> 16) | (p1.y & 0xffff0000u), (p1.z >> 16) | (p1.w & 0xffff0000u));
-    }
-    if (__all(okw)) break;
-    if (wt.expired(__builtin_amdgcn_readfirstlane(stw))) {
-      raise_abort(a, ph, wt.why, wt.polls);
-      return;
-    }
-  }
-  DH_MARK(a, ph, 1);
+  for (int c = 0; c < C; ++c) av[c] = S.sx[min(lane + 64 * c, nchunk - 1)];
   float s0 = 0.f, s1 = 0.f, s2 = 0.f;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
@@ -1300,7 +1311,7 @@ __global__ __launch_bounds__(kPT) void decode_persistent_kernel(PArgs a) {
       fetch_scan(ps, a, Lt, t);
       const int p_g = ph++;
       DH_MARK(a, p_g, 0);
-      run_gates(a, pg, Lt, t, p_in, p_g, tg);
+      run_gates(a, S, pg, Lt, t, p_in, p_g, tg);
       DH_MARK(a, p_g, 2);
       fetch_ffn_up(pu, a, Lt);
       const int p_s = ph++;
