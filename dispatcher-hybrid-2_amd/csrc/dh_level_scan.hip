@@ -22,6 +22,8 @@
 // consecutive dispatch slots, so those lines are fetched once into that XCD's L2.
 #include "dh_common.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int kThreads = 512;
@@ -336,6 +338,32 @@ __global__ __launch_bounds__(1024) void level_scan_wide_kernel(ScanArgs a) {
       }
     }
     fetch(l + 1 < a.n_lv ? l + 1 : l);                 // next level's gates fly during the exchange
+    if (shift >= NT) {                                   // uniform
+      // lags of whole slots (2^l = K * NT): the source of position tid + j * NT is this thread's
+      // slot j - K, so the level needs no exchange and no barrier. Slots update in descending order,
+      // so slot j - K still holds the previous level's state. Without a source (j < K) a = 0, and
+      // the clamped slot 0 stands in, as the exchange's clamped read of position 0 does.
+      auto step = [&](auto kc) {
+        constexpr int K = decltype(kc)::value;
+#pragma unroll
+        for (int j = PPT - 1; j >= 0; --j) {
+          const int sj = j - K >= 0 ? j - K : 0;
+          const float coef = ad[j] * rg[sj];
+#pragma unroll
+          for (int q = 0; q < C / 2; ++q) {
+            const float w0 = V[sj][2 * q], w1 = V[sj][2 * q + 1];
+            V[j][2 * q] = fg[j] * V[j][2 * q] + coef * w0;
+            V[j][2 * q + 1] = fg[j] * V[j][2 * q + 1] + coef * w1;
+          }
+        }
+      };
+      const int k = shift / NT;
+      if (k == 1) step(std::integral_constant<int, 1>{});
+      else if (k == 2) step(std::integral_constant<int, 2>{});
+      else step(std::integral_constant<int, PPT>{});   // k >= PPT: no position has a source
+      write_slab(l + 1);
+      continue;
+    }
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
       const int t = tid + j * NT;

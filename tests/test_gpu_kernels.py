@@ -172,6 +172,32 @@ def test_level_scan_known_answers_exact(dtype):
         assert torch.equal(V[0], V0[0, src])
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_level_scan_known_answers_long_lags(dtype):
+    """Lags of whole 1024-position slots (T = 4096: levels 10 and 11, lags 1024 and 2048) take their
+    source from the thread's own registers instead of the LDS exchange. V0[t] = e_(t mod 128) with
+    saturated gates: the window sums count each residue class's positions (at most 32, exact in
+    every dtype) and the pure shifts move rows; both are checked bit for bit."""
+    from dispatcher_hybrid.fused_gates import fused_level_scan
+    T, H, hd = 4096, 2, 64
+    C = H * hd
+    t = torch.arange(T, device=DEV)
+    V0 = torch.zeros(1, T, C, dtype=dtype, device=DEV)
+    V0[0, t, t % C] = 1
+    onehot = torch.zeros(T, C, device=DEV)
+    onehot[t, t % C] = 1
+    for n_lv in (11, 12):
+        print(f"level_scan long lags n_lv={n_lv} dtype={dtype}", flush=True)
+        on = torch.full((1, T, n_lv, H), 30.0, dtype=dtype, device=DEV)
+        off = torch.full((1, T, n_lv, H), -200.0, dtype=dtype, device=DEV)
+        V = fused_level_scan(on, on, on, None, V0, H, n_lv)       # window sums of width 2^n_lv
+        win = ((t[None, :] <= t[:, None]) & (t[None, :] > t[:, None] - (1 << n_lv))).float()
+        assert torch.equal(V[0], (win @ onehot).to(dtype))
+        V = fused_level_scan(on, off, on, None, V0, H, n_lv)      # pure shift by 2^n_lv - 1
+        src = (t - ((1 << n_lv) - 1)).clamp(min=0)
+        assert torch.equal(V[0], V0[0, src])
+
+
 # --------------------------------------------------------------------------------------------
 # gate_scan_fwd: activated, masked gates written head-major by the pre-activation kernel, then the
 # scan in its activated mode
