@@ -54,6 +54,7 @@ struct GemvArgs {
   int nseg;
   int B, K, Nrows;
   Cand* cand;                   // nullable (B = 1): the launch's argmax candidate per workgroup
+  int tile_rows;                // batched matrix-core GEMV: real weight rows per 16-row MFMA tile (16 or 8)
 };
 
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
@@ -687,7 +688,7 @@ __device__ __forceinline__ void norm_chunk(unsigned char* row, int c, float rs, 
   *reinterpret_cast<uint4*>(row + c * 16) = Vec<bf16_t>::pack(xf);
 }
 
-template <int KSPLIT, int TPW, int KSW, bool SW, bool GA>
+template <int KSPLIT, int TPW, int KSW, bool SW, bool GA, bool HALF>
 __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(GemvArgs a, int steps_per_wave) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NT = 64 * KSPLIT * TPW;               // TPW 16-row tiles per workgroup share the staging
@@ -701,11 +702,15 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
   const int rowb = K * 2 + 16;                         // padded LDS row (bytes)
   unsigned char* hs = smem;                            // [16][rowb] staged rows
   float* red = reinterpret_cast<float*>(smem + 16 * rowb);   // [TPW][KSPLIT][NW][64][4] partial tiles
-  const int n0 = min((blockIdx.x * TPW + tile) * 16, ((a.Nrows - 1) / 16) * 16);   // past the end: last tile
-  const bool tile_live = (blockIdx.x * TPW + tile) * 16 < a.Nrows;
+  // tiles of tr real rows (16, or 8 for outputs with few tiles: twice the workgroups stream the
+  // weights; lanes r >= 8 then read nothing and their output columns are dropped)
+  constexpr int trs = HALF ? 3 : 4;                   // log2 of the real rows per tile (a compile-time
+  constexpr int tr = 1 << trs;                         // choice: read from the arguments it cost a wait)
+  const int n0 = min((int)(blockIdx.x * TPW + tile) << trs, ((a.Nrows - 1) >> trs) << trs);   // past the end: last tile
+  const bool tile_live = ((int)(blockIdx.x * TPW + tile) << trs) < a.Nrows;
   const RowSeg seg0 = SW ? RowSeg{0, n0} : row_segment(a, n0);
   // a partial last tile (one segment only) reads its last real row in place of the missing ones
-  const bool row_ok = n0 + r < a.Nrows;
+  const bool row_ok = r < tr && n0 + r < a.Nrows;
   const int wrow = seg0.local + (row_ok ? r : a.Nrows - 1 - n0);
   // this tile's weight rows (segment rows seg0.local .. +15; a lane reads row wrow)
   const bf16_t* wt0 = (const bf16_t*)pick_seg(seg0.s, a.seg[0].W, a.seg[1].W, a.seg[2].W) + (int64_t)seg0.local * K;
@@ -748,7 +753,7 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
     const __amdgpu_buffer_rsrc_t rw1 = buf_rsrc(wt1, wbytes);
 #pragma unroll
     for (int j = 0; j < KSW; ++j) {
-      const uint32_t off = j < my_steps ? (uint32_t)((wr * K + (s0 + j) * 32 + 8 * g) * 2) : kOOB;
+      const uint32_t off = j < my_steps && r < tr ? (uint32_t)((wr * K + (s0 + j) * 32 + 8 * g) * 2) : kOOB;
       wf[0][j] = bld16(rw0, off);
       if (SW) wf[NW - 1][j] = bld16(rw1, off);
     }
@@ -1049,12 +1054,14 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_pers_kerne
 template <int KSPLIT, int TPW, int KSW, bool SW>
 void launch_mfma_k(const GemvArgs& a, int steps_per_wave, hipStream_t s) {
   const size_t lds = (size_t)16 * (a.K * 2 + 16) + (size_t)TPW * KSPLIT * (SW ? 2 : 1) * 64 * 16;
-  auto kern = a.x_rows || a.resid_rows ? &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, true>
-                                       : &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, false>;
+  auto kern = a.x_rows || a.resid_rows ? &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, true, false>
+                                       : &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, false, false>;
+  if constexpr (!SW && TPW == 1)
+    if (a.tile_rows == 8) kern = &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, false, true>;
   if (lds > 64 * 1024)
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)lds);
-  const int tiles = (a.Nrows + 15) / 16;
+  const int tiles = (a.Nrows + a.tile_rows - 1) / a.tile_rows;
   kern<<<dim3((tiles + TPW - 1) / TPW), dim3(64 * KSPLIT * TPW), lds, s>>>(a, steps_per_wave);
 }
 
@@ -1074,8 +1081,12 @@ bool mfma_gemv_fits(const GemvArgs& a, bool swiglu) {
 }
 
 template <bool SW>
-void launch_mfma(const GemvArgs& a, hipStream_t s) {
-  const int tiles = (a.Nrows + 15) / 16, nsteps = a.K / 32;
+void launch_mfma(const GemvArgs& a0, hipStream_t s) {
+  // outputs of fewer than 128 sixteen-row tiles (the 1024-row projections) run tiles of 8 real rows:
+  // twice the workgroups streaming the weights (rows in place only)
+  GemvArgs a = a0;
+  if (!SW && a.nseg == 1 && !a.x_rows && !a.resid_rows && (a.Nrows + 15) / 16 < 128) a.tile_rows = 8;
+  const int tiles = (a.Nrows + a.tile_rows - 1) / a.tile_rows, nsteps = a.K / 32;
   constexpr int kmax = SW ? 8 : 16;
   int ks = 4;
   while (ks < kmax && (tiles * ks < 1024 || a.K > 256 * ks)) ks *= 2;
@@ -1236,6 +1247,7 @@ extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const
     total = N[0];
   }
   a.Nrows = total;
+  a.tile_rows = 16;
   const int C = (K / vec + 63) / 64;
   DH_REQUIRE(C <= 12, DH_ERR_UNSUPPORTED_SHAPE, "%s: K=%d exceeds %d elements per row", who, K, 12 * 64 * vec);
   const int esz = dtype == DH_BF16 ? 2 : 4;
