@@ -314,6 +314,7 @@ DECODE_CASES = [
     (2, 24, 4096, 1024, 16, 64, 12),    # release shapes (first positions)
     (8, 30, 128, 256, 4, 32, 8),        # batched gate readouts (four rows per wave)
     (5, 24, 64, 128, 8, 16, 7),         # the same with a partial last group of rows
+    (16, 20, 64, 128, 8, 16, 6),        # 128 (row, head) pairs: one row per mixer-step workgroup
 ]
 
 
