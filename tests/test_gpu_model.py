@@ -344,6 +344,34 @@ def test_release_prefill_fused_gates_tolerances(release_models):
     bf16_vs_truth(f16, e16, e32, "C2 bf16")
 
 
+def test_release_graphed_forward_equals_fused_forward(release_models):
+    """graphed_logits (the C2 prefill as one HIP graph replay) against the fused forward it captured,
+    bit for bit: several replays, new token ids between them (one with an EOT, so the doc-reset mask
+    changes), the eager forward run between replays, and a second shape with its own graph."""
+    cfgd, m32, m16 = release_models
+    g = torch.Generator(device=DEV).manual_seed(5)
+    m16.enable_fused_gates()
+    try:
+        with torch.no_grad():
+            for rep in range(4):
+                ids = torch.randint(0, cfgd["vocab_size"], (1, 1024), device=DEV, generator=g)
+                if rep == 2:
+                    ids[0, 500] = cfgd["eot_token"]
+                print(f"graphed forward replay {rep}", flush=True)
+                got = m16.graphed_logits(ids).clone()
+                torch.cuda.synchronize()
+                ref = m16(ids).logits
+                torch.cuda.synchronize()
+                assert torch.equal(got, ref), f"replay {rep} differs from the fused forward"
+            ids2 = torch.randint(0, cfgd["vocab_size"], (2, 256), device=DEV, generator=g)
+            got2 = m16.graphed_logits(ids2).clone()
+            assert torch.equal(got2, m16(ids2).logits)
+            assert torch.equal(m16.graphed_logits(ids), m16(ids).logits)   # the first shape's graph again
+    finally:
+        m16.release_graphs()
+        m16.enable_fused_gates(False)
+
+
 def test_release_gate_preacts_bf16_per_layer(release_models):
     """Per-layer gate pre-activations (the fused op's outputs) against the eager formula on the
     same bf16 A and B (C5-style check at B=2, T=2048, doc mask on): |d| <= 3e-2, or one bf16 ulp
