@@ -10,13 +10,17 @@ out-projection + residual, RMSNorm + SwiGLU, down-projection + residual). A step
 (reference scripts/benchmark_decode.py:21-28 protocol). Also reported in the same JSON line:
   decode_b16_*      lockstep batch-16 decode with temperature 0.8 / top-k 50 sampling (dh_sample_topk)
   decoder_prefill_* the decoders' C3 prefill (3840 tokens, all decode state): fused vs eager
-  prefill_*         C2: 292M bf16 forward at B=1, T=1024, fused gates vs eager
-  forward_c5_*      C5: 292M bf16 forward at B=8, T=4096, fused gates vs eager (+ peak HBM)
+  prefill_*         C2: 292M bf16 forward at B=1, T=1024: graphed fused forward (graphed_logits), the
+                    fused forward launched from the host, eager
+  forward_c5_*      C5: 292M bf16 forward at B=8, T=4096: graphed fused forward (graphed_logits), the
+                    fused forward launched from the host, eager (+ peak HBM of the launched ones)
   gate_path_c5_*    one mixer layer at the C5 shape, fused vs eager
   prefill_kernels_c5  the parallel path's kernels at the C5 shape, HIP-event timed, each against its
                     roofline (gate pre-activations and banded attention: MFMA; level scan: HBM)
-  roofline          dh_decode_gemv, the dominant kernel (57 of the 97 launches of a step, ~55% of
-                    its time): algorithmic bytes / HIP-event-timed launch duration
+  roofline          decode_persistent_kernel (dh_decode_persistent_step), the only kernel of a
+                    batch-1 step: algorithmic bytes / HIP-event-timed launch duration (with
+                    --graph-step: dh_decode_gemv's launches of the graph of launches)
+  gemv_chain        dh_decode_gemv's 57 launches of the graph-of-launches step, the same measure
   mixer_step        the decoder's mixer step (dh_decode_gates + dh_decode_scan) per tree layer
   step_roofline     whole decode step: bf16 weight bytes per token x tok/s vs 8 TB/s
   parity_bf16       the north star's bf16 quantities (logit max-abs, greedy-argmax agreement) of the
@@ -788,12 +792,15 @@ def main():
         ids[:, 1000] = EOT
         f_tok, f_ms, f_peak = time_forward(torch, model, ids, True, reps=2)
         e_tok, e_ms, e_peak = time_forward(torch, model, ids, False, reps=2)
-        out["forward_c5_tok_s"] = round(f_tok, 1)
+        gc_tok, _ = time_forward_graphed(torch, model, ids, reps=3)
+        out["forward_c5_tok_s"] = round(gc_tok, 1)
+        out["forward_c5_host_launched_tok_s"] = round(f_tok, 1)
         out["forward_c5_eager_tok_s"] = round(e_tok, 1)
-        out["forward_c5_speedup_vs_eager"] = round(f_tok / e_tok, 3)
+        out["forward_c5_speedup_vs_eager"] = round(gc_tok / e_tok, 3)
         out["forward_c5_peak_gb"] = round(f_peak / 1e9, 2)
         out["forward_c5_eager_peak_gb"] = round(e_peak / 1e9, 2)
-        log(f"C5 forward: fused {f_tok:.0f} tok/s ({f_peak / 1e9:.1f} GB), eager {e_tok:.0f} tok/s ({e_peak / 1e9:.1f} GB)")
+        log(f"C5 forward: graphed {gc_tok:.0f} tok/s, fused launched from the host {f_tok:.0f} tok/s "
+            f"({f_peak / 1e9:.1f} GB), eager {e_tok:.0f} tok/s ({e_peak / 1e9:.1f} GB)")
 
         mixer = next(b.mixer for b in model.blocks if hasattr(b, "mixer"))
         x = torch.randn(8, 4096, 1024, device=dev, dtype=torch.bfloat16, generator=g)
