@@ -22,6 +22,7 @@ Importing this module loads the kernel library and raises ImportError if it is m
 """
 
 import ctypes
+import weakref
 from typing import List, Optional
 
 import torch
@@ -56,12 +57,32 @@ def _preacts_launch(A_, B_, Wi_, Wf_, Wr_, bi_, bf_, br_, mask, outs, ostrides, 
     _hip.check(st, what)
 
 
+# fp32 copies of bf16 gate biases (the kernel reads fp32 biases), one per bias tensor, refreshed
+# when the tensor's version counter moves (an in-place update): three cast launches per layer and
+# forward otherwise. A HIP graph captured over a forward keeps the copy it was captured with.
+# (keyed by id, with a weak reference that drops the entry when the tensor goes: a tensor cannot
+# be a WeakKeyDictionary key, whose lookups compare keys with ==)
+_BIAS_F32 = {}
+
+
+def _bias_f32(v, n_lv):
+    if v.dtype == torch.float32 or (v.requires_grad and torch.is_grad_enabled()):
+        return v[:n_lv].contiguous().float()
+    k = id(v)
+    ent = _BIAS_F32.get(k)
+    if ent is None or ent[0]() is not v or ent[1] != v._version or ent[2] != n_lv:
+        ref = weakref.ref(v, lambda _r, k=k: _BIAS_F32.pop(k, None))
+        ent = (ref, v._version, n_lv, v[:n_lv].contiguous().float())
+        _BIAS_F32[k] = ent
+    return ent[3]
+
+
 def _prep_gate_inputs(A, B, Wi, Wf, Wr, bi, bf, br, n_lv):
     cd = _compute_dtype(A)
     A_ = A.contiguous().to(cd)
     B_ = B.contiguous().to(cd)
     Wi_, Wf_, Wr_ = (w[:n_lv].contiguous().to(cd) for w in (Wi, Wf, Wr))
-    bi_, bf_, br_ = (v[:n_lv].contiguous().float() for v in (bi, bf, br))
+    bi_, bf_, br_ = (_bias_f32(v, n_lv) for v in (bi, bf, br))
     return A_, B_, Wi_, Wf_, Wr_, bi_, bf_, br_
 
 

@@ -20,6 +20,7 @@ Two implementations of the mixer, selected per module by `use_fused_gates`:
 """
 
 import math
+import sys
 
 import torch
 import torch.nn as nn
@@ -230,20 +231,22 @@ class WindowAttention(nn.Module):
         self.linear_k = nn.Linear(d, d, bias=False)
         self.linear_v = nn.Linear(d, d, bias=False)
         self.linear_out = nn.Linear(d, d, bias=False)
-        self._rope_key = None
+        self._rope_cache = {}
         self.use_fused = False      # gfx950 banded-attention kernel for inference (enable_fused_gates)
 
     def rope_tables(self, length, device, dtype):
-        """cos/sin of angle t * 10000^(-2i/hd), (length, hd/2), cached per (length, device, dtype).
-        Not a buffer: derived data stays out of checkpoints (reference :144-161)."""
+        """cos/sin of angle t * 10000^(-2i/hd), (length, hd/2), cached per (length, device, dtype)
+        -- one entry each, never replaced: a HIP graph captured over a forward keeps reading the
+        tables it was captured with. Not a buffer: derived data stays out of checkpoints
+        (reference :144-161)."""
         key = (length, device, dtype)
-        if self._rope_key != key:
+        tables = self._rope_cache.get(key)
+        if tables is None:
             inv_freq = torch.pow(10000.0, -torch.arange(0, self.head_dim, 2, device=device,
                                                         dtype=torch.float32) / self.head_dim)
             ang = torch.outer(torch.arange(length, device=device, dtype=torch.float32), inv_freq)
-            self._rope = (ang.cos().to(dtype), ang.sin().to(dtype))
-            self._rope_key = key
-        return self._rope
+            tables = self._rope_cache[key] = (ang.cos().to(dtype), ang.sin().to(dtype))
+        return tables
 
     def apply_rope(self, x, length):
         cos, sin = self.rope_tables(length, x.device, x.dtype)
@@ -358,19 +361,20 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
             for i in range(config.num_layers))
         self.norm_out = nn.RMSNorm(config.d_model)
         self.lm_head = nn.Linear(config.d_model, config.vocab_size, bias=False)
-        self._mask_key = None
+        self._mask_cache = {}
+        self._src_cache = {}
         self.post_init()
 
     def level_mask(self, length, device=None, dtype=torch.float32):
         """mask[t, l] = 1 iff position t has a predecessor 2^l back (t >= 2^l), (T, L).
         This is what keeps roll()'s wrapped (future) rows out of the eager mixer."""
         key = (length, device, dtype)
-        if self._mask_key != key:
+        mask = self._mask_cache.get(key)
+        if mask is None:                  # one entry per key, never replaced (see WindowAttention.rope_tables)
             t = torch.arange(length, device=device).unsqueeze(1)
             lag = torch.tensor([1 << l for l in range(self.config.levels)], device=device)
-            self._mask_cache = ((t >= lag) & (lag < length)).to(dtype)
-            self._mask_key = key
-        return self._mask_cache
+            mask = self._mask_cache[key] = ((t >= lag) & (lag < length)).to(dtype)
+        return mask
 
     def get_input_embeddings(self):
         return self.embedding
@@ -395,10 +399,20 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
             return mask
         is_eot = (input_ids == self.config.eot_token).to(mask.dtype)
         doc = torch.cumsum(is_eot, dim=1) - is_eot
-        t = torch.arange(length, device=input_ids.device)
-        same = torch.stack([doc == doc[:, (t - (1 << l)) % length] for l in range(self.config.levels)],
-                           dim=-1).to(mask.dtype)
+        # every level's source index (t - 2^l) mod T in one (T, L) table (cached with the level mask),
+        # so the comparison is one gather instead of a few launches per level
+        src = self._src_index(length, input_ids.device)
+        same = (doc.unsqueeze(-1) == doc[:, src]).to(mask.dtype)
         return mask.unsqueeze(0) * same[..., :mask.shape[-1]]
+
+    def _src_index(self, length, device):
+        key = (length, device)
+        src = self._src_cache.get(key)
+        if src is None:
+            t = torch.arange(length, device=device).unsqueeze(1)
+            lag = torch.tensor([1 << l for l in range(self.config.levels)], device=device)
+            src = self._src_cache[key] = (t - lag) % length
+        return src
 
     def forward(self, input_ids=None, attention_mask=None, labels=None, inputs_embeds=None,
                 use_cache=None, output_attentions=None, output_hidden_states=None,
@@ -461,9 +475,11 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
         The first call for a shape runs two warm-up forwards on a side stream and captures one
         forward; every call copies input_ids into the graph's input buffer and replays. The result
         is the graph's output buffer: the next call with the same shape overwrites it (clone it to
-        keep it). The parameters must stay where they are between calls (in-place updates are
-        seen); the path captured is the one active at the first call, so call enable_fused_gates()
-        first for the fused kernels. Bit for bit equal to self(input_ids).logits on that path.
+        keep it). The parameters must stay where they are between calls; in-place updates of the
+        weights are seen, but the fused path reads bf16 gate biases through fp32 copies made when a
+        forward runs, so after changing those call release_graphs() to capture again. The path
+        captured is the one active at the first call, so call enable_fused_gates() first for the
+        fused kernels. Bit for bit equal to self(input_ids).logits on that path.
         """
         if not input_ids.is_cuda:
             raise ValueError("graphed_logits needs input_ids on a GPU")
@@ -481,8 +497,12 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 out = self(static_ids).logits
-            entry = graphs[key] = (graph, static_ids, out)
-        graph, static_ids, out = entry
+            # the graph reads the fp32 gate-bias copies made by the warm-up forwards: keep them alive
+            # even if a later forward replaces them (after a bias update)
+            fg = sys.modules.get(__package__ + ".fused_gates")
+            keep = [e[3] for e in getattr(fg, "_BIAS_F32", {}).values()]
+            entry = graphs[key] = (graph, static_ids, out, keep)
+        graph, static_ids, out, _ = entry
         static_ids.copy_(input_ids)
         graph.replay()
         return out

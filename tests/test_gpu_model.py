@@ -50,6 +50,26 @@ def test_fused_forward_bf16_tracks_eager(tiny_gpu):
     assert argmax_agree(fused, eager) > 0.95
 
 
+def test_fused_forward_sees_in_place_bias_updates(tiny_gpu):
+    """The fused path reads bf16 gate biases through cached fp32 copies: an in-place update of a
+    bias must reach the next fused forward (the copy follows the tensor's version counter)."""
+    name, cfgd, sd, m = tiny_gpu
+    mb = product_model(cfgd, sd, device=DEV, dtype=torch.bfloat16).enable_fused_gates()
+    torch.manual_seed(1)
+    ids = torch.randint(0, cfgd["vocab_size"] - 1, (1, 48), device=DEV)
+    with torch.no_grad():
+        before = mb(ids).logits.clone()
+        for blk in mb.blocks:
+            if hasattr(blk, "mixer"):
+                blk.mixer.reset_out_bias.add_(-3.0)
+                blk.mixer.gate_out_bias.add_(1.5)
+        after = mb(ids).logits
+        mb.enable_fused_gates(False)
+        eager = mb(ids).logits
+    assert not torch.equal(before, after)
+    assert argmax_agree(after.float(), eager.float()) > 0.95
+
+
 def test_fused_autograd_matches_eager():
     """Gradients through dispatcher::gate_preacts_fwd/bwd equal the eager mixer's (fp32)."""
     cfgd, sd = tiny("tiny_a")

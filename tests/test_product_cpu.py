@@ -104,6 +104,30 @@ def test_doc_reset_bounds_cross_document_influence():
         assert (m2(a).logits[0, 21:] - m2(b).logits[0, 21:]).abs().max().item() == 0.0
 
 
+def test_doc_reset_mask_one_gather_equals_per_level_form():
+    """The doc-reset mask built with one gather of the cached (T, L) source-index table equals the
+    per-level form of reference modeling_dispatcher.py:311-323 (doc ids compared at (t - 2^l) mod T,
+    level by level), bit for bit, over lengths around the level horizons and EOT patterns."""
+    for name in sorted(TINY_CONFIGS):
+        cfgd, sd = tiny(name)
+        m = product_model(cfgd, sd)
+        if not m.config.doc_reset:
+            continue
+        g = torch.Generator().manual_seed(3)
+        for T in (1, 2, 5, 37, 64):
+            ids = torch.randint(0, cfgd["vocab_size"], (3, T), generator=g)
+            ids[0, T // 2] = m.config.eot_token
+            ids[2, ::3] = m.config.eot_token
+            got = m._tree_mask(ids, T)
+            mask = m.level_mask(T, ids.device, m.embedding.weight.dtype)
+            is_eot = (ids == m.config.eot_token).to(mask.dtype)
+            doc = torch.cumsum(is_eot, dim=1) - is_eot
+            t = torch.arange(T)
+            same = torch.stack([doc == doc[:, (t - (1 << l)) % T] for l in range(m.config.levels)], dim=-1)
+            ref = mask.unsqueeze(0) * same.to(mask.dtype)[..., :mask.shape[-1]]
+            assert torch.equal(got, ref), (name, T)
+
+
 def test_batched_matches_single():
     """reference tests/test_decoding.py:134-153."""
     from dispatcher_hybrid.decoding import IncrementalDecoder
