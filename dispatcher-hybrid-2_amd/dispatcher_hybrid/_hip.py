@@ -15,7 +15,7 @@ import os
 
 import torch
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 _LIB_NAME = "libdh_mixer.so"
 
 DH_F32, DH_BF16 = 0, 1
@@ -88,6 +88,7 @@ def _load():
         "dh_decode_persistent_trace": ([vp, vp, i32, vp, vp, ctypes.c_float] + [i32] * 8
                                        + [vp, vp, vp, i64, vp, vp, i64, vp, i64, vp], i32),
         "dh_decode_persistent_phases": ([vp, i32], i32),
+        "dh_silu_mul": ([i32, vp, vp, vp, i64, vp], i32),
     }
     for name, (argtypes, restype) in sigs.items():
         fn = getattr(lib, name)

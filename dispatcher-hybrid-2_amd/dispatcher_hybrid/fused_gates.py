@@ -18,6 +18,8 @@ Also registered here: ``dispatcher::level_scan_fwd``, the sigmoid/mask/level-sca
 mixer (``dh_level_scan_fwd``), which the reference runs as eager torch ops
 (reference dispatcher_hybrid/modeling_dispatcher.py:86-88, 111-121).
 
+``silu_mul`` is the feed-forward block's SwiGLU activation in one launch (``dh_silu_mul``).
+
 Importing this module loads the kernel library and raises ImportError if it is missing.
 """
 
@@ -363,3 +365,23 @@ def input_projections(x, mixer):
             and all(l.weight.shape[0] % 4 == 0 for l in lins)):
         return fused_projections(x, [l.weight for l in lins])
     return tuple(l(x) for l in lins)
+
+
+def silu_mul(gate, up, out=None):
+    """silu(gate) * up in one launch (``dh_silu_mul``): the SwiGLU activation of reference
+    dispatcher_hybrid/modeling_dispatcher.py:197, F.silu(linear_gate(h)) * linear_up(h), at its
+    eager rounding points (bf16: silu rounded to bf16, then the product rounded). gate and up:
+    same shape, fp32 or bf16 CUDA tensors; out (optional) may be gate or up. Inference only."""
+    _hip.require_gpu(gate, "silu_mul")
+    if up.shape != gate.shape or up.dtype != gate.dtype or gate.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("silu_mul: gate and up need one shape and one dtype, fp32 or bf16")
+    # contiguous and 16-byte aligned (a view at an odd storage offset is copied)
+    g = gate.contiguous() if gate.is_contiguous() and gate.data_ptr() % 16 == 0 else gate.clone()
+    u = up.contiguous() if up.is_contiguous() and up.data_ptr() % 16 == 0 else up.clone()
+    o = torch.empty_like(g) if out is None else out
+    if o.shape != g.shape or o.dtype != g.dtype or not o.is_contiguous():
+        raise ValueError("silu_mul: out must be a contiguous tensor of gate's shape and dtype")
+    st = _hip.lib.dh_silu_mul(_hip.dtype_code(g.dtype), _hip.ptr(g), _hip.ptr(u), _hip.ptr(o), g.numel(),
+                              _hip.stream_handle(g.device))
+    _hip.check(st, "dh_silu_mul")
+    return o

@@ -283,6 +283,12 @@ class WindowAttention(nn.Module):
 
 
 class SwiGLU(nn.Module):
+    """linear_down(silu(linear_gate(h)) * linear_up(h)) (reference modeling_dispatcher.py:188-197).
+    With use_fused (set by enable_fused_gates) and no autograd, the activation is one dh_silu_mul
+    launch at the same rounding points instead of a SiLU and a product launch."""
+
+    use_fused = False
+
     def __init__(self, config: DispatcherConfig):
         super().__init__()
         d, ff = config.d_model, config.dim_feedforward
@@ -291,6 +297,10 @@ class SwiGLU(nn.Module):
         self.linear_down = nn.Linear(ff, d, bias=False)
 
     def forward(self, h):
+        if self.use_fused and h.is_cuda and not torch.is_grad_enabled():
+            from .fused_gates import silu_mul
+            g = self.linear_gate(h)
+            return self.linear_down(silu_mul(g, self.linear_up(h), out=g))
         return self.linear_down(F.silu(self.linear_gate(h)) * self.linear_up(h))
 
 
@@ -451,7 +461,8 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
 
     def enable_fused_gates(self, enabled=True):
         """Run every mixer's gate pipeline and level scan on the gfx950 HIP kernels (and, without
-        autograd in bf16, every attention layer on the banded-attention kernel).
+        autograd, every SwiGLU activation on dh_silu_mul and, in bf16, every attention layer on the
+        banded-attention kernel).
 
         Loads the kernel library now (raising ImportError if it is missing) rather than in the
         middle of a forward. The fused path needs GPU tensors; returns self.
@@ -464,6 +475,9 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
             if hasattr(blk, "attn"):
                 # inference only: attention layers take the banded-attention kernel (bf16)
                 blk.attn.use_fused = bool(enabled)
+            if hasattr(blk, "ffn"):
+                # inference only: the SwiGLU activation in one launch
+                blk.ffn.use_fused = bool(enabled)
         return self
 
     @torch.no_grad()

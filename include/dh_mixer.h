@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 13
+#define DH_ABI_VERSION 14
 
 enum dh_status {
   DH_OK = 0,
@@ -130,6 +130,17 @@ int dh_level_scan_fwd(int dtype, const void* pre_i, const void* pre_f, const voi
                       const void* mask, int64_t stride_mb, int64_t stride_mt, int64_t stride_ml,
                       const void* V0, int64_t stride_vb, int64_t stride_vt, void* V, int b, int T, int H,
                       int hd, int n_lv, int activated, void* ring, int ring_L, void* stream);
+
+/*
+ * The feed-forward block's SwiGLU activation over n elements:
+ *   out[i] = silu(gate[i]) * up[i],  silu(x) = x / (1 + e^-x)
+ * Replaces F.silu(linear_gate(h)) * linear_up(h) of reference
+ * dispatcher_hybrid/modeling_dispatcher.py:197 (SwiGLU.forward), two launches and a rounded
+ * intermediate, at the eager rounding points: in bf16, silu is rounded to bf16 before the product
+ * and the product is rounded again. dtype DH_F32 or DH_BF16; gate, up and out contiguous and
+ * 16-byte aligned (out may alias gate or up). n == 0 is a no-op.
+ */
+int dh_silu_mul(int dtype, const void* gate, const void* up, void* out, int64_t n, void* stream);
 
 /*
  * One decode step of one tree layer: all L levels' gate readouts plus the L-level recurrence over

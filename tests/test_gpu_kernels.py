@@ -533,3 +533,52 @@ def test_scan_out_residual_rows_in_place_and_range():
                                       W_out, emb, x, resid_rows=rows)
     torch.cuda.synchronize()
     assert torch.equal(st.V_ring, ring0) and torch.equal(st.Y, Y0) and torch.equal(x, x3)
+
+
+# ---- dh_silu_mul: the SwiGLU activation (reference modeling_dispatcher.py:197) ----
+
+def _bf16_round_np(x):
+    """fp32 -> bf16 -> fp32, round to nearest even (numpy, the CPU statement of the rounding)."""
+    b = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFF0000
+    return b.astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("n", [0, 1, 7, 8, 9, 4096 + 5, 1024 * 2816 + 3])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_silu_mul_matches_eager_swiglu(n, dtype):
+    from dispatcher_hybrid.fused_gates import silu_mul
+    g = (torch.randn(n, generator=torch.Generator().manual_seed(n)) * 4).to("cuda", dtype)
+    u = torch.randn(n, generator=torch.Generator().manual_seed(n + 1)).to("cuda", dtype)
+    out = silu_mul(g, u)
+    ref = torch.nn.functional.silu(g) * u          # the reference's eager activation
+    # CPU statement of the same rounding points in float64 math
+    g64, u64 = _np(g).astype(np.float64), _np(u).astype(np.float64)
+    s = g64 / (1.0 + np.exp(-g64))
+    if dtype == torch.bfloat16:
+        cpu = _bf16_round_np(_bf16_round_np(s.astype(np.float32)).astype(np.float64) * u64)
+        # exact against torch's kernel, up to a 1-ulp rounding flip where exp's last bit decides it
+        d = (out.float() - ref.float()).abs()
+        ulp = ref.float().abs().clamp_min(1e-30) * 2.0 ** -7
+        assert bool((d <= ulp).all())
+        assert int((d > 0).sum()) <= max(1, n // 10000)
+        dc = np.abs(_np(out).astype(np.float64) - cpu)
+        assert (dc <= np.maximum(np.abs(cpu), 1e-30) * 2.0 ** -7).all()
+    else:
+        assert rel_err(_np(out), _np(ref)) <= 1e-6 if n else True
+        if n:
+            assert np.allclose(_np(out), s * u64, rtol=2e-6, atol=1e-30)
+
+
+def test_silu_mul_in_place_and_unaligned_views():
+    from dispatcher_hybrid.fused_gates import silu_mul
+    base_g = torch.randn(10001, device="cuda", dtype=torch.bfloat16)
+    base_u = torch.randn(10001, device="cuda", dtype=torch.bfloat16)
+    g, u = base_g[1:], base_u[1:]                 # 2-byte storage offset: copied by the wrapper
+    want = silu_mul(g.clone(), u.clone())
+    assert torch.equal(silu_mul(g, u), want)
+    gi = g.clone()
+    got = silu_mul(gi, u.clone(), out=gi)          # in place over gate, as SwiGLU's fused forward does
+    assert got.data_ptr() == gi.data_ptr() and torch.equal(got, want)
+    with pytest.raises(ValueError):
+        silu_mul(g, u.float())
