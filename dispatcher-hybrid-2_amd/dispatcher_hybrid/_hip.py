@@ -15,7 +15,7 @@ import os
 
 import torch
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 _LIB_NAME = "libdh_mixer.so"
 
 DH_F32, DH_BF16 = 0, 1
@@ -89,6 +89,7 @@ def _load():
                                        + [vp, vp, vp, i64, vp, vp, i64, vp, i64, vp], i32),
         "dh_decode_persistent_phases": ([vp, i32], i32),
         "dh_silu_mul": ([i32, vp, vp, vp, i64, vp], i32),
+        "dh_add_rmsnorm": ([i32, vp, vp, vp, ctypes.c_float, vp, vp, i64, i32, vp], i32),
     }
     for name, (argtypes, restype) in sigs.items():
         fn = getattr(lib, name)

@@ -18,7 +18,8 @@ Also registered here: ``dispatcher::level_scan_fwd``, the sigmoid/mask/level-sca
 mixer (``dh_level_scan_fwd``), which the reference runs as eager torch ops
 (reference dispatcher_hybrid/modeling_dispatcher.py:86-88, 111-121).
 
-``silu_mul`` is the feed-forward block's SwiGLU activation in one launch (``dh_silu_mul``).
+``silu_mul`` is the feed-forward block's SwiGLU activation in one launch (``dh_silu_mul``);
+``add_rmsnorm`` a residual add and the RMSNorm after it (``dh_add_rmsnorm``).
 
 Importing this module loads the kernel library and raises ImportError if it is missing.
 """
@@ -385,3 +386,34 @@ def silu_mul(gate, up, out=None):
                               _hip.stream_handle(g.device))
     _hip.check(st, "dh_silu_mul")
     return o
+
+
+def _rms_eps(norm):
+    # nn.RMSNorm(eps=None) uses the machine epsilon of its fp32 computation type
+    return norm.eps if norm.eps is not None else torch.finfo(torch.float32).eps
+
+
+def add_rmsnorm(x, y, norm, out=None):
+    """(x + y, norm(x + y)) in one launch (``dh_add_rmsnorm``): the residual add of a block and the
+    RMSNorm after it (reference dispatcher_hybrid/modeling_dispatcher.py:210-212, 225-227, 341-348).
+    x, y: (..., d) fp32 or bf16 CUDA tensors of one shape and dtype; norm: an nn.RMSNorm over d with
+    a weight of x's dtype. The sum is written to `out` (x itself may be passed) or a new tensor.
+    Inference only."""
+    _hip.require_gpu(x, "add_rmsnorm")
+    d = x.shape[-1]
+    w = norm.weight
+    if (y.shape != x.shape or y.dtype != x.dtype or x.dtype not in (torch.float32, torch.bfloat16)
+            or w is None or w.dtype != x.dtype or tuple(w.shape) != (d,) or tuple(norm.normalized_shape) != (d,)):
+        raise ValueError("add_rmsnorm: x, y need one shape and dtype (fp32 or bf16) and a weighted RMSNorm over "
+                         "their last dimension in that dtype")
+    xs = x if x.is_contiguous() and x.data_ptr() % 16 == 0 else x.contiguous().clone()
+    ys = y if y.is_contiguous() and y.data_ptr() % 16 == 0 else y.contiguous().clone()
+    xo = torch.empty_like(xs) if out is None else out
+    if xo.shape != x.shape or xo.dtype != x.dtype or not xo.is_contiguous():
+        raise ValueError("add_rmsnorm: out must be a contiguous tensor of x's shape and dtype")
+    h = torch.empty_like(xs)
+    st = _hip.lib.dh_add_rmsnorm(_hip.dtype_code(x.dtype), _hip.ptr(xs), _hip.ptr(ys), _hip.ptr(w),
+                                 float(_rms_eps(norm)), _hip.ptr(xo), _hip.ptr(h), xs.numel() // d, d,
+                                 _hip.stream_handle(x.device))
+    _hip.check(st, "dh_add_rmsnorm")
+    return xo, h

@@ -437,14 +437,17 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
         mask = self._tree_mask(input_ids, length)
         hidden_states = () if output_hidden_states else None
         x = self.embedding(input_ids)
-        for block in self.blocks:
-            if output_hidden_states:
-                hidden_states = hidden_states + (x,)
-            if getattr(self, "gradient_checkpointing", False) and self.training:
-                x = self._gradient_checkpointing_func(block.__call__, x, mask)
-            else:
-                x = block(x, mask)
-        x = self.norm_out(x)
+        if self._fused_norm_ok(x, output_hidden_states):
+            x = self._blocks_fused_norms(x, mask)
+        else:
+            for block in self.blocks:
+                if output_hidden_states:
+                    hidden_states = hidden_states + (x,)
+                if getattr(self, "gradient_checkpointing", False) and self.training:
+                    x = self._gradient_checkpointing_func(block.__call__, x, mask)
+                else:
+                    x = block(x, mask)
+            x = self.norm_out(x)
         if output_hidden_states:
             hidden_states = hidden_states + (x,)
         logits = self.lm_head(x)
@@ -459,10 +462,34 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
     def prepare_inputs_for_generation(self, input_ids, **kwargs):
         return {"input_ids": input_ids[:, -self.config.max_len:]}
 
+    def _fused_norm_ok(self, x, output_hidden_states):
+        if not (getattr(self, "_fused_norms", False) and x.is_cuda and not torch.is_grad_enabled()
+                and not output_hidden_states and x.dtype in (torch.float32, torch.bfloat16) and len(self.blocks)):
+            return False
+        norms = [self.norm_out] + [n for blk in self.blocks for n in (blk.norm1, blk.norm2)]
+        return all(n.weight is not None and n.weight.dtype == x.dtype for n in norms)
+
+    def _blocks_fused_norms(self, x, mask):
+        """The blocks and norm_out with every residual add fused into the RMSNorm that follows it
+        (dh_add_rmsnorm): norm1 of the first block, then per block sublayer -> add + norm2 ->
+        SwiGLU -> add + the next block's norm1 (norm_out after the last). Same sums as the
+        block-by-block loop, bf16-rounded at the same points; returns norm_out's output."""
+        from .fused_gates import add_rmsnorm
+        blocks = list(self.blocks)
+        h = blocks[0].norm1(x)
+        x = x.contiguous()
+        for i, blk in enumerate(blocks):
+            y = blk.attn(h) if hasattr(blk, "attn") else blk.mixer(h, mask)
+            x, h = add_rmsnorm(x, y, blk.norm2, out=x)
+            y = blk.ffn(h)
+            nxt = blocks[i + 1].norm1 if i + 1 < len(blocks) else self.norm_out
+            x, h = add_rmsnorm(x, y, nxt, out=x)
+        return h
+
     def enable_fused_gates(self, enabled=True):
         """Run every mixer's gate pipeline and level scan on the gfx950 HIP kernels (and, without
-        autograd, every SwiGLU activation on dh_silu_mul and, in bf16, every attention layer on the
-        banded-attention kernel).
+        autograd, every SwiGLU activation on dh_silu_mul, every residual add and the RMSNorm after
+        it on dh_add_rmsnorm and, in bf16, every attention layer on the banded-attention kernel).
 
         Loads the kernel library now (raising ImportError if it is missing) rather than in the
         middle of a forward. The fused path needs GPU tensors; returns self.
@@ -478,6 +505,8 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
             if hasattr(blk, "ffn"):
                 # inference only: the SwiGLU activation in one launch
                 blk.ffn.use_fused = bool(enabled)
+        # inference only: each residual add fused with the RMSNorm after it
+        self._fused_norms = bool(enabled)
         return self
 
     @torch.no_grad()

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 14
+#define DH_ABI_VERSION 15
 
 enum dh_status {
   DH_OK = 0,
@@ -141,6 +141,18 @@ int dh_level_scan_fwd(int dtype, const void* pre_i, const void* pre_f, const voi
  * 16-byte aligned (out may alias gate or up). n == 0 is a no-op.
  */
 int dh_silu_mul(int dtype, const void* gate, const void* up, void* out, int64_t n, void* stream);
+
+/*
+ * Residual add + RMSNorm over `rows` rows of d elements (row-contiguous, 16-byte aligned):
+ *   x_out = x + y;  h_out = x_out * rsqrt(mean(x_out^2) + eps) * weight
+ * Replaces the add and the next nn.RMSNorm of the residual stream of reference
+ * dispatcher_hybrid/modeling_dispatcher.py:210-212, :225-227 (x = x + sublayer(...); norm(x)) and
+ * :341-348 (the last block's add, then norm_out). bf16: the sum is rounded to bf16 (as the eager
+ * add), the norm computed in fp32 and rounded once. x_out may alias x or y. d a multiple of 8 (bf16)
+ * / 4 (fp32), at most 8192 / 4096. rows == 0 is a no-op.
+ */
+int dh_add_rmsnorm(int dtype, const void* x, const void* y, const void* weight, float eps, void* x_out,
+                   void* h_out, int64_t rows, int d, void* stream);
 
 /*
  * One decode step of one tree layer: all L levels' gate readouts plus the L-level recurrence over

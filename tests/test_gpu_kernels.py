@@ -582,3 +582,57 @@ def test_silu_mul_in_place_and_unaligned_views():
     assert got.data_ptr() == gi.data_ptr() and torch.equal(got, want)
     with pytest.raises(ValueError):
         silu_mul(g, u.float())
+
+
+# ---- dh_add_rmsnorm: residual add + the RMSNorm after it (reference modeling_dispatcher.py:210-212) ----
+
+@pytest.mark.parametrize("rows,d", [(0, 1024), (1, 1024), (7, 1024), (1030, 1024), (5, 776), (3, 8), (9, 4096),
+                                    (2, 8192)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_add_rmsnorm_matches_eager_add_and_norm(rows, d, dtype):
+    from dispatcher_hybrid.fused_gates import add_rmsnorm
+    if dtype == torch.float32 and d > 4096:
+        pytest.skip("fp32 rows are limited to 4096 elements")
+    gen = torch.Generator().manual_seed(rows * 7 + d)
+    x = (torch.randn(rows, d, generator=gen) * 3).to("cuda", dtype)
+    y = torch.randn(rows, d, generator=gen).to("cuda", dtype)
+    norm = torch.nn.RMSNorm(d).to("cuda", dtype)
+    with torch.no_grad():
+        norm.weight.copy_(torch.rand(d, generator=gen) + 0.5)
+        s_ref = x + y                                   # the eager residual add
+        h_ref = norm(s_ref)                             # the eager RMSNorm (eps None: fp32 epsilon)
+        xo, h = add_rmsnorm(x, y, norm)
+    assert torch.equal(xo, s_ref)                       # the sum: same rounding, bit-exact
+    # the norm in fp64 from the (exact) bf16/fp32 sum: a reduction-order-free statement of the formula
+    s64 = s_ref.double()
+    truth = s64 * torch.rsqrt((s64 * s64).mean(-1, keepdim=True) + torch.finfo(torch.float32).eps) * norm.weight.double()
+    if rows == 0:
+        assert h.shape == (0, d)
+        return
+    if dtype == torch.bfloat16:
+        tol = truth.abs() * 2.0 ** -8 + 1e-30         # half a bf16 ulp of rounding + fp32 noise
+        assert bool(((h.double() - truth).abs() <= tol * 1.01).all())
+        # and against torch's kernel: at most one bf16 ulp apart, rarely
+        d_ = (h.float() - h_ref.float()).abs()
+        assert bool((d_ <= h_ref.float().abs() * 2.0 ** -7 + 1e-30).all())
+        assert int((d_ > 0).sum()) <= max(2, h.numel() // 500)
+    else:
+        assert rel_err(h, truth) <= 2e-6
+        assert rel_err(h, h_ref) <= 2e-6
+
+
+def test_add_rmsnorm_in_place_and_errors():
+    from dispatcher_hybrid.fused_gates import add_rmsnorm
+    x = torch.randn(64, 1024, device="cuda", dtype=torch.bfloat16)
+    y = torch.randn(64, 1024, device="cuda", dtype=torch.bfloat16)
+    norm = torch.nn.RMSNorm(1024, eps=1e-5).to("cuda", torch.bfloat16)
+    with torch.no_grad():
+        want_x, want_h = add_rmsnorm(x, y, norm)
+        xi = x.clone()
+        got_x, got_h = add_rmsnorm(xi, y, norm, out=xi)   # the fused block loop writes the sum over x
+        assert got_x.data_ptr() == xi.data_ptr()
+        assert torch.equal(got_x, want_x) and torch.equal(got_h, want_h)
+        with pytest.raises(ValueError):
+            add_rmsnorm(x, y.float(), norm)
+        with pytest.raises(ValueError):
+            add_rmsnorm(x, y, torch.nn.RMSNorm(1024).to("cuda"))   # fp32 weight with bf16 rows
