@@ -362,6 +362,21 @@ bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
 
 constexpr int64_t kWideMinTiles = 256;    // 256 x 256 tiles: one per CU at least
 constexpr int64_t kWideGrid = 256;        // persistent workgroups: one per CU (128 KB of LDS each)
+constexpr int64_t kSmallMinTiles = 768;   // below the 256 x 256 launch: three tiles per CU at least
+
+// One workgroup per tile of the ping-pong kernel with 4 waves (BM = 32 TM, BN = 32 TN).
+template <int TM, int TN>
+int launch_pp_tiles(GemmArgs& a, hipStream_t s, const char* who) {
+  constexpr int BM = 32 * TM, BN = 32 * TN;
+  a.mtiles = (a.M + BM - 1) / BM;
+  a.ntiles = (a.Ntot + BN - 1) / BN;
+  const int64_t nvirt = (int64_t)((a.mtiles + 7) / 8) * 8 * a.ntiles;
+  DH_REQUIRE(nvirt < (1ll << 31), DH_ERR_UNSUPPORTED_SHAPE, "%s: M=%d too large", who, a.M);
+  proj_gemm_pp_kernel<TM, TN, 2, 2><<<dim3((unsigned)nvirt), dim3(256), 0, s>>>(a);
+  return dh_check_launch(who);
+}
+
+int64_t tiles_of(int M, int N, int BM, int BN) { return (int64_t)((M + BM - 1) / BM) * ((N + BN - 1) / BN); }
 
 }  // namespace
 
@@ -398,8 +413,9 @@ extern "C" int dh_proj_gemm(int dtype, const void* X, int64_t ldx, int M, int K,
   a.Ntot = total;
   hipStream_t s = (hipStream_t)stream;
   // bf16 launches with at least one 256 x 256 output tile per CU take the persistent 8-wave kernel
-  // (32-bit operand offsets, segment widths multiples of 8, 16-byte aligned output rows); the rest
-  // the 128 x 128 register-staged kernel, which keeps all 256 CUs busy on fewer rows.
+  // (32-bit operand offsets, segment widths multiples of 8, 16-byte aligned output rows), smaller
+  // bf16 launches that meet the same conditions its 4-wave form; the rest (fp32 among them) the
+  // 128 x 128 register-staged kernel.
   bool wide = dtype == DH_BF16 && (int64_t)M * ldx * esz < (1ll << 31);
   for (int i = 0; i < nseg; ++i)
     wide = wide && N[i] % 8 == 0 && (int64_t)N[i] * K * esz < (1ll << 31) && ldo[i] % 8 == 0 && aligned(out[i], 16);
@@ -412,6 +428,16 @@ extern "C" int dh_proj_gemm(int dtype, const void* X, int64_t ldx, int M, int K,
     const unsigned grid = (unsigned)(nvirt < kWideGrid ? nvirt : kWideGrid);
     proj_gemm_pp_kernel<8, 4, 2, 4><<<dim3(grid), dim3(512), 0, s>>>(a);
     return dh_check_launch(who);
+  }
+  // Fewer rows: the same ping-pong kernel, 4 waves, with the largest of 128 x 128, 64 x 128 and
+  // 64 x 64 tiles that still gives three tiles per CU (measured on MI355X at N = 3072, K = 1024:
+  // M = 1024 12.5 us with 64 x 64 against 18.8 for the 128 x 128 register-staged kernel; M = 2048
+  // 19.0 us with 64 x 128 against 27.0; M = 4096 35.6 with 128 x 128 against 40.3). Same sums in the
+  // same k order: the outputs are bit-identical.
+  if (wide) {
+    if (tiles_of(M, total, 128, 128) >= kSmallMinTiles) return launch_pp_tiles<4, 4>(a, s, who);
+    if (tiles_of(M, total, 64, 128) >= kSmallMinTiles) return launch_pp_tiles<2, 4>(a, s, who);
+    return launch_pp_tiles<2, 2>(a, s, who);
   }
   a.mtiles = (M + kBM - 1) / kBM;
   a.ntiles = (total + kBN - 1) / kBN;

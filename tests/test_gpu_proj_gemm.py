@@ -16,7 +16,10 @@ CASES = [
     (1, 64, [64]),
     (130, 128, [128, 128, 128]),          # ragged M, three segments
     (1000, 256, [64, 192, 128]),          # segments that straddle the 128-column tiles
-    (4096, 1024, [1024, 1024, 1024]),     # the released mixer (d = gh = 1024)
+    (4096, 1024, [1024, 1024, 1024]),     # the released mixer (d = gh = 1024): 128 x 128 tiles
+    (2048, 1024, [1024, 1024, 1024]),     # 64 x 128 tiles
+    (2000, 512, [1000, 1024, 1048]),      # 64 x 128 tiles, ragged rows, segments straddling tiles
+    (1024, 1024, [1024, 1024, 1024]),     # the C2 layer (T = 1024): 64 x 64 tiles
     (257, 1024, [1024]),
     # bf16 launches with >= 256 output tiles of 256 x 256 take the persistent 8-wave kernel:
     (6000, 1024, [1000, 1024, 1048]),     # ragged rows, segments straddling its 256-column tiles
@@ -59,3 +62,18 @@ def test_proj_gemm_batched_view_and_rejects():
         fused_projections(torch.zeros(4, 100, device=DEV), [torch.zeros(8, 100, device=DEV)])   # K % 32
     with pytest.raises(ValueError):
         fused_projections(x, [torch.zeros(6, 128, device=DEV)])                                  # N % 4
+
+
+def test_proj_gemm_rows_independent_of_tile_kernel():
+    """A row's outputs do not depend on the launch's row count: the 256 x 256 persistent kernel and
+    the 128 x 128, 64 x 128 and 64 x 64 tile forms picked for fewer rows form the same sums in the
+    same k order, so the first rows of a 9000-row launch equal those of shorter launches bit for bit."""
+    from dispatcher_hybrid.fused_gates import fused_projections
+    g = torch.Generator(device=DEV).manual_seed(11)
+    x = torch.randn(9000, 1024, device=DEV, generator=g).to(torch.bfloat16)
+    Ws = [(torch.randn(1024, 1024, device=DEV, generator=g) / 32).to(torch.bfloat16) for _ in range(3)]
+    full = fused_projections(x, Ws)
+    for M in (4096, 2048, 1024, 100, 1):
+        part = fused_projections(x[:M].contiguous(), Ws)
+        for o, f in zip(part, full):
+            assert torch.equal(o, f[:M]), M
