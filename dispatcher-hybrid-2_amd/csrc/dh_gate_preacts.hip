@@ -472,16 +472,68 @@ __global__ __launch_bounds__(kThreads, (LdsOcc<LG, MB>::value)) void gate_preact
     __syncthreads();
   };
 
-  w_fetch(0);
-  fetch(0, xA, xB);
-  w_store(0);
-  __syncthreads();
-  int c = 0;
-  for (; c + 1 < nchunk_; c += 2) {
-    chunk(c, xA, xB, yA, yB);
-    chunk(c + 1, yA, yB, xA, xB);
+  if constexpr (LG == 1) {
+    // One-level tiles (short prefills: one workgroup per CU, nothing else to hide a round trip):
+    // weights and fragments are requested two chunks ahead, in three register sets each, so
+    // neither the compute of chunk c nor the LDS write of c+1's weights waits on a load issued in
+    // chunk c.
+    uint4 zA[2][MB], zB[2][MB][LG];
+    uint4 w0[PPT], w1[PPT], w2[PPT];
+    auto w_fetch3 = [&](int k0, uint4 (&ws)[PPT]) {
+      const uint32_t kb = (uint32_t)(k0 * (int)sizeof(T));
+#pragma unroll
+      for (int i = 0; i < PPT; ++i) {
+        const int jx = min(2 * i + (wave_u >> 1), 3 * LG - 1);
+        const int x = jx % 3;
+        const __amdgpu_buffer_rsrc_t rw = x == 0 ? rW[0] : (x == 1 ? rW[1] : rW[2]);
+        ws[i] = bld16(rw, wsrc[i], kb);
+      }
+    };
+    auto w_store3 = [&](int buf, const uint4 (&ws)[PPT]) {
+#pragma unroll
+      for (int i = 0; i < PPT; ++i)
+        if (tid + i * kThreads < PIECES) *reinterpret_cast<uint4*>(&wl[buf][wdst[i]]) = ws[i];
+    };
+    // chunk c computes from set c % 3, requests chunk c+2 into set (c+2) % 3 (whose chunk c-1 is
+    // done) and writes the weights of c+1 (set (c+1) % 3, requested in chunk c-1) to LDS
+    auto chunk3 = [&](int c, const uint4 (&cA)[2][MB], const uint4 (&cB)[2][MB][LG], uint4 (&fA)[2][MB],
+                      uint4 (&fB)[2][MB][LG], const uint4 (&w_next)[PPT], uint4 (&w_far)[PPT]) {
+      if (c + 2 < nchunk_) {                             // uniform
+        w_fetch3((c + 2) * kLdsKC, w_far);
+        fetch((c + 2) * kLdsKC, fA, fB);
+      }
+      compute(cA, cB, c & 1);
+      if (c + 1 < nchunk_) w_store3((c + 1) & 1, w_next);
+      __syncthreads();
+    };
+    w_fetch3(0, w0);
+    fetch(0, xA, xB);
+    if (nchunk_ > 1) {
+      w_fetch3(kLdsKC, w1);
+      fetch(kLdsKC, yA, yB);
+    }
+    w_store3(0, w0);
+    __syncthreads();
+    int c = 0;
+    for (; c + 2 < nchunk_; c += 3) {
+      chunk3(c, xA, xB, zA, zB, w1, w2);
+      chunk3(c + 1, yA, yB, xA, xB, w2, w0);
+      chunk3(c + 2, zA, zB, yA, yB, w0, w1);
+    }
+    if (c < nchunk_) chunk3(c, xA, xB, zA, zB, w1, w2);
+    if (c + 1 < nchunk_) chunk3(c + 1, yA, yB, xA, xB, w2, w0);
+  } else {
+    w_fetch(0);
+    fetch(0, xA, xB);
+    w_store(0);
+    __syncthreads();
+    int c = 0;
+    for (; c + 1 < nchunk_; c += 2) {
+      chunk(c, xA, xB, yA, yB);
+      chunk(c + 1, yA, yB, xA, xB);
+    }
+    if (c < nchunk_) chunk(c, xA, xB, yA, yB);
   }
-  if (c < nchunk_) chunk(c, xA, xB, yA, yB);
 
   // ---- epilogue: C fragment column (head) r, rows 4g + i of row block mb
 #pragma unroll
