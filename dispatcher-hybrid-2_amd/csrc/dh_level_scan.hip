@@ -396,15 +396,23 @@ __global__ __launch_bounds__(1024) void level_scan_wide_kernel(ScanArgs a) {
   }
 }
 
-template <typename T, int PPT>
-void launch_wide(const ScanArgs& a, int mode, hipStream_t s) {
-  constexpr int C = 8;                    // measured: 4 columns (two workgroups per CU) is slower
+template <typename T, int PPT, int C>
+void launch_wide_c(const ScanArgs& a, int mode, hipStream_t s) {
   const int nchunks = a.hd / C;
   const int grid = ((a.b * a.H + 7) / 8) * 8 * nchunks;
   auto go = [&](auto kern) { kern<<<dim3(grid), dim3(1024), 0, s>>>(a); };
   if (mode == kActivated) go(level_scan_wide_kernel<T, C, PPT, kActivated>);
   else if (mode == kPreMask) go(level_scan_wide_kernel<T, C, PPT, kPreMask>);
   else go(level_scan_wide_kernel<T, C, PPT, kPreNoMask>);
+}
+
+// 8 columns per workgroup; 4 when 8 would leave CUs without a workgroup (a short single-row
+// prefill: b = 1, 16 heads x 64 gives 128). With enough workgroups, 4 columns (two workgroups per
+// CU) measured slower.
+template <typename T, int PPT>
+void launch_wide(const ScanArgs& a, int mode, hipStream_t s) {
+  if ((int64_t)a.b * a.H * (a.hd / 8) < 256) launch_wide_c<T, PPT, 4>(a, mode, s);
+  else launch_wide_c<T, PPT, 8>(a, mode, s);
 }
 
 template <typename T, int C, int PPT>
