@@ -353,6 +353,15 @@ def fused_projections(x, weights):
     return outs
 
 
+def projections_fit(x, linears):
+    """True when dh_proj_gemm takes x . W^T for these bias-free nn.Linear layers: CUDA input, weights
+    of x's dtype, K a multiple of 64 (bf16) / 32 (fp32), output widths multiples of 4."""
+    return (x.is_cuda and len(linears) <= 3 and all(l.bias is None for l in linears)
+            and all(l.weight.dtype == x.dtype and l.weight.is_contiguous() for l in linears)
+            and x.shape[-1] % (64 if x.dtype == torch.bfloat16 else 32) == 0
+            and all(l.weight.shape[0] % 4 == 0 for l in linears))
+
+
 def input_projections(x, mixer):
     """V0 = linear_in(x), A = gate_hidden(x), B = gate_hidden_src(x) (reference
     modeling_dispatcher.py:63-74): one dh_proj_gemm launch for a bias-free mixer whose widths the
@@ -360,10 +369,7 @@ def input_projections(x, mixer):
     count, the 4096 x 8 rows of a C5 layer included; the three nn.Linear calls only for other
     layers. Inference only."""
     lins = (mixer.linear_in, mixer.gate_hidden, mixer.gate_hidden_src)
-    if (x.is_cuda and all(l.bias is None for l in lins)
-            and all(l.weight.dtype == x.dtype for l in lins)
-            and x.shape[-1] % (64 if x.dtype == torch.bfloat16 else 32) == 0
-            and all(l.weight.shape[0] % 4 == 0 for l in lins)):
+    if projections_fit(x, lins):
         return fused_projections(x, [l.weight for l in lins])
     return tuple(l(x) for l in lins)
 

@@ -285,7 +285,9 @@ class WindowAttention(nn.Module):
 class SwiGLU(nn.Module):
     """linear_down(silu(linear_gate(h)) * linear_up(h)) (reference modeling_dispatcher.py:188-197).
     With use_fused (set by enable_fused_gates) and no autograd, the activation is one dh_silu_mul
-    launch at the same rounding points instead of a SiLU and a product launch."""
+    launch at the eager rounding points instead of a SiLU and a product launch. (linear_gate and
+    linear_up as one dh_proj_gemm launch measured slower in the graphed C2 forward than the two
+    library GEMMs: 2.245 vs 2.217 ms.)"""
 
     use_fused = False
 
