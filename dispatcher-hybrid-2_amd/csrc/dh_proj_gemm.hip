@@ -362,7 +362,8 @@ bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
 
 constexpr int64_t kWideMinTiles = 256;    // 256 x 256 tiles: one per CU at least
 constexpr int64_t kWideGrid = 256;        // persistent workgroups: one per CU (128 KB of LDS each)
-constexpr int64_t kSmallMinTiles = 768;   // below the 256 x 256 launch: three tiles per CU at least
+constexpr int64_t kSmallMinTiles = 768;   // below the 256 x 256 launch: three tiles per CU at least,
+constexpr int64_t kMidMinTiles = 512;     // two for the 128 x 128 tiles
 
 // One workgroup per tile of the ping-pong kernel with 4 waves (BM = 32 TM, BN = 32 TN).
 template <int TM, int TN>
@@ -429,13 +430,13 @@ extern "C" int dh_proj_gemm(int dtype, const void* X, int64_t ldx, int M, int K,
     proj_gemm_pp_kernel<8, 4, 2, 4><<<dim3(grid), dim3(512), 0, s>>>(a);
     return dh_check_launch(who);
   }
-  // Fewer rows: the same ping-pong kernel, 4 waves, with the largest of 128 x 128, 64 x 128 and
-  // 64 x 64 tiles that still gives three tiles per CU (measured on MI355X at N = 3072, K = 1024:
+  // Fewer rows: the same ping-pong kernel, 4 waves, with 128 x 128 tiles from two tiles per CU,
+  // else 64 x 128 from three, else 64 x 64 (measured on MI355X at N = 3072, K = 1024:
   // M = 1024 12.5 us with 64 x 64 against 18.8 for the 128 x 128 register-staged kernel; M = 2048
   // 19.0 us with 64 x 128 against 27.0; M = 4096 35.6 with 128 x 128 against 40.3). Same sums in the
   // same k order: the outputs are bit-identical.
   if (wide) {
-    if (tiles_of(M, total, 128, 128) >= kSmallMinTiles) return launch_pp_tiles<4, 4>(a, s, who);
+    if (tiles_of(M, total, 128, 128) >= kMidMinTiles) return launch_pp_tiles<4, 4>(a, s, who);
     if (tiles_of(M, total, 64, 128) >= kSmallMinTiles) return launch_pp_tiles<2, 4>(a, s, who);
     return launch_pp_tiles<2, 2>(a, s, who);
   }

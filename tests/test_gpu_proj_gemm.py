@@ -17,6 +17,7 @@ CASES = [
     (130, 128, [128, 128, 128]),          # ragged M, three segments
     (1000, 256, [64, 192, 128]),          # segments that straddle the 128-column tiles
     (4096, 1024, [1024, 1024, 1024]),     # the released mixer (d = gh = 1024): 128 x 128 tiles
+    (3840, 1024, [1024, 1024, 1024]),     # the C3 decoder prefill: 128 x 128 tiles from two per CU
     (2048, 1024, [1024, 1024, 1024]),     # 64 x 128 tiles
     (2000, 512, [1000, 1024, 1048]),      # 64 x 128 tiles, ragged rows, segments straddling tiles
     (1024, 1024, [1024, 1024, 1024]),     # the C2 layer (T = 1024): 64 x 64 tiles
@@ -73,7 +74,7 @@ def test_proj_gemm_rows_independent_of_tile_kernel():
     x = torch.randn(9000, 1024, device=DEV, generator=g).to(torch.bfloat16)
     Ws = [(torch.randn(1024, 1024, device=DEV, generator=g) / 32).to(torch.bfloat16) for _ in range(3)]
     full = fused_projections(x, Ws)
-    for M in (4096, 2048, 1024, 100, 1):
+    for M in (4096, 3840, 2048, 1024, 100, 1):
         part = fused_projections(x[:M].contiguous(), Ws)
         for o, f in zip(part, full):
             assert torch.equal(o, f[:M]), M
