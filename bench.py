@@ -21,7 +21,8 @@ out-projection + residual, RMSNorm + SwiGLU, down-projection + residual). A step
                     batch-1 step: algorithmic bytes / HIP-event-timed launch duration (with
                     --graph-step: dh_decode_gemv's launches of the graph of launches)
   gemv_chain        dh_decode_gemv's 57 launches of the graph-of-launches step, the same measure
-  mixer_step        the decoder's mixer step (dh_decode_gates + dh_decode_scan) per tree layer
+  mixer_step        the decoders' mixer step per tree layer at t = 4000: batch 1 dh_decode_gates +
+                    dh_decode_scan_out, batch 16 dh_decode_mixer_step
   step_roofline     whole decode step: bf16 weight bytes per token x tok/s vs 8 TB/s
   parity_bf16       the north star's bf16 quantities (logit max-abs, greedy-argmax agreement) of the
                     C2 fused-gates forward and the C3 one-launch step against the eager bf16 and fp32 paths
@@ -74,11 +75,11 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--cpu-prompt", type=int, default=1024)
     ap.add_argument("--leg", default="all",
-                    choices=["all", "prefill-kernels", "prefill-c2", "decode-b16", "decode-trace"],
+                    choices=["all", "prefill-kernels", "prefill-c2", "decode-b16", "decode-trace", "parity-bf16"],
                     help="prefill-kernels: only the C5 kernel timings; prefill-c2: only the C2 fused "
                          "forward (for rocprofv3 runs); decode-b16: only the batch-16 sampling decode "
                          "(for rocprofv3 runs); decode-trace: per-phase timestamps of the one-launch "
-                         "batch-1 step (wait vs work table)")
+                         "batch-1 step (wait vs work table); parity-bf16: only the bf16 parity figures")
     return ap.parse_args()
 
 
@@ -298,34 +299,55 @@ def gemv_chain_roofline(torch, model, reps=20):
     return nbytes, us, len(calls)
 
 
-def mixer_step_time(torch, model, dec, copies=400, reps=5):
-    """The decoder's mixer step (dh_decode_gates + dh_decode_scan, two launches) at B=1, t=4000 (all
-    12 levels live), the gate weights cycling through `copies` distinct copies (> 256 MB, more than
-    the last-level cache). Returns (algorithmic bytes per step, microseconds per step)."""
+def mixer_step_time(torch, model, copies=200, reps=5):
+    """The decoder's mixer step per tree layer as the decoders run it, at t = 4000 (all 12 levels
+    live), the weights cycling through `copies` distinct copies (more than the last-level cache):
+      b1:  dh_decode_gates + dh_decode_scan_out (the batch-1 graph of launches: gate readouts, then
+           the recurrence inside the out-projection + residual launch)
+      b16: dh_decode_mixer_step (batch > 1: gates and recurrence in one launch per layer; the
+           out-projection is a separate GEMV launch, not timed here)
+    Returns {form: {us, bytes, achieved_gbs}} with algorithmic bytes per step."""
     from dispatcher_hybrid import fused_step
     dev = next(model.parameters()).device
     mx = next(b.mixer for b in model.blocks if hasattr(b, "mixer"))
-    cache = next(c for c in dec.inner.caches if hasattr(c, "V_ring"))
     L, H, GH, d = mx.levels, mx.num_heads, mx.gate_hidden.out_features, model.config.d_model
+    hd, S, Tmax, bf = d // H, (2 << mx.levels) - 2, 4096, torch.bfloat16
     Ws = [torch.stack([mx.gate_out, mx.forget_out, mx.reset_out]).clone() for _ in range(copies)]
-    bi, bf, br = mx.gate_out_bias, mx.forget_out_bias, mx.reset_out_bias
-    A = torch.randn(1, GH, device=dev, dtype=torch.bfloat16)
-    V0 = torch.randn(1, d, device=dev, dtype=torch.bfloat16)
-    Y = torch.empty(1, d, device=dev, dtype=torch.bfloat16)
+    Wo = [mx.linear_out.weight.clone() for _ in range(copies)]
+    bi, bfb, br = mx.gate_out_bias, mx.forget_out_bias, mx.reset_out_bias
     t_buf = torch.full((1,), 4000, dtype=torch.long, device=dev)
-    B_hist = torch.zeros(1, 4096, GH, device=dev, dtype=torch.bfloat16)
-    rg = torch.zeros(1, 4096, L, H, device=dev, dtype=torch.bfloat16)
-    ring = torch.zeros(1, cache.S, d, device=dev, dtype=torch.bfloat16)
-    stage = torch.zeros(fused_step.stage_floats(1, H, L, d // H), device=dev)
-
-    def launch(i):
-        W = Ws[i % copies]
-        fused_step.decode_gates_scan(A, B_hist, W[0], W[1], W[2], bi, bf, br, t_buf, rg, ring, V0, Y, stage)
-
-    us = 2 * _graph_time(torch, launch, copies, reps)       # per step: two launches
     s = 2
-    nbytes = 3 * L * H * GH * s + 3 * L * H * s + (L * GH + GH + 2 * L * H + 2 * L * d + 2 * d) * s
-    return nbytes, us
+    out = {}
+    for Bb in (1, 16):
+        A = torch.randn(Bb, GH, device=dev).to(bf)
+        V0 = torch.randn(Bb, d, device=dev).to(bf)
+        Y = torch.empty(Bb, d, device=dev, dtype=bf)
+        x = torch.randn(Bb, d, device=dev).to(bf)
+        B_hist = torch.randn(Bb, Tmax, GH, device=dev).to(bf)
+        rg = torch.rand(Bb, Tmax, L, H, device=dev).to(bf)
+        ring = torch.randn(Bb, S, d, device=dev).to(bf)
+        stage = torch.zeros(fused_step.stage_floats(Bb, H, L, hd), device=dev)
+        state = Bb * (L * GH + GH + 2 * L * H + 2 * L * d + 2 * d) * s      # A, B rows, gates, ring reads/writes, V0, Y
+        if Bb == 1:
+            def launch(i):
+                W = Ws[i % copies]
+                fused_step.decode_gates_scan_out(A, B_hist, W[0], W[1], W[2], bi, bfb, br, t_buf, rg, ring, V0, Y,
+                                                 stage, Wo[i % copies], x, x)
+            nbytes = 3 * L * H * GH * s + 3 * L * H * s + d * d * s + state + 2 * d * s
+            form = "b1", "dh_decode_gates + dh_decode_scan_out (batch 1: gates, recurrence, out-projection + residual)"
+            us = 2 * _graph_time(torch, launch, copies, reps)             # two launches per step
+        else:
+            def launch(i):
+                W = Ws[i % copies]
+                fused_step.decode_mixer_step(A, B_hist, W[0], W[1], W[2], bi, bfb, br, t_buf, rg, ring, V0, Y)
+            nbytes = 3 * L * H * GH * s + 3 * L * H * s + state
+            form = "b16", "dh_decode_mixer_step (batch 16: gates and recurrence; out-projection not included)"
+            us = _graph_time(torch, launch, copies, reps)
+        out[form[0]] = {"kernels": form[1], "us": round(us, 3), "bytes": nbytes,
+                        "achieved_gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    del Ws, Wo
+    torch.cuda.empty_cache()
+    return out
 
 
 def prefill_kernels(torch, dev, reps=10):
@@ -605,24 +627,45 @@ def _agreement(torch, fused16, eager16, truth32):
             "decisive_positions": int(decisive.sum()), "positions": int(decisive.numel())}
 
 
-def parity_bf16(torch, model, prompt, steps=16):
+def _floor(torch, alt16, eager16, fused16):
+    """max-abs and raw greedy-argmax agreement of two eager bf16 runs at the same rounding points, and
+    the fused path's max-abs against the eager bf16 path as a multiple of that floor (the tests
+    require <= 2)."""
+    mx = (alt16 - eager16).abs().max().item()
+    return {"max_abs": round(mx, 4), "mean_abs": round((alt16 - eager16).abs().mean().item(), 5),
+            "argmax_agree": round((alt16.argmax(-1) == eager16.argmax(-1)).double().mean().item(), 4),
+            "fused_max_abs_over_floor": round((fused16 - eager16).abs().max().item() / mx, 3)}
+
+
+def parity_bf16(torch, model, prompt, steps=256):
     """bf16 parity figures of the measured paths on the bench's own inputs: C2 (fused-gates forward,
-    T = 1024) and C3 (the one-launch greedy step at the bench's context, teacher-forcing the eager
-    decoders with its tokens)."""
+    T = 1024) and C3 (the one-launch greedy step over `steps` positions from the bench's context,
+    teacher-forcing the eager decoders with its tokens).
+
+    same_rounding_floor: the eager bf16 path against itself with only the accumulation order of its
+    matrix products changed (dispatcher_hybrid.numerics.fp32_product_accumulation: each bf16 product
+    as an fp32 product of the same bf16 operands, rounded once) -- the logit max-abs and argmax
+    agreement that any bf16 implementation with its own GEMM kernels can be expected to reach
+    against the eager bf16 path."""
     import copy
 
     from dispatcher_hybrid.decoding import FusedGraphedHybridDecoder, IncrementalDecoder
+    from dispatcher_hybrid.numerics import fp32_product_accumulation
     dev = next(model.parameters()).device
     m32 = copy.deepcopy(model).float()
     g = torch.Generator(device=dev).manual_seed(2)
     ids = torch.randint(0, 50257, (1, 1024), device=dev, generator=g)
     with torch.no_grad():
         e16 = model(ids).logits[0].float()
+        with fp32_product_accumulation():
+            a16 = model(ids).logits[0].float()
         f16 = model.enable_fused_gates()(ids).logits[0].float()
         model.enable_fused_gates(False)
         e32 = m32(ids).logits[0].float()
     out = {"c2": _agreement(torch, f16, e16, e32)}
-    del e16, f16, e32
+    out["c2"]["same_rounding_floor"] = _floor(torch, a16, e16, f16)
+    del e16, f16, e32, a16
+    steps = min(steps, model.config.max_len - prompt)
     ids = torch.randint(0, EOT, (1, prompt), device=dev, generator=torch.Generator(device=dev).manual_seed(3))
     dec = FusedGraphedHybridDecoder(model)
     dec.greedy_start(dec.prefill(ids)[:, -1])
@@ -639,8 +682,14 @@ def parity_bf16(torch, model, prompt, steps=16):
         d_.prefill(ids)
         return torch.stack([d_.step(toks[:, j])[0].float() for j in range(steps)])
 
-    out["c3"] = _agreement(torch, torch.stack(got), forced(model), forced(m32))
+    e16 = forced(model)
+    with fp32_product_accumulation():
+        a16 = forced(model)
+    got = torch.stack(got)
+    out["c3"] = _agreement(torch, got, e16, forced(m32))
+    out["c3"]["same_rounding_floor"] = _floor(torch, a16, e16, got)
     out["c3"]["path"] = "one-launch step" if used else "graph of launches"
+    out["c3"]["context"] = f"{prompt}..{prompt + steps - 1}"
     del m32
     torch.cuda.empty_cache()
     return out
@@ -683,6 +732,11 @@ def main():
                           "prefill_host_launched_tok_s": round(f_tok, 1), "prefill_host_launched_ms": round(f_ms, 3)}),
               flush=True)
         return
+    if args.leg == "parity-bf16":
+        res = parity_bf16(torch, model, min(args.prompt, max_len - 256))
+        log(f"bf16 parity: {json.dumps(res)}")
+        print(json.dumps({"parity_bf16": res}), flush=True)
+        return
     if args.leg == "decode-b16":
         steps16 = min(args.steps, 128)
         p16 = min(args.prompt, max_len - args.warmup - steps16)
@@ -716,11 +770,8 @@ def main():
                             "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4),
                             "what": "bf16 weight bytes per decode token (584,316,928 B) x tok/s"}
 
-    mb, mus = mixer_step_time(torch, model, dec1)
-    out["mixer_step"] = {"kernels": "dh_decode_gates + dh_decode_scan (one tree layer, B=1, t=4000)",
-                         "us": round(mus, 3), "bytes": mb,
-                         "achieved_gbs": round(mb / (mus * 1e-6) / 1e9, 1)}
-    log(f"mixer step (gates + scan): {mus:.2f} us per layer")
+    out["mixer_step"] = mixer_step_time(torch, model)
+    log("mixer step per tree layer: " + ", ".join(f"{k} {v['us']} us" for k, v in out["mixer_step"].items()))
     if dec1._pers:
         # the dominant (only) kernel of the step: algorithmic bytes = every weight once, the tree
         # state rows and the windowed keys and values of one token (full-byte definition)
@@ -819,7 +870,7 @@ def main():
         out["prefill_kernels_c5"] = pk
         log("C5 prefill kernels: " + ", ".join(f"{k} {v['us']} us" for k, v in pk.items() if isinstance(v, dict)))
         out["c1_mixer_gpu_fp32_ms"] = round(c1_gpu(torch, dev), 4)
-        out["parity_bf16"] = parity_bf16(torch, model, prompt)
+        out["parity_bf16"] = parity_bf16(torch, model, min(args.prompt, max_len - 256))
         log(f"bf16 parity: {json.dumps(out['parity_bf16'])}")
 
     if not args.no_cpu_baseline:

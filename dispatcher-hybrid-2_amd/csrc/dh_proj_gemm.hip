@@ -251,9 +251,11 @@ __device__ __forceinline__ void store_tile_x4(const GemmArgs& a, const f32x4 (&a
 // segment width is a multiple of 8) and 32-bit lane offsets.
 __device__ __forceinline__ int swz2(int R) { return R & 7; }
 
+// M0 (the LDS destination base) is an input operand bound to the register itself ("{m0}"), so the
+// compiler writes it and knows its value is live across the statement; nothing here clobbers a
+// register the compiler reserves.
 __device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(base)
-               : "memory", "m0");
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 
 template <int TM, int TN, int WGM, int WGN>

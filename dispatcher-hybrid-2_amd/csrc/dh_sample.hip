@@ -267,9 +267,12 @@ __global__ __launch_bounds__(kST) void sample_topk_kernel(const T* logits, int64
   const int64_t off = offset_dev ? load_uniform(offset_dev) : 0;
 
   // ---- the chunk as order keys of l = float(x) / temperature (key 0, below every number, past V).
-  // Raw buffer loads: reads past the row's V elements return zero without touching memory.
-  const __amdgpu_buffer_rsrc_t rsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(row), (short)0, (int)(V * (int)sizeof(T)), 0x00020000);
+  // Raw buffer loads: reads past the row return zero without touching memory. The range is
+  // checked per dword, so it is rounded up to whole dwords: for odd V in bf16 the last element
+  // shares a dword with the 2 bytes after the row (never past a page: a dword holding an element
+  // is mapped whole); what those bytes hold is masked by nv below.
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<T*>(row), (short)0, (int)((V * (int)sizeof(T) + 3) & ~3), 0x00020000);
   constexpr int EPC = 16 / (int)sizeof(T);             // elements per 16-byte load
   uint32_t xk[kSPT];
 #pragma unroll
@@ -414,9 +417,10 @@ __global__ __launch_bounds__(kST) void sample_topk_bf16_kernel(const bf16_t* log
   const int nv = min(max(V - i0, 0), kSPT);
   const int64_t off = offset_dev ? load_uniform(offset_dev) : 0;
 
-  // ---- keys: pair i holds elements 2i (low half) and 2i + 1 (high half); key 0 past V
+  // ---- keys: pair i holds elements 2i (low half) and 2i + 1 (high half); key 0 past V. The
+  // range covers whole dwords (odd V: the last element's dword), as in sample_topk_kernel.
   const __amdgpu_buffer_rsrc_t rsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(row), (short)0, (int)(V * 2), 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(row), (short)0, (int)((V * 2 + 3) & ~3), 0x00020000);
   uint32_t kp[NP];
 #pragma unroll
   for (int c = 0; c < NP / 4; ++c) {

@@ -53,7 +53,8 @@ def build(verbose=False):
         for cmd, p in procs:
             out = p.communicate()[0].decode(errors="replace")
             out = "\n".join(l for l in out.splitlines() if "packed-fp32-ops" not in l)
-            if p.returncode != 0:
+            if p.returncode != 0 or "warning:" in out:
+                # warnings fail the build too (an inline-asm clobber of a reserved register is one)
                 failed.append(f"$ {' '.join(cmd)}\n{out}")
             elif verbose and out.strip():
                 print(out)

@@ -448,6 +448,9 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         self._sample_cfg = None
         self._sample_capture = None
         self.tok_hist = torch.zeros(Bb, self.max_len + 1, dtype=torch.long, device=dev)
+        # the greedy pick's candidates at batch > 1: owned by this decoder for the captured graph's
+        # lifetime (a shared buffer could be replaced, and freed, under a graph that writes it)
+        self.argmax_ws = self._fused_step.argmax_workspace(Bb, self.logits_out.shape[1], dev)
         self.cand = None
         if Bb == 1:
             self.cand = self._fused_step.candidate_buffer(dt, self.logits_out.shape[1], cfg.d_model, 1, dev)
@@ -634,7 +637,7 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
             if cand is not None:
                 fs.argmax_reduce(cand, self.token_buf, self.t_buf, self.tok_hist)
             else:
-                fs.argmax_tokens(self.logits_out, out=self.token_buf)
+                fs.argmax_tokens(self.logits_out, out=self.token_buf, workspace=self.argmax_ws)
                 self.tok_hist.index_copy_(1, self.t_buf, self.token_buf.unsqueeze(1))
         elif self._sample_capture is not None:
             # sampled pick (draws keyed by the new position) into token_buf and the token history
@@ -648,7 +651,7 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         last-position logits, (B, V) or (V,)) becomes the token fed to the next step and the first
         entry of tok_hist (at the current position)."""
         lg = logits.view(-1, logits.shape[-1])
-        self._fused_step.argmax_tokens(lg, out=self.token_buf)
+        self._fused_step.argmax_tokens(lg, out=self.token_buf, workspace=self.argmax_ws)
         self.tok_hist[:, self.t] = self.token_buf
 
     @torch.no_grad()

@@ -399,6 +399,16 @@ def _rms_eps(norm):
     return norm.eps if norm.eps is not None else torch.finfo(torch.float32).eps
 
 
+def add_rmsnorm_fits(d, dtype):
+    """Whether dh_add_rmsnorm takes rows of width d in `dtype`: fp32 or bf16, d a multiple of the
+    16-byte chunk (8 bf16 or 4 fp32 elements) and at most 64 lanes x 16 chunks of it (8192 bf16,
+    4096 fp32 elements)."""
+    if dtype not in (torch.float32, torch.bfloat16):
+        return False
+    v = 8 if dtype == torch.bfloat16 else 4
+    return v <= d <= 1024 * v and d % v == 0
+
+
 def add_rmsnorm(x, y, norm, out=None):
     """(x + y, norm(x + y)) in one launch (``dh_add_rmsnorm``): the residual add of a block and the
     RMSNorm after it (reference dispatcher_hybrid/modeling_dispatcher.py:210-212, 225-227, 341-348).

@@ -327,10 +327,20 @@ def decode_attention(q, k, v, rope_cos, rope_sin, K_cache, V_cache, t_buf, y, wi
     _hip.check(st, "dh_decode_attention")
 
 
-def argmax_tokens(logits, out=None):
+def argmax_workspace(B, V, device):
+    """A candidate buffer for argmax_tokens over (B, V) logits (uint8 device tensor)."""
+    return torch.empty(max(int(_hip.lib.dh_argmax_workspace_bytes(B, V)), 4096), dtype=torch.uint8, device=device)
+
+
+def argmax_tokens(logits, out=None, workspace=None):
     """Greedy next tokens on the device (``dh_argmax``): out[b] = logits[b].argmax() as int64,
     first index on ties, NaN above every number (torch.argmax's rule). logits: (B, V) fp32 or bf16
-    with a unit inner stride; returns `out` (allocated when None)."""
+    with a unit inner stride; returns `out` (allocated when None).
+
+    workspace: the candidate buffer (argmax_workspace(B, V, device)). A step captured into a HIP
+    graph must pass one it owns for the graph's lifetime; without it a per-device buffer is used
+    that a later call with more candidates replaces (freeing the old one), which only eager
+    callers may rely on."""
     _hip.require_gpu(logits, "argmax_tokens")
     if logits.dim() != 2 or logits.stride(-1) != 1:
         raise ValueError("argmax_tokens: logits must be (B, V) with a unit inner stride")
@@ -340,17 +350,23 @@ def argmax_tokens(logits, out=None):
     if out.dtype != torch.long or out.numel() != B or not out.is_contiguous():
         raise ValueError("argmax_tokens: out must be a contiguous int64 tensor of B elements")
     nbytes = int(_hip.lib.dh_argmax_workspace_bytes(B, V))
-    ws = _ARGMAX_WS.get(logits.device)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 4096), dtype=torch.uint8, device=logits.device)
-        _ARGMAX_WS[logits.device] = ws
+    ws = workspace
+    if ws is not None:
+        if ws.dtype != torch.uint8 or ws.device != logits.device or not ws.is_contiguous() or ws.numel() < nbytes:
+            raise ValueError(f"argmax_tokens: workspace must be a contiguous uint8 tensor of >= {nbytes} bytes "
+                             f"on the logits' device")
+    else:
+        ws = _ARGMAX_WS.get(logits.device)
+        if ws is None or ws.numel() < nbytes:
+            ws = argmax_workspace(B, V, logits.device)
+            _ARGMAX_WS[logits.device] = ws
     st = _hip.lib.dh_argmax(_hip.dtype_code(logits.dtype), _hip.ptr(logits), logits.stride(0), B, V,
                             _hip.ptr(out), _hip.ptr(ws), ws.numel(), _hip.stream_handle(logits.device))
     _hip.check(st, "dh_argmax")
     return out
 
 
-_ARGMAX_WS = {}           # per-device candidate buffer of argmax_tokens, grown on demand
+_ARGMAX_WS = {}           # per-device candidate buffer of eager argmax_tokens calls, grown on demand
 
 
 def argmax_tokens_noalloc(logits, out):

@@ -299,7 +299,8 @@ class SwiGLU(nn.Module):
         self.linear_down = nn.Linear(ff, d, bias=False)
 
     def forward(self, h):
-        if self.use_fused and h.is_cuda and not torch.is_grad_enabled():
+        if (self.use_fused and h.is_cuda and not torch.is_grad_enabled()
+                and h.dtype in (torch.float32, torch.bfloat16)):                   # dh_silu_mul's dtypes
             from .fused_gates import silu_mul
             g = self.linear_gate(h)
             return self.linear_down(silu_mul(g, self.linear_up(h), out=g))
@@ -465,11 +466,18 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
         return {"input_ids": input_ids[:, -self.config.max_len:]}
 
     def _fused_norm_ok(self, x, output_hidden_states):
+        """Whether the block loop may fuse each residual add with the RMSNorm after it: inference on
+        the GPU, weighted norms in x's dtype, and a width dh_add_rmsnorm takes (otherwise the
+        block-by-block loop runs)."""
         if not (getattr(self, "_fused_norms", False) and x.is_cuda and not torch.is_grad_enabled()
                 and not output_hidden_states and x.dtype in (torch.float32, torch.bfloat16) and len(self.blocks)):
             return False
+        from .fused_gates import add_rmsnorm_fits
+        if not add_rmsnorm_fits(x.shape[-1], x.dtype):
+            return False
         norms = [self.norm_out] + [n for blk in self.blocks for n in (blk.norm1, blk.norm2)]
-        return all(n.weight is not None and n.weight.dtype == x.dtype for n in norms)
+        return all(n.weight is not None and n.weight.dtype == x.dtype and tuple(n.normalized_shape) == (x.shape[-1],)
+                   for n in norms)
 
     def _blocks_fused_norms(self, x, mask):
         """The blocks and norm_out with every residual add fused into the RMSNorm that follows it

@@ -60,22 +60,52 @@ def decisive_argmax_agree(got, ref, margin=0.75):
     return bool((agree | ~decisive).all())
 
 
+def ulp_bf16(x):
+    """One bf16 unit in the last place at |x| (fp32 tensor): 2^(floor(log2 |x|) - 7), and the
+    smallest normal's ulp (2^-133) at zero."""
+    m, e = torch.frexp(x.float().abs().clamp_min(2.0 ** -126))      # |x| = m 2^e, m in [0.5, 1)
+    return torch.ldexp(torch.ones_like(m), e - 8)
+
+
+def preact_bound(got, ref, bias, abs_sum):
+    """How far the fused gate pre-activation `got` = rnd(P_f + b) may lie from the eager one `ref`
+    = rnd(rnd(P_e) + b) (reference modeling_dispatcher.py:103-109: the bf16 einsum rounds the
+    product P, then the bias add rounds again), both from the same bf16 hidden tile (a + b, relu and
+    the square rounded at the same points) and fp32 accumulations P_f, P_e of the same exact
+    products in different orders:
+        |got - ref| <= 0.5 ulp(P) + 0.5 ulp(ref) + 0.5 ulp(got) + |P_f - P_e|,
+    with |P_f - P_e| <= 2^-12 * sum_g |hid_g W_g| (abs_sum; 1024-term fp32 sums in any order).
+    All fp32 tensors of one shape; returns the bound."""
+    ref, got, bias = ref.float(), got.float(), bias.float()
+    # |P| <= |ref - b| + ulp(ref): the eager product lies within the final rounding of ref - b
+    p_mag = (ref - bias).abs() + ulp_bf16(ref)
+    return (0.5 * ulp_bf16(p_mag) + 0.5 * ulp_bf16(ref) + 0.5 * ulp_bf16(got)
+            + 2.0 ** -12 * abs_sum.float())
+
+
 def bf16_round(x):
     return torch.as_tensor(x).to(torch.bfloat16).to(torch.float64)
 
 
-def bf16_vs_truth(fused16, eager16, truth32, what):
+def bf16_vs_truth(fused16, eager16, truth32, what, alt16=None):
     """bf16 criterion at model level, and the north-star quantities printed beside it.
 
     The north star asks for logit max-abs <= 3e-2 and >= 99% greedy-argmax agreement between the
-    fused bf16 path and the eager bf16 path. On the random-init 292M model the eager path's own
-    bf16 noise (eager-bf16 against eager-fp32) is ~0.17 max-abs, larger than that bound, and its
-    top-2 logit margins are often below that noise, so any two bf16 implementations that round at
-    different points differ by more. The fused bf16 path is therefore held to: (a) its error
-    against the fp32 eager path is no larger than the eager bf16 path's own (max-abs within 1.25x,
-    mean-abs within 1.10x), and (b) >= 99% greedy-argmax agreement with the fp32 eager path where
-    its top-2 margin exceeds the bf16 noise (0.1). The raw fused-vs-eager-bf16 max-abs and argmax
-    agreement are printed and returned."""
+    fused bf16 path and the eager bf16 path. That bound lies below the eager path's own bf16 noise
+    floor at its own rounding points: the eager bf16 path against itself with only the accumulation
+    order of its matrix products changed (dispatcher_hybrid.numerics.fp32_product_accumulation)
+    differs by 0.102 logit max-abs with 94.4% argmax agreement on the random-init 292M model at
+    C2 (T = 1024), and by 0.111 with 91.0% over 256 decode positions at C3 (t = 3840..4095), measured
+    on MI355X. No bf16 implementation with GEMM kernels of its own can do better than that floor
+    against the eager path. The fused bf16 path is therefore held to:
+      (a) its error against the fp32 eager path is no larger than the eager bf16 path's own
+          (max-abs within 1.25x, mean-abs within 1.10x);
+      (b) >= 99% greedy-argmax agreement with the fp32 eager path where its top-2 margin exceeds
+          the bf16 noise (0.1);
+      (c) when `alt16` (the eager bf16 run under fp32_product_accumulation, i.e. the floor) is
+          given: max-abs against the eager bf16 path within 2x the floor's max-abs, and argmax
+          agreement with it no more than 0.05 below the floor's.
+    The raw fused-vs-eager-bf16 max-abs and argmax agreement are printed and returned."""
     ef, ee = (fused16 - truth32).abs(), (eager16 - truth32).abs()
     top2 = torch.topk(truth32, 2, dim=-1).values
     decisive = (top2[..., 0] - top2[..., 1]) > 0.1
@@ -92,4 +122,13 @@ def bf16_vs_truth(fused16, eager16, truth32, what):
     assert ef.max().item() <= 1.25 * ee.max().item()
     assert ef.mean().item() <= 1.10 * ee.mean().item()
     assert dec_agree >= 0.99
+    if alt16 is not None:
+        floor = (alt16 - eager16).abs().max().item()
+        floor_agree = (alt16.argmax(-1) == eager16.argmax(-1)).double().mean().item()
+        raw.update(floor_max_abs=floor, floor_argmax=floor_agree)
+        print(f"{what}: same-rounding floor (eager16 vs eager16 with fp32 product accumulation): max-abs "
+              f"{floor:.4f} argmax {floor_agree:.4f} | fused/floor max-abs {raw['max_abs_vs_eager16'] / floor:.2f}",
+              flush=True)
+        assert raw["max_abs_vs_eager16"] <= 2.0 * floor
+        assert raw["argmax_vs_eager16"] >= floor_agree - 0.05
     return raw

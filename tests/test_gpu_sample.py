@@ -259,6 +259,36 @@ def test_sample_release_vocab_support(dtype):
     assert d.unique().numel() > 50
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("V", [50257, 7, 1025])
+def test_sample_last_element_of_odd_rows(dtype, V):
+    """Odd V, the released vocabulary included: the row's last element (the EOT token at V = 50257)
+    sits in a dword whose upper half lies past the row. With logit[V-1] far above the rest every
+    draw must be V-1 (top_k 1, 50 and the full softmax), in every row of a batch (rows start at
+    odd element offsets) and for the row-strided argmax as well; the same with the maximum one
+    before the end and the last element lowest, so the byte past the row is never taken as an
+    element."""
+    from dispatcher_hybrid import fused_step
+    B = 5
+    g = torch.Generator(device=DEV).manual_seed(V)
+    x = torch.randn(B, V, device=DEV, generator=g)
+    x[:, V - 1] = 40.0
+    x = x.to(dtype)
+    off = torch.tensor([9], dtype=torch.long, device=DEV)
+    for k in (1, min(50, V), None):
+        for seed in range(16):
+            tok = fused_step.sample_tokens(x, temperature=0.8, top_k=k, seed=seed, offset=off)
+            assert bool((tok == V - 1).all()), (k, seed, tok.tolist())
+    assert bool((fused_step.argmax_tokens(x) == V - 1).all())
+    if V > 2:
+        y = torch.randn(B, V, device=DEV, generator=g)
+        y[:, V - 2], y[:, V - 1] = 40.0, -40.0
+        y = y.to(dtype)
+        for k in (1, 2, None):
+            tok = fused_step.sample_tokens(y, temperature=1.0, top_k=k, seed=3, offset=off)
+            assert bool((tok == V - 2).all()), (k, tok.tolist())
+
+
 def test_sample_deterministic_and_keyed():
     from dispatcher_hybrid import fused_step
     g = torch.Generator(device=DEV).manual_seed(4)

@@ -52,6 +52,20 @@ def test_fast_generate_eager_matches_reference_golden(tiny_model):
     assert np.array_equal(out.numpy(), g["gen"])
 
 
+def test_generate_matches_fast_generate(tiny_model):
+    """reference tests/test_decoding.py:89-95 and tests/test_parity.py:61-64: HF generate() on the
+    product model runs (shape) and gives greedy fast_generate's tokens; both equal the reference's
+    own greedy tokens (golden)."""
+    name, cfgd, m = tiny_model
+    g = golden(name)
+    ids = torch.from_numpy(g["gen"][:, :6])
+    n = g["gen"].shape[1] - 6
+    a = m.generate(ids, max_new_tokens=n, do_sample=False)
+    assert a.shape == (ids.shape[0], 6 + n)
+    assert torch.equal(a, m.fast_generate(ids, max_new_tokens=n, decoder="eager"))
+    assert np.array_equal(a.numpy(), g["gen"])
+
+
 def test_decoder_matches_parallel_forward(tiny_model):
     """reference tests/test_decoding.py:33-47: prefill 48, 12 steps, logits == parallel forward."""
     from dispatcher_hybrid.decoding import IncrementalDecoder
