@@ -407,7 +407,9 @@ def prefill_kernels(torch, dev, reps=10):
         "input_projections": {"us": round(proj_us, 1), "bound": "mfma", "achieved": round(tf(proj_fl, proj_us), 1),
                               "peak": MFMA_BF16_TFLOPS, "unit": "TFLOP/s",
                               "frac": round(tf(proj_fl, proj_us) / MFMA_BF16_TFLOPS, 4), "flops": proj_fl,
-                              "three_library_gemms_us": round(lib_us, 1)},
+                              "three_library_gemms_us": round(lib_us, 1),
+                              "product_runs": "the three library GEMMs (above PROJ_GEMM_MAX_ROWS = 8192 rows; "
+                                              "dh_proj_gemm at or below)"},
         "gate_preacts": {"us": round(gate_us, 1), "bound": "mfma", "achieved": round(tf(gate_fl, gate_us), 1),
                          "peak": MFMA_BF16_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf(gate_fl, gate_us) / MFMA_BF16_TFLOPS, 4),

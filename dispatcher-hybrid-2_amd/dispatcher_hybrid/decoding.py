@@ -405,6 +405,9 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
     """
 
     _prefill_cls = _FusedPrefillDecoder
+    # (row, head) pairs up to which each head's attention window is split over several workgroups
+    # (dh_decode_attention_split + a combine launch) instead of one workgroup per pair
+    attn_split_pairs = 64
 
     def __init__(self, model, max_len=None, dtype=None, persistent=True):
         from . import fused_step                          # loads libdh_mixer.so
@@ -456,7 +459,7 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
             self.cand = self._fused_step.candidate_buffer(dt, self.logits_out.shape[1], cfg.d_model, 1, dev)
         att0 = next((b.attn for b in self.m.blocks if isinstance(b, AttentionBlock)), None)
         self.attn_ws = None
-        if att0 is not None and Bb * att0.num_heads <= 64:
+        if att0 is not None and Bb * att0.num_heads <= self.attn_split_pairs:
             self.attn_ws = self._fused_step.attention_workspace(Bb, att0.num_heads, att0.head_dim, dev)
 
     def _persistent_setup(self):

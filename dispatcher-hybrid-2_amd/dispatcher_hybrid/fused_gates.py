@@ -362,14 +362,24 @@ def projections_fit(x, linears):
             and all(l.weight.shape[0] % 4 == 0 for l in linears))
 
 
+# Rows above which the three library GEMMs (hipBLASLt through nn.Linear) beat dh_proj_gemm for the
+# mixer's input projections (measured on MI355X at K = 1024, N = 3 x 1024, bf16, HIP events over 20
+# launches: dh_proj_gemm 36 / 61 / 92 / 96 / 190 us against 58 / 63 / 79 / 90 / 173 us for the
+# library at M = 4096 / 8192 / 12288 / 16384 / 32768; below 4096 rows dh_proj_gemm takes half the
+# library's time or less).
+PROJ_GEMM_MAX_ROWS = 8192
+
+
 def input_projections(x, mixer):
     """V0 = linear_in(x), A = gate_hidden(x), B = gate_hidden_src(x) (reference
     modeling_dispatcher.py:63-74): one dh_proj_gemm launch for a bias-free mixer whose widths the
-    kernel takes (K a multiple of 64 for bf16 / 32 for fp32, widths multiples of 4) -- every row
-    count, the 4096 x 8 rows of a C5 layer included; the three nn.Linear calls only for other
-    layers. Inference only."""
+    kernel takes (K a multiple of 64 for bf16 / 32 for fp32, widths multiples of 4) up to
+    PROJ_GEMM_MAX_ROWS rows (the C2 forward and the decoders' prompt prefills); the three nn.Linear
+    calls for more rows (the C5 forward's 32768), where the library is faster, and for other layers.
+    Inference only."""
     lins = (mixer.linear_in, mixer.gate_hidden, mixer.gate_hidden_src)
-    if projections_fit(x, lins):
+    rows = x.numel() // max(x.shape[-1], 1)
+    if rows <= PROJ_GEMM_MAX_ROWS and projections_fit(x, lins):
         return fused_projections(x, [l.weight for l in lins])
     return tuple(l(x) for l in lins)
 

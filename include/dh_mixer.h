@@ -277,7 +277,10 @@ int dh_decode_attention_split(int dtype, const void* q, const void* k, const voi
                               int window, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
- * dh_decode_mixer_step as two launches with a wider first one, for the graphed decoder:
+ * dh_decode_mixer_step as two launches with a wider first one. The graphed decoder runs
+ * dh_decode_gates with dh_decode_scan_out (below) at batch 1 and dh_decode_mixer_step at batch > 1;
+ * dh_decode_scan is on no product path: it is the plain two-launch form the tests compare the
+ * fused forms with.
  * dh_decode_gates runs one wave per (level, head, group of rows) -- the gate weights stream through
  * H*L compute units -- writes rg_hist[:, t] and a staging record per (b, h, l):
  *   stage[((b*H + h)*L + l)*(4 + hd) + ...] = {ig, fg, r_src, 0, V_src[0..hd)}   (fp32)

