@@ -898,12 +898,20 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
 // staged and normalised once per workgroup instead of once per group, and each group's weights are
 // requested before the previous group's matrix-core steps, so the weight stream does not stop at a
 // group boundary. Per output element the arithmetic is the kernel above's.
-template <int KSPLIT, int TPW, int KSW>
+// Every request is straight-line: the activation rows and the norm weight through raw buffer loads
+// (past the rows: zeros, no memory request), and with FULL (every wave owns exactly KSW k-steps:
+// K = 32 * KSPLIT * KSW) the weight loads and the k-steps without a predicate, and the next group's
+// weights requested unconditionally (past the last group: the clamped last tile, loaded and unused).
+// A predicated request makes the compiler wait for every load before the first use of any, which
+// here meant waiting for the NEXT group's weights before each group's k-steps (measured: the
+// batch-16 vocabulary head streamed at ~3 TB/s).
+template <int KSPLIT, int TPW, int KSW, bool FULL>
 __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_pers_kernel(GemvArgs a, int steps_per_wave,
                                                                                   int ngroups) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NT = 64 * KSPLIT * TPW;
   constexpr int XC = 8;                                // staged 16-byte chunks per thread (host: 2K <= XC*NT)
+  constexpr uint32_t kOOB = 0x80000000u;               // past every resource below (each < 2 GB)
   const int lane = threadIdx.x & 63, wwave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tile = wwave / KSPLIT, wave = wwave % KSPLIT;
   const int r = lane & 15, g = lane >> 4;
@@ -913,56 +921,53 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_pers_kerne
   unsigned char* hs = smem;                            // [16][rowb] staged rows
   float* red = reinterpret_cast<float*>(smem + 16 * rowb);   // [TPW][KSPLIT][64][4] partial tiles
 
+  // rows in place (the host launches this kernel only without gathered rows)
   uint4 xs[XC];
-  if (a.x_rows == nullptr) {                          // uniform (as in the kernel above)
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, (uint32_t)(((int64_t)(B - 1) * a.x_bstride + K) * 2));
 #pragma unroll
-    for (int j = 0; j < XC; ++j) {
-      const int i = threadIdx.x + j * NT;
-      xs[j] = make_uint4(0u, 0u, 0u, 0u);
-      if (i < B * kc) xs[j] = ld16((const bf16_t*)a.x + (int64_t)(i / kc) * a.x_bstride + (int64_t)(i % kc) * 8);
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < XC; ++j) {
-      const int i = threadIdx.x + j * NT;
-      xs[j] = make_uint4(0u, 0u, 0u, 0u);
-      if (i < B * kc) {
-        const int b = i / kc;
-        const int64_t xrow = load_uniform(a.x_rows + b);
-        xs[j] = ld16((const bf16_t*)a.x + xrow * a.x_bstride + (int64_t)(i % kc) * 8);
-      }
-    }
+  for (int j = 0; j < XC; ++j) {
+    const int i = threadIdx.x + j * NT;
+    const uint32_t off = i < B * kc ? (uint32_t)(((int64_t)(i / kc) * a.x_bstride + (i % kc) * 8) * 2) : kOOB;
+    xs[j] = bld16(rx, off);
   }
   constexpr int GC = 4;
-  const bool g_early = a.g != nullptr && kc <= 64 * GC;
+  // FULL: K = 32 * KSPLIT * KSW <= 1024, so the norm weight always fits the early registers
+  const bool g_early = a.g != nullptr && (FULL || kc <= 64 * GC);
   uint4 gv[GC];
+  const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.g, g_early ? (uint32_t)(K * 2) : 0u);
 #pragma unroll
-  for (int i = 0; i < GC; ++i) {
-    gv[i] = make_uint4(0u, 0u, 0u, 0u);
-    if (g_early && lane + 64 * i < kc) gv[i] = ld16((const bf16_t*)a.g + (lane + 64 * i) * 8);
-  }
+  for (int i = 0; i < GC; ++i) gv[i] = bld16(rg, (uint32_t)(lane + 64 * i) * 16u);   // past K: zeros
   const int nsteps = K / 32;
   const int s0 = wave * steps_per_wave;
-  const int my_steps = min(steps_per_wave, nsteps - s0);
-  // a group's tile geometry for this wave: first row, real rows, the weight row this lane reads
-  struct Geo { int n0, loc, s; bool live, row_ok; const bf16_t* w; };
+  const int my_steps = FULL ? KSW : min(steps_per_wave, nsteps - s0);
+  // a group's tile geometry for this wave: first row, real rows, the tile's first weight row and the
+  // row this lane reads within it; `valid`: the group exists (a request past the last one reads nothing)
+  struct Geo { int n0, loc, s, wr; bool live, row_ok, valid; const bf16_t* wt; };
   auto geo = [&](int grp) {
     Geo q;
     const int tl = grp * TPW + tile;
+    q.valid = grp < ngroups;
     q.n0 = min(tl * 16, ((a.Nrows - 1) / 16) * 16);
     q.live = tl * 16 < a.Nrows;
     const RowSeg sg = row_segment(a, q.n0);
     q.s = sg.s;
     q.row_ok = q.n0 + r < a.Nrows;
     q.loc = sg.local + r;
-    const int wrow = sg.local + (q.row_ok ? r : a.Nrows - 1 - q.n0);
-    q.w = (const bf16_t*)pick_seg(sg.s, a.seg[0].W, a.seg[1].W, a.seg[2].W) + (int64_t)wrow * K;
+    q.wr = q.row_ok ? r : a.Nrows - 1 - q.n0;
+    q.wt = (const bf16_t*)pick_seg(sg.s, a.seg[0].W, a.seg[1].W, a.seg[2].W) + (int64_t)sg.local * K;
     return q;
   };
   auto load_w = [&](uint4 (&wf)[KSW], const Geo& q) {
+    if constexpr (FULL) {
+      const __amdgpu_buffer_rsrc_t rw = buf_rsrc(q.wt, (uint32_t)(16 * K * 2));
 #pragma unroll
-    for (int j = 0; j < KSW; ++j)
-      if (j < my_steps) wf[j] = ld16(q.w + (s0 + j) * 32 + 8 * g);
+      for (int j = 0; j < KSW; ++j)
+        wf[j] = bld16(rw, q.valid ? (uint32_t)((q.wr * K + (s0 + j) * 32 + 8 * g) * 2) : kOOB);
+    } else {
+#pragma unroll
+      for (int j = 0; j < KSW; ++j)
+        if (j < my_steps) wf[j] = ld16(q.wt + (int64_t)q.wr * K + (s0 + j) * 32 + 8 * g);
+    }
   };
   uint4 wa[KSW], wb[KSW];
   Geo ga = geo(blockIdx.x);
@@ -991,7 +996,7 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_pers_kerne
       }
       const float rs = rsqrtf(wave_sum(ss) / (float)K + a.eps);
       unsigned char* row = hs + b * rowb;
-      if (g_early) {                                   // uniform
+      if (FULL || g_early) {                           // uniform
 #pragma unroll
         for (int i = 0; i < GC; ++i)
           if (lane + 64 * i < kc) norm_chunk(row, lane + 64 * i, rs, gv[i]);
@@ -1003,17 +1008,19 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_pers_kerne
   }
 
   // ---- one group: the next group's weights requested first, then this group's k-steps, partial
-  // tiles through LDS, wave 0 of each tile sums them and writes (row n0 + r, batch rows 4g + i)
+  // tiles through LDS, wave 0 of each tile sums them and writes (row n0 + r, batch rows 4g + i).
+  // With FULL every wave of the tile sums them and the stores go through a buffer resource whose
+  // offsets drop the other waves' and the dead outputs' stores: no branch around a memory request.
   auto group = [&](int grp, const Geo& q, const uint4 (&wf)[KSW], uint4 (&wn)[KSW], Geo& qn) {
     const int nxt = grp + (int)gridDim.x;
-    if (nxt < ngroups) {                               // uniform
+    if (FULL || nxt < ngroups) {                       // FULL: unconditional (past the last group: no request)
       qn = geo(nxt);
       load_w(wn, qn);
     }
     mf_f32x4 acc = mf_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < KSW; ++j) {
-      if (j < my_steps) {                              // uniform
+      if (FULL || j < my_steps) {                      // uniform
         mf_bf16x8 av, bv;
         const uint4 xa = *reinterpret_cast<const uint4*>(hs + r * rowb + ((s0 + j) * 32 + 8 * g) * 2);
         __builtin_memcpy(&av, &xa, 16);
@@ -1023,7 +1030,27 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_pers_kerne
     }
     *reinterpret_cast<mf_f32x4*>(red + ((tile * KSPLIT + wave) * 64 + lane) * 4) = acc;
     __syncthreads();
-    if (wave == 0 && q.live) {
+    if constexpr (FULL) {
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w2 = 0; w2 < KSPLIT; ++w2) {
+        const mf_f32x4 p = *reinterpret_cast<const mf_f32x4*>(red + ((tile * KSPLIT + w2) * 64 + lane) * 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] += p[i];
+      }
+      bf16_t* ob = (bf16_t*)pick_seg(q.s, a.seg[0].out, a.seg[1].out, a.seg[2].out) +
+                   t * pick_seg(q.s, a.seg[0].t_stride, a.seg[1].t_stride, a.seg[2].t_stride);
+      const int64_t bs = pick_seg(q.s, a.seg[0].out_bstride, a.seg[1].out_bstride, a.seg[2].out_bstride);
+      const int ns = pick_seg(q.s, a.seg[0].N, a.seg[1].N, a.seg[2].N);
+      const __amdgpu_buffer_rsrc_t ro = buf_rsrc(ob, (uint32_t)(((int64_t)(B - 1) * bs + ns) * 2));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int b = 4 * g + i;
+        const bool st = wave == 0 && q.live && b < B && q.row_ok;
+        __builtin_amdgcn_raw_buffer_store_b16((unsigned short)f32_to_bf16(v[i]), ro,
+                                              st ? (uint32_t)(((int64_t)b * bs + q.loc) * 2) : kOOB, 0, 0);
+      }
+    } else if (wave == 0 && q.live) {
       float v[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int w2 = 0; w2 < KSPLIT; ++w2) {
@@ -1096,7 +1123,7 @@ void launch_mfma(const GemvArgs& a0, hipStream_t s) {
     // many tiles (the vocabulary head): four tiles per workgroup share one staging of the rows; with
     // no residual, persistent workgroups walk the tile groups
     if (ks == 4 && tiles >= 4 * 512) {
-      if (a.resid == nullptr) {
+      if (a.resid == nullptr && a.x_rows == nullptr) {
         const int ngroups = (tiles + 3) / 4;
         int dev = 0, ncu = 0;
         if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
@@ -1108,7 +1135,12 @@ void launch_mfma(const GemvArgs& a0, hipStream_t s) {
             (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
           kern<<<dim3(grid), dim3(1024), lds, s>>>(a, spw, ngroups);
         };
-        if (small) go(&decode_gemv_mfma_pers_kernel<4, 4, 4>); else go(&decode_gemv_mfma_pers_kernel<4, 4, 8>);
+        const bool full = nsteps == 4 * (small ? 4 : 8);   // every wave exactly KSW k-steps
+        if (small) {
+          if (full) go(&decode_gemv_mfma_pers_kernel<4, 4, 4, true>); else go(&decode_gemv_mfma_pers_kernel<4, 4, 4, false>);
+        } else {
+          if (full) go(&decode_gemv_mfma_pers_kernel<4, 4, 8, true>); else go(&decode_gemv_mfma_pers_kernel<4, 4, 8, false>);
+        }
         return;
       }
       if (small) launch_mfma_k<4, 4, 4, SW>(a, spw, s); else launch_mfma_k<4, 4, 8, SW>(a, spw, s);
