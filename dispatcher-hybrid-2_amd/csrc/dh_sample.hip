@@ -254,7 +254,8 @@ __device__ __forceinline__ uint32_t radix_kth(const uint32_t* vals, int n, int k
 template <typename T>
 __global__ __launch_bounds__(kST) void sample_topk_kernel(const T* logits, int64_t row_stride, int V,
                                                           float temperature, int top_k, uint64_t seed,
-                                                          const int64_t* offset_dev, int64_t* out) {
+                                                          const int64_t* offset_dev, int64_t* out, int64_t* tok_hist,
+                                                          int64_t hist_stride, int64_t hist_len) {
   __shared__ uint32_t buf[kCap + 1];                   // + a slot for unselected writes
   __shared__ float fred[kST / 64];
   __shared__ uint32_t ured[kST / 64];
@@ -379,7 +380,11 @@ __global__ __launch_bounds__(kST) void sample_topk_kernel(const T* logits, int64
     atomicMax(&fallback, last);
   }
   __syncthreads();
-  if (tid == 0) out[b] = chosen != 0x7fffffff ? chosen : (fallback >= 0 ? fallback : 0);
+  if (tid == 0) {
+    const int64_t tok = chosen != 0x7fffffff ? chosen : (fallback >= 0 ? fallback : 0);
+    out[b] = tok;
+    if (tok_hist && off >= 0 && off < hist_len) tok_hist[b * hist_stride + off] = tok;   // history at the position
+  }
 }
 
 // bf16 logits with 0 < top_k <= kST: the same selection, weights and draw on 16-bit order keys of
@@ -404,7 +409,8 @@ __device__ __forceinline__ float key16_value(uint32_t k) {  // inverse of one ha
 
 __global__ __launch_bounds__(kST) void sample_topk_bf16_kernel(const bf16_t* logits, int64_t row_stride, int V,
                                                                float temperature, int top_k, uint64_t seed,
-                                                               const int64_t* offset_dev, int64_t* out) {
+                                                               const int64_t* offset_dev, int64_t* out, int64_t* tok_hist,
+                                                               int64_t hist_stride, int64_t hist_len) {
   constexpr int NP = kSPT / 2;                         // registers of packed key pairs
   __shared__ uint32_t buf[kCap + 1];
   __shared__ float fred[kST / 64];
@@ -545,14 +551,21 @@ __global__ __launch_bounds__(kST) void sample_topk_bf16_kernel(const bf16_t* log
     atomicMax(&fallback, last);
   }
   __syncthreads();
-  if (tid == 0) out[b] = chosen != 0x7fffffff ? chosen : (fallback >= 0 ? fallback : 0);
+  if (tid == 0) {
+    const int64_t tok = chosen != 0x7fffffff ? chosen : (fallback >= 0 ? fallback : 0);
+    out[b] = tok;
+    if (tok_hist && off >= 0 && off < hist_len) tok_hist[b * hist_stride + off] = tok;   // history at the position
+  }
 }
 
 }  // namespace
 
-extern "C" int dh_sample_topk(int dtype, const void* logits, int64_t row_stride, int B, int V, float temperature,
-                              int top_k, uint64_t seed, const int64_t* offset_dev, int64_t* out, void* stream) {
-  const char* who = "dh_sample_topk";
+extern "C" int dh_sample_topk_hist(int dtype, const void* logits, int64_t row_stride, int B, int V, float temperature,
+                                   int top_k, uint64_t seed, const int64_t* offset_dev, int64_t* out, int64_t* tok_hist,
+                                   int64_t hist_stride, int64_t hist_len, void* stream) {
+  const char* who = tok_hist ? "dh_sample_topk_hist" : "dh_sample_topk";
+  DH_REQUIRE(!tok_hist || (offset_dev && hist_stride >= hist_len && hist_len >= 0), DH_ERR_INVALID_ARG,
+             "%s: a token history needs the position (offset_dev) and rows of hist_stride >= hist_len", who);
   DH_REQUIRE(dtype == DH_F32 || dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d", who, dtype);
   DH_REQUIRE(B >= 1 && B <= 65535 && V >= 1 && row_stride >= V, DH_ERR_INVALID_ARG, "%s: B=%d V=%d row_stride=%lld",
              who, B, V, (long long)row_stride);
@@ -565,14 +578,20 @@ extern "C" int dh_sample_topk(int dtype, const void* logits, int64_t row_stride,
   hipStream_t s = (hipStream_t)stream;
   if (dtype == DH_BF16 && top_k > 0 && top_k <= kST && top_k < V)
     sample_topk_bf16_kernel<<<B, kST, 0, s>>>((const bf16_t*)logits, row_stride, V, temperature, top_k, seed,
-                                               offset_dev, out);
+                                               offset_dev, out, tok_hist, hist_stride, hist_len);
   else if (dtype == DH_BF16)
     sample_topk_kernel<bf16_t><<<B, kST, 0, s>>>((const bf16_t*)logits, row_stride, V, temperature, top_k, seed,
-                                                  offset_dev, out);
+                                                  offset_dev, out, tok_hist, hist_stride, hist_len);
   else
     sample_topk_kernel<float><<<B, kST, 0, s>>>((const float*)logits, row_stride, V, temperature, top_k, seed,
-                                                 offset_dev, out);
+                                                 offset_dev, out, tok_hist, hist_stride, hist_len);
   return dh_check_launch(who);
+}
+
+extern "C" int dh_sample_topk(int dtype, const void* logits, int64_t row_stride, int B, int V, float temperature,
+                              int top_k, uint64_t seed, const int64_t* offset_dev, int64_t* out, void* stream) {
+  return dh_sample_topk_hist(dtype, logits, row_stride, B, V, temperature, top_k, seed, offset_dev, out, nullptr, 0,
+                             0, stream);
 }
 
 extern "C" int64_t dh_argmax_workspace_bytes(int B, int V) {

@@ -645,8 +645,8 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         elif self._sample_capture is not None:
             # sampled pick (draws keyed by the new position) into token_buf and the token history
             temperature, top_k, seed = self._sample_capture
-            fs.sample_tokens(self.logits_out, temperature, top_k, seed, self.t_buf, out=self.token_buf)
-            self.tok_hist.index_copy_(1, self.t_buf, self.token_buf.unsqueeze(1))
+            fs.sample_tokens(self.logits_out, temperature, top_k, seed, self.t_buf, out=self.token_buf,
+                             hist=self.tok_hist)
 
     @torch.no_grad()
     def greedy_start(self, logits):

@@ -386,13 +386,17 @@ def argmax_tokens_noalloc(logits, out):
     return out
 
 
-def sample_tokens(logits, temperature=1.0, top_k=None, seed=0, offset=None, out=None):
+def sample_tokens(logits, temperature=1.0, top_k=None, seed=0, offset=None, out=None, hist=None):
     """Temperature / top-k sampling on the device (``dh_sample_topk``), the do_sample branch of
     fast_generate (reference modeling_dispatcher.py:426-441): logits.float() / temperature, every
     element below the top_k-th largest masked out (ties with it kept), one draw per row from
     softmax. The draw of row b comes from Philox4x32-10 keyed by `seed` with counter (offset[0], b):
     pass the decoder's device position as `offset` so each step draws afresh (also under graph
-    replay). logits: (B, V) fp32 or bf16, unit inner stride, V <= 65536. Returns int64 `out`."""
+    replay). logits: (B, V) fp32 or bf16, unit inner stride, V <= 65536. Returns int64 `out`.
+
+    hist: an optional (B, L) int64 token history (unit inner stride); the kernel also writes each
+    row's token to hist[b, offset[0]] when 0 <= offset[0] < L (``dh_sample_topk_hist``), the
+    history update after the pick, with no launch of its own. Needs `offset`."""
     _hip.require_gpu(logits, "sample_tokens")
     if logits.dim() != 2 or logits.stride(-1) != 1:
         raise ValueError("sample_tokens: logits must be (B, V) with a unit inner stride")
@@ -408,10 +412,23 @@ def sample_tokens(logits, temperature=1.0, top_k=None, seed=0, offset=None, out=
         out = torch.empty(B, dtype=torch.long, device=logits.device)
     if out.dtype != torch.long or out.numel() != B or not out.is_contiguous():
         raise ValueError("sample_tokens: out must be a contiguous int64 tensor of B elements")
-    st = _hip.lib.dh_sample_topk(_hip.dtype_code(logits.dtype), _hip.ptr(logits), logits.stride(0), B, V,
-                                 ctypes.c_float(float(temperature)), k, ctypes.c_uint64(int(seed) & (2 ** 64 - 1)),
-                                 _hip.ptr(offset), _hip.ptr(out), _hip.stream_handle(logits.device))
-    _hip.check(st, "dh_sample_topk")
+    if hist is None:
+        st = _hip.lib.dh_sample_topk(_hip.dtype_code(logits.dtype), _hip.ptr(logits), logits.stride(0), B, V,
+                                     ctypes.c_float(float(temperature)), k, ctypes.c_uint64(int(seed) & (2 ** 64 - 1)),
+                                     _hip.ptr(offset), _hip.ptr(out), _hip.stream_handle(logits.device))
+        _hip.check(st, "dh_sample_topk")
+        return out
+    if offset is None:
+        raise ValueError("sample_tokens: a token history needs the position (offset)")
+    if (hist.dtype != torch.long or hist.dim() != 2 or hist.shape[0] != B or hist.stride(1) != 1
+            or hist.device != logits.device):
+        raise ValueError("sample_tokens: hist must be a (B, L) int64 tensor with a unit inner stride on the "
+                         "logits' device")
+    st = _hip.lib.dh_sample_topk_hist(_hip.dtype_code(logits.dtype), _hip.ptr(logits), logits.stride(0), B, V,
+                                      ctypes.c_float(float(temperature)), k,
+                                      ctypes.c_uint64(int(seed) & (2 ** 64 - 1)), _hip.ptr(offset), _hip.ptr(out),
+                                      _hip.ptr(hist), hist.stride(0), hist.shape[1], _hip.stream_handle(logits.device))
+    _hip.check(st, "dh_sample_topk_hist")
     return out
 
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 15
+#define DH_ABI_VERSION 16
 
 enum dh_status {
   DH_OK = 0,
@@ -360,6 +360,16 @@ int dh_argmax_reduce(const void* cand, int B, int ncand, int64_t* out, const int
  */
 int dh_sample_topk(int dtype, const void* logits, int64_t row_stride, int B, int V, float temperature, int top_k,
                    uint64_t seed, const int64_t* offset_dev, int64_t* out, void* stream);
+/*
+ * dh_sample_topk that also writes each row's token into a position-indexed history,
+ * hist[b * hist_stride + p] with p = *offset_dev when 0 <= p < hist_len (nothing otherwise): the
+ * token-history update after the pick in fast_generate's sampling loop (the decoder's tok_hist),
+ * folded into the sampler's launch. hist nullable (then exactly dh_sample_topk); a history needs
+ * offset_dev.
+ */
+int dh_sample_topk_hist(int dtype, const void* logits, int64_t row_stride, int B, int V, float temperature,
+                        int top_k, uint64_t seed, const int64_t* offset_dev, int64_t* out, int64_t* hist,
+                        int64_t hist_stride, int64_t hist_len, void* stream);
 
 /*
  * The two halves of dh_decode_mixer_step as separate launches, with the reference's own buffer

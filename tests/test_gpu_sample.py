@@ -304,6 +304,28 @@ def test_sample_deterministic_and_keyed():
     assert not torch.equal(a, c) and not torch.equal(a, e)
 
 
+@pytest.mark.parametrize("dtype,k", [(torch.float32, 100), (torch.bfloat16, 50), (torch.bfloat16, None)])
+def test_sample_history_write(dtype, k):
+    """dh_sample_topk_hist: the same draws as dh_sample_topk, each row's token also stored at
+    hist[b, offset] (rows of stride 37 > L = 30), every other history entry untouched; an offset
+    at or past L writes no history."""
+    from dispatcher_hybrid import fused_step
+    g = torch.Generator(device=DEV).manual_seed(9)
+    logits = torch.randn(16, 50257, device=DEV, generator=g).to(dtype)
+    base = torch.randint(0, 1000, (16, 37), device=DEV, generator=g)
+    for pos in (0, 17, 29, 30, 31):
+        off = torch.full((1,), pos, dtype=torch.long, device=DEV)
+        ref = fused_step.sample_tokens(logits, 0.8, k, seed=5, offset=off)
+        hist = base.clone()
+        got = fused_step.sample_tokens(logits, 0.8, k, seed=5, offset=off, hist=hist[:, :30])
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref)
+        want = base.clone()
+        if pos < 30:
+            want[:, pos] = ref
+        assert torch.equal(hist, want), pos
+
+
 def test_sample_top1_and_tiny_temperature_are_argmax():
     from dispatcher_hybrid import fused_step
     g = torch.Generator(device=DEV).manual_seed(6)
@@ -327,6 +349,12 @@ def test_sample_rejects_bad_arguments():
         fused_step.sample_tokens(x, 0.0, 5)
     with pytest.raises(ValueError, match="65536"):
         fused_step.sample_tokens(torch.zeros(1, 70000, device=DEV), 1.0, 5)
+    hist = torch.zeros(2, 8, dtype=torch.long, device=DEV)
+    with pytest.raises(ValueError, match="offset"):
+        fused_step.sample_tokens(x, 1.0, 5, hist=hist)
+    off = torch.zeros(1, dtype=torch.long, device=DEV)
+    with pytest.raises(ValueError, match="hist"):
+        fused_step.sample_tokens(x, 1.0, 5, offset=off, hist=hist[:1])
 
 
 @pytest.mark.parametrize("batch", [1, 16])
