@@ -665,8 +665,9 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_staged_kernel(GemvArgs a
 // ---------------------------------------------------------------------------------------------
 // Batched decode GEMV on the matrix cores (bf16, 2 <= B <= 16). out[b, n] = W[n] . h[b] for a batch
 // of up to 16 rows is a skinny GEMM whose batch dimension is exactly the 16 rows of
-// v_mfma_f32_16x16x32_bf16: A = the (normalised) activation rows staged in LDS (rows padded to
-// K*2 + 16 bytes: conflict-free 16-byte reads; rows past B are zero), B = 16 weight rows straight
+// v_mfma_f32_16x16x32_bf16: A = the (normalised) activation rows -- loaded per lane straight from
+// memory (DX, rows in place), or for gathered rows staged in LDS (rows padded to K*2 + 16 bytes:
+// conflict-free 16-byte reads); rows past B are zero --, B = 16 weight rows straight
 // from memory (lane (row n, k-group g) holds 16 bytes of W[n]), and the C fragment already holds
 // one output row per lane column and four batch rows per lane -- no cross-lane reduction, where the
 // batched CUDA-style kernel above reduces every (row, batch row) dot product across a wave. A
@@ -674,7 +675,14 @@ __global__ __launch_bounds__(kThreads) void decode_gemv_staged_kernel(GemvArgs a
 // waves (4..16, so a launch keeps ~1000+ waves streaming weights); their partial tiles are summed
 // through LDS by wave 0, which applies the same epilogues and rounding points as the kernels above.
 // Requests: the activation rows first (small, from L2), then every weight fragment of the wave,
-// then the waits.
+// then the waits. With rows in place (DX) no row is staged: each lane loads its own A fragments
+// (batch row r, the wave's k-steps) straight from memory next to its weight fragments. Without an
+// RMSNorm prologue the k-steps then wait for those loads only -- no LDS round trip and no barrier
+// before the matrix-core steps, and the same sums as the staged form. With one, each lane also
+// loads the norm weight's fragments; the row's sum of squares is the lane's fragment sums, summed
+// over the row's four lanes (shuffles) and over the waves (16 floats per wave through LDS, one
+// barrier), and each fragment is scaled in registers: round(x * rsqrt(ss / K + eps) * w), the
+// staged form's formula (its sum of squares runs in another order).
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short mf_bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float mf_f32x4;
 
@@ -688,8 +696,9 @@ __device__ __forceinline__ void norm_chunk(unsigned char* row, int c, float rs, 
   *reinterpret_cast<uint4*>(row + c * 16) = Vec<bf16_t>::pack(xf);
 }
 
-template <int KSPLIT, int TPW, int KSW, bool SW, bool GA, bool HALF>
+template <int KSPLIT, int TPW, int KSW, bool SW, bool GA, bool HALF, bool DX>
 __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(GemvArgs a, int steps_per_wave) {
+  static_assert(!(DX && GA), "direct fragments read rows in place");
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int NT = 64 * KSPLIT * TPW;               // TPW 16-row tiles per workgroup share the staging
   constexpr int NW = SW ? 2 : 1;
@@ -700,8 +709,8 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
   const int K = a.K, B = a.B;
   const int kc = K / 8;                                // 16-byte chunks per row
   const int rowb = K * 2 + 16;                         // padded LDS row (bytes)
-  unsigned char* hs = smem;                            // [16][rowb] staged rows
-  float* red = reinterpret_cast<float*>(smem + 16 * rowb);   // [TPW][KSPLIT][NW][64][4] partial tiles
+  unsigned char* hs = smem;                            // [16][rowb] staged rows (not with DX)
+  float* red = reinterpret_cast<float*>(smem + (DX ? 0 : 16 * rowb));   // [TPW][KSPLIT][NW][64][4] partial tiles
   // tiles of tr real rows (16, or 8 for outputs with few tiles: twice the workgroups stream the
   // weights; lanes r >= 8 then read nothing and their output columns are dropped)
   constexpr int trs = HALF ? 3 : 4;                   // log2 of the real rows per tile (a compile-time
@@ -730,24 +739,41 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
   const int s0 = wave * steps_per_wave;
   const int my_steps = min(steps_per_wave, nsteps - s0);
   const int wr = wrow - seg0.local;                    // 0..15
-  uint4 xs[XC], gv[GC], wf[NW][KSW];
+  uint4 xs[XC], gv[GC], wf[NW][KSW], xd[KSW], gd[KSW];
   uint32_t rres[4] = {0u, 0u, 0u, 0u};
   if constexpr (!GA) {
-    // (whole slots past the rows are skipped by a uniform branch: the loads issued after every
-    // activation slot do not depend on it, so the waits stay exact)
     const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, (uint32_t)(((int64_t)(B - 1) * a.x_bstride + K) * 2));
+    if constexpr (DX) {
+      // this lane's A fragments: batch row r (zeros past B), 16 bytes of each of the wave's k-steps
 #pragma unroll
-    for (int j = 0; j < XC; ++j) {
-      xs[j] = make_uint4(0u, 0u, 0u, 0u);
-      if (j * NT < B * kc) {                           // uniform
-        const int i = threadIdx.x + j * NT;
-        const uint32_t off = i < B * kc ? (uint32_t)(((int64_t)(i / kc) * a.x_bstride + (i % kc) * 8) * 2) : kOOB;
-        xs[j] = bld16(rx, off);
+      for (int j = 0; j < KSW; ++j) {
+        const uint32_t off = j < my_steps && r < B
+                                 ? (uint32_t)(((int64_t)r * a.x_bstride + (s0 + j) * 32 + 8 * g) * 2) : kOOB;
+        xd[j] = bld16(rx, off);
+      }
+      // the norm weight's fragments of the same k-steps (no norm: an empty resource, no requests)
+      const __amdgpu_buffer_rsrc_t rgd = buf_rsrc(a.g, a.g != nullptr ? (uint32_t)(K * 2) : 0u);
+#pragma unroll
+      for (int j = 0; j < KSW; ++j)
+        gd[j] = bld16(rgd, j < my_steps ? (uint32_t)(((s0 + j) * 32 + 8 * g) * 2) : kOOB);
+    } else {
+      // (whole slots past the rows are skipped by a uniform branch: the loads issued after every
+      // activation slot do not depend on it, so the waits stay exact)
+#pragma unroll
+      for (int j = 0; j < XC; ++j) {
+        xs[j] = make_uint4(0u, 0u, 0u, 0u);
+        if (j * NT < B * kc) {                         // uniform
+          const int i = threadIdx.x + j * NT;
+          const uint32_t off = i < B * kc ? (uint32_t)(((int64_t)(i / kc) * a.x_bstride + (i % kc) * 8) * 2) : kOOB;
+          xs[j] = bld16(rx, off);
+        }
       }
     }
-    const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.g, g_early ? (uint32_t)(K * 2) : 0u);
+    if constexpr (!DX) {
+      const __amdgpu_buffer_rsrc_t rg = buf_rsrc(a.g, g_early ? (uint32_t)(K * 2) : 0u);
 #pragma unroll
-    for (int i = 0; i < GC; ++i) gv[i] = bld16(rg, (uint32_t)(lane + 64 * i) * 16u);   // past K: zeros
+      for (int i = 0; i < GC; ++i) gv[i] = bld16(rg, (uint32_t)(lane + 64 * i) * 16u);   // past K: zeros
+    }
     const uint32_t wbytes = (uint32_t)(16 * K * 2);
     const __amdgpu_buffer_rsrc_t rw0 = buf_rsrc(wt0, wbytes);
     const __amdgpu_buffer_rsrc_t rw1 = buf_rsrc(wt1, wbytes);
@@ -807,6 +833,7 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
   DH_ISSUE_FENCE();
 
   // ---- stage the rows (zeros past B), then normalise each once (wave w: rows w, w + KSPLIT, ...)
+  if constexpr (!DX) {
 #pragma unroll
   for (int j = 0; j < XC; ++j) {
     const int i = threadIdx.x + j * NT;
@@ -816,7 +843,8 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
     }
   }
   __syncthreads();
-  if (a.g != nullptr) {                                // uniform
+  }
+  if (!DX && a.g != nullptr) {                         // uniform
     for (int b = wwave; b < B; b += KSPLIT * TPW) {
       float ss = 0.f;
       for (int c = lane; c < kc; c += 64) {
@@ -838,6 +866,29 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
     __syncthreads();
   }
 
+  // ---- DX with a norm: the rows' sums of squares (lane -> row's four lanes -> waves), then rsqrt
+  float rsd = 1.f;
+  const bool dnorm = DX && a.g != nullptr;
+  if (dnorm) {                                         // uniform
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < KSW; ++j) {
+      float xf[8];
+      Vec<bf16_t>::unpack(xd[j], xf);                  // past the wave's steps: zeros
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += xf[e] * xf[e];
+    }
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    float* ssx = red + TPW * KSPLIT * NW * 64 * 4;     // [TPW * KSPLIT][16]
+    if (g == 0) ssx[wwave * 16 + r] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < KSPLIT; ++w2) tot += ssx[(tile * KSPLIT + w2) * 16 + r];
+    rsd = rsqrtf(tot / (float)K + a.eps);
+  }
+
   // ---- this wave's k-steps on the matrix cores
   mf_f32x4 acc[NW];
 #pragma unroll
@@ -846,7 +897,15 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
   for (int j = 0; j < KSW; ++j) {
     if (j < my_steps) {                                // uniform
       mf_bf16x8 av, bv;
-      const uint4 xa = *reinterpret_cast<const uint4*>(hs + r * rowb + ((s0 + j) * 32 + 8 * g) * 2);
+      uint4 xa = DX ? xd[j] : *reinterpret_cast<const uint4*>(hs + r * rowb + ((s0 + j) * 32 + 8 * g) * 2);
+      if (dnorm) {                                     // uniform
+        float xf[8], gw[8];
+        Vec<bf16_t>::unpack(xa, xf);
+        Vec<bf16_t>::unpack(gd[j], gw);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[e] = Elem<bf16_t>::round(xf[e] * rsd * gw[e]);
+        xa = Vec<bf16_t>::pack(xf);
+      }
       __builtin_memcpy(&av, &xa, 16);
 #pragma unroll
       for (int q = 0; q < NW; ++q) {
@@ -1080,11 +1139,16 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_pers_kerne
 
 template <int KSPLIT, int TPW, int KSW, bool SW>
 void launch_mfma_k(const GemvArgs& a, int steps_per_wave, hipStream_t s) {
-  const size_t lds = (size_t)16 * (a.K * 2 + 16) + (size_t)TPW * KSPLIT * (SW ? 2 : 1) * 64 * 16;
-  auto kern = a.x_rows || a.resid_rows ? &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, true, false>
-                                       : &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, false, false>;
+  const bool dx = !a.x_rows && !a.resid_rows;         // rows in place: no staging (see the kernel)
+  const size_t lds = (dx ? (size_t)TPW * KSPLIT * 16 * 4 : (size_t)16 * (a.K * 2 + 16)) +
+                     (size_t)TPW * KSPLIT * (SW ? 2 : 1) * 64 * 16;
+  auto kern = a.x_rows || a.resid_rows ? &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, true, false, false>
+                                       : &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, false, false, false>;
+  if (dx) kern = &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, false, false, true>;
   if constexpr (!SW && TPW == 1)
-    if (a.tile_rows == 8) kern = &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, false, true>;
+    if (a.tile_rows == 8)
+      kern = dx ? &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, false, true, true>
+                : &decode_gemv_mfma_kernel<KSPLIT, TPW, KSW, SW, false, true, false>;
   if (lds > 64 * 1024)
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)lds);
@@ -1093,7 +1157,9 @@ void launch_mfma_k(const GemvArgs& a, int steps_per_wave, hipStream_t s) {
 }
 
 // K split: enough waves to stream the weights (~1024+ per launch), at least 4 per workgroup (they
-// share the staged rows) and enough for the staging (2K <= 8 * 64 * KSPLIT)
+// share the staged rows) and enough for the staging (2K <= 8 * 64 * KSPLIT). The normalised
+// launches keep it without staging too: measured at batch 16, 4 or 16 waves per workgroup instead
+// of 8 made the decode step 1-3% slower.
 // (SwiGLU: at most 8 waves -- two weight tiles per wave do not fit 16 waves' registers)
 bool mfma_gemv_fits(const GemvArgs& a, bool swiglu) {
   if (a.B < 2 || a.B > 16 || a.K % 32 != 0 || a.K > (swiglu ? 2048 : 4096)) return false;
@@ -1144,6 +1210,27 @@ void launch_mfma(const GemvArgs& a0, hipStream_t s) {
         return;
       }
       if (small) launch_mfma_k<4, 4, 4, SW>(a, spw, s); else launch_mfma_k<4, 4, 8, SW>(a, spw, s);
+      return;
+    }
+  }
+  if constexpr (!SW) {
+    // rows in place without a norm (no staging: each wave loads its own A fragments): fewer, longer
+    // waves -- the fewest (at least 4) whose k-steps fit 12 per wave. Measured at batch 16: the
+    // 1024 x 2816 down projection 7.36 -> 6.53 us per launch with 8 waves of 11 k-steps instead of
+    // 16 of 6 (4 waves of 22: 7.0 us); the staged, normalised launches lose with fewer waves.
+    if (a.g == nullptr && !a.x_rows && !a.resid_rows) {
+      int k2 = 4;
+      while (k2 < 16 && nsteps > 12 * k2) k2 *= 2;
+      const int sp = (nsteps + k2 - 1) / k2;           // <= 8 at k2 = 16 (K <= 4096)
+      if (k2 == 4) {
+        if (sp <= 4) launch_mfma_k<4, 1, 4, SW>(a, sp, s);
+        else if (sp <= 8) launch_mfma_k<4, 1, 8, SW>(a, sp, s);
+        else launch_mfma_k<4, 1, 12, SW>(a, sp, s);
+      } else if (k2 == 8) {
+        if (sp <= 8) launch_mfma_k<8, 1, 8, SW>(a, sp, s); else launch_mfma_k<8, 1, 12, SW>(a, sp, s);
+      } else {
+        if (sp <= 4) launch_mfma_k<16, 1, 4, SW>(a, sp, s); else launch_mfma_k<16, 1, 8, SW>(a, sp, s);
+      }
       return;
     }
   }
