@@ -113,6 +113,12 @@ __device__ __forceinline__ uint4 ld16(const void* p) {
   const gu32x4 v = *DH_GLOBAL(gu32x4, p);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+// weight rows, streamed once per step: non-temporal loads, so they do not push the step's state
+// (ring slots, history rows, cached keys and values) out of L2
+__device__ __forceinline__ uint4 ldw16(const void* p) {
+  const gu32x4 v = __builtin_nontemporal_load(DH_GLOBAL(gu32x4, p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ uint2 ld8(const void* p) {
   const gu32x2 v = *DH_GLOBAL(gu32x2, p);
   return make_uint2(v.x, v.y);
@@ -408,7 +414,7 @@ __device__ __forceinline__ void load_rows(uint4 (&w)[R][NW][CG], const bf16_t* c
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int q = 0; q < NW; ++q) w[r][q][c] = ld16(rows[r][q] + (int64_t)ch * 8);
+      for (int q = 0; q < NW; ++q) w[r][q][c] = ldw16(rows[r][q] + (int64_t)ch * 8);
   }
 }
 
@@ -474,7 +480,7 @@ __device__ __forceinline__ void fetch_in3(PreFirst& f, const PArgs& a, int n0, i
     const bf16_t* W = n < n0 ? W0 : (n < n0 + n1 ? W1 : W2);
     const int loc = n < n0 ? n : (n < n0 + n1 ? n - n0 : n - n0 - n1);
 #pragma unroll
-    for (int c = 0; c < 2; ++c) f.w[r][0][c] = ld16(W + (int64_t)loc * a.d + (int64_t)min(lane + 64 * c, nchunk - 1) * 8);
+    for (int c = 0; c < 2; ++c) f.w[r][0][c] = ldw16(W + (int64_t)loc * a.d + (int64_t)min(lane + 64 * c, nchunk - 1) * 8);
   }
 }
 
@@ -604,9 +610,9 @@ __device__ __forceinline__ void fetch_gates(PreGates& f, const PArgs& a, LayerRe
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const int64_t k = (int64_t)min(lane + 64 * c, nchunk - 1) * 8;
-    f.w[0][c] = ld16((const bf16_t*)(intptr_t)Lt[F_WI] + wrow + k);
-    f.w[1][c] = ld16((const bf16_t*)(intptr_t)Lt[F_WF] + wrow + k);
-    f.w[2][c] = ld16((const bf16_t*)(intptr_t)Lt[F_WR] + wrow + k);
+    f.w[0][c] = ldw16((const bf16_t*)(intptr_t)Lt[F_WI] + wrow + k);
+    f.w[1][c] = ldw16((const bf16_t*)(intptr_t)Lt[F_WF] + wrow + k);
+    f.w[2][c] = ldw16((const bf16_t*)(intptr_t)Lt[F_WR] + wrow + k);
   }
   const int64_t gi = (int64_t)l * H + h;
   f.bi = ld2((const bf16_t*)(intptr_t)Lt[F_BI] + gi);

@@ -208,6 +208,13 @@ template <> struct Chunk<float> {
 };
 
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+// gate weights, streamed once per step: non-temporal loads (they leave the ring slots and history
+// rows this step reads back in L2)
+typedef unsigned int nt_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ldw16(const void* p) {
+  const nt_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 // Raw element bits, so a load's consumer (the conversion) can sit after every load is issued.
 template <typename T> struct Raw;
@@ -259,9 +266,9 @@ __global__ __launch_bounds__(kFusedThreads) void decode_mixer_step_kernel(StepAr
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const int64_t k = (int64_t)min(lane + 64 * c, nchunk - 1) * V;
-      w[0][c] = ld16((const T*)a.Wi + wrow + k);
-      w[1][c] = ld16((const T*)a.Wf + wrow + k);
-      w[2][c] = ld16((const T*)a.Wr + wrow + k);
+      w[0][c] = ldw16((const T*)a.Wi + wrow + k);
+      w[1][c] = ldw16((const T*)a.Wf + wrow + k);
+      w[2][c] = ldw16((const T*)a.Wr + wrow + k);
 #pragma unroll
       for (int r = 0; r < RPB; ++r) av[r][c] = ld16((const T*)a.A + (int64_t)(b0 + min(r, nb - 1)) * GH + k);
     }
@@ -425,9 +432,9 @@ __global__ __launch_bounds__(64) void decode_gates_kernel(StepArgs a, float* sta
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const int64_t k = (int64_t)min(lane + 64 * c, nchunk - 1) * V;
-    w[0][c] = ld16((const T*)a.Wi + wrow + k);
-    w[1][c] = ld16((const T*)a.Wf + wrow + k);
-    w[2][c] = ld16((const T*)a.Wr + wrow + k);
+    w[0][c] = ldw16((const T*)a.Wi + wrow + k);
+    w[1][c] = ldw16((const T*)a.Wf + wrow + k);
+    w[2][c] = ldw16((const T*)a.Wr + wrow + k);
 #pragma unroll
     for (int r = 0; r < RB; ++r) av[r][c] = ld16((const T*)a.A + (int64_t)min(b0 + r, a.B - 1) * GH + k);
   }
