@@ -154,6 +154,68 @@ def test_down_projection_release_shape(B, dtype):
     assert rel_err(x, ref) < (1e-5 if dtype == torch.float32 else 1e-2)
 
 
+@pytest.mark.parametrize("resid", [False, True])
+@pytest.mark.parametrize("B", [2, 7, 16])
+@pytest.mark.parametrize("K,N", [(1024, 1000), (2816, 1024), (352, 96)])
+def test_batched_gemv_per_element(B, K, N, resid):
+    """Every output of the matrix-core batched GEMV (rows in place: each lane loads its own
+    activation fragments, no LDS staging; K = 2816 on 8 waves of 11 k-steps) within the rounding of
+    the exact sum. The products of bf16 operands are exact in fp32, so only the fp32 accumulation
+    order and the roundings differ from the exact value:
+        |round(acc) - S| <= 0.5 ulp + K 2^-24 sum_k |w_k h_k|,   S = sum_k w_k h_k (float64),
+    and with the residual, |round(round(acc) + r) - (S + r)| <= that + 0.5 ulp of the result.
+    The same rows gathered through x_rows (the LDS-staged form, another K split over the waves) are
+    held to the same bound."""
+    from dispatcher_hybrid import fused_step
+    from helpers import ulp_bf16
+    print(f"batched gemv B={B} K={K} N={N} resid={resid}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(1000 + 17 * B + K + int(resid))
+    x = torch.randn(B, K, device=DEV, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, K, device=DEV, generator=g) / K ** 0.5).to(torch.bfloat16)
+    r = torch.randn(B, N, device=DEV, generator=g).to(torch.bfloat16)
+    t_buf = torch.zeros(1, dtype=torch.long, device=DEV)
+    outs = []
+    for rows in (None, torch.arange(B, device=DEV)):
+        out = torch.full((B, N), 9.0, device=DEV, dtype=torch.bfloat16)
+        fused_step.decode_gemv(x, [(W, out, N, 0)], t_buf, resid=r if resid else None, x_rows=rows)
+        outs.append(out)
+    torch.cuda.synchronize()
+    exact = x.double() @ W.double().T
+    absum = x.double().abs() @ W.double().abs().T
+    bound = 0.5 * ulp_bf16(exact.float()).double() + K * 2.0 ** -24 * absum
+    if resid:
+        exact = exact + r.double()
+    for form, out in zip(("in place", "gathered"), outs):
+        b = bound + (0.5 * ulp_bf16(out.float()).double() if resid else 0.0)
+        excess = ((out.double() - exact).abs() - b).max().item()
+        assert excess <= 0.0, f"{form}: an output lies {excess:.3g} past its rounding bound"
+
+
+@pytest.mark.parametrize("B", [2, 16])
+def test_batched_gemv_norm_direct_vs_staged(B):
+    """The RMSNorm prologue of the batched GEMV: rows in place (the sum of squares over each lane's
+    fragments, the row's four lanes and the waves, the fragments scaled in registers) against the
+    same rows gathered through x_rows (staged in LDS, normalised once): the two sums of squares run
+    in different orders, so the scale may differ in its last bit and flip a rounded activation:
+    at least 99% of the outputs are equal bit for bit and the rest within 1e-3 of the largest."""
+    from dispatcher_hybrid import fused_step
+    g = torch.Generator(device=DEV).manual_seed(77 + B)
+    K, N = 1024, 3072
+    x = torch.randn(B, K, device=DEV, generator=g).to(torch.bfloat16)
+    w = torch.rand(K, device=DEV, generator=g).add(0.5).to(torch.bfloat16)
+    W = (torch.randn(N, K, device=DEV, generator=g) / K ** 0.5).to(torch.bfloat16)
+    t_buf = torch.zeros(1, dtype=torch.long, device=DEV)
+    outs = []
+    for rows in (None, torch.arange(B, device=DEV)):
+        out = torch.empty(B, N, device=DEV, dtype=torch.bfloat16)
+        fused_step.decode_gemv(x, [(W, out, N, 0)], t_buf, norm_weight=w, x_rows=rows)
+        outs.append(out)
+    torch.cuda.synchronize()
+    d = (outs[0].float() - outs[1].float()).abs()
+    assert (d == 0).double().mean().item() >= 0.99
+    assert rel_err(outs[0], outs[1]) < 1e-3
+
+
 @pytest.mark.parametrize("B", [1, 2, 16])
 def test_lm_head_shape(B):
     """A vocabulary-sized output (N = 50257, not a multiple of the row tiling; batch 2 and 16 take
