@@ -251,6 +251,51 @@ __device__ __forceinline__ uint32_t radix_kth(const uint32_t* vals, int n, int k
   return prefix << (8 * (4 - NP));
 }
 
+// The ND dwords of bytes [mis + byte0, mis + byte0 + 4 ND) of a raw buffer whose base is 16-byte
+// aligned (a row that starts mis < 16 bytes past an aligned address; mis is uniform): ND / 4 + 1
+// aligned 16-byte loads, then a funnel shift by mis bytes -- the whole-dword part Q through a uniform
+// branch (register indices stay static), the in-dword part, 8 (mis & 3) bits, by v_alignbit. Rows
+// read with 16-byte loads at their own misaligned address cost ~45% more (measured on a
+// 50257-element bf16 row, whose odd rows in a (B, V) tensor start 2 bytes off: 25-26 vs 17-18 us).
+template <int ND, int Q>
+__device__ __forceinline__ void shift_words(uint32_t (&w)[ND + 4], uint32_t sh) {
+#pragma unroll
+  for (int j = 0; j < ND; ++j) w[j] = __builtin_amdgcn_alignbit(w[j + Q + 1], w[j + Q], sh);
+}
+template <int ND>
+__device__ __forceinline__ void row_words(__amdgpu_buffer_rsrc_t r, uint32_t byte0, uint32_t mis,
+                                          uint32_t (&w)[ND + 4]) {
+  const int nload = mis != 0u ? ND / 4 + 1 : ND / 4;  // uniform: an aligned row needs no extra load
+#pragma unroll
+  for (int c = 0; c <= ND / 4; ++c) {
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (c < nload)
+      v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte0 + c * 16, 0, 0));
+    w[4 * c] = v.x;
+    w[4 * c + 1] = v.y;
+    w[4 * c + 2] = v.z;
+    w[4 * c + 3] = v.w;
+  }
+  if (mis == 0u) return;                               // uniform
+  const uint32_t sh = (mis & 3u) * 8u;
+  switch (mis >> 2) {                                  // uniform
+    case 0: shift_words<ND, 0>(w, sh); break;
+    case 1: shift_words<ND, 1>(w, sh); break;
+    case 2: shift_words<ND, 2>(w, sh); break;
+    default: shift_words<ND, 3>(w, sh); break;
+  }
+}
+// a raw buffer over row[0, V) from the 16-byte aligned address at or below row; mis: row's offset
+// from it. The range is checked per dword, so it is rounded up to whole dwords: for odd V in bf16
+// the last element shares a dword with the 2 bytes after the row (never past a page: a dword
+// holding an element is mapped whole); what those bytes hold is masked by the callers.
+template <typename T>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t aligned_row(const T* row, int V, uint32_t& mis) {
+  mis = (uint32_t)(reinterpret_cast<uintptr_t>(row) & 15u);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(reinterpret_cast<const char*>(row) - mis), (short)0,
+                                           (int)((mis + (uint32_t)V * sizeof(T) + 3u) & ~3u), 0x00020000);
+}
+
 template <typename T>
 __global__ __launch_bounds__(kST) void sample_topk_kernel(const T* logits, int64_t row_stride, int V,
                                                           float temperature, int top_k, uint64_t seed,
@@ -268,26 +313,20 @@ __global__ __launch_bounds__(kST) void sample_topk_kernel(const T* logits, int64
   const int64_t off = offset_dev ? load_uniform(offset_dev) : 0;
 
   // ---- the chunk as order keys of l = float(x) / temperature (key 0, below every number, past V).
-  // Raw buffer loads: reads past the row return zero without touching memory. The range is
-  // checked per dword, so it is rounded up to whole dwords: for odd V in bf16 the last element
-  // shares a dword with the 2 bytes after the row (never past a page: a dword holding an element
-  // is mapped whole); what those bytes hold is masked by nv below.
-  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<T*>(row), (short)0, (int)((V * (int)sizeof(T) + 3) & ~3), 0x00020000);
-  constexpr int EPC = 16 / (int)sizeof(T);             // elements per 16-byte load
+  // Raw buffer loads: reads past the row return zero without touching memory; what lies past V
+  // inside the last dword is masked by nv below.
+  uint32_t mis;
+  const __amdgpu_buffer_rsrc_t rsrc = aligned_row(row, V, mis);
+  constexpr int ND = kSPT * (int)sizeof(T) / 4;        // dwords of the thread's elements
+  uint32_t wd[ND + 4];
+  row_words<ND>(rsrc, (uint32_t)(i0 * (int)sizeof(T)), mis, wd);
   uint32_t xk[kSPT];
 #pragma unroll
-  for (int c = 0; c < kSPT / EPC; ++c) {
-    const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   rsrc, (uint32_t)(i0 * (int)sizeof(T)) + c * 16, 0, 0));
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int e = 0; e < EPC; ++e) {
-      if constexpr (sizeof(T) == 2)
-        xk[c * EPC + e] = (e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16);
-      else
-        xk[c * EPC + e] = w[e];
-    }
+  for (int j = 0; j < kSPT; ++j) {
+    if constexpr (sizeof(T) == 2)
+      xk[j] = (j & 1) ? (wd[j >> 1] & 0xffff0000u) : (wd[j >> 1] << 16);
+    else
+      xk[j] = wd[j];
   }
   uint32_t kmax = 0u;
 #pragma unroll
@@ -423,20 +462,15 @@ __global__ __launch_bounds__(kST) void sample_topk_bf16_kernel(const bf16_t* log
   const int nv = min(max(V - i0, 0), kSPT);
   const int64_t off = offset_dev ? load_uniform(offset_dev) : 0;
 
-  // ---- keys: pair i holds elements 2i (low half) and 2i + 1 (high half); key 0 past V. The
-  // range covers whole dwords (odd V: the last element's dword), as in sample_topk_kernel.
-  const __amdgpu_buffer_rsrc_t rsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(row), (short)0, (int)((V * 2 + 3) & ~3), 0x00020000);
+  // ---- keys: pair i holds elements 2i (low half) and 2i + 1 (high half); key 0 past V. The row
+  // is read from the aligned address at or below it, as in sample_topk_kernel.
+  uint32_t mis;
+  const __amdgpu_buffer_rsrc_t rsrc = aligned_row(row, V, mis);
+  uint32_t wd[NP + 4];
+  row_words<NP>(rsrc, (uint32_t)(i0 * 2), mis, wd);
   uint32_t kp[NP];
 #pragma unroll
-  for (int c = 0; c < NP / 4; ++c) {
-    const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   rsrc, (uint32_t)(i0 * 2) + c * 16, 0, 0));
-    kp[4 * c] = key16x2(v.x);
-    kp[4 * c + 1] = key16x2(v.y);
-    kp[4 * c + 2] = key16x2(v.z);
-    kp[4 * c + 3] = key16x2(v.w);
-  }
+  for (int i = 0; i < NP; ++i) kp[i] = key16x2(wd[i]);
   uint32_t kmax = 0u;
 #pragma unroll
   for (int i = 0; i < NP; ++i) {

@@ -326,6 +326,29 @@ def test_sample_history_write(dtype, k):
         assert torch.equal(hist, want), pos
 
 
+@pytest.mark.parametrize("dtype,k", [(torch.bfloat16, 50), (torch.bfloat16, None), (torch.float32, 50),
+                                     (torch.float32, 2000)])
+def test_sample_misaligned_rows(dtype, k):
+    """Rows that start off 16-byte alignment (every element offset 0..7 past it: views into a wider
+    tensor, as the odd rows of a (B, 50257) bf16 tensor are) are read from the aligned address below
+    them and shifted into place: the same draws as the same values in 16-byte aligned rows, bit for
+    bit, on the bf16 top-k kernel and the general one (no top-k, or k > 1024, or fp32)."""
+    from dispatcher_hybrid import fused_step
+    g = torch.Generator(device=DEV).manual_seed(31)
+    B, V = 8, 50257
+    big = torch.randn(B, V + 16, device=DEV, generator=g).to(dtype)
+    off = torch.full((1,), 123, dtype=torch.long, device=DEV)
+    aligned = torch.zeros(B, V + 7, device=DEV, dtype=dtype)[:, :V]
+    assert aligned.stride(0) % 8 == 0 and aligned.data_ptr() % 16 == 0
+    for o in range(8):
+        view = big[:, o:o + V]                     # row b starts (b (V + 16) + o) elements in
+        aligned.copy_(view)
+        got = fused_step.sample_tokens(view, 0.8, k, seed=9, offset=off)
+        ref = fused_step.sample_tokens(aligned, 0.8, k, seed=9, offset=off)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), o
+
+
 def test_sample_top1_and_tiny_temperature_are_argmax():
     from dispatcher_hybrid import fused_step
     g = torch.Generator(device=DEV).manual_seed(6)
