@@ -74,6 +74,9 @@ __device__ __forceinline__ void load4(const bf16_t* p, float (&o)[4]) {
 // Saturates to exactly 1.0 for x >= ~17 (1 + e^-x rounds to 1, whose reciprocal is exact) and to
 // exactly 0.0 for x <= -~89 (e^-x overflows to +inf).
 __device__ __forceinline__ float dh_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+// SiLU at the eager bf16 path's precision: x / (1 + e^-x) with the library exp and an IEEE divide,
+// the SwiGLU activation of the parallel path (dh_silu_mul and the fused SwiGLU GEMM epilogue)
+__device__ __forceinline__ float dh_silu_exact(float x) { return x / (1.0f + expf(-x)); }
 
 // DPP lane move of a float: lanes in the rows of ROWMASK read the lane CTRL selects, others get 0
 template <int CTRL, int ROWMASK>

@@ -239,6 +239,38 @@ __device__ __forceinline__ void store_tile_x4(const GemmArgs& a, const f32x4 (&a
   }
 }
 
+// SwiGLU output of a bf16 tile (the fused gate/up GEMM): MFMA column tiles j < TN/2 of a wave hold
+// W_gate rows and tiles j + TN/2 the W_up rows of the same output features, so lane (r, g) holds
+// gate and up of features f .. f + 3 (f = the wave's first feature + 16 j + 4 g) for output row r
+// of each row tile and writes h = round(round(silu(round(gate))) * round(up)) as 8 bytes: the eager
+// path's rounding points (two GEMM outputs in bf16, silu rounded, the product rounded) and
+// dh_silu_mul's arithmetic.
+template <int TM, int TN, int WGM>
+__device__ __forceinline__ void store_tile_swiglu(const GemmArgs& a, const f32x4 (&acc)[TN][TM], int m0, int n0,
+                                                  int wm, int wn, int r, int g) {
+  static_assert(TN % 2 == 0, "gate and up column tiles in pairs");
+  bf16_t* o = (bf16_t*)a.out[0];
+  const int64_t ld = a.ldo[0];
+#pragma unroll
+  for (int p = 0; p < TN / 2; ++p) {
+    const int f = n0 / 2 + wn * 8 * TN + p * 16 + 4 * g;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm * 16 * TM + i * 16 + r;
+      const f32x4& G = acc[p][i];
+      const f32x4& U = acc[p + TN / 2][i];
+      float h[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        h[e] = Elem<bf16_t>::round(Elem<bf16_t>::round(dh_silu_exact(Elem<bf16_t>::round(G[e]))) *
+                                   Elem<bf16_t>::round(U[e]));
+      const uint32_t lo = (uint32_t)f32_to_bf16(h[0]) | ((uint32_t)f32_to_bf16(h[1]) << 16);
+      const uint32_t hi = (uint32_t)f32_to_bf16(h[2]) | ((uint32_t)f32_to_bf16(h[3]) << 16);
+      if (m < a.M && f < a.N[0]) *reinterpret_cast<uint2*>(o + (int64_t)m * ld + f) = make_uint2(lo, hi);
+    }
+  }
+}
+
 // Fragment ping-pong variant (bf16, 2 LDS stages): the MFMA operands of a K tile's two 32-k steps
 // live in two register sets, so the LDS reads of one step are in flight while the MFMAs of the other
 // run, across the K-tile boundary too: the barrier sits between the two steps' MFMAs. Row swizzle:
@@ -258,7 +290,10 @@ __device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds) : "memory");
 }
 
-template <int TM, int TN, int WGM, int WGN>
+// SWI: the fused SwiGLU GEMM (segments 0 = W_gate, 1 = W_up, both N[0] rows): column tile nt covers
+// output features [nt BN / 2, (nt + 1) BN / 2), each wave's 16 TN columns the gate rows then the
+// up rows of its 8 TN features, and the epilogue is store_tile_swiglu.
+template <int TM, int TN, int WGM, int WGN, bool SWI>
 __global__ __launch_bounds__(64 * WGM * WGN) void proj_gemm_pp_kernel(GemmArgs a) {
   typedef bf16_t T;
   typedef Frag<T> F;
@@ -323,13 +358,24 @@ __global__ __launch_bounds__(64 * WGM * WGN) void proj_gemm_pp_kernel(GemmArgs a
     for (int q = 0; q < GW; ++q) {
       const int R = 8 * (NW * q + wave) + (lane >> 3);
       int loc;
-      const int n = min(n0 + R, a.Ntot - 1);
-      wsg[q] = __builtin_amdgcn_readfirstlane(seg_of(a, n, loc));
+      if constexpr (SWI) {
+        // tile row R = wave column wc, MFMA column tile j, row rr: gate (j < TN/2) or up row of
+        // feature n0/2 + 8 TN wc + 16 (j mod TN/2) + rr (an 8-row group lies in one 16-row tile)
+        const int wc = R / (16 * TN), j = (R / 16) % TN, rr = R % 16;
+        loc = min(n0 / 2 + 8 * TN * wc + 16 * (j % (TN / 2)) + rr, a.N[0] - 1);
+        wsg[q] = __builtin_amdgcn_readfirstlane(j < TN / 2 ? 0 : 1);
+      } else {
+        const int n = min(n0 + R, a.Ntot - 1);
+        wsg[q] = __builtin_amdgcn_readfirstlane(seg_of(a, n, loc));
+      }
       wo[q] = ((uint32_t)loc * (uint32_t)a.K + (uint32_t)(((lane & 7) ^ swz2(R)) * 8)) * 2u;
     }
     __syncthreads();                                   // the previous tile's LDS reads are done
     issue(0, 0);
-    if (pm0 >= 0) store_tile_x4<TM, TN, WGM>(a, acc, pm0, pn0, wm, wn, r, g);   // under K tile 0's loads
+    if (pm0 >= 0) {                                    // under K tile 0's loads
+      if constexpr (SWI) store_tile_swiglu<TM, TN, WGM>(a, acc, pm0, pn0, wm, wn, r, g);
+      else store_tile_x4<TM, TN, WGM>(a, acc, pm0, pn0, wm, wn, r, g);
+    }
     pm0 = m0;
     pn0 = n0;
 #pragma unroll
@@ -357,29 +403,61 @@ __global__ __launch_bounds__(64 * WGM * WGN) void proj_gemm_pp_kernel(GemmArgs a
     }
     wait_vm<0>();                                      // repeated tail loads land before LDS is reused
   }
-  if (pm0 >= 0) store_tile_x4<TM, TN, WGM>(a, acc, pm0, pn0, wm, wn, r, g);
+  if (pm0 >= 0) {
+    if constexpr (SWI) store_tile_swiglu<TM, TN, WGM>(a, acc, pm0, pn0, wm, wn, r, g);
+    else store_tile_x4<TM, TN, WGM>(a, acc, pm0, pn0, wm, wn, r, g);
+  }
 }
 
 bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
 
-constexpr int64_t kWideMinTiles = 256;    // 256 x 256 tiles: one per CU at least
-constexpr int64_t kWideGrid = 256;        // persistent workgroups: one per CU (128 KB of LDS each)
-constexpr int64_t kSmallMinTiles = 768;   // below the 256 x 256 launch: three tiles per CU at least,
-constexpr int64_t kMidMinTiles = 512;     // two for the 128 x 128 tiles
-
 // One workgroup per tile of the ping-pong kernel with 4 waves (BM = 32 TM, BN = 32 TN).
-template <int TM, int TN>
+template <int TM, int TN, bool SWI>
 int launch_pp_tiles(GemmArgs& a, hipStream_t s, const char* who) {
   constexpr int BM = 32 * TM, BN = 32 * TN;
   a.mtiles = (a.M + BM - 1) / BM;
   a.ntiles = (a.Ntot + BN - 1) / BN;
   const int64_t nvirt = (int64_t)((a.mtiles + 7) / 8) * 8 * a.ntiles;
   DH_REQUIRE(nvirt < (1ll << 31), DH_ERR_UNSUPPORTED_SHAPE, "%s: M=%d too large", who, a.M);
-  proj_gemm_pp_kernel<TM, TN, 2, 2><<<dim3((unsigned)nvirt), dim3(256), 0, s>>>(a);
+  proj_gemm_pp_kernel<TM, TN, 2, 2, SWI><<<dim3((unsigned)nvirt), dim3(256), 0, s>>>(a);
   return dh_check_launch(who);
 }
 
 int64_t tiles_of(int M, int N, int BM, int BN) { return (int64_t)((M + BM - 1) / BM) * ((N + BN - 1) / BN); }
+
+constexpr int64_t kWideMinTiles = 160;    // 256 x 256 tiles from ~0.6 per CU (persistent, one per CU)
+constexpr int64_t kWideGrid = 256;        // persistent workgroups: one per CU (128 KB of LDS each)
+
+// The ping-pong kernel's tile for M x Ntot (Ntot: concatenated output columns; the fused SwiGLU
+// GEMM's gate and up rows count both). Measured on MI355X in captured graphs, bf16, K = 1024
+// unless noted (us; 64x64 / 64x128 / 128x64 / 128x128 / 256x256):
+//   M = 1024  N = 3072          13.6 / 14.7 / 14.3 / 16.4 / 28.0
+//   M = 1024  N = 2 x 2816      28.4 / 21.6 / 21.5 / 21.7 / 28.8
+//   M = 2048  N = 3072          26.1 / 19.6 / 19.8 / 19.6 / 27.8
+//   M = 2048  N = 2 x 2816      51.4 / 42.4 / 39.9 / 37.1 / 30.6
+//   M = 4096  N = 3072          49.3 / 40.1 / 38.9 / 36.9 / 30.0
+//   M = 4096  N = 1024          14.7 / 13.3 / 12.7 / 15.7 / 26.0
+//   M = 4096  N = 1024 K = 2816 38.8 / 30.0 / 29.8 / 34.1 / 62.3
+// i.e. 256 x 256 tiles from ~160 of them, else 64 x 64 while there are at most 768 of those (three
+// per CU), else the largest count of 64 x 128 (>= 768) or 128 x 64 (>= 512) tiles, else 128 x 128.
+// Every form sums the same products in the same k order: outputs are bit-identical across forms.
+template <bool SWI>
+int launch_wide(GemmArgs& a, hipStream_t s, const char* who) {
+  const int M = a.M, N = a.Ntot;
+  if (tiles_of(M, N, 256, 256) >= kWideMinTiles) {
+    a.mtiles = (M + 255) / 256;
+    a.ntiles = (N + 255) / 256;
+    const int64_t nvirt = (int64_t)((a.mtiles + 7) / 8) * 8 * a.ntiles;
+    DH_REQUIRE(nvirt < (1ll << 31), DH_ERR_UNSUPPORTED_SHAPE, "%s: M=%d too large", who, M);
+    const unsigned grid = (unsigned)(nvirt < kWideGrid ? nvirt : kWideGrid);
+    proj_gemm_pp_kernel<8, 4, 2, 4, SWI><<<dim3(grid), dim3(512), 0, s>>>(a);
+    return dh_check_launch(who);
+  }
+  if (tiles_of(M, N, 64, 64) <= 768) return launch_pp_tiles<2, 2, SWI>(a, s, who);
+  if (tiles_of(M, N, 64, 128) >= 768) return launch_pp_tiles<2, 4, SWI>(a, s, who);
+  if (tiles_of(M, N, 128, 64) >= 512) return launch_pp_tiles<4, 2, SWI>(a, s, who);
+  return launch_pp_tiles<4, 4, SWI>(a, s, who);
+}
 
 }  // namespace
 
@@ -415,33 +493,13 @@ extern "C" int dh_proj_gemm(int dtype, const void* X, int64_t ldx, int M, int K,
   }
   a.Ntot = total;
   hipStream_t s = (hipStream_t)stream;
-  // bf16 launches with at least one 256 x 256 output tile per CU take the persistent 8-wave kernel
-  // (32-bit operand offsets, segment widths multiples of 8, 16-byte aligned output rows), smaller
-  // bf16 launches that meet the same conditions its 4-wave form; the rest (fp32 among them) the
-  // 128 x 128 register-staged kernel.
+  // bf16 launches whose operands and outputs meet the ping-pong kernels' conditions (32-bit operand
+  // offsets, segment widths multiples of 8, 16-byte aligned output rows) take them (launch_wide);
+  // the rest (fp32 among them) the 128 x 128 register-staged kernel.
   bool wide = dtype == DH_BF16 && (int64_t)M * ldx * esz < (1ll << 31);
   for (int i = 0; i < nseg; ++i)
     wide = wide && N[i] % 8 == 0 && (int64_t)N[i] * K * esz < (1ll << 31) && ldo[i] % 8 == 0 && aligned(out[i], 16);
-  const int64_t tiles256 = (int64_t)((M + 255) / 256) * ((total + 255) / 256);
-  if (wide && tiles256 >= kWideMinTiles) {
-    a.mtiles = (M + 255) / 256;
-    a.ntiles = (total + 255) / 256;
-    const int64_t nvirt = (int64_t)((a.mtiles + 7) / 8) * 8 * a.ntiles;
-    DH_REQUIRE(nvirt < (1ll << 31), DH_ERR_UNSUPPORTED_SHAPE, "%s: M=%d too large", who, M);
-    const unsigned grid = (unsigned)(nvirt < kWideGrid ? nvirt : kWideGrid);
-    proj_gemm_pp_kernel<8, 4, 2, 4><<<dim3(grid), dim3(512), 0, s>>>(a);
-    return dh_check_launch(who);
-  }
-  // Fewer rows: the same ping-pong kernel, 4 waves, with 128 x 128 tiles from two tiles per CU,
-  // else 64 x 128 from three, else 64 x 64 (measured on MI355X at N = 3072, K = 1024:
-  // M = 1024 12.5 us with 64 x 64 against 18.8 for the 128 x 128 register-staged kernel; M = 2048
-  // 19.0 us with 64 x 128 against 27.0; M = 4096 35.6 with 128 x 128 against 40.3). Same sums in the
-  // same k order: the outputs are bit-identical.
-  if (wide) {
-    if (tiles_of(M, total, 128, 128) >= kMidMinTiles) return launch_pp_tiles<4, 4>(a, s, who);
-    if (tiles_of(M, total, 64, 128) >= kSmallMinTiles) return launch_pp_tiles<2, 4>(a, s, who);
-    return launch_pp_tiles<2, 2>(a, s, who);
-  }
+  if (wide) return launch_wide<false>(a, s, who);
   a.mtiles = (M + kBM - 1) / kBM;
   a.ntiles = (total + kBN - 1) / kBN;
   const int64_t grid = (int64_t)((a.mtiles + 7) / 8) * 8 * a.ntiles;
@@ -453,3 +511,34 @@ extern "C" int dh_proj_gemm(int dtype, const void* X, int64_t ldx, int M, int K,
   return dh_check_launch(who);
 }
 
+// out[m, f] = round(round(silu(round(X[m] . Wg[f]))) * round(X[m] . Wu[f])): a SwiGLU layer's
+// gate and up GEMMs and its activation (reference dispatcher_hybrid/modeling_dispatcher.py:188-197,
+// F.silu(linear_gate(h)) * linear_up(h)) as one launch of the ping-pong kernel over the 2N
+// concatenated weight rows, bf16 only. Without it: two GEMMs writing gate and up to memory, then
+// dh_silu_mul reading them back.
+extern "C" int dh_proj_gemm_swiglu(int dtype, const void* X, int64_t ldx, int M, int K, const void* Wg,
+                                   const void* Wu, int N, void* out, int64_t ldo, void* stream) {
+  const char* who = "dh_proj_gemm_swiglu";
+  DH_REQUIRE(dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d (bf16 only)", who, dtype);
+  DH_REQUIRE(X && Wg && Wu && out, DH_ERR_INVALID_ARG, "%s: null pointer argument", who);
+  DH_REQUIRE(M >= 1 && K >= 64 && K % 64 == 0 && N >= 8 && N % 8 == 0, DH_ERR_UNSUPPORTED_SHAPE,
+             "%s: M=%d K=%d N=%d (K a positive multiple of 64, N of 8)", who, M, K, N);
+  DH_REQUIRE(ldx >= K && ldx % 8 == 0 && aligned(X, 16) && aligned(Wg, 16) && aligned(Wu, 16) &&
+                 ldo >= N && ldo % 8 == 0 && aligned(out, 16),
+             DH_ERR_INVALID_ARG, "%s: operands need 16-byte aligned rows (ldx >= K, ldo >= N)", who);
+  DH_REQUIRE((int64_t)M * ldx * 2 < (1ll << 31) && (int64_t)N * K * 2 < (1ll << 31), DH_ERR_UNSUPPORTED_SHAPE,
+             "%s: operands past 2 GB", who);
+  GemmArgs a{};
+  a.X = X;
+  a.ldx = ldx;
+  a.nseg = 2;
+  a.M = M;
+  a.K = K;
+  a.W[0] = Wg;
+  a.W[1] = Wu;
+  a.out[0] = out;
+  a.ldo[0] = ldo;
+  a.N[0] = a.N[1] = N;
+  a.Ntot = 2 * N;
+  return launch_wide<true>(a, (hipStream_t)stream, who);
+}

@@ -384,6 +384,63 @@ def input_projections(x, mixer):
     return tuple(l(x) for l in lins)
 
 
+# Rows up to which one dh_proj_gemm launch beats the library for an attention layer's q, k, v
+# (three 1024-wide nn.Linear GEMMs) and for a single 1024 x 1024 output projection (the mixer's and
+# attention's linear_out), measured on MI355X in captured graphs (bf16, K = 1024; us, ours against
+# the library): q, k, v 13.3 / 23.8 at 1024 rows, 19.6 / 29.7 at 2048, 30.0 / 37.4 at 4096, 60 / 59
+# at 8192; linear_out 6.5 / 7.9 at 1024, 7.8 / 9.7 at 2048, 12.7 / 12.4 at 4096.
+QKV_GEMM_MAX_ROWS = 4096
+OUT_GEMM_MAX_ROWS = 2048
+
+
+def project(x, linears, max_rows):
+    """[l(x) for l in linears] (bias-free nn.Linear layers over the same input) as one dh_proj_gemm
+    launch when x has at most max_rows rows and the kernel takes the shapes (projections_fit), else
+    the library calls. Inference only."""
+    rows = x.numel() // max(x.shape[-1], 1)
+    if rows <= max_rows and projections_fit(x, linears):
+        return fused_projections(x, [l.weight for l in linears])
+    return [l(x) for l in linears]
+
+
+def swiglu_fits(x, gate, up):
+    """True when dh_proj_gemm_swiglu takes silu(gate(x)) * up(x) for these bias-free nn.Linear
+    layers: a bf16 CUDA input with 16-byte aligned rows, bf16 contiguous weights of one shape, K a
+    multiple of 64 and N of 8."""
+    K = x.shape[-1]
+    return (x.is_cuda and x.dtype == torch.bfloat16 and gate.bias is None and up.bias is None
+            and gate.weight.dtype == up.weight.dtype == torch.bfloat16
+            and gate.weight.shape == up.weight.shape and gate.weight.shape[1] == K
+            and gate.weight.is_contiguous() and up.weight.is_contiguous()
+            and K % 64 == 0 and gate.weight.shape[0] % 8 == 0)
+
+
+def fused_swiglu(x, w_gate, w_up):
+    """silu(x . w_gate^T) * (x . w_up^T) as ONE launch (``dh_proj_gemm_swiglu``): the SwiGLU block's
+    gate and up GEMMs and its activation (reference dispatcher_hybrid/modeling_dispatcher.py:188-197)
+    at the eager rounding points -- both GEMM outputs rounded to bf16, silu rounded, the product
+    rounded -- without the two GEMM outputs ever reaching memory. x: (..., K) bf16; w_gate, w_up:
+    (N, K) bf16. Returns (..., N). Inference only (no autograd)."""
+    _hip.require_gpu(x, "fused_swiglu")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
+        x2 = x2.clone(memory_format=torch.contiguous_format)      # a fresh, aligned copy
+    N = w_gate.shape[0]
+    if (x.dtype != torch.bfloat16 or w_gate.dtype != torch.bfloat16 or w_up.dtype != torch.bfloat16
+            or w_gate.shape != (N, K) or w_up.shape != (N, K) or not w_gate.is_contiguous()
+            or not w_up.is_contiguous()):
+        raise ValueError("fused_swiglu: bf16 x (..., K) and contiguous bf16 (N, K) gate and up weights")
+    out = torch.empty(*x.shape[:-1], N, device=x.device, dtype=x.dtype)
+    M = x2.shape[0]
+    if M == 0:
+        return out
+    st = _hip.lib.dh_proj_gemm_swiglu(_hip.DH_BF16, _hip.ptr(x2), x2.stride(0), M, K, _hip.ptr(w_gate),
+                                      _hip.ptr(w_up), N, _hip.ptr(out), N, _hip.stream_handle(x.device))
+    _hip.check(st, "dh_proj_gemm_swiglu")
+    return out
+
+
 def silu_mul(gate, up, out=None):
     """silu(gate) * up in one launch (``dh_silu_mul``): the SwiGLU activation of reference
     dispatcher_hybrid/modeling_dispatcher.py:197, F.silu(linear_gate(h)) * linear_up(h), at its

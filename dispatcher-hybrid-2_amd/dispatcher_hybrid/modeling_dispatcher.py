@@ -182,6 +182,8 @@ class DispatcherMixer(nn.Module):
         else:
             # inference: activated gates written head-major, then the level scan (two launches)
             V = fused_gate_scan(A, Bs, Wi, Wf, Wr, bi, bf, br, n_lv, m3, V0, H)
+            from .fused_gates import OUT_GEMM_MAX_ROWS, project
+            return project(V, [self.linear_out], OUT_GEMM_MAX_ROWS)[0]
         return self.linear_out(V)
 
 
@@ -257,11 +259,13 @@ class WindowAttention(nn.Module):
         if self.use_fused and not torch.is_grad_enabled() and x.is_cuda:
             from . import fused_attention as fa
             if fa.supported(x.dtype, self.head_dim):
-                # RoPE, banded scores, softmax and the value average in one launch, (B, T, d) in/out
+                from .fused_gates import OUT_GEMM_MAX_ROWS, QKV_GEMM_MAX_ROWS, project
+                # q, k, v as one GEMM launch (up to QKV_GEMM_MAX_ROWS rows); RoPE, banded scores,
+                # softmax and the value average in one launch, (B, T, d) in/out
+                q, k, v = project(x, [self.linear_q, self.linear_k, self.linear_v], QKV_GEMM_MAX_ROWS)
                 cos, sin = self.rope_tables(T, x.device, x.dtype)
-                y = fa.window_attention(self.linear_q(x), self.linear_k(x), self.linear_v(x), cos, sin,
-                                        self.num_heads, self.band(T))
-                return self.linear_out(y)
+                y = fa.window_attention(q, k, v, cos, sin, self.num_heads, self.band(T))
+                return project(y, [self.linear_out], OUT_GEMM_MAX_ROWS)[0]
         return self._forward_eager(x)
 
     def band(self, T):
@@ -284,10 +288,10 @@ class WindowAttention(nn.Module):
 
 class SwiGLU(nn.Module):
     """linear_down(silu(linear_gate(h)) * linear_up(h)) (reference modeling_dispatcher.py:188-197).
-    With use_fused (set by enable_fused_gates) and no autograd, the activation is one dh_silu_mul
-    launch at the eager rounding points instead of a SiLU and a product launch. (linear_gate and
-    linear_up as one dh_proj_gemm launch measured slower in the graphed C2 forward than the two
-    library GEMMs: 2.245 vs 2.217 ms.)"""
+    With use_fused (set by enable_fused_gates) and no autograd, bf16 layers run linear_gate,
+    linear_up and the activation as one dh_proj_gemm_swiglu launch (the two GEMM outputs never
+    reach memory), other fp32/bf16 layers the two GEMMs and one dh_silu_mul launch; both at the
+    eager rounding points."""
 
     use_fused = False
 
@@ -301,7 +305,9 @@ class SwiGLU(nn.Module):
     def forward(self, h):
         if (self.use_fused and h.is_cuda and not torch.is_grad_enabled()
                 and h.dtype in (torch.float32, torch.bfloat16)):                   # dh_silu_mul's dtypes
-            from .fused_gates import silu_mul
+            from .fused_gates import fused_swiglu, silu_mul, swiglu_fits
+            if swiglu_fits(h, self.linear_gate, self.linear_up):
+                return self.linear_down(fused_swiglu(h, self.linear_gate.weight, self.linear_up.weight))
             g = self.linear_gate(h)
             return self.linear_down(silu_mul(g, self.linear_up(h), out=g))
         return self.linear_down(F.silu(self.linear_gate(h)) * self.linear_up(h))

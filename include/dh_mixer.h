@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 16
+#define DH_ABI_VERSION 17
 
 enum dh_status {
   DH_OK = 0,
@@ -141,6 +141,20 @@ int dh_level_scan_fwd(int dtype, const void* pre_i, const void* pre_f, const voi
  * 16-byte aligned (out may alias gate or up). n == 0 is a no-op.
  */
 int dh_silu_mul(int dtype, const void* gate, const void* up, void* out, int64_t n, void* stream);
+
+/*
+ * The feed-forward block's gate and up projections and its SwiGLU activation as one MFMA GEMM:
+ *   out[m*ldo + f] = round(round(silu(round(sum_k X[m*ldx + k] Wg[f*K + k])))
+ *                          * round(sum_k X[m*ldx + k] Wu[f*K + k]))            f < N, m < M
+ * Replaces silu(linear_gate(h)) * linear_up(h) of reference
+ * dispatcher_hybrid/modeling_dispatcher.py:188-197 (SwiGLU.forward): the two GEMMs, their bf16
+ * outputs in memory and the activation pass, with the eager rounding points (each GEMM output
+ * rounded to bf16, silu rounded, the product rounded) and dh_silu_mul's arithmetic. bf16 only;
+ * Wg, Wu (N, K) row-major (nn.Linear weight layout); K a multiple of 64, N of 8; X, Wg, Wu and out
+ * 16-byte aligned with row strides ldx >= K and ldo >= N multiples of 8 elements.
+ */
+int dh_proj_gemm_swiglu(int dtype, const void* X, int64_t ldx, int M, int K, const void* Wg, const void* Wu,
+                        int N, void* out, int64_t ldo, void* stream);
 
 /*
  * Residual add + RMSNorm over `rows` rows of d elements (row-contiguous, 16-byte aligned):

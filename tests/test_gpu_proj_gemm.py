@@ -12,17 +12,19 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 CASES = [
-    # M, K, segment widths
+    # M, K, segment widths (bf16 tile form in the comment; fp32 takes the register-staged kernel)
     (1, 64, [64]),
     (130, 128, [128, 128, 128]),          # ragged M, three segments
-    (1000, 256, [64, 192, 128]),          # segments that straddle the 128-column tiles
-    (4096, 1024, [1024, 1024, 1024]),     # the released mixer (d = gh = 1024): 128 x 128 tiles
-    (3840, 1024, [1024, 1024, 1024]),     # the C3 decoder prefill: 128 x 128 tiles from two per CU
+    (1000, 256, [64, 192, 128]),          # segments that straddle the column tiles
+    (1024, 1024, [1024, 1024, 1024]),     # the C2 layer (T = 1024): 64 x 64 tiles (768)
     (2048, 1024, [1024, 1024, 1024]),     # 64 x 128 tiles
     (2000, 512, [1000, 1024, 1048]),      # 64 x 128 tiles, ragged rows, segments straddling tiles
-    (1024, 1024, [1024, 1024, 1024]),     # the C2 layer (T = 1024): 64 x 64 tiles
+    (4096, 1024, [1024]),                 # 128 x 64 tiles (an out-projection)
+    (1600, 1024, [2048]),                 # 128 x 128 tiles
     (257, 1024, [1024]),
-    # bf16 launches with >= 256 output tiles of 256 x 256 take the persistent 8-wave kernel:
+    # bf16 launches with >= 160 output tiles of 256 x 256 take the persistent 8-wave kernel:
+    (4096, 1024, [1024, 1024, 1024]),     # the released mixer (d = gh = 1024) at 4096 rows
+    (3840, 1024, [1024, 1024, 1024]),     # the C3 decoder prefill
     (6000, 1024, [1000, 1024, 1048]),     # ragged rows, segments straddling its 256-column tiles
     (9000, 512, [3000]),                  # one segment, width not a multiple of 256
     (32768, 1024, [1024, 1024, 1024]),    # the C5 layer: b = 8, T = 4096 rows
@@ -67,8 +69,8 @@ def test_proj_gemm_batched_view_and_rejects():
 
 def test_proj_gemm_rows_independent_of_tile_kernel():
     """A row's outputs do not depend on the launch's row count: the 256 x 256 persistent kernel and
-    the 128 x 128, 64 x 128 and 64 x 64 tile forms picked for fewer rows form the same sums in the
-    same k order, so the first rows of a 9000-row launch equal those of shorter launches bit for bit."""
+    the 64 x 128 and 64 x 64 tile forms picked for fewer rows form the same sums in the same k
+    order, so the first rows of a 9000-row launch equal those of shorter launches bit for bit."""
     from dispatcher_hybrid.fused_gates import fused_projections
     g = torch.Generator(device=DEV).manual_seed(11)
     x = torch.randn(9000, 1024, device=DEV, generator=g).to(torch.bfloat16)
@@ -78,3 +80,88 @@ def test_proj_gemm_rows_independent_of_tile_kernel():
         part = fused_projections(x[:M].contiguous(), Ws)
         for o, f in zip(part, full):
             assert torch.equal(o, f[:M]), M
+
+
+# ---- dh_proj_gemm_swiglu: SwiGLU's gate and up GEMMs and its activation in one launch
+
+SWIGLU_CASES = [
+    # M, K, N (tile form of the 2N concatenated rows)
+    (1, 64, 8),              # 64 x 64 tiles, one row, a partial feature tile
+    (100, 128, 96),          # 64 x 64, ragged
+    (1024, 1024, 2816),      # the C2 feed-forward (T = 1024): 128 x 64 tiles
+    (1600, 1024, 1024),      # 128 x 128 tiles
+    (2048, 1024, 2816),      # 256 x 256 persistent kernel
+    (5000, 512, 1000),       # persistent kernel, ragged rows, N not a multiple of the tile's 128 features
+    (1000, 1024, 2056),      # 64 x 128 tiles, a partial last feature tile
+]
+
+
+def _swiglu_ref(x, wg, wu):
+    """The unfused product path: the two GEMMs as one dh_proj_gemm launch (same sums, same k order)
+    and dh_silu_mul at the eager rounding points."""
+    from dispatcher_hybrid.fused_gates import fused_projections, silu_mul
+    g, u = fused_projections(x, [wg, wu])
+    return silu_mul(g, u)
+
+
+@pytest.mark.parametrize("case", SWIGLU_CASES)
+def test_proj_gemm_swiglu_equals_gemms_then_silu_mul(case):
+    """Bit-identical to the two GEMMs followed by dh_silu_mul, and within the bf16 rounding bound of
+    a float64 silu(x Wg^T) * (x Wu^T) (reference modeling_dispatcher.py:197)."""
+    from dispatcher_hybrid.fused_gates import fused_swiglu
+    M, K, N = case
+    print(f"proj_gemm_swiglu M={M} K={K} N={N}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(M * 7 + N)
+    x = torch.randn(M, K, device=DEV, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(N, K, device=DEV, generator=g) / K ** 0.5).to(torch.bfloat16)
+    wu = (torch.randn(N, K, device=DEV, generator=g) / K ** 0.5).to(torch.bfloat16)
+    h = fused_swiglu(x, wg, wu)
+    ref = _swiglu_ref(x, wg, wu)
+    torch.cuda.synchronize()
+    assert h.shape == (M, N) and h.dtype == torch.bfloat16
+    assert torch.equal(h, ref)
+    gd, ud = x.double() @ wg.double().T, x.double() @ wu.double().T
+    exact = torch.nn.functional.silu(gd) * ud
+    # four bf16 roundings (gate, up, silu, product), each 2^-8 relative, plus the fp32 sums
+    bound = exact.abs() * 4 * 2.0 ** -8 + (gd.abs() + ud.abs()) * 2.0 ** -8 * (ud.abs() + gd.abs()) + 1e-3
+    assert bool(((h.double() - exact).abs() <= bound).all())
+
+
+def test_proj_gemm_swiglu_rows_independent_of_tile_kernel():
+    """As the plain GEMM: the first rows of a 5000-row launch (persistent kernel) equal those of
+    shorter launches (128 x 64, 128 x 128 and 64 x 64 tiles) bit for bit."""
+    from dispatcher_hybrid.fused_gates import fused_swiglu
+    g = torch.Generator(device=DEV).manual_seed(13)
+    x = torch.randn(5000, 1024, device=DEV, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(2816, 1024, device=DEV, generator=g) / 32).to(torch.bfloat16)
+    wu = (torch.randn(2816, 1024, device=DEV, generator=g) / 32).to(torch.bfloat16)
+    full = fused_swiglu(x, wg, wu)
+    for M in (2048, 1024, 300, 1):
+        assert torch.equal(fused_swiglu(x[:M].contiguous(), wg, wu), full[:M]), M
+
+
+def test_proj_gemm_swiglu_batched_view_and_rejects():
+    from dispatcher_hybrid import _hip
+    from dispatcher_hybrid.fused_gates import fused_swiglu
+    g = torch.Generator(device=DEV).manual_seed(17)
+    x = torch.randn(2, 300, 128, device=DEV, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(96, 128, device=DEV, generator=g) / 12).to(torch.bfloat16)
+    wu = (torch.randn(96, 128, device=DEV, generator=g) / 12).to(torch.bfloat16)
+    h = fused_swiglu(x, wg, wu)
+    assert h.shape == (2, 300, 96)
+    assert torch.equal(h.view(600, 96), _swiglu_ref(x.view(600, 128), wg, wu))
+    # a row-misaligned view of x is copied, not rejected
+    buf = torch.zeros(600 * 128 + 1, device=DEV, dtype=torch.bfloat16)
+    xv = buf[1:].view(600, 128)
+    xv.copy_(x.view(600, 128))
+    assert torch.equal(fused_swiglu(xv, wg, wu), h.view(600, 96))
+    with pytest.raises(ValueError):
+        fused_swiglu(x.float(), wg.float(), wu.float())                   # bf16 only
+    with pytest.raises(ValueError):
+        fused_swiglu(x, wg, wu[:64])                                       # gate / up shapes differ
+    # the C-ABI's own checks: N a multiple of 8, fp32 refused
+    null = _hip.ptr(h)
+    assert _hip.lib.dh_proj_gemm_swiglu(_hip.DH_BF16, _hip.ptr(x), 128, 600, 128, _hip.ptr(wg), _hip.ptr(wu), 12,
+                                        null, 96, _hip.stream_handle(x.device)) != 0
+    assert _hip.lib.dh_proj_gemm_swiglu(_hip.DH_F32, _hip.ptr(x), 128, 600, 128, _hip.ptr(wg), _hip.ptr(wu), 96,
+                                        null, 96, _hip.stream_handle(x.device)) != 0
