@@ -251,8 +251,13 @@ __global__ __launch_bounds__(kThreads) void level_scan_kernel(ScanArgs a) {
 template <typename T, int C, int PPT, int MODE>
 __global__ __launch_bounds__(1024) void level_scan_wide_kernel(ScanArgs a) {
   constexpr int NT = 1024, TC = PPT * NT;
-  __shared__ float2 vs[C / 2][TC];
-  __shared__ float rs[TC];
+  // Double-buffered when two copies fit the 160 KB of LDS (T <= 2048): level l exchanges through
+  // buffer l % 2, so the barrier after its reads is not needed (the next level writes the other
+  // buffer, and a buffer is written again only after the following level's barrier). T = 2048:
+  // 15.4 -> 14.0 us per launch. At T = 4096 (144 KB) one buffer and two barriers per level.
+  constexpr int NB = (TC * (C * 4 + 4) * 2 <= 160 * 1024) ? 2 : 1;
+  __shared__ float2 vs_[NB][C / 2][TC];
+  __shared__ float rs_[NB][TC];
   const int nchunks = a.hd / C;
   const int ngroups = a.b * a.H;
   const int bid = blockIdx.x;
@@ -290,21 +295,27 @@ __global__ __launch_bounds__(1024) void level_scan_wide_kernel(ScanArgs a) {
     goff[j] = tc * (uint32_t)a.spt;
     moff[j] = tc * (uint32_t)a.smt;
   }
-  uint32_t ri[PPT], rf[PPT], rr[PPT], rm[PPT];
-  auto fetch = [&](int l) {
+  struct GSet { uint32_t i[PPT], f[PPT], r[PPT], m[PPT]; };
+  auto fetch = [&](int l, GSet& g) {
     const T* li = pi + (int64_t)l * a.spl;
     const T* lf = pf + (int64_t)l * a.spl;
     const T* lr = pr + (int64_t)l * a.spl;
     const T* lm = mk + (int64_t)l * a.sml;
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-      ri[j] = Raw<T>::load(li + goff[j]);
-      rf[j] = Raw<T>::load(lf + goff[j]);
-      rr[j] = Raw<T>::load(lr + goff[j]);
-      if (MODE == kPreMask) rm[j] = Raw<T>::load(lm + moff[j]);
+      g.i[j] = Raw<T>::load(li + goff[j]);
+      g.f[j] = Raw<T>::load(lf + goff[j]);
+      g.r[j] = Raw<T>::load(lr + goff[j]);
+      if (MODE == kPreMask) g.m[j] = Raw<T>::load(lm + moff[j]);
     }
   };
-  fetch(0);
+  // Two register sets of gates: level l reads set l % 2, then requests level l + 2 into it, so a
+  // level's gates are in flight for two levels of work (one level ahead left the loads' round trip
+  // exposed: T = 1024 9.0 -> 8.0 us per launch; three or four sets measured slower, C5 143 / 194 us
+  // against 120, from the registers they take).
+  GSet gs0, gs1;
+  fetch(0, gs0);
+  fetch(min(1, a.n_lv - 1), gs1);
 
   const int64_t d = (int64_t)a.H * a.hd;
   auto write_slab = [&](int j) {
@@ -320,7 +331,11 @@ __global__ __launch_bounds__(1024) void level_scan_wide_kernel(ScanArgs a) {
   };
   write_slab(0);
 
-  for (int l = 0; l < a.n_lv; ++l) {
+  auto level = [&](int l, GSet& g) {
+    const uint32_t (&ri)[PPT] = g.i;
+    const uint32_t (&rf)[PPT] = g.f;
+    const uint32_t (&rr)[PPT] = g.r;
+    const uint32_t (&rm)[PPT] = g.m;
     const int shift = 1 << l;
     float rg[PPT], ad[PPT], fg[PPT];
 #pragma unroll
@@ -337,7 +352,7 @@ __global__ __launch_bounds__(1024) void level_scan_wide_kernel(ScanArgs a) {
         rg[j] = dh_sigmoid(Raw<T>::f(rr[j]));
       }
     }
-    fetch(l + 1 < a.n_lv ? l + 1 : l);                 // next level's gates fly during the exchange
+    fetch(min(l + 2, a.n_lv - 1), g);                  // two levels ahead, into the set just consumed
     if (shift >= NT) {                                   // uniform
       // lags of whole slots (2^l = K * NT): the source of position tid + j * NT is this thread's
       // slot j - K, so the level needs no exchange and no barrier. Slots update in descending order,
@@ -352,8 +367,8 @@ __global__ __launch_bounds__(1024) void level_scan_wide_kernel(ScanArgs a) {
 #pragma unroll
           for (int q = 0; q < C / 2; ++q) {
             const float w0 = V[sj][2 * q], w1 = V[sj][2 * q + 1];
-            V[j][2 * q] = fg[j] * V[j][2 * q] + coef * w0;
-            V[j][2 * q + 1] = fg[j] * V[j][2 * q + 1] + coef * w1;
+            V[j][2 * q] = __builtin_fmaf(coef, w0, fg[j] * V[j][2 * q]);
+            V[j][2 * q + 1] = __builtin_fmaf(coef, w1, fg[j] * V[j][2 * q + 1]);
           }
         }
       };
@@ -362,8 +377,11 @@ __global__ __launch_bounds__(1024) void level_scan_wide_kernel(ScanArgs a) {
       else if (k == 2) step(std::integral_constant<int, 2>{});
       else step(std::integral_constant<int, PPT>{});   // k >= PPT: no position has a source
       write_slab(l + 1);
-      continue;
+      return;
     }
+    const int bsel = NB == 2 ? (l & 1) : 0;
+    auto& vs = vs_[bsel];
+    auto& rs = rs_[bsel];
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
       const int t = tid + j * NT;
@@ -380,12 +398,18 @@ __global__ __launch_bounds__(1024) void level_scan_wide_kernel(ScanArgs a) {
 #pragma unroll
       for (int q = 0; q < C / 2; ++q) {
         const float2 w = vs[q][s];
-        V[j][2 * q] = fg[j] * V[j][2 * q] + coef * w.x;
-        V[j][2 * q + 1] = fg[j] * V[j][2 * q + 1] + coef * w.y;
+        // V = coef * w + f * V as one explicit FMA in both update paths (left to the compiler, the
+        // contraction it picks differs between them)
+        V[j][2 * q] = __builtin_fmaf(coef, w.x, fg[j] * V[j][2 * q]);
+        V[j][2 * q + 1] = __builtin_fmaf(coef, w.y, fg[j] * V[j][2 * q + 1]);
       }
     }
     write_slab(l + 1);
-    __syncthreads();
+    if (NB == 1) __syncthreads();
+  };
+  for (int l = 0; l < a.n_lv; l += 2) {
+    level(l, gs0);
+    if (l + 1 < a.n_lv) level(l + 1, gs1);                // uniform
   }
   for (int j = a.n_lv + 1; j < a.ring_L; ++j) write_slab(j);
 
