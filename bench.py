@@ -75,9 +75,11 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--cpu-prompt", type=int, default=1024)
     ap.add_argument("--leg", default="all",
-                    choices=["all", "prefill-kernels", "prefill-c2", "decode-b16", "decode-trace", "parity-bf16"],
+                    choices=["all", "prefill-kernels", "prefill-c2", "forward-c5", "decode-b16", "decode-trace",
+                             "parity-bf16"],
                     help="prefill-kernels: only the C5 kernel timings; prefill-c2: only the C2 fused "
-                         "forward (for rocprofv3 runs); decode-b16: only the batch-16 sampling decode "
+                         "forward (for rocprofv3 runs); forward-c5: only the C5 graphed forward (for "
+                         "rocprofv3 runs); decode-b16: only the batch-16 sampling decode "
                          "(for rocprofv3 runs); decode-trace: per-phase timestamps of the one-launch "
                          "batch-1 step (wait vs work table); parity-bf16: only the bf16 parity figures")
     return ap.parse_args()
@@ -733,6 +735,14 @@ def main():
         print(json.dumps({"prefill_tok_s": round(g_tok, 1), "prefill_ms": round(g_ms, 3),
                           "prefill_host_launched_tok_s": round(f_tok, 1), "prefill_host_launched_ms": round(f_ms, 3)}),
               flush=True)
+        return
+    if args.leg == "forward-c5":
+        g = torch.Generator(device=dev).manual_seed(6)
+        ids = torch.randint(0, 50257, (8, 4096), device=dev, generator=g)
+        ids[:, 1000] = EOT
+        gc_tok, gc_ms = time_forward_graphed(torch, model, ids, reps=3)
+        log(f"C5 forward: graphed {gc_tok:.0f} tok/s ({gc_ms:.2f} ms)")
+        print(json.dumps({"forward_c5_tok_s": round(gc_tok, 1), "forward_c5_ms": round(gc_ms, 3)}), flush=True)
         return
     if args.leg == "parity-bf16":
         res = parity_bf16(torch, model, min(args.prompt, max_len - 256))

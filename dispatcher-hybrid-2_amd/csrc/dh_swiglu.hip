@@ -46,6 +46,13 @@ template <> struct Vec16<float> {
   }
 };
 
+// bf16 inputs: the hardware-exp form (equal after rounding for every bf16 input); fp32: torch's
+template <typename T>
+__device__ __forceinline__ float silu_of(float x) {
+  if constexpr (sizeof(T) == 2) return dh_silu_bf16in(x);
+  else return dh_silu_exact(x);
+}
+
 template <typename T>
 __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const T* g, const T* u,
                                                             T* out, int64_t n) {
@@ -59,13 +66,13 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const T* g, const T*
     Vec16<T>::unpack(gv, gf);
     Vec16<T>::unpack(uv, uf);
 #pragma unroll
-    for (int e = 0; e < V; ++e) gf[e] = Elem<T>::round(Elem<T>::round(dh_silu_exact(gf[e])) * uf[e]);
+    for (int e = 0; e < V; ++e) gf[e] = Elem<T>::round(Elem<T>::round(silu_of<T>(gf[e])) * uf[e]);
     reinterpret_cast<uint4*>(out)[i] = Vec16<T>::pack(gf);
   }
   // tail (n % V elements): the first threads of the grid
   const int64_t t = nvec * V + (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (t < n) {
-    const float s = Elem<T>::round(dh_silu_exact(Elem<T>::load(g + t)));
+    const float s = Elem<T>::round(silu_of<T>(Elem<T>::load(g + t)));
     Elem<T>::store(out + t, Elem<T>::round(s * Elem<T>::load(u + t)));
   }
 }

@@ -570,6 +570,23 @@ def test_silu_mul_matches_eager_swiglu(n, dtype):
             assert np.allclose(_np(out), s * u64, rtol=2e-6, atol=1e-30)
 
 
+def test_silu_mul_bf16_every_input():
+    """All 65536 bf16 gate patterns (NaN aside) with up = 1: dh_silu_mul's bf16 activation (silu with
+    the hardware exp and an IEEE divide, then the product) equals torch's bf16 SiLU bit for bit, so
+    the faster exp never moves a rounded result (the fused SwiGLU GEMM epilogue evaluates the same)."""
+    from dispatcher_hybrid.fused_gates import silu_mul
+    g = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).to("cuda")
+    u = torch.ones(65536, device="cuda", dtype=torch.bfloat16)
+    out = silu_mul(g, u)
+    ref = torch.nn.functional.silu(g) * u
+    keep = ~torch.isnan(g.float())
+    assert int(keep.sum()) == 65536 - 254
+    rn = torch.isnan(ref.float())                    # silu(-inf) = -inf / inf: a NaN (of either sign)
+    assert torch.equal(torch.isnan(out.float())[keep], rn[keep])
+    num = keep & ~rn
+    assert torch.equal(out.view(torch.int16)[num], ref.view(torch.int16)[num])
+
+
 def test_silu_mul_in_place_and_unaligned_views():
     from dispatcher_hybrid.fused_gates import silu_mul
     base_g = torch.randn(10001, device="cuda", dtype=torch.bfloat16)
