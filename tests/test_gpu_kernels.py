@@ -557,11 +557,9 @@ def test_silu_mul_matches_eager_swiglu(n, dtype):
     s = g64 / (1.0 + np.exp(-g64))
     if dtype == torch.bfloat16:
         cpu = _bf16_round_np(_bf16_round_np(s.astype(np.float32)).astype(np.float64) * u64)
-        # exact against torch's kernel, up to a 1-ulp rounding flip where exp's last bit decides it
-        d = (out.float() - ref.float()).abs()
-        ulp = ref.float().abs().clamp_min(1e-30) * 2.0 ** -7
-        assert bool((d <= ulp).all())
-        assert int((d > 0).sum()) <= max(1, n // 10000)
+        # bit-exact against torch's kernel: the bf16 silu equals torch's for every bf16 input (see
+        # test_silu_mul_bf16_every_input) and the product of two bf16 values is exact in fp32
+        assert torch.equal(out, ref)
         dc = np.abs(_np(out).astype(np.float64) - cpu)
         assert (dc <= np.maximum(np.abs(cpu), 1e-30) * 2.0 ** -7).all()
     else:
