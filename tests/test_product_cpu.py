@@ -247,6 +247,23 @@ def test_fused_gates_switch_and_cpu_refusal():
         assert torch.equal(m(ids).logits, before)
 
 
+def test_fused_wrappers_refuse_cpu_tensors():
+    """The HIP wrappers have no CPU implementation: CPU tensors raise before any library call, and
+    the module-level routing helpers report that the fused GEMMs do not apply to them."""
+    from dispatcher_hybrid import fused_gates as fg
+    x = torch.randn(4, 64, dtype=torch.bfloat16)
+    w = torch.randn(8, 64, dtype=torch.bfloat16)
+    for call in (lambda: fg.fused_swiglu(x, w, w), lambda: fg.fused_projections(x, [w]),
+                 lambda: fg.silu_mul(x, x)):
+        with pytest.raises(RuntimeError, match="must be on the GPU"):
+            call()
+    lin = torch.nn.Linear(64, 8, bias=False).to(torch.bfloat16)
+    assert not fg.swiglu_fits(x, lin, lin)
+    assert not fg.projections_fit(x, [lin])
+    # on the CPU the routing helper is the library call itself
+    assert torch.equal(fg.project(x, [lin], fg.OUT_GEMM_MAX_ROWS)[0], lin(x))
+
+
 def test_reference_init_scheme():
     """The product's own init: N(0, 0.02), W1s zero, biases -2/+2/+2, tied head."""
     from dispatcher_hybrid import DispatcherHybridForCausalLM
