@@ -4,10 +4,13 @@
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 
 Headline (`value`): steady-state batch-1 bf16 greedy decode tok/s of the 292M model at 3840-4096
-context through FusedGraphedHybridDecoder (one HIP-graph replay per token; five gfx950 launches per tree
-layer: fused RMSNorm/projections, the mixer step's gate readouts, its recurrence fused with the
-out-projection + residual, RMSNorm + SwiGLU, down-projection + residual). A step is one decode token; prefill and graph capture are outside the timed region
-(reference scripts/benchmark_decode.py:21-28 protocol). Also reported in the same JSON line:
+context through FusedGraphedHybridDecoder: the whole step as ONE persistent launch per token
+(dh_decode_persistent_step; with --graph-step the graph of launches instead: one HIP-graph replay
+per token, five gfx950 launches per tree layer -- fused RMSNorm/projections, the mixer step's gate
+readouts, its recurrence fused with the out-projection + residual, RMSNorm + SwiGLU,
+down-projection + residual). A step is one decode token; prefill and graph capture are outside the
+timed region (reference scripts/benchmark_decode.py:21-28 protocol). Also reported in the same JSON
+line:
   decode_b16_*      lockstep batch-16 decode with temperature 0.8 / top-k 50 sampling (dh_sample_topk)
   decoder_prefill_* the decoders' C3 prefill (3840 tokens, all decode state): fused vs eager
   prefill_*         C2: 292M bf16 forward at B=1, T=1024: graphed fused forward (graphed_logits), the
@@ -30,7 +33,7 @@ out-projection + residual, RMSNorm + SwiGLU, down-projection + residual). A step
   cpu_baseline      the oracle's eager torch path (reference algorithm) on the host CPU, fp32: C3 decode
                     (value), C2 prefill and the C1 mixer layer
 All inputs are synthetic (uniform token ids) and the weights are a random init of the released
-architecture. Rank 0 prints one JSON line.
+architecture. Rank 0 prints one JSON line. --leg runs one part alone (for rocprofv3 runs): see --help.
 """
 
 import argparse
