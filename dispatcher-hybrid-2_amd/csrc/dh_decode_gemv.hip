@@ -1033,7 +1033,9 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_pers_kerne
       const __amdgpu_buffer_rsrc_t rw = buf_rsrc(q.wt, (uint32_t)(16 * K * 2));
 #pragma unroll
       for (int j = 0; j < KSW; ++j)
-        wf[j] = bld16w(rw, q.valid ? (uint32_t)((q.wr * K + (s0 + j) * 32 + 8 * g) * 2) : kOOB);
+        // ordinary loads (not bld16w's non-temporal ones): part of the head's rows then survives in the
+        // memory-side cache until the next step's head (batch 16: 0.652 -> 0.650 ms per step)
+        wf[j] = bld16(rw, q.valid ? (uint32_t)((q.wr * K + (s0 + j) * 32 + 8 * g) * 2) : kOOB);
     } else {
 #pragma unroll
       for (int j = 0; j < KSW; ++j)
