@@ -59,7 +59,7 @@ EOT = 50256
 TRAFFIC_GEMV_LAUNCH = 9_453_050
 # HBM bytes per decode_persistent_kernel launch (one batch-1 step), same counters and factors, from
 # profiles/decode_c3_b1_persistent.md
-TRAFFIC_PERSISTENT_LAUNCH = 616_291_708
+TRAFFIC_PERSISTENT_LAUNCH = 616_437_816
 # algorithmic bytes of one batch-1 step at context >= 1024: weights 584,316,928 + tree state
 # 1,224,704 + windowed keys and values 8,396,800
 STEP_BYTES = 584_316_928 + 1_224_704 + 8_396_800
