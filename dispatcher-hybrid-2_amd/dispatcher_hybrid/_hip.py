@@ -15,7 +15,7 @@ import os
 
 import torch
 
-ABI_VERSION = 17
+ABI_VERSION = 18
 _LIB_NAME = "libdh_mixer.so"
 
 DH_F32, DH_BF16 = 0, 1
@@ -78,6 +78,7 @@ def _load():
         "dh_decode_scan_out": ([i32] + [vp] * 8 + [i64, vp] + [i32] * 6 + [vp], i32),
         "dh_proj_gemm": ([i32, vp, i64, i32, i32, i32, vp, vp, vp, vp, vp], i32),
         "dh_proj_gemm_swiglu": ([i32, vp, i64, i32, i32, vp, vp, i32, vp, i64, vp], i32),
+        "dh_tree_mask": ([i32, vp, i64, i32, i32, i32, i64, vp, vp], i32),
         "dh_sample_topk": ([i32, vp, i64, i32, i32, ctypes.c_float, i32, ctypes.c_uint64, vp, vp, vp], i32),
         "dh_sample_topk_hist": ([i32, vp, i64, i32, i32, ctypes.c_float, i32, ctypes.c_uint64, vp, vp, vp, i64, i64,
                                  vp], i32),

@@ -441,6 +441,32 @@ def fused_swiglu(x, w_gate, w_up):
     return out
 
 
+TREE_MASK_MAX_LEN = 16384          # the kernel keeps a row's EOT counts in LDS
+TREE_MASK_MAX_LEVELS = 30
+
+
+def tree_mask(input_ids, levels, eot, dtype):
+    """The parallel forward's tree mask with document resets in ONE launch (``dh_tree_mask``):
+    mask[b, t, l] = 1 iff t >= 2^l and no EOT lies among input_ids[b, t-2^l .. t-1], else 0 (the
+    level mask times "source and destination in the same document", reference
+    dispatcher_hybrid/modeling_dispatcher.py:282-297, 311-323). input_ids: (b, T) int64 CUDA tensor;
+    dtype float32 or bfloat16. Returns a contiguous (b, T, levels) tensor of exact 0s and 1s."""
+    _hip.require_gpu(input_ids, "tree_mask")
+    if input_ids.dim() != 2 or input_ids.dtype != torch.int64 or dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("tree_mask: (b, T) int64 input_ids and a float32 or bfloat16 mask dtype")
+    b, T = input_ids.shape
+    if not (1 <= levels <= TREE_MASK_MAX_LEVELS) or T > TREE_MASK_MAX_LEN:
+        raise ValueError(f"tree_mask: levels={levels} (1..{TREE_MASK_MAX_LEVELS}), T={T} (<= {TREE_MASK_MAX_LEN})")
+    ids = input_ids if input_ids.stride(1) == 1 else input_ids.contiguous()
+    out = torch.empty(b, T, levels, device=ids.device, dtype=dtype)
+    if b == 0 or T == 0:
+        return out
+    st = _hip.lib.dh_tree_mask(_hip.dtype_code(dtype), _hip.ptr(ids), ids.stride(0), b, T, levels, int(eot),
+                               _hip.ptr(out), _hip.stream_handle(ids.device))
+    _hip.check(st, "dh_tree_mask")
+    return out
+
+
 def silu_mul(gate, up, out=None):
     """silu(gate) * up in one launch (``dh_silu_mul``): the SwiGLU activation of reference
     dispatcher_hybrid/modeling_dispatcher.py:197, F.silu(linear_gate(h)) * linear_up(h), at its

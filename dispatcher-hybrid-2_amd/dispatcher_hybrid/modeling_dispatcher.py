@@ -413,7 +413,14 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
         doc(t) counts the EOTs strictly before t, so an EOT belongs to the document it ends;
         level l's edge t <- t-2^l (index taken mod T, as roll() does) is kept iff the two doc ids
         match (reference modeling_dispatcher.py:311-323)."""
-        mask = self.level_mask(length, input_ids.device, self.embedding.weight.dtype)
+        dtype = self.embedding.weight.dtype
+        if (self.config.doc_reset and getattr(self, "_fused_norms", False) and input_ids.is_cuda
+                and input_ids.dtype == torch.int64 and dtype in (torch.float32, torch.bfloat16)):
+            from .fused_gates import TREE_MASK_MAX_LEN, TREE_MASK_MAX_LEVELS, tree_mask
+            if length <= TREE_MASK_MAX_LEN and 1 <= self.config.levels <= TREE_MASK_MAX_LEVELS:
+                # the same 0/1 values in one launch (dh_tree_mask) instead of the eight below
+                return tree_mask(input_ids, self.config.levels, self.config.eot_token, dtype)
+        mask = self.level_mask(length, input_ids.device, dtype)
         if not self.config.doc_reset:
             return mask
         is_eot = (input_ids == self.config.eot_token).to(mask.dtype)

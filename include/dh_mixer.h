@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 17
+#define DH_ABI_VERSION 18
 
 enum dh_status {
   DH_OK = 0,
@@ -155,6 +155,17 @@ int dh_silu_mul(int dtype, const void* gate, const void* up, void* out, int64_t 
  */
 int dh_proj_gemm_swiglu(int dtype, const void* X, int64_t ldx, int M, int K, const void* Wg, const void* Wu,
                         int N, void* out, int64_t ldo, void* stream);
+
+/*
+ * The parallel forward's tree mask with document resets, (b, T, L) contiguous, values 0 or 1:
+ *   out[(b*T + t)*L + l] = [t >= 2^l] * [no EOT among ids[b*ids_stride + t - 2^l .. t - 1]]
+ * Replaces the torch computation of the level mask times "source and destination in the same
+ * document" (reference dispatcher_hybrid/modeling_dispatcher.py:282-297, 311-323: doc(t) counts the
+ * EOTs before t; the edge t <- t - 2^l is kept iff doc(t) == doc(t - 2^l)). ids int64 (b, T) with row
+ * stride ids_stride >= T; dtype DH_F32 or DH_BF16 (the mask's dtype); T <= 16384, L <= 30.
+ */
+int dh_tree_mask(int dtype, const int64_t* ids, int64_t ids_stride, int b, int T, int L, int64_t eot, void* out,
+                 void* stream);
 
 /*
  * Residual add + RMSNorm over `rows` rows of d elements (row-contiguous, 16-byte aligned):

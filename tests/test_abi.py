@@ -21,7 +21,7 @@ def test_header_declares_the_entry_points():
     names = declared_functions()
     for must in ("dh_abi_version", "dh_last_error", "dh_gate_preacts_fwd", "dh_gate_preacts_bwd",
                  "dh_level_scan_fwd", "dh_decode_mixer_step", "dh_decode_gemv", "dh_decode_attention", "dh_argmax",
-                 "dh_decode_gates", "dh_decode_scan", "dh_argmax_workspace_bytes", "dh_sample_topk", "dh_sample_topk_hist", "dh_proj_gemm", "dh_proj_gemm_swiglu", "dh_decode_scan_out", "dh_decode_attention_split",
+                 "dh_decode_gates", "dh_decode_scan", "dh_argmax_workspace_bytes", "dh_sample_topk", "dh_sample_topk_hist", "dh_proj_gemm", "dh_proj_gemm_swiglu", "dh_tree_mask", "dh_decode_scan_out", "dh_decode_attention_split",
                  "dh_decode_attention_workspace_bytes", "dh_window_attention_fwd",
                  "dh_step_gates", "dh_step_scan"):
         assert must in names

@@ -651,3 +651,73 @@ def test_add_rmsnorm_in_place_and_errors():
             add_rmsnorm(x, y.float(), norm)
         with pytest.raises(ValueError):
             add_rmsnorm(x, y, torch.nn.RMSNorm(1024).to("cuda"))   # fp32 weight with bf16 rows
+
+
+# --------------------------------------------------------------------------------------------
+# tree mask with document resets
+# --------------------------------------------------------------------------------------------
+TREE_MASK_CASES = [
+    # b, T, L, eot placement
+    (1, 1, 3, "none"),
+    (3, 5, 12, "random"),               # levels whose lag is >= T stay all zero
+    (2, 37, 6, "edges"),                # EOT at the first and the last position
+    (2, 1025, 11, "random"),            # one position past a multiple of the 1024 threads
+    (4, 4096, 12, "random"),            # C2/C5 row length
+    (2, 4096, 12, "dense"),             # every other token an EOT
+    (1, 16384, 14, "random"),           # the longest row the kernel takes
+]
+
+
+def _tree_ids(case, eot=7):
+    b, T, L, kind = case
+    rng = np.random.default_rng(T * 31 + b)
+    ids = rng.integers(0, 50, size=(b, T))
+    ids[ids == eot] = eot + 1
+    if kind == "random":
+        ids[rng.random((b, T)) < 8.0 / T + 0.003] = eot
+        if b > 1:
+            ids[-1] = eot               # an all-EOT row
+        if b > 2:
+            ids[1] = eot + 1            # a row without one
+    elif kind == "edges":
+        ids[:, 0] = eot
+        ids[:, -1] = eot
+    elif kind == "dense":
+        ids[:, ::2] = eot
+    return ids, eot
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", TREE_MASK_CASES)
+def test_tree_mask_equals_oracle(case, dtype):
+    """dh_tree_mask's 0/1 values bit-exact against the oracle's tree_mask (level mask x doc reset)."""
+    from dispatcher_hybrid.fused_gates import tree_mask
+    print(f"tree_mask case={case} dtype={dtype}", flush=True)
+    ids, eot = _tree_ids(case)
+    L = case[2]
+    got = tree_mask(torch.as_tensor(ids, dtype=torch.int64, device=DEV), L, eot, dtype)
+    assert got.shape == (*ids.shape, L) and got.dtype == dtype and got.is_contiguous()
+    ref = torch.as_tensor(om.tree_mask(ids, L, eot)).to(dtype)
+    assert torch.equal(got.cpu(), ref)
+
+
+def test_tree_mask_strided_ids_and_rejects():
+    """A row-strided view of the ids (a slice of a wider batch) reads the right rows; shapes and
+    dtypes outside the kernel's range raise before any launch."""
+    from dispatcher_hybrid.fused_gates import tree_mask
+    ids, eot = _tree_ids((3, 300, 9, "random"))
+    wide = torch.zeros(3, 512, dtype=torch.int64, device=DEV)
+    wide[:, 100:400] = torch.as_tensor(ids, device=DEV)
+    view = wide[:, 100:400]
+    assert view.stride(0) == 512
+    got = tree_mask(view, 9, eot, torch.float32)
+    assert torch.equal(got.cpu(), torch.as_tensor(om.tree_mask(ids, 9, eot)).float())
+    t = torch.as_tensor(ids, device=DEV)
+    with pytest.raises(ValueError):
+        tree_mask(t.to(torch.int32), 9, eot, torch.float32)
+    with pytest.raises(ValueError):
+        tree_mask(t, 9, eot, torch.float16)
+    with pytest.raises(ValueError):
+        tree_mask(t, 31, eot, torch.float32)
+    with pytest.raises(ValueError):
+        tree_mask(torch.zeros(1, 16385, dtype=torch.int64, device=DEV), 9, eot, torch.float32)

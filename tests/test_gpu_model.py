@@ -51,6 +51,27 @@ def test_fused_forward_bf16_tracks_eager(tiny_gpu):
     assert argmax_agree(fused, eager) > 0.95
 
 
+def test_fused_tree_mask_equals_eager_tree_mask():
+    """With enable_fused_gates() the doc-reset tree mask comes from dh_tree_mask: the same values,
+    shape and dtype as the torch formula the eager forward uses."""
+    for name in sorted(TINY_CONFIGS):
+        cfgd, sd = tiny(name)
+        for dtype in (torch.float32, torch.bfloat16):
+            m = product_model(cfgd, sd, device=DEV, dtype=dtype)
+            if not m.config.doc_reset:
+                continue
+            g = torch.Generator().manual_seed(5)
+            for T in (1, 3, 64, 200):
+                ids = torch.randint(0, cfgd["vocab_size"], (3, T), generator=g)
+                ids[0, T // 2] = m.config.eot_token
+                ids[2, ::3] = m.config.eot_token
+                ids = ids.to(DEV)
+                ref = m._tree_mask(ids, T)
+                got = m.enable_fused_gates()._tree_mask(ids, T)
+                m.enable_fused_gates(False)
+                assert got.dtype == ref.dtype and torch.equal(got, ref), (name, dtype, T)
+
+
 def test_fused_forward_sees_in_place_bias_updates(tiny_gpu):
     """The fused path reads bf16 gate biases through cached fp32 copies: an in-place update of a
     bias must reach the next fused forward (the copy follows the tensor's version counter)."""
