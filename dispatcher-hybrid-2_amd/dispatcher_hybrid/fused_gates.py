@@ -385,12 +385,14 @@ def input_projections(x, mixer):
 
 
 # Rows up to which one dh_proj_gemm launch beats the library for an attention layer's q, k, v
-# (three 1024-wide nn.Linear GEMMs) and for a single 1024 x 1024 output projection (the mixer's and
-# attention's linear_out), measured on MI355X in captured graphs (bf16, K = 1024; us, ours against
-# the library): q, k, v 13.3 / 23.8 at 1024 rows, 19.6 / 29.7 at 2048, 30.0 / 37.4 at 4096, 60 / 59
-# at 8192; linear_out 6.5 / 7.9 at 1024, 7.8 / 9.7 at 2048, 12.7 / 12.4 at 4096.
+# (three 1024-wide nn.Linear GEMMs), measured on MI355X in captured graphs (bf16, K = 1024; us, ours
+# against the library): 13.3 / 23.8 at 1024 rows, 19.6 / 29.7 at 2048, 30.0 / 37.4 at 4096, 60 / 59
+# at 8192. A single output projection (the mixer's and attention's 1024 x 1024 linear_out) or the
+# SwiGLU down projection (1024 x 2816) stays on the library at every row count: over 18 distinct
+# weights per graph, as in the forward, the library took 8.9 / 10.4 / 13.0 us at 1024 / 2048 / 4096
+# rows against 9.9 / 10.4 / 13.4 (down: 14.0 / 18.8 / 28.1 against 21.7 / 22.3 / 29.6), and the C2
+# forward 1.950 ms against 1.969 with the out-projections on dh_proj_gemm.
 QKV_GEMM_MAX_ROWS = 4096
-OUT_GEMM_MAX_ROWS = 2048
 
 
 def project(x, linears, max_rows):

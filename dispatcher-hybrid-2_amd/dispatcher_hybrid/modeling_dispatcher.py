@@ -182,8 +182,6 @@ class DispatcherMixer(nn.Module):
         else:
             # inference: activated gates written head-major, then the level scan (two launches)
             V = fused_gate_scan(A, Bs, Wi, Wf, Wr, bi, bf, br, n_lv, m3, V0, H)
-            from .fused_gates import OUT_GEMM_MAX_ROWS, project
-            return project(V, [self.linear_out], OUT_GEMM_MAX_ROWS)[0]
         return self.linear_out(V)
 
 
@@ -259,13 +257,13 @@ class WindowAttention(nn.Module):
         if self.use_fused and not torch.is_grad_enabled() and x.is_cuda:
             from . import fused_attention as fa
             if fa.supported(x.dtype, self.head_dim):
-                from .fused_gates import OUT_GEMM_MAX_ROWS, QKV_GEMM_MAX_ROWS, project
+                from .fused_gates import QKV_GEMM_MAX_ROWS, project
                 # q, k, v as one GEMM launch (up to QKV_GEMM_MAX_ROWS rows); RoPE, banded scores,
                 # softmax and the value average in one launch, (B, T, d) in/out
                 q, k, v = project(x, [self.linear_q, self.linear_k, self.linear_v], QKV_GEMM_MAX_ROWS)
                 cos, sin = self.rope_tables(T, x.device, x.dtype)
                 y = fa.window_attention(q, k, v, cos, sin, self.num_heads, self.band(T))
-                return project(y, [self.linear_out], OUT_GEMM_MAX_ROWS)[0]
+                return self.linear_out(y)
         return self._forward_eager(x)
 
     def band(self, T):
