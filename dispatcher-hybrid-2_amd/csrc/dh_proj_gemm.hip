@@ -273,7 +273,8 @@ __device__ __forceinline__ void store_tile_swiglu(const GemmArgs& a, const f32x4
   }
 }
 
-// Fragment ping-pong variant (bf16, 2 LDS stages): the MFMA operands of a K tile's two 32-k steps
+// Fragment ping-pong variant (bf16, S LDS stages: S - 1 K tiles in flight while one is multiplied;
+// the persistent form and well-occupied launches use two): the MFMA operands of a K tile's two 32-k steps
 // live in two register sets, so the LDS reads of one step are in flight while the MFMAs of the other
 // run, across the K-tile boundary too: the barrier sits between the two steps' MFMAs. Row swizzle:
 // slot p of row R holds chunk p ^ (R & 7). Measured with the LDS counters on MI355X, the fragment
@@ -295,7 +296,7 @@ __device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t
 // SWI: the fused SwiGLU GEMM (segments 0 = W_gate, 1 = W_up, both N[0] rows): column tile nt covers
 // output features [nt BN / 2, (nt + 1) BN / 2), each wave's 16 TN columns the gate rows then the
 // up rows of its 8 TN features, and the epilogue is store_tile_swiglu.
-template <int TM, int TN, int WGM, int WGN, bool SWI>
+template <int TM, int TN, int WGM, int WGN, bool SWI, int S>
 __global__ __launch_bounds__(64 * WGM * WGN) void proj_gemm_pp_kernel(GemmArgs a) {
   typedef bf16_t T;
   typedef Frag<T> F;
@@ -304,8 +305,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void proj_gemm_pp_kernel(GemmArgs a
   constexpr int GX = BM / 8 / NW, GW = BN / 8 / NW;    // 8-row load groups per wave and operand
   static_assert(GX * 8 * NW == BM && GW * 8 * NW == BN, "tile rows must split into 8-row groups per wave");
   static_assert(F::KSTEPS == 2, "two 32-k steps per 128-byte K tile");
-  __shared__ __align__(1024) unsigned char sw[2][BN * kRowBytes];   // weight tiles
-  __shared__ __align__(1024) unsigned char sx[2][BM * kRowBytes];   // activation tiles
+  static_assert(S >= 2, "at least two LDS stages");
+  constexpr int PER = GX + GW;                         // DMA instructions per K tile and wave
+  __shared__ __align__(1024) unsigned char sw[S][BN * kRowBytes];   // weight tiles
+  __shared__ __align__(1024) unsigned char sx[S][BM * kRowBytes];   // activation tiles
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
@@ -374,6 +377,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void proj_gemm_pp_kernel(GemmArgs a
     }
     __syncthreads();                                   // the previous tile's LDS reads are done
     issue(0, 0);
+#pragma unroll
+    for (int q = 1; q + 1 < S; ++q) issue(min(q, nk - 1), q);
     if (pm0 >= 0) {                                    // under K tile 0's loads
       if constexpr (SWI) store_tile_swiglu<TM, TN, WGM>(a, acc, pm0, pn0, wm, wn, r, g);
       else store_tile_x4<TM, TN, WGM>(a, acc, pm0, pn0, wm, wn, r, g);
@@ -384,24 +389,28 @@ __global__ __launch_bounds__(64 * WGM * WGN) void proj_gemm_pp_kernel(GemmArgs a
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int i = 0; i < TM; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    wait_vm<0>();                                      // K tile 0 (and the stores) done
+    wait_vm<0>();                                      // K tiles 0 .. S-2 (and the stores) done
     __syncthreads();
-    issue(min(1, nk - 1), 1);
+    issue(min(S - 1, nk - 1), S - 1);
     read(aw, ax, 0, c0);
+    int st = 0;                                        // stage of tile kt: kt mod S
     for (int kt = 0; kt < nk; ++kt) {
-      const int st = kt & 1;
+      const int nst = st + 1 == S ? 0 : st + 1;
       read(bw, bx, st, c1);                            // step 1 of tile kt ...
       mma_all(aw, ax);                                 // ... in flight under step 0's MFMAs
       // Scheduling fences: without them the compiler sinks step 0's MFMAs below the barrier (they
       // touch no memory), which leaves step 1's reads waited on with nothing in flight under them.
       __builtin_amdgcn_sched_barrier(0);
-      wait_vm<0>();                                    // tile kt + 1 has landed (this wave's part)
+      // tile kt + 1 has landed (this wave's part): loads complete in issue order, and the S - 2
+      // tiles issued after it may still be in flight
+      wait_vm<(S - 2) * PER>();
       __syncthreads();                                 // everyone's; every read of stage st is done
-      issue(min(kt + 2, nk - 1), st);                  // (repeats of the last tile are harmless)
-      if (kt + 1 < nk) read(aw, ax, st ^ 1, c0);       // step 0 of tile kt + 1 ...
+      issue(min(kt + S, nk - 1), st);                  // (repeats of the last tile are harmless)
+      if (kt + 1 < nk) read(aw, ax, nst, c0);          // step 0 of tile kt + 1 ...
       __builtin_amdgcn_sched_barrier(0);
       mma_all(bw, bx);                                 // ... under step 1's MFMAs
       __builtin_amdgcn_sched_barrier(0);
+      st = nst;
     }
     wait_vm<0>();                                      // repeated tail loads land before LDS is reused
   }
@@ -413,15 +422,15 @@ __global__ __launch_bounds__(64 * WGM * WGN) void proj_gemm_pp_kernel(GemmArgs a
 
 bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p % n) == 0; }
 
-// One workgroup per tile of the ping-pong kernel with 4 waves (BM = 32 TM, BN = 32 TN).
-template <int TM, int TN, bool SWI>
+// One workgroup per tile of the ping-pong kernel with 4 waves (BM = 32 TM, BN = 32 TN), S LDS stages.
+template <int TM, int TN, bool SWI, int S = 2>
 int launch_pp_tiles(GemmArgs& a, hipStream_t s, const char* who) {
   constexpr int BM = 32 * TM, BN = 32 * TN;
   a.mtiles = (a.M + BM - 1) / BM;
   a.ntiles = (a.Ntot + BN - 1) / BN;
   const int64_t nvirt = (int64_t)((a.mtiles + 7) / 8) * 8 * a.ntiles;
   DH_REQUIRE(nvirt < (1ll << 31), DH_ERR_UNSUPPORTED_SHAPE, "%s: M=%d too large", who, a.M);
-  proj_gemm_pp_kernel<TM, TN, 2, 2, SWI><<<dim3((unsigned)nvirt), dim3(256), 0, s>>>(a);
+  proj_gemm_pp_kernel<TM, TN, 2, 2, SWI, S><<<dim3((unsigned)nvirt), dim3(256), 0, s>>>(a);
   return dh_check_launch(who);
 }
 
@@ -442,7 +451,14 @@ constexpr int64_t kWideGrid = 256;        // persistent workgroups: one per CU (
 //   M = 4096  N = 1024 K = 2816 38.8 / 30.0 / 29.8 / 34.1 / 62.3
 // i.e. 256 x 256 tiles from ~160 of them, else 64 x 64 while there are at most 768 of those (three
 // per CU), else the largest count of 64 x 128 (>= 768) or 128 x 64 (>= 512) tiles, else 128 x 128.
-// Every form sums the same products in the same k order: outputs are bit-identical across forms.
+// With at most one or two 64 x 64 tiles per CU nothing else on the CU covers a K tile's round trip,
+// so those launches keep three (<= 256 tiles) or two (<= 512) K tiles in flight in four or three
+// LDS stages instead of one in two. Measured over 18 distinct weights per graph (us, two / three /
+// four stages): M = 1024 N = 1024 9.8 / 7.1 / 6.7, M = 1024 N = 1024 K = 2816 21.7 / 13.5 / 12.1,
+// M = 2048 N = 1024 10.4 / 9.1 / 9.6, M = 2048 N = 1024 K = 2816 22.3 / 19.8 / 20.4; with more tiles
+// per CU the extra LDS costs occupancy (M = 1024 N = 3072: 12.6 / 14.3 / 16.3).
+// Every form sums the same products in the same k order: outputs are bit-identical across forms
+// and stage counts.
 template <bool SWI>
 int launch_wide(GemmArgs& a, hipStream_t s, const char* who) {
   const int M = a.M, N = a.Ntot;
@@ -452,10 +468,13 @@ int launch_wide(GemmArgs& a, hipStream_t s, const char* who) {
     const int64_t nvirt = (int64_t)((a.mtiles + 7) / 8) * 8 * a.ntiles;
     DH_REQUIRE(nvirt < (1ll << 31), DH_ERR_UNSUPPORTED_SHAPE, "%s: M=%d too large", who, M);
     const unsigned grid = (unsigned)(nvirt < kWideGrid ? nvirt : kWideGrid);
-    proj_gemm_pp_kernel<8, 4, 2, 4, SWI><<<dim3(grid), dim3(512), 0, s>>>(a);
+    proj_gemm_pp_kernel<8, 4, 2, 4, SWI, 2><<<dim3(grid), dim3(512), 0, s>>>(a);
     return dh_check_launch(who);
   }
-  if (tiles_of(M, N, 64, 64) <= 768) return launch_pp_tiles<2, 2, SWI>(a, s, who);
+  const int64_t t64 = tiles_of(M, N, 64, 64);
+  if (t64 <= 256) return launch_pp_tiles<2, 2, SWI, 4>(a, s, who);
+  if (t64 <= 512) return launch_pp_tiles<2, 2, SWI, 3>(a, s, who);
+  if (t64 <= 768) return launch_pp_tiles<2, 2, SWI>(a, s, who);
   if (tiles_of(M, N, 64, 128) >= 768) return launch_pp_tiles<2, 4, SWI>(a, s, who);
   if (tiles_of(M, N, 128, 64) >= 512) return launch_pp_tiles<4, 2, SWI>(a, s, who);
   return launch_pp_tiles<4, 4, SWI>(a, s, who);

@@ -384,15 +384,16 @@ def input_projections(x, mixer):
     return tuple(l(x) for l in lins)
 
 
-# Rows up to which one dh_proj_gemm launch beats the library for an attention layer's q, k, v
-# (three 1024-wide nn.Linear GEMMs), measured on MI355X in captured graphs (bf16, K = 1024; us, ours
-# against the library): 13.3 / 23.8 at 1024 rows, 19.6 / 29.7 at 2048, 30.0 / 37.4 at 4096, 60 / 59
-# at 8192. A single output projection (the mixer's and attention's 1024 x 1024 linear_out) or the
-# SwiGLU down projection (1024 x 2816) stays on the library at every row count: over 18 distinct
-# weights per graph, as in the forward, the library took 8.9 / 10.4 / 13.0 us at 1024 / 2048 / 4096
-# rows against 9.9 / 10.4 / 13.4 (down: 14.0 / 18.8 / 28.1 against 21.7 / 22.3 / 29.6), and the C2
-# forward 1.950 ms against 1.969 with the out-projections on dh_proj_gemm.
+# Rows up to which one dh_proj_gemm launch beats the library, measured on MI355X in captured graphs
+# (bf16; us, ours against the library): an attention layer's q, k, v (three 1024-wide nn.Linear
+# GEMMs, K = 1024) 13.3 / 23.8 at 1024 rows, 19.6 / 29.7 at 2048, 30.0 / 37.4 at 4096, 60 / 59 at
+# 8192; over 18 distinct weights per graph, as in the forward, a single 1024 x 1024 output
+# projection (the mixer's and attention's linear_out) 6.7 / 8.9 at 1024, 9.1 / 10.4 at 2048,
+# 12.9 / 13.0 at 4096, and the SwiGLU down projection (1024 x 2816) 12.1 / 14.0 at 1024, 19.8 / 18.8
+# at 2048 (the launches of at most 512 tiles keep two or three K tiles in flight).
 QKV_GEMM_MAX_ROWS = 4096
+OUT_GEMM_MAX_ROWS = 2048
+DOWN_GEMM_MAX_ROWS = 1024
 
 
 def project(x, linears, max_rows):

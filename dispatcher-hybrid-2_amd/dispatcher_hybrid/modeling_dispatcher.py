@@ -182,6 +182,8 @@ class DispatcherMixer(nn.Module):
         else:
             # inference: activated gates written head-major, then the level scan (two launches)
             V = fused_gate_scan(A, Bs, Wi, Wf, Wr, bi, bf, br, n_lv, m3, V0, H)
+            from .fused_gates import OUT_GEMM_MAX_ROWS, project
+            return project(V, [self.linear_out], OUT_GEMM_MAX_ROWS)[0]
         return self.linear_out(V)
 
 
@@ -257,13 +259,13 @@ class WindowAttention(nn.Module):
         if self.use_fused and not torch.is_grad_enabled() and x.is_cuda:
             from . import fused_attention as fa
             if fa.supported(x.dtype, self.head_dim):
-                from .fused_gates import QKV_GEMM_MAX_ROWS, project
+                from .fused_gates import OUT_GEMM_MAX_ROWS, QKV_GEMM_MAX_ROWS, project
                 # q, k, v as one GEMM launch (up to QKV_GEMM_MAX_ROWS rows); RoPE, banded scores,
                 # softmax and the value average in one launch, (B, T, d) in/out
                 q, k, v = project(x, [self.linear_q, self.linear_k, self.linear_v], QKV_GEMM_MAX_ROWS)
                 cos, sin = self.rope_tables(T, x.device, x.dtype)
                 y = fa.window_attention(q, k, v, cos, sin, self.num_heads, self.band(T))
-                return self.linear_out(y)
+                return project(y, [self.linear_out], OUT_GEMM_MAX_ROWS)[0]
         return self._forward_eager(x)
 
     def band(self, T):
@@ -289,7 +291,7 @@ class SwiGLU(nn.Module):
     With use_fused (set by enable_fused_gates) and no autograd, bf16 layers run linear_gate,
     linear_up and the activation as one dh_proj_gemm_swiglu launch (the two GEMM outputs never
     reach memory), other fp32/bf16 layers the two GEMMs and one dh_silu_mul launch; both at the
-    eager rounding points."""
+    eager rounding points. In bf16, linear_down runs on dh_proj_gemm up to DOWN_GEMM_MAX_ROWS rows."""
 
     use_fused = False
 
@@ -303,11 +305,14 @@ class SwiGLU(nn.Module):
     def forward(self, h):
         if (self.use_fused and h.is_cuda and not torch.is_grad_enabled()
                 and h.dtype in (torch.float32, torch.bfloat16)):                   # dh_silu_mul's dtypes
-            from .fused_gates import fused_swiglu, silu_mul, swiglu_fits
+            from .fused_gates import DOWN_GEMM_MAX_ROWS, fused_swiglu, project, silu_mul, swiglu_fits
             if swiglu_fits(h, self.linear_gate, self.linear_up):
-                return self.linear_down(fused_swiglu(h, self.linear_gate.weight, self.linear_up.weight))
-            g = self.linear_gate(h)
-            return self.linear_down(silu_mul(g, self.linear_up(h), out=g))
+                a = fused_swiglu(h, self.linear_gate.weight, self.linear_up.weight)
+            else:
+                g = self.linear_gate(h)
+                a = silu_mul(g, self.linear_up(h), out=g)
+            # (bf16: the shapes it was measured on; fp32 stays on the library)
+            return project(a, [self.linear_down], DOWN_GEMM_MAX_ROWS if a.dtype == torch.bfloat16 else 0)[0]
         return self.linear_down(F.silu(self.linear_gate(h)) * self.linear_up(h))
 
 

@@ -22,6 +22,11 @@ CASES = [
     (4096, 1024, [1024]),                 # 128 x 64 tiles (an out-projection)
     (1600, 1024, [2048]),                 # 128 x 128 tiles
     (257, 1024, [1024]),
+    # at most 256 / 512 tiles of 64 x 64 keep three / two K tiles in flight (four / three LDS stages)
+    (1024, 1024, [1024]),                 # the C2 out-projection: 256 tiles, four stages
+    (1024, 2816, [1024]),                 # the C2 down projection: four stages, 44 K tiles
+    (2048, 1024, [1024]),                 # 512 tiles, three stages
+    (1500, 192, [1000]),                  # three stages, three K tiles, ragged rows and columns
     # bf16 launches with >= 160 output tiles of 256 x 256 take the persistent 8-wave kernel:
     (4096, 1024, [1024, 1024, 1024]),     # the released mixer (d = gh = 1024) at 4096 rows
     (3840, 1024, [1024, 1024, 1024]),     # the C3 decoder prefill
@@ -69,8 +74,9 @@ def test_proj_gemm_batched_view_and_rejects():
 
 def test_proj_gemm_rows_independent_of_tile_kernel():
     """A row's outputs do not depend on the launch's row count: the 256 x 256 persistent kernel and
-    the 64 x 128 and 64 x 64 tile forms picked for fewer rows form the same sums in the same k
-    order, so the first rows of a 9000-row launch equal those of shorter launches bit for bit."""
+    the 64 x 128, 128 x 64 and 64 x 64 tile forms (two, three or four LDS stages) picked for fewer
+    rows form the same sums in the same k order, so the first rows of a 9000-row launch equal those
+    of shorter launches bit for bit."""
     from dispatcher_hybrid.fused_gates import fused_projections
     g = torch.Generator(device=DEV).manual_seed(11)
     x = torch.randn(9000, 1024, device=DEV, generator=g).to(torch.bfloat16)
@@ -80,6 +86,11 @@ def test_proj_gemm_rows_independent_of_tile_kernel():
         part = fused_projections(x[:M].contiguous(), Ws)
         for o, f in zip(part, full):
             assert torch.equal(o, f[:M]), M
+    # one 1024-wide segment: 128 x 64 tiles (4096 rows, two stages), 64 x 64 tiles in three stages
+    # (2048) and four (1024, 100) against the 64 x 128 tiles of the 9000-row launch
+    full = fused_projections(x, Ws[:1])[0]
+    for M in (4096, 2048, 1024, 100):
+        assert torch.equal(fused_projections(x[:M].contiguous(), Ws[:1])[0], full[:M]), M
 
 
 # ---- dh_proj_gemm_swiglu: SwiGLU's gate and up GEMMs and its activation in one launch

@@ -261,7 +261,7 @@ def test_fused_wrappers_refuse_cpu_tensors():
     assert not fg.swiglu_fits(x, lin, lin)
     assert not fg.projections_fit(x, [lin])
     # on the CPU the routing helper is the library call itself
-    assert torch.equal(fg.project(x, [lin], fg.QKV_GEMM_MAX_ROWS)[0], lin(x))
+    assert torch.equal(fg.project(x, [lin], fg.OUT_GEMM_MAX_ROWS)[0], lin(x))
 
 
 def test_reference_init_scheme():
