@@ -22,6 +22,8 @@
 // so every step keeps enough bytes in flight.
 #include "dh_common.h"
 
+#include <utility>
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -322,6 +324,21 @@ __global__ __launch_bounds__(kThreads) void gate_preacts_fwd_kernel(FwdArgs a) {
 // buffer at its end (one barrier per chunk). Same arithmetic, rounding points and outputs as the
 // kernel above.
 // ---------------------------------------------------------------------------------------------
+// Register sets of the one-level kernel's prefetch: chunks requested two ahead. Measured on MI355X
+// (activated readouts + scan per layer, b = 1, us at T = 1024 / 2048 / 3840): three sets 22.4 /
+// 32.3 / 45.8, four 22.2 / 32.3 / 46.8, five 22.3 / 32.4 / 47.2 (six spill at the occupancy the
+// launch bounds ask for).
+constexpr int kSets = 3;
+static_assert(kSets >= 2, "at least the chunk computed and the one in flight");
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(integral_constant<0>) ... f(integral_constant<N - 1>), unrolled with compile-time indices
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 constexpr int kLdsKC = 64;                      // k elements per LDS weight chunk (2 MFMA k-steps)
 constexpr int kLdsRow = kLdsKC * 2 + 16;         // padded LDS row: 144 bytes
 
@@ -474,11 +491,12 @@ __global__ __launch_bounds__(kThreads, (LdsOcc<LG, MB>::value)) void gate_preact
 
   if constexpr (LG == 1) {
     // One-level tiles (short prefills: one workgroup per CU, nothing else to hide a round trip):
-    // weights and fragments are requested two chunks ahead, in three register sets each, so
+    // weights and fragments are requested kSets - 1 chunks ahead, in kSets register sets each, so
     // neither the compute of chunk c nor the LDS write of c+1's weights waits on a load issued in
-    // chunk c.
-    uint4 zA[2][MB], zB[2][MB][LG];
-    uint4 w0[PPT], w1[PPT], w2[PPT];
+    // the last kSets - 2 chunks. Chunk c computes from set c % kSets, requests chunk c + kSets - 1
+    // into the set chunk c - 1 used, and writes the weights of chunk c + 1 to LDS.
+    constexpr int NS = kSets;
+    uint4 sA[NS][2][MB], sB[NS][2][MB][LG], sW[NS][PPT];
     auto w_fetch3 = [&](int k0, uint4 (&ws)[PPT]) {
       const uint32_t kb = (uint32_t)(k0 * (int)sizeof(T));
 #pragma unroll
@@ -494,34 +512,31 @@ __global__ __launch_bounds__(kThreads, (LdsOcc<LG, MB>::value)) void gate_preact
       for (int i = 0; i < PPT; ++i)
         if (tid + i * kThreads < PIECES) *reinterpret_cast<uint4*>(&wl[buf][wdst[i]]) = ws[i];
     };
-    // chunk c computes from set c % 3, requests chunk c+2 into set (c+2) % 3 (whose chunk c-1 is
-    // done) and writes the weights of c+1 (set (c+1) % 3, requested in chunk c-1) to LDS
-    auto chunk3 = [&](int c, const uint4 (&cA)[2][MB], const uint4 (&cB)[2][MB][LG], uint4 (&fA)[2][MB],
-                      uint4 (&fB)[2][MB][LG], const uint4 (&w_next)[PPT], uint4 (&w_far)[PPT]) {
-      if (c + 2 < nchunk_) {                             // uniform
-        w_fetch3((c + 2) * kLdsKC, w_far);
-        fetch((c + 2) * kLdsKC, fA, fB);
+    auto step = [&](int c, auto uc) {
+      constexpr int u = decltype(uc)::value;             // c % NS
+      constexpr int uf = (u + NS - 1) % NS, un = (u + 1) % NS;
+      if (c + NS - 1 < nchunk_) {                        // uniform
+        w_fetch3((c + NS - 1) * kLdsKC, sW[uf]);
+        fetch((c + NS - 1) * kLdsKC, sA[uf], sB[uf]);
       }
-      compute(cA, cB, c & 1);
-      if (c + 1 < nchunk_) w_store3((c + 1) & 1, w_next);
+      compute(sA[u], sB[u], c & 1);
+      if (c + 1 < nchunk_) w_store3((c + 1) & 1, sW[un]);
       __syncthreads();
     };
-    w_fetch3(0, w0);
-    fetch(0, xA, xB);
-    if (nchunk_ > 1) {
-      w_fetch3(kLdsKC, w1);
-      fetch(kLdsKC, yA, yB);
-    }
-    w_store3(0, w0);
+    static_for<NS - 1>([&](auto uc) {
+      constexpr int u = decltype(uc)::value;
+      if (u < nchunk_) {
+        w_fetch3(u * kLdsKC, sW[u]);
+        fetch(u * kLdsKC, sA[u], sB[u]);
+      }
+    });
+    w_store3(0, sW[0]);
     __syncthreads();
     int c = 0;
-    for (; c + 2 < nchunk_; c += 3) {
-      chunk3(c, xA, xB, zA, zB, w1, w2);
-      chunk3(c + 1, yA, yB, xA, xB, w2, w0);
-      chunk3(c + 2, zA, zB, yA, yB, w0, w1);
-    }
-    if (c < nchunk_) chunk3(c, xA, xB, zA, zB, w1, w2);
-    if (c + 1 < nchunk_) chunk3(c + 1, yA, yB, xA, xB, w2, w0);
+    for (; c + NS - 1 < nchunk_; c += NS) static_for<NS>([&](auto uc) { step(c + decltype(uc)::value, uc); });
+    static_for<NS - 1>([&](auto uc) {
+      if (c + decltype(uc)::value < nchunk_) step(c + decltype(uc)::value, uc);
+    });
   } else {
     w_fetch(0);
     fetch(0, xA, xB);
