@@ -379,7 +379,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void proj_gemm_pp_kernel(GemmArgs a
     issue(0, 0);
 #pragma unroll
     for (int q = 1; q + 1 < S; ++q) issue(min(q, nk - 1), q);
-    if (pm0 >= 0) {                                    // under K tile 0's loads
+    const bool first = pm0 < 0;                        // uniform: no output of this workgroup yet
+    if (!first) {                                      // under K tile 0's loads
       if constexpr (SWI) store_tile_swiglu<TM, TN, WGM>(a, acc, pm0, pn0, wm, wn, r, g);
       else store_tile_x4<TM, TN, WGM>(a, acc, pm0, pn0, wm, wn, r, g);
     }
@@ -389,7 +390,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void proj_gemm_pp_kernel(GemmArgs a
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int i = 0; i < TM; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    wait_vm<0>();                                      // K tiles 0 .. S-2 (and the stores) done
+    // K tile 0 has landed: in a workgroup's first tile only loads are in flight and they complete in
+    // issue order, so tiles 1 .. S-2 may still be on their way; after an output, everything
+    if (first) wait_vm<(S - 2) * PER>();
+    else wait_vm<0>();
     __syncthreads();
     issue(min(S - 1, nk - 1), S - 1);
     read(aw, ax, 0, c0);
