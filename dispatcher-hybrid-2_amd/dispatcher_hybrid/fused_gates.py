@@ -460,7 +460,8 @@ def tree_mask(input_ids, levels, eot, dtype):
     b, T = input_ids.shape
     if not (1 <= levels <= TREE_MASK_MAX_LEVELS) or T > TREE_MASK_MAX_LEN:
         raise ValueError(f"tree_mask: levels={levels} (1..{TREE_MASK_MAX_LEVELS}), T={T} (<= {TREE_MASK_MAX_LEN})")
-    ids = input_ids if input_ids.stride(1) == 1 else input_ids.contiguous()
+    # rows of unit stride at least T apart (an expanded batch, stride 0, is copied)
+    ids = input_ids if input_ids.stride(1) == 1 and input_ids.stride(0) >= T else input_ids.contiguous()
     out = torch.empty(b, T, levels, device=ids.device, dtype=dtype)
     if b == 0 or T == 0:
         return out

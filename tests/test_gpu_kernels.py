@@ -712,6 +712,10 @@ def test_tree_mask_strided_ids_and_rejects():
     assert view.stride(0) == 512
     got = tree_mask(view, 9, eot, torch.float32)
     assert torch.equal(got.cpu(), torch.as_tensor(om.tree_mask(ids, 9, eot)).float())
+    # an expanded batch (row stride 0) is read as the repeated row
+    one = torch.as_tensor(ids[:1], dtype=torch.int64, device=DEV).expand(3, -1)
+    got = tree_mask(one, 9, eot, torch.bfloat16)
+    assert torch.equal(got.cpu(), torch.as_tensor(om.tree_mask(np.repeat(ids[:1], 3, 0), 9, eot)).to(torch.bfloat16))
     t = torch.as_tensor(ids, device=DEV)
     with pytest.raises(ValueError):
         tree_mask(t.to(torch.int32), 9, eot, torch.float32)
