@@ -444,7 +444,8 @@ def fused_swiglu(x, w_gate, w_up):
     return out
 
 
-TREE_MASK_MAX_LEN = 16384          # the kernel keeps a row's EOT counts in LDS
+TREE_MASK_MAX_LEN = 16384
+TREE_MASK_MAX_ROWS = 65535
 TREE_MASK_MAX_LEVELS = 30
 
 
@@ -458,8 +459,9 @@ def tree_mask(input_ids, levels, eot, dtype):
     if input_ids.dim() != 2 or input_ids.dtype != torch.int64 or dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("tree_mask: (b, T) int64 input_ids and a float32 or bfloat16 mask dtype")
     b, T = input_ids.shape
-    if not (1 <= levels <= TREE_MASK_MAX_LEVELS) or T > TREE_MASK_MAX_LEN:
-        raise ValueError(f"tree_mask: levels={levels} (1..{TREE_MASK_MAX_LEVELS}), T={T} (<= {TREE_MASK_MAX_LEN})")
+    if not (1 <= levels <= TREE_MASK_MAX_LEVELS) or T > TREE_MASK_MAX_LEN or b > TREE_MASK_MAX_ROWS:
+        raise ValueError(f"tree_mask: levels={levels} (1..{TREE_MASK_MAX_LEVELS}), T={T} (<= {TREE_MASK_MAX_LEN}), "
+                         f"b={b} (<= {TREE_MASK_MAX_ROWS})")
     # rows of unit stride at least T apart (an expanded batch, stride 0, is copied)
     ids = input_ids if input_ids.stride(1) == 1 and input_ids.stride(0) >= T else input_ids.contiguous()
     out = torch.empty(b, T, levels, device=ids.device, dtype=dtype)

@@ -419,8 +419,9 @@ class DispatcherHybridForCausalLM(DispatcherPreTrainedModel, GenerationMixin):
         dtype = self.embedding.weight.dtype
         if (self.config.doc_reset and getattr(self, "_fused_norms", False) and input_ids.is_cuda
                 and input_ids.dtype == torch.int64 and dtype in (torch.float32, torch.bfloat16)):
-            from .fused_gates import TREE_MASK_MAX_LEN, TREE_MASK_MAX_LEVELS, tree_mask
-            if length <= TREE_MASK_MAX_LEN and 1 <= self.config.levels <= TREE_MASK_MAX_LEVELS:
+            from .fused_gates import TREE_MASK_MAX_LEN, TREE_MASK_MAX_LEVELS, TREE_MASK_MAX_ROWS, tree_mask
+            if (length <= TREE_MASK_MAX_LEN and 1 <= self.config.levels <= TREE_MASK_MAX_LEVELS
+                    and input_ids.shape[0] <= TREE_MASK_MAX_ROWS):
                 # the same 0/1 values in one launch (dh_tree_mask) instead of the eight below
                 return tree_mask(input_ids, self.config.levels, self.config.eot_token, dtype)
         mask = self.level_mask(length, input_ids.device, dtype)

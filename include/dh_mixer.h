@@ -162,7 +162,8 @@ int dh_proj_gemm_swiglu(int dtype, const void* X, int64_t ldx, int M, int K, con
  * Replaces the torch computation of the level mask times "source and destination in the same
  * document" (reference dispatcher_hybrid/modeling_dispatcher.py:282-297, 311-323: doc(t) counts the
  * EOTs before t; the edge t <- t - 2^l is kept iff doc(t) == doc(t - 2^l)). ids int64 (b, T) with row
- * stride ids_stride >= T; dtype DH_F32 or DH_BF16 (the mask's dtype); T <= 16384, L <= 30.
+ * stride ids_stride >= T; dtype DH_F32 or DH_BF16 (the mask's dtype); T <= 16384, L <= 30, b <= 65535;
+ * out 16-byte aligned.
  */
 int dh_tree_mask(int dtype, const int64_t* ids, int64_t ids_stride, int b, int T, int L, int64_t eot, void* out,
                  void* stream);
