@@ -253,8 +253,9 @@ def test_fused_wrappers_refuse_cpu_tensors():
     from dispatcher_hybrid import fused_gates as fg
     x = torch.randn(4, 64, dtype=torch.bfloat16)
     w = torch.randn(8, 64, dtype=torch.bfloat16)
+    ids = torch.zeros(2, 16, dtype=torch.int64)
     for call in (lambda: fg.fused_swiglu(x, w, w), lambda: fg.fused_projections(x, [w]),
-                 lambda: fg.silu_mul(x, x)):
+                 lambda: fg.silu_mul(x, x), lambda: fg.tree_mask(ids, 4, 7, torch.bfloat16)):
         with pytest.raises(RuntimeError, match="must be on the GPU"):
             call()
     lin = torch.nn.Linear(64, 8, bias=False).to(torch.bfloat16)
