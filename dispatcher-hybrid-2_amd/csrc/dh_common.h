@@ -82,6 +82,16 @@ __device__ __forceinline__ float dh_silu_exact(float x) { return x / (1.0f + exp
 // torch's bf16 SiLU bit for bit (an exhaustive test covers all 65536 patterns). The IEEE divide
 // stays: a reciprocal with one residual correction differs at x = -87.5 .. -88.5 and +inf.
 __device__ __forceinline__ float dh_silu_bf16in(float x) { return x / (1.0f + __expf(-x)); }
+// The same as dh_silu_bf16in with x times the reciprocal of 1 + e^-x refined by one Newton step in
+// place of the IEEE divide (~6 instructions fewer): equal to it after rounding to bf16 for every
+// bf16 input x >= -87 (exhaustive test; without the Newton step one input, 5.9375, rounds the other
+// way). Below -87 the reciprocal leaves the normal range: callers take dh_silu_bf16in for any group
+// of values holding such an input.
+__device__ __forceinline__ float dh_silu_bf16in_rcp(float x) {
+  const float d = 1.0f + __expf(-x);
+  const float r = __builtin_amdgcn_rcpf(d);
+  return x * __builtin_fmaf(r, __builtin_fmaf(-d, r, 1.0f), r);
+}
 
 // DPP lane move of a float: lanes in the rows of ROWMASK read the lane CTRL selects, others get 0
 template <int CTRL, int ROWMASK>

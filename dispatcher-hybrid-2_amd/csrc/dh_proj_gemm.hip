@@ -253,24 +253,37 @@ __device__ __forceinline__ void store_tile_swiglu(const GemmArgs& a, const f32x4
   static_assert(TN % 2 == 0, "gate and up column tiles in pairs");
   bf16_t* o = (bf16_t*)a.out[0];
   const int64_t ld = a.ldo[0];
+  auto out = [&](auto silu) {
 #pragma unroll
-  for (int p = 0; p < TN / 2; ++p) {
-    const int f = n0 / 2 + wn * 8 * TN + p * 16 + 4 * g;
+    for (int p = 0; p < TN / 2; ++p) {
+      const int f = n0 / 2 + wn * 8 * TN + p * 16 + 4 * g;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int m = m0 + wm * 16 * TM + i * 16 + r;
-      const f32x4& G = acc[p][i];
-      const f32x4& U = acc[p + TN / 2][i];
-      float h[4];
+      for (int i = 0; i < TM; ++i) {
+        const int m = m0 + wm * 16 * TM + i * 16 + r;
+        const f32x4& G = acc[p][i];
+        const f32x4& U = acc[p + TN / 2][i];
+        float h[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        h[e] = Elem<bf16_t>::round(Elem<bf16_t>::round(dh_silu_bf16in(Elem<bf16_t>::round(G[e]))) *
-                                   Elem<bf16_t>::round(U[e]));
-      const uint32_t lo = (uint32_t)f32_to_bf16(h[0]) | ((uint32_t)f32_to_bf16(h[1]) << 16);
-      const uint32_t hi = (uint32_t)f32_to_bf16(h[2]) | ((uint32_t)f32_to_bf16(h[3]) << 16);
-      if (m < a.M && f < a.N[0]) *reinterpret_cast<uint2*>(o + (int64_t)m * ld + f) = make_uint2(lo, hi);
+        for (int e = 0; e < 4; ++e)
+          h[e] = Elem<bf16_t>::round(Elem<bf16_t>::round(silu(Elem<bf16_t>::round(G[e]))) * Elem<bf16_t>::round(U[e]));
+        const uint32_t lo = (uint32_t)f32_to_bf16(h[0]) | ((uint32_t)f32_to_bf16(h[1]) << 16);
+        const uint32_t hi = (uint32_t)f32_to_bf16(h[2]) | ((uint32_t)f32_to_bf16(h[3]) << 16);
+        if (m < a.M && f < a.N[0]) *reinterpret_cast<uint2*>(o + (int64_t)m * ld + f) = make_uint2(lo, hi);
+      }
     }
-  }
+  };
+  // the reciprocal form unless some gate output of the wave's tile is below -87 (one uniform branch)
+  float gmin = 0.f;
+#pragma unroll
+  for (int p = 0; p < TN / 2; ++p)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) gmin = fminf(gmin, acc[p][i][e]);
+  if (__builtin_amdgcn_ballot_w64(gmin < -87.0f))
+    out([](float x) { return dh_silu_bf16in(x); });
+  else
+    out([](float x) { return dh_silu_bf16in_rcp(x); });
 }
 
 // Fragment ping-pong variant (bf16, S LDS stages: S - 1 K tiles in flight while one is multiplied;

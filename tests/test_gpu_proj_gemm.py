@@ -138,6 +138,25 @@ def test_proj_gemm_swiglu_equals_gemms_then_silu_mul(case):
     assert bool(((h.double() - exact).abs() <= bound).all())
 
 
+def test_proj_gemm_swiglu_extreme_gates():
+    """Gate outputs far below zero (rows of x scaled by 60, so some gates pass -87, where the epilogue
+    takes the IEEE divide instead of the refined reciprocal for the whole tile) and rows of ordinary
+    size: bit-identical to the two GEMMs followed by dh_silu_mul in both cases."""
+    from dispatcher_hybrid.fused_gates import fused_swiglu
+    g = torch.Generator(device=DEV).manual_seed(31)
+    M, K, N = 1024, 1024, 2816
+    x = torch.randn(M, K, device=DEV, generator=g)
+    x[::7] *= 60.0                                  # every seventh row: |gate| up to several hundred
+    x = x.to(torch.bfloat16)
+    wg = (torch.randn(N, K, device=DEV, generator=g) / K ** 0.5).to(torch.bfloat16)
+    wu = (torch.randn(N, K, device=DEV, generator=g) / K ** 0.5).to(torch.bfloat16)
+    h = fused_swiglu(x, wg, wu)
+    ref = _swiglu_ref(x, wg, wu)
+    gate = x.float() @ wg.float().T
+    assert float(gate.min()) < -87.0                # the divide branch is taken somewhere
+    assert torch.equal(h, ref)
+
+
 def test_proj_gemm_swiglu_rows_independent_of_tile_kernel():
     """As the plain GEMM: the first rows of a 5000-row launch (persistent kernel) equal those of
     shorter launches (128 x 64, 128 x 128 and 64 x 64 tiles) bit for bit."""
