@@ -157,6 +157,35 @@ def test_proj_gemm_swiglu_extreme_gates():
     assert torch.equal(h, ref)
 
 
+def test_proj_gemm_swiglu_every_bf16_gate():
+    """The epilogue's SiLU over every bf16 gate value: x one-hot, W_gate's first column the 65536 bf16
+    bit patterns and W_up's ones, so gate = the pattern and up = 1 exactly, and the output is
+    round(silu(gate)). Equal to torch's bf16 SiLU bit for bit at every pattern (NaN where torch gives
+    NaN), in tiles on the refined reciprocal and in the tiles holding gates below -87 (the divide).
+    Subnormal gates are left out (the matrix cores flush them to zero), and so is -0: a sum that
+    starts from +0 gives +0 for it, as the library GEMM does."""
+    from dispatcher_hybrid.fused_gates import fused_swiglu
+    M, K, N = 16, 64, 65536
+    x = torch.zeros(M, K, device=DEV, dtype=torch.bfloat16)
+    x[:, 0] = 1.0
+    pat = torch.arange(N, device=DEV, dtype=torch.int32).to(torch.int16)
+    wg = torch.zeros(N, K, device=DEV, dtype=torch.bfloat16)
+    wg[:, 0] = pat.view(torch.bfloat16)
+    wu = torch.zeros(N, K, device=DEV, dtype=torch.bfloat16)
+    wu[:, 0] = 1.0
+    h = fused_swiglu(x, wg, wu)[0]
+    gate = pat.view(torch.bfloat16)
+    ref = torch.nn.functional.silu(gate)
+    bits = torch.arange(N, device=DEV)
+    normal = ((bits >> 7) & 0xff) != 0                    # exponent field non-zero (or zero mantissa)
+    normal |= (bits & 0x7f) == 0
+    normal[0x8000] = False                               # -0: the GEMM's sum is +0
+    nan_h, nan_r = torch.isnan(h), torch.isnan(ref)
+    assert torch.equal(nan_h[normal], nan_r[normal])
+    keep = normal & ~nan_r
+    assert torch.equal(h[keep].view(torch.int16), ref[keep].view(torch.int16))
+
+
 def test_proj_gemm_swiglu_rows_independent_of_tile_kernel():
     """As the plain GEMM: the first rows of a 5000-row launch (persistent kernel) equal those of
     shorter launches (128 x 64, 128 x 128 and 64 x 64 tiles) bit for bit."""
