@@ -55,6 +55,10 @@ struct GemvArgs {
   int B, K, Nrows;
   Cand* cand;                   // nullable (B = 1): the launch's argmax candidate per workgroup
   int tile_rows;                // batched matrix-core GEMV: real weight rows per 16-row MFMA tile (16 or 8)
+  // batched matrix-core GEMV, 16-row MFMA fragment order (16-byte chunk (s * 64 + 16 g + r) holds
+  // row r's elements s * 32 + 8 g .. + 7): frag_out writes the outputs so (a SwiGLU launch's h),
+  // frag_in reads the activations so, one contiguous 1 KB per wave and k-step
+  int frag_out, frag_in;
 };
 
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
@@ -754,13 +758,17 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
   uint4 xs[XC], gv[GC], wf[NW][KSW], xd[KSW], gd[KSW];
   uint32_t rres[4] = {0u, 0u, 0u, 0u};
   if constexpr (!GA) {
-    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, (uint32_t)(((int64_t)(B - 1) * a.x_bstride + K) * 2));
+    const __amdgpu_buffer_rsrc_t rx =
+        buf_rsrc(a.x, a.frag_in ? (uint32_t)(K * 32) : (uint32_t)(((int64_t)(B - 1) * a.x_bstride + K) * 2));
     if constexpr (DX) {
       // this lane's A fragments: batch row r (zeros past B), 16 bytes of each of the wave's k-steps
+      // (in fragment order: chunk (s * 64 + lane), so a wave's request is one contiguous 1 KB)
 #pragma unroll
       for (int j = 0; j < KSW; ++j) {
         const uint32_t off = j < my_steps && r < B
-                                 ? (uint32_t)(((int64_t)r * a.x_bstride + (s0 + j) * 32 + 8 * g) * 2) : kOOB;
+                                 ? (a.frag_in ? (uint32_t)(((s0 + j) * 64 + lane) * 16)
+                                              : (uint32_t)(((int64_t)r * a.x_bstride + (s0 + j) * 32 + 8 * g) * 2))
+                                 : kOOB;
         xd[j] = bld16(rx, off);
       }
       // the norm weight's fragments of the same k-steps (no norm: an empty resource, no requests)
@@ -958,7 +966,11 @@ __global__ __launch_bounds__(64 * KSPLIT * TPW) void decode_gemv_mfma_kernel(Gem
         out = Elem<bf16_t>::round(v[0][i]);
         if (a.resid) out = Elem<bf16_t>::round(out + Raw<bf16_t>::f(rres[i]));
       }
-      Elem<bf16_t>::store(out_ptr<bf16_t>(a, seg0.s, b, t, loc), out);
+      if (a.frag_out)                                  // fragment order (one segment, no t_stride)
+        ((bf16_t*)a.seg[0].out)[((((int64_t)(loc >> 5) * 64 + ((loc >> 3) & 3) * 16 + b)) << 3) + (loc & 7)] =
+            f32_to_bf16(out);
+      else
+        Elem<bf16_t>::store(out_ptr<bf16_t>(a, seg0.s, b, t, loc), out);
     }
   }
   advance_position(a);
@@ -1333,9 +1345,12 @@ extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const
                               const void* norm_w, float eps, int nseg, const void* const* W,
                               void* const* out, const int64_t* out_bstride, const int64_t* out_t_stride,
                               const int* N, const void* resid, int64_t resid_bstride,
-                              const int64_t* resid_rows, int swiglu, const int64_t* t_dev, int64_t* t_advance,
+                              const int64_t* resid_rows, int flags, const int64_t* t_dev, int64_t* t_advance,
                               void* argmax_cand, int B, int K, void* stream) {
   const char* who = "dh_decode_gemv";
+  DH_REQUIRE(flags >= 0 && flags <= 7, DH_ERR_INVALID_ARG, "%s: flags %d", who, flags);
+  const int swiglu = flags & DH_GEMV_SWIGLU;
+  const bool frag_out = (flags & DH_GEMV_FRAG_OUT) != 0, frag_in = (flags & DH_GEMV_FRAG_IN) != 0;
   DH_REQUIRE(dtype == DH_F32 || dtype == DH_BF16, DH_ERR_UNSUPPORTED_DTYPE, "%s: dtype %d", who, dtype);
   const int vec = dtype == DH_BF16 ? 8 : 4;             // elements per 16-byte chunk
   DH_REQUIRE(B >= 1 && K >= vec && K % vec == 0, DH_ERR_UNSUPPORTED_SHAPE,
@@ -1386,6 +1401,22 @@ extern "C" int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const
   const int esz = dtype == DH_BF16 ? 2 : 4;
   const int R = rows_per_wave(B, a.Nrows, K, esz, swiglu != 0);
   hipStream_t s = (hipStream_t)stream;
+  if (frag_out || frag_in) {
+    // fragment order exists on the batched matrix-core path only, with the rows in place (the kernels
+    // that read their activation fragments straight from memory), and not on the persistent
+    // vocabulary-head form (many tiles without a residual), which stages its rows
+    DH_REQUIRE(dtype == DH_BF16 && !argmax_cand && !x_rows && !resid_rows && mfma_gemv_fits(a, swiglu != 0) &&
+                   (swiglu || resid || (a.Nrows + 15) / 16 < 4 * 512),
+               DH_ERR_INVALID_ARG,
+               "%s: fragment-ordered activations need the batched matrix-core path (bf16, 2 <= B <= 16, rows in place)",
+               who);
+    DH_REQUIRE(!frag_out || (swiglu && out_t_stride[0] == 0 && N[0] % 32 == 0), DH_ERR_INVALID_ARG,
+               "%s: fragment-ordered outputs need a SwiGLU launch with N a multiple of 32 and no t_stride", who);
+    DH_REQUIRE(!frag_in || (K % 32 == 0 && aligned(x, 16)), DH_ERR_INVALID_ARG,
+               "%s: fragment-ordered activations need K a multiple of 32", who);
+    a.frag_out = frag_out;
+    a.frag_in = frag_in;
+  }
   if (dtype == DH_BF16 && !argmax_cand && mfma_gemv_fits(a, swiglu != 0)) {
     if (swiglu) launch_mfma<true>(a, s); else launch_mfma<false>(a, s);
     return dh_check_launch(who);

@@ -15,7 +15,7 @@ import os
 
 import torch
 
-ABI_VERSION = 18
+ABI_VERSION = 19
 _LIB_NAME = "libdh_mixer.so"
 
 DH_F32, DH_BF16 = 0, 1

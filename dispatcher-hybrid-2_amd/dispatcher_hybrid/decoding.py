@@ -440,7 +440,12 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         self.x_buf = z(cfg.d_model)            # residual stream
         self.v0_buf, self.y_buf = z(cfg.d_model), z(cfg.d_model)
         self.a_buf = z(gh)
-        self.h_buf = z(cfg.dim_feedforward)
+        # the feed-forward's hidden row, written by the up launch and read only by the down launch:
+        # on the batched matrix-core path it is kept in MFMA fragment order, (16, ff) whatever the batch
+        ff = cfg.dim_feedforward
+        self._ffn_frag = (dt == torch.bfloat16 and 2 <= Bb <= 16 and ff % 32 == 0 and ff <= 4096
+                          and cfg.d_model % 32 == 0 and cfg.d_model <= 2048)
+        self.h_buf = torch.zeros(16, ff, device=dev, dtype=dt) if self._ffn_frag else z(ff)
         self.q_buf, self.k_buf, self.v_buf = z(cfg.d_model), z(cfg.d_model), z(cfg.d_model)
         # staging of the two-launch mixer step, shared by every tree layer (same shapes)
         self.stage = torch.zeros(self._fused_step.stage_floats(Bb, mix0.num_heads, mix0.levels,
@@ -577,11 +582,13 @@ class FusedGraphedHybridDecoder(GraphedHybridDecoder):
         fs = self._fused_step
         f, d = blk.ffn, self.x_buf.shape[1]
         ff = self.h_buf.shape[1]
+        fr = self._ffn_frag
         fs.decode_gemv(self.x_buf, [(f.linear_gate.weight, self.h_buf, ff, 0),
                                     (f.linear_up.weight, self.h_buf, ff, 0)], self.t_buf,
-                       norm_weight=blk.norm2.weight, eps=self._eps(blk.norm2, self.dtype), swiglu=True)
-        fs.decode_gemv(self.h_buf, [(f.linear_down.weight, self.x_buf, d, 0)], self.t_buf,
-                       resid=self.x_buf)
+                       norm_weight=blk.norm2.weight, eps=self._eps(blk.norm2, self.dtype), swiglu=True,
+                       frag_out=fr)
+        h = self.h_buf[:self.x_buf.shape[0]] if fr else self.h_buf   # B rows for the launch's batch size
+        fs.decode_gemv(h, [(f.linear_down.weight, self.x_buf, d, 0)], self.t_buf, resid=self.x_buf, frag_in=fr)
 
     def _input(self, first):
         """The block's input rows: the embedding rows of the tokens for the first block."""

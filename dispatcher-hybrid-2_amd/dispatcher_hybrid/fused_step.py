@@ -83,7 +83,7 @@ def decode_mixer_step(A, B_hist, Wi, Wf, Wr, bi, bf, br, t_buf, rg_hist, V_ring,
 
 
 def decode_gemv(x, segments, t_buf, norm_weight=None, eps=None, resid=None, swiglu=False,
-                x_rows=None, resid_rows=None, t_advance=None, argmax_cand=None):
+                x_rows=None, resid_rows=None, t_advance=None, argmax_cand=None, frag_out=False, frag_in=False):
     """Fused matrix-vector products of the decode step (``dh_decode_gemv``).
 
     x: (B, K) activations (or the embedding table with ``x_rows`` = token ids: row b is
@@ -96,6 +96,9 @@ def decode_gemv(x, segments, t_buf, norm_weight=None, eps=None, resid=None, swig
     decode step's position advance, folded into its last launch; outputs may then not use
     t_stride). argmax_cand: a buffer of ``gemv_candidates(dtype, N, K)`` 8-byte records (batch 1,
     one plain segment) that receives each workgroup's best (value, row) for ``argmax_reduce``.
+    frag_out (a SwiGLU launch) / frag_in: the output / x in 16-row MFMA fragment order -- a (16, N)
+    buffer whatever the batch, element (b, n) at ((n // 32) * 64 + (n // 8 % 4) * 16 + b) * 8 + n % 8
+    -- for a hidden row only the next launch reads (bf16, 2 <= B <= 16; see the C header).
     Everything in one dtype (fp32 or bf16) on one GPU.
     """
     _hip.require_gpu(x, "decode_gemv")
@@ -117,7 +120,8 @@ def decode_gemv(x, segments, t_buf, norm_weight=None, eps=None, resid=None, swig
     st = _hip.lib.dh_decode_gemv(
         _hip.dtype_code(dt), p(x), x.stride(0), p(x_rows), p(norm_weight), float(eps or 0.0), n,
         Ws, outs, obs, ots, Ns, p(resid), resid.stride(0) if resid is not None else 0, p(resid_rows),
-        int(bool(swiglu)), p(t_buf), p(t_advance), p(argmax_cand), B, K, _hip.stream_handle(x.device))
+        int(bool(swiglu)) | (2 if frag_out else 0) | (4 if frag_in else 0), p(t_buf), p(t_advance),
+        p(argmax_cand), B, K, _hip.stream_handle(x.device))
     _hip.check(st, "dh_decode_gemv")
 
 

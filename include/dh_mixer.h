@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define DH_ABI_VERSION 18
+#define DH_ABI_VERSION 19
 
 enum dh_status {
   DH_OK = 0,
@@ -229,11 +229,22 @@ int dh_decode_mixer_step(int dtype, const void* A, const void* B_hist, const voi
  * All activations and weights in dtype; fp32 accumulation. The array arguments W, out, out_bstride,
  * out_t_stride and N are host arrays of nseg entries. K must be a multiple of 8 (bf16) or 4 (fp32):
  * rows are read in 16-byte chunks.
+ * flags: DH_GEMV_SWIGLU (the swiglu form above); DH_GEMV_FRAG_OUT: a SwiGLU launch writes out[0] in
+ * 16-row MFMA fragment order instead of rows -- element (b, n) at ((n/32)*64 + ((n/8)%4)*16 + b)*8
+ * + n%8, a (16, N) buffer whatever B is (N a multiple of 32, out_t_stride[0] = 0); DH_GEMV_FRAG_IN:
+ * x is read in that order (x_bstride ignored). Both only on the batched matrix-core path (bf16,
+ * 2 <= B <= 16, rows in place, K a multiple of 32, no argmax_cand); a launch outside it with either
+ * flag is rejected. The decoder's feed-forward uses them for its hidden row h (up: FRAG_OUT, down:
+ * FRAG_IN), which nothing else reads: each wave then requests its activation fragments as one
+ * contiguous 1 KB per k-step (batch-16 down projection 7.6 -> 6.4 us per launch).
  */
+#define DH_GEMV_SWIGLU 1
+#define DH_GEMV_FRAG_OUT 2
+#define DH_GEMV_FRAG_IN 4
 int dh_decode_gemv(int dtype, const void* x, int64_t x_bstride, const int64_t* x_rows,
                    const void* norm_w, float eps, int nseg, const void* const* W, void* const* out,
                    const int64_t* out_bstride, const int64_t* out_t_stride, const int* N,
-                   const void* resid, int64_t resid_bstride, const int64_t* resid_rows, int swiglu,
+                   const void* resid, int64_t resid_bstride, const int64_t* resid_rows, int flags,
                    const int64_t* t_dev, int64_t* t_advance, void* argmax_cand, int B, int K,
                    void* stream);
 
