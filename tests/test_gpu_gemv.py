@@ -250,3 +250,41 @@ def test_position_advance(B):
     torch.cuda.synchronize()
     assert int(pos.item()) == 10 and int(t_buf.item()) == 41
     assert rel_err(out, x.double() @ W.double().T) < 1e-5
+
+
+@pytest.mark.parametrize("B", [2, 5, 16])
+def test_ffn_fragment_order_equals_rows(B):
+    """The decoder's feed-forward with its hidden row in MFMA fragment order (the SwiGLU launch writes
+    h as (16, ff) chunks, the down projection reads them contiguously) gives the same bits as the row
+    layout, and h itself is the row-layout h reordered; launches off the batched matrix-core path
+    reject the flags."""
+    from dispatcher_hybrid import fused_step as fs
+    g = torch.Generator(device=DEV).manual_seed(B)
+    d, ff = 1024, 2816
+    dt = torch.bfloat16
+    x = torch.randn(B, d, device=DEV, generator=g).to(dt)
+    nw = (torch.rand(d, device=DEV, generator=g) + 0.5).to(dt)
+    wg = (torch.randn(ff, d, device=DEV, generator=g) * 0.03).to(dt)
+    wu = (torch.randn(ff, d, device=DEV, generator=g) * 0.03).to(dt)
+    wd = (torch.randn(d, ff, device=DEV, generator=g) * 0.02).to(dt)
+    res = torch.randn(B, d, device=DEV, generator=g).to(dt)
+    t_buf = torch.zeros(1, dtype=torch.long, device=DEV)
+    h_rows = torch.zeros(B, ff, device=DEV, dtype=dt)
+    fs.decode_gemv(x, [(wg, h_rows, ff, 0), (wu, h_rows, ff, 0)], t_buf, norm_weight=nw, swiglu=True)
+    out_rows = res.clone()
+    fs.decode_gemv(h_rows, [(wd, out_rows, d, 0)], t_buf, resid=out_rows)
+    h_frag = torch.zeros(16, ff, device=DEV, dtype=dt)
+    fs.decode_gemv(x, [(wg, h_frag, ff, 0), (wu, h_frag, ff, 0)], t_buf, norm_weight=nw, swiglu=True, frag_out=True)
+    out_frag = res.clone()
+    fs.decode_gemv(h_frag[:B], [(wd, out_frag, d, 0)], t_buf, resid=out_frag, frag_in=True)
+    torch.cuda.synchronize()
+    # element (b, n) of the fragment layout: chunk (n // 32) * 64 + (n // 8 % 4) * 16 + b, offset n % 8
+    n = torch.arange(ff, device=DEV)
+    for b in range(B):
+        idx = ((n // 32) * 64 + (n // 8 % 4) * 16 + b) * 8 + n % 8
+        assert torch.equal(h_frag.view(-1)[idx], h_rows[b])
+    assert torch.equal(out_frag, out_rows)
+    with pytest.raises(ValueError):                   # batch 1 runs the row kernel: no fragment order
+        fs.decode_gemv(h_frag[:1], [(wd, out_frag[:1], d, 0)], t_buf, resid=out_frag[:1], frag_in=True)
+    with pytest.raises(ValueError):                   # fragment-ordered outputs only from a SwiGLU launch
+        fs.decode_gemv(x, [(wu, h_frag, ff, 0)], t_buf, norm_weight=nw, frag_out=True)
