@@ -57,16 +57,21 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(const T* x, const
   const int64_t row = (int64_t)blockIdx.x * kRowsPerWG + (threadIdx.x >> 6);
   if (row >= rows) return;  // the whole wave leaves; the kernel has no barrier
   const int64_t base = row * (int64_t)d;
-  uint4 xv[NCH], yv[NCH];
+  // the norm weight is requested with the rows: xo may alias w for the compiler, so a load of w
+  // after the xo stores would wait for them (two more round trips per row; 2.91 -> 2.75 us per
+  // launch at 1024 x 1024 bf16 in captured graphs)
+  uint4 xv[NCH], yv[NCH], wv[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int e = (c * 64 + lane) * V;
     if (EXACT || e < d) {
       xv[c] = *reinterpret_cast<const uint4*>(x + base + e);
       yv[c] = *reinterpret_cast<const uint4*>(y + base + e);
+      wv[c] = *reinterpret_cast<const uint4*>(w + e);
     } else {
       xv[c] = make_uint4(0, 0, 0, 0);
       yv[c] = xv[c];
+      wv[c] = xv[c];
     }
   }
   float v[NCH][V];
@@ -92,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(const T* x, const
     const int e = (c * 64 + lane) * V;
     if (EXACT || e < d) {
       float wf[V];
-      Pack16<T>::unpack(*reinterpret_cast<const uint4*>(w + e), wf);
+      Pack16<T>::unpack(wv[c], wf);
 #pragma unroll
       for (int j = 0; j < V; ++j) wf[j] = (v[c][j] * rstd) * wf[j];
       *reinterpret_cast<uint4*>(ho + base + e) = Pack16<T>::pack(wf);
